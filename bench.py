@@ -1,0 +1,235 @@
+"""Benchmark of the Qwen2 token loop on one MI355X.
+
+Headline (BASELINE.json metric): decode throughput of the Qwen2.5-3B-shape
+model (random-init bf16 weights, tied embeddings) at batch 40 with
+600-token prompts, measured with the reference harness's formula
+(test/generate_token.py:58-67): the timed window holds K forwards of the
+batch -- the prefill forward plus K-1 greedy decode steps -- and
+value = K * 40 / wall seconds. One "step" is one forward of the batch.
+W untimed warmup forwards run first on a separate batch (the reference warms
+up with one prefill, generate_token.py:43-48).
+
+Also reported on the same JSON line:
+  roofline      paged decode attention at the BASELINE config-2 shape
+                (40 seqs x 600 ctx, H 12 / KVH 2, D 128, bf16, random slot
+                permutation), cycling 28 independent pools (688 MB > the
+                256 MB MALL), HIP events on the launch stream;
+  decode_step   bytes and time of the steady decode step;
+  cpu_baseline  the CPU oracle (oracle/qwen2.py) timed on the host cores
+                on a bounded sample of the same decode workload.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+HBM_PEAK_GBS = 8000.0
+B, PROMPT = 40, 600
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# ------------------------------------------------------------------ attention
+def bench_decode_attention(dev, iters=200, pools=28):
+    """Config 2: returns (avg seconds per launch, algorithmic bytes per launch)."""
+    from lite_lang_amd import ops
+    H, KVH, D, L = 12, 2, 128, 600
+    P = B * L
+    g = torch.Generator(device=dev).manual_seed(0)
+    q = torch.randn(B, H, D, generator=g, device=dev).bfloat16()
+    pool_list = [torch.randn(P, 2 * KVH, D, generator=g, device=dev).bfloat16() for _ in range(pools)]
+    perm = torch.from_numpy(np.random.RandomState(0).permutation(P).astype(np.int32)).view(B, L).to(dev)
+    rids = torch.arange(B, dtype=torch.int32, device=dev)
+    lens = torch.full((B,), L, dtype=torch.int64, device=dev)
+    out = torch.empty_like(q)
+
+    def launch(i):
+        p = pool_list[i % pools]
+        ops.decode_attention(q, perm, rids, lens, L, p[:, :KVH], p[:, KVH:], out)
+
+    for i in range(2 * pools):
+        launch(i)
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for i in range(iters):
+        launch(i)
+    e1.record(st)
+    torch.cuda.synchronize()
+    sec = e0.elapsed_time(e1) / 1e3 / iters
+    nbytes = B * L * 2 * KVH * D * 2 + 2 * B * H * D * 2 + B * L * 4 + B * 8
+    return sec, nbytes
+
+
+# ------------------------------------------------------------------ model
+def build_runner(dev, cfg, max_length, seed=0):
+    from lite_lang_amd.models.qwen2 import Qwen2ModelRunner
+    kv_slots = B * max_length * 2 + 1024
+    runner = Qwen2ModelRunner(cfg.layer_nums, B, cfg, tp_rank=0, world_size=1, model_path=None,
+                              max_length=max_length, mem_usage=0.5, use_radix_cache=False,
+                              dtype=torch.bfloat16, seed=seed, kv_max_size=kv_slots, device=dev)
+    runner.init_model()
+    return runner
+
+
+def messages(prompt_len, seed):
+    rs = np.random.RandomState(seed)
+    return [{"id": i, "input_tokens": rs.randint(0, 151936, size=prompt_len).tolist(),
+             "temperature": 0.0, "top_p": 1.0, "top_k": 1, "do_sample": False,
+             "ignore_eos": True} for i in range(B)]
+
+
+def run_window(runner, msgs, n_forwards, dev):
+    """The generate_token.py loop: n forwards (prefill first), greedy."""
+    from lite_lang_amd.models.runner_batch import RunnerBatch
+    batch = RunnerBatch.create_batch(msgs, "bench", is_prefill=True, model_runner=runner)
+    torch.cuda.synchronize(dev)
+    t0 = time.perf_counter()
+    t_prefill = None
+    for i in range(n_forwards):
+        out = runner.forward(batch)
+        batch.update_forward_message(out)
+        if i == 0:
+            torch.cuda.synchronize(dev)
+            t_prefill = time.perf_counter() - t0
+    torch.cuda.synchronize(dev)
+    wall = time.perf_counter() - t0
+    runner.free_reqs(list(batch.request_mapping.values()))
+    return wall, t_prefill
+
+
+# ------------------------------------------------------------------ CPU baseline
+def cpu_baseline(max_seconds=30.0):
+    """CPU oracle decode step at the 3B shape, batch 40, context 600.
+
+    Sample: one decode forward with 1 layer and one with 2 layers (same
+    weights shapes as Qwen2.5-3B, random KV pool of 600 tokens per request,
+    no prefill), extrapolated to 36 layers: t = t1 + 35 * (t2 - t1).
+    """
+    from oracle.qwen2 import Qwen2Cfg, Qwen2Oracle
+    from oracle.runner_batch import Req
+    from lite_lang_amd.models.qwen2.weights import Qwen2Config, random_state_dict
+    cores = os.cpu_count() or 1
+    torch.set_num_threads(cores)
+    times = {}
+    for nl in (1, 2):
+        cfg = Qwen2Config(layer_nums=nl, hidden_size=2048, num_heads=16, num_key_value_heads=2,
+                          intermediate_size=11008, vocab_size=151936)
+        sd = random_state_dict(cfg, seed=0)
+        oc = Qwen2Cfg(num_layers=nl, hidden=2048, heads=16, kv_heads=2, intermediate=11008,
+                      vocab=151936)
+        orc = Qwen2Oracle(oc, sd, torch.bfloat16, B, PROMPT + 8, B * (PROMPT + 2))
+        del sd
+        reqs = []
+        for i in range(B):
+            r = Req(rid=orc.cache.alloc_req(), input_tokens=[0] * PROMPT, output_tokens=[1])
+            orc.cache.alloc_token_idxs([r.rid], [0], [PROMPT])
+            reqs.append(r)
+        g = torch.Generator().manual_seed(1)
+        orc.pool.normal_(generator=g)
+        t0 = time.perf_counter()
+        orc.forward(reqs, False, [1] * B)
+        times[nl] = time.perf_counter() - t0
+        del orc
+    per_layer = max(times[2] - times[1], 1e-9)
+    step = times[1] + 35 * per_layer
+    return {"value": B / step, "unit": "tok/s", "cores": cores, "kind": "port",
+            "sample": (f"CPU oracle (float64 math, bf16 storage emulation) decode forward of "
+                       f"the 3B shape at batch {B}, context {PROMPT}, no prefill; 1- and 2-layer "
+                       f"runs ({times[1]:.2f}s, {times[2]:.2f}s) extrapolated to 36 layers "
+                       f"= {step:.2f}s/step")}
+
+
+# ------------------------------------------------------------------ main
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=600)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this build runs on one GPU (tp=1, no collectives); "
+              f"--gpus {args.gpus} is not supported", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(2)
+    dev = torch.device("cuda:0")
+    from lite_lang_amd.models.qwen2.weights import qwen25_3b_config
+    cfg = qwen25_3b_config()
+    K, W = args.steps, args.warmup
+
+    log("decode attention microbench (config 2)")
+    attn_sec, attn_bytes = bench_decode_attention(dev)
+    attn_gbs = attn_bytes / attn_sec / 1e9
+    log(f"attention: {attn_sec * 1e6:.2f} us, {attn_gbs:.0f} GB/s")
+
+    log("building Qwen2.5-3B-shape runner (random init, bf16)")
+    max_length = PROMPT + max(K, W) + 2
+    runner = build_runner(dev, cfg, max_length)
+    if W > 0:
+        log(f"warmup: {W} forwards")
+        run_window(runner, messages(PROMPT, seed=1), W, dev)
+    log(f"timed window: {K} forwards (prefill + {K - 1} decode)")
+    wall, t_prefill = run_window(runner, messages(PROMPT, seed=2), K, dev)
+    value = K * B / wall
+    decode_wall = wall - t_prefill
+    decode_tok_s = (K - 1) * B / decode_wall if K > 1 else None
+    wbytes = runner.model_ins_.w.nbytes_streamed_per_decode()
+    kv_ctx_mean = PROMPT + K / 2
+    step_bytes = wbytes + cfg.layer_nums * B * kv_ctx_mean * 2 * cfg.num_key_value_heads * cfg.head_dim * 2
+    step_sec = decode_wall / max(K - 1, 1)
+    log(f"window {wall:.3f}s prefill {t_prefill * 1e3:.1f}ms decode {step_sec * 1e3:.3f} ms/step")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("CPU baseline (oracle)")
+        try:
+            cpu = cpu_baseline()
+        except Exception as e:  # reported, not fatal
+            cpu = {"value": None, "unit": "tok/s", "cores": os.cpu_count(), "kind": "port",
+                   "sample": f"failed: {e!r}"}
+
+    res = {
+        "metric": "decode tok/s Qwen2.5-3B bs40 ctx600 + paged-decode attn % HBM peak",
+        "value": round(value, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(wall / K * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": round(value / 864.21, 3),
+        "dtype": "bf16",
+        "data": "synthetic (random-init weights N(0,0.02), uniform random prompt ids)",
+        "config": {"workload": "Qwen2.5-3B-shape decode, batch 40, 600-token prompts, "
+                               "reference-harness window (prefill + K-1 decode steps)",
+                   "global_batch": B, "seq_len": PROMPT, "parallelism": "tp1"},
+        "prefill_tok_s": round(B * PROMPT / t_prefill, 1),
+        "decode_tok_s": round(decode_tok_s, 1) if decode_tok_s else None,
+        "decode_step": {"ms": round(step_sec * 1e3, 4), "bytes": int(step_bytes),
+                        "hbm_frac": round(step_bytes / step_sec / 1e9 / HBM_PEAK_GBS, 4)},
+        "roofline": {"kernel": "decode_attn_mfma_kernel (config 2)", "bound": "hbm",
+                     "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "avg_us": round(attn_sec * 1e6, 3), "bytes_per_launch": attn_bytes},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

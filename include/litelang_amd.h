@@ -1,0 +1,170 @@
+/*
+ * lite_lang_amd — C ABI of the MI355X (gfx950) kernels behind the Qwen2
+ * token loop of lite_lang.
+ *
+ * Conventions (all entry points):
+ *   - plain device pointers, element strides (not bytes), int64 sizes;
+ *   - `dtype` is one of LL_DTYPE_* and selects the element type of every
+ *     floating-point tensor argument of the call unless stated otherwise;
+ *   - index arrays that the reference builds with torch.tensor(list) (int64)
+ *     are accepted as int32 or int64 via the matching `*_i64` flag;
+ *   - every call is asynchronous on `stream` and returns LL_OK (0) or a
+ *     negative LL_ERR_* code; ll_last_error() then holds the reason. Argument
+ *     errors are raised before anything is launched.
+ *   - workspaces are caller-owned device buffers. Where a workspace holds
+ *     tickets (decode attention, argmax) it must be zero-filled once when it
+ *     is allocated; the kernels leave the tickets at zero again. Calls that
+ *     share one workspace must not overlap in time.
+ */
+#ifndef LITELANG_AMD_H
+#define LITELANG_AMD_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LL_ABI_VERSION 1
+
+#define LL_DTYPE_F32 0
+#define LL_DTYPE_F16 1
+#define LL_DTYPE_BF16 2
+
+#define LL_OK 0
+#define LL_ERR_ARG (-1)
+#define LL_ERR_UNSUPPORTED (-2)
+#define LL_ERR_HIP (-3)
+
+/* Library identification and error text (no reference counterpart: the
+ * reference raises Python exceptions from Triton). */
+int ll_version(void);
+const char* ll_last_error(void);
+
+/* ---------------------------------------------------------------- attention */
+
+/* Paged GQA decode attention, split-K with in-launch combine.
+ * Replaces token_decode_attention_flash_decoding
+ *   (litelang/kernel/develop_flash_attn/flash_decoding.py:262-312).
+ * q [batch, q_heads, head_dim]; k_cache / v_cache [P, kv_heads, head_dim]
+ * views of the pool (last dim contiguous); req_to_tokens [max_batch, max_len]
+ * int32 slot table; out [batch, q_heads, head_dim]. max_len_in_batch is an
+ * upper bound of b_seq_len (it sizes the split count and the workspace). */
+int64_t ll_decode_attention_workspace_size(int64_t batch, int64_t q_heads, int64_t kv_heads,
+                                           int64_t head_dim, int64_t max_len_in_batch);
+int ll_decode_attention(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                        const void* k_cache, int64_t k_stride_tok, int64_t k_stride_head,
+                        const void* v_cache, int64_t v_stride_tok, int64_t v_stride_head,
+                        const int32_t* req_to_tokens, int64_t req_to_tokens_stride,
+                        const void* b_req_idx, int req_idx_i64, const void* b_seq_len,
+                        int seq_len_i64, void* out, int64_t out_stride_b, int64_t out_stride_h,
+                        int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                        int64_t max_len_in_batch, float sm_scale, int dtype, void* workspace,
+                        int64_t workspace_bytes, hipStream_t stream);
+
+/* NoPad varlen causal prefill attention reading K/V through the slot table,
+ * with an optional shared (prompt-cache) prefix per request.
+ * b_shared_seq_len == NULL replaces context_attention_fwd_with_no_pad_and_kv_cache
+ *   (litelang/kernel/develop_flash_attn/flash_attn_v2.py:513-566);
+ * b_shared_seq_len != NULL replaces
+ *   context_attention_fwd_with_no_pad_and_kv_cache_and_prompt_cache
+ *   (flash_attn_v2.py:699-762).
+ * q / o [T, q_heads, head_dim] hold, for request b, the rows
+ * b_start_loc[b] .. b_start_loc[b] + (b_seq_len[b] - shared[b]) - 1; the keys
+ * are the first b_seq_len[b] slots of row b_req_idx[b] of req_to_tokens. */
+int ll_prefill_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_h,
+                         const void* k_cache, int64_t k_stride_tok, int64_t k_stride_head,
+                         const void* v_cache, int64_t v_stride_tok, int64_t v_stride_head,
+                         void* out, int64_t out_stride_tok, int64_t out_stride_h,
+                         const int32_t* req_to_tokens, int64_t req_to_tokens_stride,
+                         const void* b_req_idx, int req_idx_i64, const void* b_start_loc,
+                         int start_loc_i64, const void* b_seq_len, int seq_len_i64,
+                         const void* b_shared_seq_len, int shared_i64, int64_t batch,
+                         int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                         int64_t max_input_len, float sm_scale, int dtype, hipStream_t stream);
+
+/* ------------------------------------------------------------- elementwise */
+
+/* RMSNorm over rows: out = (x / sqrt(mean(x^2) + eps)) * gamma in fp32.
+ * Replaces rmsnorm (litelang/kernel/develop_rmsnorm/rms_norm.py:71-98).
+ * If residual != NULL, x is first updated in place to x + residual (rounded
+ * to dtype) and the updated x is normalised: this fuses the residual add_
+ * of transformer_layer.py:69,76 into the following norm. */
+int ll_rmsnorm(void* x, int64_t x_row_stride, const void* residual, int64_t residual_row_stride,
+               const void* gamma, void* out, int64_t out_row_stride, int64_t M, int64_t N,
+               float eps, int dtype, hipStream_t stream);
+
+/* In-place rotate-half RoPE on q [T, q_heads, D] and k [T, k_heads, D] with
+ * per-token cos/sin [T, D/2] (cs_dtype may differ from dtype).
+ * Replaces rotary_emb_fwd (litelang/kernel/develop_rope/rope.py:154-198). */
+int ll_rotary_emb(void* q, int64_t q_tok_stride, int64_t q_head_stride, int64_t q_heads, void* k,
+                  int64_t k_tok_stride, int64_t k_head_stride, int64_t k_heads, const void* cos,
+                  int64_t cos_tok_stride, const void* sin, int64_t sin_tok_stride, int64_t ntok,
+                  int64_t head_dim, int dtype, int cs_dtype, hipStream_t stream);
+
+/* Fused RoPE + KV-cache scatter for one layer: rotates the q heads of the
+ * projection output qkv [T, (q_heads + 2*kv_heads)*D] in place, and writes
+ * rotated K and plain V to pool_layer[slots[t], 0:2*kv_heads, :].
+ * Replaces the index_select + rotary_emb_fwd + gather/index_put sequence of
+ *   litelang/models/qwen2/layer/transformer_layer.py:102-115,142-143. */
+int ll_rope_kv_scatter(void* qkv, int64_t qkv_row_stride, int64_t ntok, int64_t q_heads,
+                       int64_t kv_heads, int64_t head_dim, const void* positions,
+                       int positions_i64, const void* cos_table, const void* sin_table,
+                       int64_t table_row_stride, int cs_dtype, const int32_t* slots,
+                       void* pool_layer, int64_t pool_slot_stride, int64_t pool_head_stride,
+                       int dtype, hipStream_t stream);
+
+/* pool[slots[t], h, :] = src[t, h, :] (plain KV write, no RoPE).
+ * Replaces the index_put of transformer_layer.py:143 when K is already rotated. */
+int ll_kv_store(const void* src, int64_t src_tok_stride, int64_t src_head_stride, int64_t heads,
+                int64_t head_dim, const int32_t* slots, void* pool, int64_t pool_slot_stride,
+                int64_t pool_head_stride, int64_t ntok, int dtype, hipStream_t stream);
+
+/* out[m, n] = up * dtype(silu(gate)), gate = x[m, n], up = x[m, N + n];
+ * out may alias x (in-place over the gate half, as the reference).
+ * Replaces silu_and_mul_fwd
+ *   (litelang/kernel/develop_silu_and_mul/silu_and_mul.py:54-78). */
+int ll_silu_and_mul(const void* x, int64_t x_row_stride, void* out, int64_t out_row_stride,
+                    int64_t M, int64_t N, int dtype, hipStream_t stream);
+
+/* out[t, :] = table[ids[t], :].
+ * Replaces torch.embedding in Qwen2PreLayer.Forward
+ *   (litelang/models/qwen2/layer/pre_layer.py:15-19). */
+int ll_embedding(const void* table, int64_t table_row_stride, int64_t vocab, const void* ids,
+                 int ids_i64, void* out, int64_t out_row_stride, int64_t ntok, int64_t hidden,
+                 int dtype, hipStream_t stream);
+
+/* out[m] = first index of max(x[m, :]) (int64).
+ * Replaces logits.argmax(dim=-1) (litelang/models/qwen2/layer/post_layer.py:105-107). */
+int64_t ll_argmax_workspace_size(int64_t M, int64_t N);
+int ll_argmax(const void* x, int64_t x_row_stride, int64_t M, int64_t N, int64_t* out,
+              void* workspace, int64_t workspace_bytes, int dtype, hipStream_t stream);
+
+/* req_to_tokens[rows[i], cols[i]] = slots[i] for i < n (int32 device arrays).
+ * Replaces the slot-table writes of PageCache.alloc_token_idxs and add_refs
+ *   (litelang/models/cache.py:238-248, 284-285); the host keeps the free-slot
+ * stack and computes (slot, row, col) exactly as the reference does. */
+int ll_assign_slots(int32_t* req_to_tokens, int64_t req_to_tokens_stride, const int32_t* slots,
+                    const int32_t* rows, const int32_t* cols, int64_t n, hipStream_t stream);
+
+/* ------------------------------------------------------------------- GEMM */
+
+/* Y[M, N] = X[M, K] . W[N, K]^T (+ bias[N]) with fp32 accumulation.
+ * W is the nn.Linear layout [out, in]. Replaces the torch.addmm / torch.mm /
+ * matmul projections of transformer_layer.py:80,82,95-109,193 and the lm_head
+ * product of post_layer.py:50-52 (the reference keeps W pre-transposed
+ * [in, out]; this library keeps [out, in] so both MFMA operands stream
+ * 16-byte k-contiguous rows). X rows may be strided; Y is written with
+ * row stride ldy. For M <= 64 with narrow N the product is split over K and
+ * needs a workspace of ll_gemm_workspace_size(M, N, K) bytes (0 otherwise). */
+int64_t ll_gemm_workspace_size(int64_t M, int64_t N, int64_t K);
+int ll_gemm(const void* X, int64_t ldx, const void* W, int64_t ldw, const void* bias, void* Y,
+            int64_t ldy, int64_t M, int64_t N, int64_t K, int dtype, void* workspace,
+            int64_t workspace_bytes, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LITELANG_AMD_H */

@@ -1,0 +1,430 @@
+// Bandwidth-bound kernels of the Qwen2 token loop:
+//   RMSNorm (+ fused residual add), RoPE (in place, drop-in form), the fused
+//   RoPE + KV-cache scatter used by the model, SiLU_and_Mul, embedding gather,
+//   and first-index argmax.
+//
+// Semantics follow the reference Triton kernels:
+//   rmsnorm      litelang/kernel/develop_rmsnorm/rms_norm.py:20-59
+//   rotary       litelang/kernel/develop_rope/rope.py:9-151
+//   silu_and_mul litelang/kernel/develop_silu_and_mul/silu_and_mul.py:7-52
+//   embedding    litelang/models/qwen2/layer/pre_layer.py:15-19
+//   argmax       litelang/models/qwen2/layer/post_layer.py:105-107
+#include "ll_common.h"
+
+#include <string.h>
+
+static thread_local char g_err[512];
+
+void ll_set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+
+extern "C" const char* ll_last_error(void) { return g_err; }
+
+extern "C" int ll_version(void) { return LL_ABI_VERSION; }
+
+// ============================================================== RMSNorm
+// One workgroup per row. Pass 1 accumulates sum(x^2) in fp32, pass 2 scales.
+// If `residual` is non-null the kernel first forms h = T(x + residual), stores
+// it back into x (the reference's `hidden_states.add_()` at
+// transformer_layer.py:69,76) and normalises h.
+template <typename T, int BLOCK>
+__global__ __launch_bounds__(BLOCK) void rmsnorm_kernel(
+    T* __restrict__ x, int64_t x_rs, const T* __restrict__ residual, int64_t r_rs,
+    const T* __restrict__ gamma, T* __restrict__ out, int64_t o_rs, int N, float eps) {
+  const int row = blockIdx.x;
+  T* xr = x + (int64_t)row * x_rs;
+  T* orow = out + (int64_t)row * o_rs;
+  float ss = 0.f;
+  if (residual != nullptr) {
+    const T* rr = residual + (int64_t)row * r_rs;
+    for (int i = threadIdx.x; i < N; i += BLOCK) {
+      T h = ll_from_f32<T>(ll_to_f32(xr[i]) + ll_to_f32(rr[i]));
+      xr[i] = h;
+      float v = ll_to_f32(h);
+      ss += v * v;
+    }
+  } else {
+    for (int i = threadIdx.x; i < N; i += BLOCK) {
+      float v = ll_to_f32(xr[i]);
+      ss += v * v;
+    }
+  }
+  __shared__ float red[BLOCK / 64];
+  ss = ll_wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int w = 0; w < BLOCK / 64; ++w) tot += red[w];
+  // reference: x / sqrt(sum(x^2)/N + eps) * gamma, all in fp32
+  const float denom = sqrtf(tot / (float)N + eps);
+  for (int i = threadIdx.x; i < N; i += BLOCK) {
+    float v = ll_to_f32(xr[i]) / denom;
+    orow[i] = ll_from_f32<T>(v * ll_to_f32(gamma[i]));
+  }
+}
+
+extern "C" int ll_rmsnorm(void* x, int64_t x_row_stride, const void* residual,
+                          int64_t residual_row_stride, const void* gamma, void* out,
+                          int64_t out_row_stride, int64_t M, int64_t N, float eps,
+                          int dtype, hipStream_t stream) {
+  LL_CHECK_ARG(x && gamma && out, "ll_rmsnorm: null pointer");
+  LL_CHECK_ARG(M >= 0 && N > 0, "ll_rmsnorm: bad shape M=%lld N=%lld", (long long)M,
+               (long long)N);
+  if (M == 0) return LL_OK;
+  return LL_DISPATCH_DTYPE(dtype, T, [&]() -> int {
+    hipLaunchKernelGGL((rmsnorm_kernel<T, 256>), dim3((unsigned)M), dim3(256), 0, stream,
+                       (T*)x, x_row_stride, (const T*)residual, residual_row_stride,
+                       (const T*)gamma, (T*)out, out_row_stride, (int)N, eps);
+    LL_RETURN_LAUNCH();
+  });
+}
+
+// ============================================================== RoPE (drop-in)
+// In place rotate-half on q [T, Hq, D] and k [T, Hk, D] (last dim contiguous,
+// arbitrary token/head strides), with cos/sin already gathered per token
+// [T, D/2]. One thread per (token, head, pair).
+template <typename T, typename C>
+__global__ void rope_kernel(T* __restrict__ q, int64_t q_st, int64_t q_sh, int Hq,
+                            T* __restrict__ k, int64_t k_st, int64_t k_sh, int Hk,
+                            const C* __restrict__ cs, int64_t c_st, const C* __restrict__ sn,
+                            int64_t s_st, int64_t ntok, int half) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t per_tok = (int64_t)(Hq + Hk) * half;
+  const int64_t t = gid / per_tok;
+  if (t >= ntok) return;
+  const int rem = (int)(gid - t * per_tok);
+  const int h = rem / half;
+  const int i = rem - h * half;
+  T* base = (h < Hq) ? (q + t * q_st + (int64_t)h * q_sh) : (k + t * k_st + (int64_t)(h - Hq) * k_sh);
+  const float c = ll_to_f32(cs[t * c_st + i]);
+  const float s = ll_to_f32(sn[t * s_st + i]);
+  const float x0 = ll_to_f32(base[i]);
+  const float x1 = ll_to_f32(base[i + half]);
+  base[i] = ll_from_f32<T>(x0 * c - x1 * s);
+  base[i + half] = ll_from_f32<T>(x0 * s + x1 * c);
+}
+
+extern "C" int ll_rotary_emb(void* q, int64_t q_tok_stride, int64_t q_head_stride, int64_t q_heads,
+                             void* k, int64_t k_tok_stride, int64_t k_head_stride, int64_t k_heads,
+                             const void* cos, int64_t cos_tok_stride, const void* sin,
+                             int64_t sin_tok_stride, int64_t ntok, int64_t head_dim, int dtype,
+                             int cs_dtype, hipStream_t stream) {
+  LL_CHECK_ARG(q && cos && sin, "ll_rotary_emb: null pointer");
+  LL_CHECK_ARG(head_dim % 2 == 0 && head_dim > 0, "ll_rotary_emb: head_dim must be even");
+  LL_CHECK_ARG(k_heads == 0 || k != nullptr, "ll_rotary_emb: null k");
+  if (ntok == 0) return LL_OK;
+  const int half = (int)(head_dim / 2);
+  const int64_t total = ntok * (q_heads + k_heads) * half;
+  const int block = 256;
+  const unsigned grid = (unsigned)((total + block - 1) / block);
+  return LL_DISPATCH_DTYPE(dtype, T, [&]() -> int {
+    return LL_DISPATCH_DTYPE(cs_dtype, C, [&]() -> int {
+      hipLaunchKernelGGL((rope_kernel<T, C>), dim3(grid), dim3(block), 0, stream, (T*)q,
+                         q_tok_stride, q_head_stride, (int)q_heads, (T*)k, k_tok_stride,
+                         k_head_stride, (int)k_heads, (const C*)cos, cos_tok_stride,
+                         (const C*)sin, sin_tok_stride, ntok, half);
+      LL_RETURN_LAUNCH();
+    });
+  });
+}
+
+// ============================================================== RoPE + KV scatter
+// Model path for one layer. `qkv` is the projection output [T, (H + 2*KVH)*D]
+// (q heads, then k heads, then v heads; row stride ld). For each token t:
+//   q heads are rotated in place inside qkv;
+//   k heads are rotated and written to pool[slot[t], 0:KVH, :];
+//   v heads are copied to pool[slot[t], KVH:2*KVH, :].
+// cos/sin come from the full table [max_len, D/2] indexed by position[t],
+// replacing the index_select + gather + index_put sequence of
+// transformer_layer.py:102-115,142-143.
+template <typename T, typename C>
+__global__ void rope_kv_scatter_kernel(T* __restrict__ qkv, int64_t ld, int H, int KVH, int D,
+                                       const void* __restrict__ pos, int pos64,
+                                       const C* __restrict__ cos_tab, const C* __restrict__ sin_tab,
+                                       int64_t tab_stride, const int32_t* __restrict__ slots,
+                                       T* __restrict__ pool, int64_t pool_slot_stride,
+                                       int64_t pool_head_stride, int64_t ntok) {
+  const int half = D / 2;
+  const int64_t per_tok = (int64_t)(H + 2 * KVH) * half;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t t = gid / per_tok;
+  if (t >= ntok) return;
+  const int rem = (int)(gid - t * per_tok);
+  const int h = rem / half;  // 0..H+2KVH-1
+  const int i = rem - h * half;
+  T* src = qkv + t * ld + (int64_t)h * D;
+  if (h < H + KVH) {
+    const int64_t p = ll_load_idx(pos, t, pos64);
+    const float c = ll_to_f32(cos_tab[p * tab_stride + i]);
+    const float s = ll_to_f32(sin_tab[p * tab_stride + i]);
+    const float x0 = ll_to_f32(src[i]);
+    const float x1 = ll_to_f32(src[i + half]);
+    const T y0 = ll_from_f32<T>(x0 * c - x1 * s);
+    const T y1 = ll_from_f32<T>(x0 * s + x1 * c);
+    if (h < H) {
+      src[i] = y0;
+      src[i + half] = y1;
+    } else {
+      T* dst = pool + (int64_t)slots[t] * pool_slot_stride + (int64_t)(h - H) * pool_head_stride;
+      dst[i] = y0;
+      dst[i + half] = y1;
+    }
+  } else {
+    T* dst = pool + (int64_t)slots[t] * pool_slot_stride + (int64_t)(h - H) * pool_head_stride;
+    dst[i] = src[i];
+    dst[i + half] = src[i + half];
+  }
+}
+
+extern "C" int ll_rope_kv_scatter(void* qkv, int64_t qkv_row_stride, int64_t ntok, int64_t q_heads,
+                                  int64_t kv_heads, int64_t head_dim, const void* positions,
+                                  int positions_i64, const void* cos_table, const void* sin_table,
+                                  int64_t table_row_stride, int cs_dtype, const int32_t* slots,
+                                  void* pool_layer, int64_t pool_slot_stride,
+                                  int64_t pool_head_stride, int dtype, hipStream_t stream) {
+  LL_CHECK_ARG(qkv && positions && cos_table && sin_table && slots && pool_layer,
+               "ll_rope_kv_scatter: null pointer");
+  LL_CHECK_ARG(head_dim % 2 == 0, "ll_rope_kv_scatter: head_dim must be even");
+  if (ntok == 0) return LL_OK;
+  const int64_t total = ntok * (q_heads + 2 * kv_heads) * (head_dim / 2);
+  const int block = 256;
+  const unsigned grid = (unsigned)((total + block - 1) / block);
+  return LL_DISPATCH_DTYPE(dtype, T, [&]() -> int {
+    return LL_DISPATCH_DTYPE(cs_dtype, C, [&]() -> int {
+      hipLaunchKernelGGL((rope_kv_scatter_kernel<T, C>), dim3(grid), dim3(block), 0, stream,
+                         (T*)qkv, qkv_row_stride, (int)q_heads, (int)kv_heads, (int)head_dim,
+                         positions, positions_i64, (const C*)cos_table, (const C*)sin_table,
+                         table_row_stride, slots, (T*)pool_layer, pool_slot_stride,
+                         pool_head_stride, ntok);
+      LL_RETURN_LAUNCH();
+    });
+  });
+}
+
+// ============================================================== KV store
+// pool[slot[t], h, :] = src[t, h, :] for h < heads (plain scatter, no RoPE).
+template <typename T>
+__global__ void kv_store_kernel(const T* __restrict__ src, int64_t s_st, int64_t s_sh, int heads,
+                                int D, const int32_t* __restrict__ slots, T* __restrict__ pool,
+                                int64_t p_ss, int64_t p_sh, int64_t ntok) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t per_tok = (int64_t)heads * D;
+  const int64_t t = gid / per_tok;
+  if (t >= ntok) return;
+  const int rem = (int)(gid - t * per_tok);
+  const int h = rem / D, d = rem - h * D;
+  pool[(int64_t)slots[t] * p_ss + (int64_t)h * p_sh + d] = src[t * s_st + (int64_t)h * s_sh + d];
+}
+
+extern "C" int ll_kv_store(const void* src, int64_t src_tok_stride, int64_t src_head_stride,
+                           int64_t heads, int64_t head_dim, const int32_t* slots, void* pool,
+                           int64_t pool_slot_stride, int64_t pool_head_stride, int64_t ntok,
+                           int dtype, hipStream_t stream) {
+  LL_CHECK_ARG(src && slots && pool, "ll_kv_store: null pointer");
+  if (ntok == 0) return LL_OK;
+  const int64_t total = ntok * heads * head_dim;
+  const unsigned grid = (unsigned)((total + 255) / 256);
+  return LL_DISPATCH_DTYPE(dtype, T, [&]() -> int {
+    hipLaunchKernelGGL((kv_store_kernel<T>), dim3(grid), dim3(256), 0, stream, (const T*)src,
+                       src_tok_stride, src_head_stride, (int)heads, (int)head_dim, slots, (T*)pool,
+                       pool_slot_stride, pool_head_stride, ntok);
+    LL_RETURN_LAUNCH();
+  });
+}
+
+// ============================================================== SiLU_and_Mul
+// out[m, n] = T( up * T(silu(gate)) ), gate = x[m, n], up = x[m, n + N].
+// silu is evaluated in fp32 and rounded to the storage type before the
+// multiply, as the reference does (silu_and_mul.py:43-50). `out` may alias x
+// (the reference writes over the gate half in place).
+template <typename T>
+__global__ void silu_and_mul_kernel(const T* x, int64_t x_rs, T* out, int64_t o_rs, int64_t M,
+                                    int N) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t m = gid / N;
+  if (m >= M) return;
+  const int n = (int)(gid - m * N);
+  const float g = ll_to_f32(x[m * x_rs + n]);
+  const float u = ll_to_f32(x[m * x_rs + n + N]);
+  const T s = ll_from_f32<T>(g / (1.0f + __expf(-g)));
+  out[m * o_rs + n] = ll_from_f32<T>(u * ll_to_f32(s));
+}
+
+extern "C" int ll_silu_and_mul(const void* x, int64_t x_row_stride, void* out,
+                               int64_t out_row_stride, int64_t M, int64_t N, int dtype,
+                               hipStream_t stream) {
+  LL_CHECK_ARG(x && out, "ll_silu_and_mul: null pointer");
+  if (M == 0 || N == 0) return LL_OK;
+  const int64_t total = M * N;
+  const unsigned grid = (unsigned)((total + 255) / 256);
+  return LL_DISPATCH_DTYPE(dtype, T, [&]() -> int {
+    hipLaunchKernelGGL((silu_and_mul_kernel<T>), dim3(grid), dim3(256), 0, stream, (const T*)x,
+                       x_row_stride, (T*)out, out_row_stride, M, (int)N);
+    LL_RETURN_LAUNCH();
+  });
+}
+
+// ============================================================== embedding
+template <typename T>
+__global__ void embedding_kernel(const T* __restrict__ table, int64_t tab_rs,
+                                 const void* __restrict__ ids, int ids64, T* __restrict__ out,
+                                 int64_t o_rs, int64_t ntok, int hidden) {
+  const int64_t t = blockIdx.x;
+  const int64_t id = ll_load_idx(ids, t, ids64);
+  const T* src = table + id * tab_rs;
+  T* dst = out + t * o_rs;
+  for (int i = threadIdx.x; i < hidden; i += blockDim.x) dst[i] = src[i];
+}
+
+extern "C" int ll_embedding(const void* table, int64_t table_row_stride, int64_t vocab,
+                            const void* ids, int ids_i64, void* out, int64_t out_row_stride,
+                            int64_t ntok, int64_t hidden, int dtype, hipStream_t stream) {
+  LL_CHECK_ARG(table && ids && out, "ll_embedding: null pointer");
+  LL_CHECK_ARG(vocab > 0, "ll_embedding: empty table");
+  if (ntok == 0) return LL_OK;
+  return LL_DISPATCH_DTYPE(dtype, T, [&]() -> int {
+    hipLaunchKernelGGL((embedding_kernel<T>), dim3((unsigned)ntok), dim3(256), 0, stream,
+                       (const T*)table, table_row_stride, ids, ids_i64, (T*)out, out_row_stride,
+                       ntok, (int)hidden);
+    LL_RETURN_LAUNCH();
+  });
+}
+
+// ============================================================== argmax
+// out[m] = first index of the maximum of row m (torch.argmax tie rule).
+// Two-level: each workgroup reduces a chunk of the row into (value, index)
+// partials, and the last workgroup of the row (atomic ticket) reduces those.
+template <typename T>
+__global__ __launch_bounds__(256) void argmax_kernel(const T* __restrict__ x, int64_t x_rs, int N,
+                                                     int chunk, float* __restrict__ pval,
+                                                     int* __restrict__ pidx,
+                                                     int* __restrict__ tickets,
+                                                     int64_t* __restrict__ out) {
+  const int row = blockIdx.y;
+  const int nchunk = gridDim.x;
+  const int c = blockIdx.x;
+  const T* xr = x + (int64_t)row * x_rs;
+  const int beg = c * chunk;
+  const int end = min(N, beg + chunk);
+  float best = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int i = beg + threadIdx.x; i < end; i += 256) {
+    float v = ll_to_f32(xr[i]);
+    if (v > best || (v == best && i < bi)) { best = v; bi = i; }
+  }
+  __shared__ float sv[256];
+  __shared__ int si[256];
+  __shared__ int last;
+  sv[threadIdx.x] = best;
+  si[threadIdx.x] = bi;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if (threadIdx.x < s) {
+      float ov = sv[threadIdx.x + s];
+      int oi = si[threadIdx.x + s];
+      if (ov > sv[threadIdx.x] || (ov == sv[threadIdx.x] && oi < si[threadIdx.x])) {
+        sv[threadIdx.x] = ov;
+        si[threadIdx.x] = oi;
+      }
+    }
+    __syncthreads();
+  }
+  if (nchunk == 1) {
+    if (threadIdx.x == 0) out[row] = (int64_t)(si[0] == 0x7fffffff ? 0 : si[0]);
+    return;
+  }
+  if (threadIdx.x == 0) {
+    pval[row * nchunk + c] = sv[0];
+    pidx[row * nchunk + c] = si[0];
+    __threadfence();
+    int t = atomicAdd(&tickets[row], 1);
+    last = (t == nchunk - 1);
+  }
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  best = -INFINITY;
+  bi = 0x7fffffff;
+  for (int i = threadIdx.x; i < nchunk; i += 256) {
+    float v = __builtin_nontemporal_load(&pval[row * nchunk + i]);
+    int ix = __builtin_nontemporal_load(&pidx[row * nchunk + i]);
+    if (v > best || (v == best && ix < bi)) { best = v; bi = ix; }
+  }
+  sv[threadIdx.x] = best;
+  si[threadIdx.x] = bi;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if (threadIdx.x < s) {
+      float ov = sv[threadIdx.x + s];
+      int oi = si[threadIdx.x + s];
+      if (ov > sv[threadIdx.x] || (ov == sv[threadIdx.x] && oi < si[threadIdx.x])) {
+        sv[threadIdx.x] = ov;
+        si[threadIdx.x] = oi;
+      }
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    out[row] = (int64_t)(si[0] == 0x7fffffff ? 0 : si[0]);
+    tickets[row] = 0;  // self-reset for the next call
+  }
+}
+
+extern "C" int64_t ll_argmax_workspace_size(int64_t M, int64_t N) {
+  const int64_t chunk = 8192;
+  const int64_t nchunk = (N + chunk - 1) / chunk;
+  return M * nchunk * 8 + M * 4 + 256;
+}
+
+extern "C" int ll_argmax(const void* x, int64_t x_row_stride, int64_t M, int64_t N, int64_t* out,
+                         void* workspace, int64_t workspace_bytes, int dtype, hipStream_t stream) {
+  LL_CHECK_ARG(x && out, "ll_argmax: null pointer");
+  LL_CHECK_ARG(N > 0, "ll_argmax: empty rows");
+  if (M == 0) return LL_OK;
+  const int chunk = 8192;
+  const int nchunk = ll_cdiv(N, chunk);
+  float* pval = nullptr;
+  int* pidx = nullptr;
+  int* tickets = nullptr;
+  if (nchunk > 1) {
+    LL_CHECK_ARG(workspace != nullptr && workspace_bytes >= ll_argmax_workspace_size(M, N),
+                 "ll_argmax: workspace too small (need %lld bytes)",
+                 (long long)ll_argmax_workspace_size(M, N));
+    char* w = (char*)workspace;
+    tickets = (int*)w;  // must be zero on first use; the kernel keeps it zero
+    pval = (float*)(w + ((M * 4 + 255) / 256) * 256);
+    pidx = (int*)(pval + M * nchunk);
+  }
+  return LL_DISPATCH_DTYPE(dtype, T, [&]() -> int {
+    hipLaunchKernelGGL((argmax_kernel<T>), dim3(nchunk, (unsigned)M), dim3(256), 0, stream,
+                       (const T*)x, x_row_stride, (int)N, chunk, pval, pidx, tickets, out);
+    LL_RETURN_LAUNCH();
+  });
+}
+
+// ============================================================== slot table
+// req_to_tokens[rows[i], cols[i]] = slots[i]: the table update of
+// PageCache.alloc_token_idxs (litelang/models/cache.py:238-248) and
+// PageCache.add_refs (cache.py:284-285), for host-computed (row, col) pairs.
+__global__ void assign_slots_kernel(int32_t* __restrict__ r2t, int64_t r2t_stride,
+                                    const int32_t* __restrict__ slots,
+                                    const int32_t* __restrict__ rows,
+                                    const int32_t* __restrict__ cols, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) r2t[(int64_t)rows[i] * r2t_stride + cols[i]] = slots[i];
+}
+
+extern "C" int ll_assign_slots(int32_t* req_to_tokens, int64_t req_to_tokens_stride,
+                               const int32_t* slots, const int32_t* rows, const int32_t* cols,
+                               int64_t n, hipStream_t stream) {
+  LL_CHECK_ARG(req_to_tokens && slots && rows && cols, "ll_assign_slots: null pointer");
+  if (n == 0) return LL_OK;
+  hipLaunchKernelGGL(assign_slots_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
+                     req_to_tokens, req_to_tokens_stride, slots, rows, cols, n);
+  LL_RETURN_LAUNCH();
+}

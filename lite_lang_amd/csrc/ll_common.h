@@ -1,0 +1,89 @@
+// Shared helpers for the lite_lang_amd HIP kernels (gfx950 / CDNA4 only).
+//
+// Storage types are the clang native `__bf16` and `_Float16`; every kernel
+// computes in fp32 and rounds once on store (round-to-nearest-even).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdarg.h>
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+#include "../../include/litelang_amd.h"
+
+// short dtype names used inside the kernels
+enum { LL_F32 = LL_DTYPE_F32, LL_F16 = LL_DTYPE_F16, LL_BF16 = LL_DTYPE_BF16 };
+
+// Per-thread last-error text, returned by ll_last_error().
+void ll_set_error(const char* fmt, ...);
+
+#define LL_CHECK_ARG(cond, ...)                 \
+  do {                                          \
+    if (!(cond)) {                              \
+      ll_set_error(__VA_ARGS__);                \
+      return LL_ERR_ARG;                        \
+    }                                           \
+  } while (0)
+
+#define LL_RETURN_LAUNCH()                                              \
+  do {                                                                  \
+    hipError_t _e = hipGetLastError();                                  \
+    if (_e != hipSuccess) {                                             \
+      ll_set_error("HIP launch failed: %s", hipGetErrorString(_e));     \
+      return LL_ERR_HIP;                                                \
+    }                                                                   \
+    return LL_OK;                                                       \
+  } while (0)
+
+// ---------------------------------------------------------------- conversions
+__device__ __forceinline__ float ll_to_f32(float x) { return x; }
+__device__ __forceinline__ float ll_to_f32(_Float16 x) { return (float)x; }
+__device__ __forceinline__ float ll_to_f32(__bf16 x) { return (float)x; }
+
+template <typename T>
+__device__ __forceinline__ T ll_from_f32(float x);
+template <>
+__device__ __forceinline__ float ll_from_f32<float>(float x) { return x; }
+template <>
+__device__ __forceinline__ _Float16 ll_from_f32<_Float16>(float x) { return (_Float16)x; }
+template <>
+__device__ __forceinline__ __bf16 ll_from_f32<__bf16>(float x) { return (__bf16)x; }
+
+// Index arrays arrive either as int32 or int64 (the reference builds them with
+// torch.tensor(list) -> int64, and the slot table is int32).
+__device__ __forceinline__ int64_t ll_load_idx(const void* p, int64_t i, int is64) {
+  return is64 ? ((const int64_t*)p)[i] : (int64_t)((const int32_t*)p)[i];
+}
+
+// ---------------------------------------------------------------- wave helpers
+__device__ __forceinline__ float ll_wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float ll_wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// Dispatch a templated launcher on the runtime dtype code.
+#define LL_DISPATCH_DTYPE(code, T, ...)                                  \
+  [&]() -> int {                                                        \
+    switch (code) {                                                     \
+      case LL_F32: { typedef float T; return __VA_ARGS__(); }           \
+      case LL_F16: { typedef _Float16 T; return __VA_ARGS__(); }        \
+      case LL_BF16: { typedef __bf16 T; return __VA_ARGS__(); }         \
+      default: ll_set_error("unsupported dtype code %d", (int)(code));   \
+               return LL_ERR_UNSUPPORTED;                               \
+    }                                                                   \
+  }()
+
+static inline int ll_cdiv(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }

@@ -1,0 +1,185 @@
+"""Qwen2 model and runner on the lite_lang_amd kernels.
+
+Counterpart of litelang/models/qwen2/model.py (Qwen2Model :23-97,
+Qwen2ModelRunner :100-175) and of the layer modules it drives
+(layer/pre_layer.py, layer/transformer_layer.py, layer/post_layer.py). The
+runner API is the reference's; the layer body is the reference dataflow with
+these fusions, each bit-identical to the unfused sequence:
+  * residual add + RMSNorm in one kernel (transformer_layer.py:69-71,76 + :61);
+  * q/k/v in one GEMM over the concatenated [q; k; v] rows;
+  * RoPE of q and k + KV-pool scatter in one kernel reading cos/sin by
+    position (transformer_layer.py:102-115,142-143);
+  * the final residual add is applied only to the rows the post layer keeps
+    (post_layer.py:56-71), fused with the final RMSNorm.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from lite_lang_amd import ops
+from lite_lang_amd.models.cache import PageCache
+from lite_lang_amd.models.radix_cache import RadixTree
+from .weights import DeviceWeights, Qwen2Config, load_state_dict, random_state_dict
+
+
+def rope_tables(max_length: int, head_dim: int, theta: float, device):
+    """cos/sin [max_length, D/2]: built in fp32 on the host and rounded to fp16
+    like Qwen2PreLayer._ComputePosition (pre_layer.py:21-30); kept as fp32
+    values on the device so every model dtype sees the same table."""
+    freqs = 1.0 / theta ** (torch.arange(0, head_dim, 2) / head_dim)
+    ang = torch.arange(0, max_length)[:, None] * freqs[None, :]
+    cos = torch.cos(ang).to(torch.float16).to(torch.float32)
+    sin = torch.sin(ang).to(torch.float16).to(torch.float32)
+    return cos.to(device).contiguous(), sin.to(device).contiguous()
+
+
+class Qwen2Model:
+    def __init__(self, layer_nums, max_length, config: Qwen2Config, tp_rank=0, world_size=1,
+                 dtype=torch.bfloat16, device="cuda"):
+        assert world_size == 1, "this build runs tp=1 (one GPU, no collectives)"
+        assert layer_nums == config.layer_nums
+        self.cfg = config
+        self.dtype = dtype
+        self.device = torch.device(device)
+        self.max_length = max_length
+        self.cos, self.sin = rope_tables(max_length, config.head_dim, config.rope_theta,
+                                         self.device)
+        self.w: DeviceWeights | None = None
+        self.last_logits = None  # logits of the latest forward (inspection only)
+
+    def load_state_dict(self, sd):
+        self.w = DeviceWeights(self.cfg, sd, self.dtype, self.device)
+
+    # ------------------------------------------------------------ forward
+    def forward(self, model_inputs, kv_cache: PageCache, mem_idxs: torch.Tensor):
+        """One forward of the NoPad batch; returns next tokens [B, 1] int64."""
+        cfg, w = self.cfg, self.w
+        H, KVH, D = cfg.num_heads, cfg.num_key_value_heads, cfg.head_dim
+        is_prefill = model_inputs.is_prefill
+        ids_h, pos_h, start_h, lens_h, shared_h, rids_h = model_inputs.host
+        ids = model_inputs.input_tokens if is_prefill else model_inputs.output_token_ids
+        T = ids.shape[0]
+        pool = kv_cache.kv_cache_
+        r2t = kv_cache.req_to_tokens_
+        max_len = max(lens_h)
+
+        h = ops.embedding(w.embed, ids)
+        attn = torch.empty((T, H, D), dtype=self.dtype, device=self.device)
+        f = None
+        for li, lw in enumerate(w.layers):
+            x = ops.rmsnorm(h, lw["ln1"], cfg.rms_norm_eps, residual=f)
+            qkv = ops.gemm(x, lw["wqkv"], lw["bqkv"])
+            ops.rope_kv_scatter(qkv, H, KVH, D, model_inputs.position_ids, self.cos, self.sin,
+                                mem_idxs, pool[li])
+            q = qkv[:, : H * D].view(T, H, D)
+            kc, vc = pool[li, :, :KVH], pool[li, :, KVH:]
+            if not is_prefill:
+                ops.decode_attention(q, r2t, model_inputs.b_rids, model_inputs.b_seq_len, max_len,
+                                     kc, vc, attn)
+            else:
+                shared = model_inputs.b_shared_seq_len if model_inputs.radix_cache is not None else None
+                ops.prefill_attention(q, kc, vc, attn, model_inputs.b_rids, model_inputs.b_start_idx,
+                                      model_inputs.b_seq_len, max_len, r2t, b_shared_seq_len=shared)
+            o = ops.gemm(attn.view(T, H * D), lw["wo"])
+            x2 = ops.rmsnorm(h, lw["ln2"], cfg.rms_norm_eps, residual=o)
+            gu = ops.gemm(x2, lw["wgu"])
+            act = ops.silu_and_mul(gu)
+            f = ops.gemm(act, lw["wdown"])
+
+        if is_prefill:  # last row of each request (post_layer.py:56-71)
+            rows = [s + (l - sh) - 1 for s, l, sh in zip(start_h, lens_h, shared_h)]
+            rows_d = torch.from_numpy(np.asarray(rows, dtype=np.int64)).pin_memory().to(
+                self.device, non_blocking=True)
+            hs = ops.embedding(h, rows_d)
+            fs = ops.embedding(f, rows_d)
+        else:
+            hs, fs = h, f
+        y = ops.rmsnorm(hs, w.norm, cfg.final_norm_eps, residual=fs)
+        logits = ops.gemm(y, w.lm_head)
+        self.last_logits = logits
+        return ops.argmax(logits).view(-1, 1)
+
+
+class Qwen2ModelRunner:
+    """Runner with the reference constructor and methods (model.py:100-175).
+
+    Extra keyword arguments (all optional): dtype (default bfloat16),
+    kv_max_size (token slots; default sized from free memory x mem_usage as
+    the reference), state_dict (weights as a HF-style dict), seed (random
+    init when neither model_path nor state_dict is given), device.
+    """
+
+    def __init__(self, layer_nums, max_batch_size, config: Qwen2Config, **runner_kwargs):
+        self.tp_rank_ = runner_kwargs.get("tp_rank", 0)
+        self.world_size_ = runner_kwargs.get("world_size", 1)
+        assert self.world_size_ == 1, "this build runs tp=1 (one GPU, no collectives)"
+        self.dtype_ = runner_kwargs.get("dtype", torch.bfloat16)
+        self.device_ = torch.device(runner_kwargs.get("device", "cuda"))
+        self.model_ins_ = Qwen2Model(layer_nums, runner_kwargs["max_length"], config,
+                                     self.tp_rank_, self.world_size_, self.dtype_, self.device_)
+        self.model_path_ = runner_kwargs.get("model_path")
+        self.state_dict_ = runner_kwargs.get("state_dict")
+        self.seed_ = runner_kwargs.get("seed", 0)
+        self.kv_max_size_arg_ = runner_kwargs.get("kv_max_size")
+        self.max_batch_size_ = max_batch_size
+        self.max_length_ = runner_kwargs["max_length"]
+        self.mem_usage_ = runner_kwargs.get("mem_usage", 0.5)
+        self.use_radix_cache_ = runner_kwargs.get("use_radix_cache", False)
+        self.radix_cache = None
+        self.kv_cache = None
+        self.layer_nums_ = layer_nums
+        self.config_ = config
+
+    def init_model(self):
+        if self.state_dict_ is not None:
+            sd = self.state_dict_
+        elif self.model_path_:
+            sd = load_state_dict(self.model_path_)
+        else:
+            sd = random_state_dict(self.config_, seed=self.seed_, device=self.device_,
+                                   dtype=self.dtype_)
+        self.model_ins_.load_state_dict(sd)
+        self.state_dict_ = None
+        self.kv_cache = PageCache(self.max_batch_size_, self.max_length_, self.mem_usage_,
+                                  self.layer_nums_, self.config_.head_dim,
+                                  self.config_.num_key_value_heads, torch_dtype=self.dtype_,
+                                  tp_rank=self.tp_rank_, tp_world_size=self.world_size_,
+                                  kv_max_size=self.kv_max_size_arg_, device=self.device_)
+        self.radix_cache = RadixTree() if self.use_radix_cache_ else None
+        return self.kv_cache.kv_max_size_
+
+    def _alloc_for_forward(self, model_inputs):
+        """Slot allocation done by layer 0 in the reference (transformer_layer.py:53-60)."""
+        _, _, _, lens, shared, rids = model_inputs.host
+        if model_inputs.is_prefill:
+            match = [len(r.match_token_idxs) if r.match_token_idxs is not None else 0
+                     for r in model_inputs.request_mapping.values()]
+            return self.kv_cache.alloc_token_idxs(rids, match, [l - m for l, m in zip(lens, match)])
+        return self.kv_cache.alloc_token_idxs(rids, [l - 1 for l in lens], [1] * len(lens))
+
+    def forward(self, model_inputs):
+        if self.radix_cache is not None:
+            self._compute_if_need_free_radix_tree(model_inputs)
+        mem_idxs = self._alloc_for_forward(model_inputs)
+        return self.model_ins_.forward(model_inputs, self.kv_cache, mem_idxs)
+
+    def _compute_if_need_free_radix_tree(self, model_inputs):
+        """Evict LRU radix leaves when the next forward needs more slots than
+        are free (model.py:128-144)."""
+        ids, _, _, lens, _, _ = model_inputs.host
+        need_now = len(ids) if model_inputs.is_prefill else len(lens)
+        need = self.kv_cache.if_need_more_tokens(need_now)
+        token_idxs = self.radix_cache.evict_node(need)
+        if token_idxs is not None:
+            self.kv_cache.free_token_idxs(token_idxs)
+
+    def _add_new_req(self, length):
+        if self.kv_cache.can_allocated(length):
+            return self.kv_cache.alloc_req()
+        return None
+
+    def free_reqs(self, reqs):
+        if self.radix_cache is not None:
+            return
+        self.kv_cache.dealloc_reqs(reqs)

@@ -1,0 +1,186 @@
+"""Qwen2 configuration and weights.
+
+Qwen2Config mirrors litelang/models/qwen2/model.py:7-21 (it reads the same
+config.json keys and derives head_dim = hidden / heads). Weights arrive as a
+Hugging Face style state dict -- from safetensors files (the loader of
+model.py:61-97) or from `random_state_dict` for the random-init benchmark
+configurations -- and are packed once into the device layout:
+
+  embed      [V, hidden]
+  wqkv       [(H + 2*KVH) * D, hidden]   rows: q heads, k heads, v heads
+  bqkv       [(H + 2*KVH) * D]
+  wo         [hidden, H * D]             (o_proj bias is ignored, as the
+                                          reference does: transformer_layer.py:193)
+  wgu        [2 * I, hidden]             rows: gate then up
+  wdown      [hidden, I]
+  ln1, ln2   [hidden]
+  norm       [hidden]
+  lm_head    [V, hidden]                 (= embed when tied)
+
+All matrices keep the nn.Linear [out, in] layout (the reference transposes to
+[in, out] for torch.mm, load_weights.py:22-28); the GEMM kernels stream both
+operands k-contiguous.
+"""
+from __future__ import annotations
+
+import json
+import os
+from dataclasses import dataclass
+
+import torch
+
+
+@dataclass
+class Qwen2Config:
+    layer_nums: int
+    hidden_size: int
+    num_heads: int
+    num_key_value_heads: int
+    intermediate_size: int
+    vocab_size: int
+    tie_word_embeddings: bool = True
+    rms_norm_eps: float = 1e-6
+    final_norm_eps: float = 1e-5   # post_layer.py:42
+    rope_theta: float = 1e6        # pre_layer.py:22
+
+    @property
+    def head_dim(self) -> int:
+        return self.hidden_size // self.num_heads  # model.py:19
+
+    @classmethod
+    def from_json(cls, config_path: str) -> "Qwen2Config":
+        with open(config_path, "r", encoding="utf-8") as f:
+            c = json.load(f)
+        return cls(layer_nums=c["num_hidden_layers"], hidden_size=c["hidden_size"],
+                   num_heads=c["num_attention_heads"],
+                   num_key_value_heads=c["num_key_value_heads"],
+                   intermediate_size=c["intermediate_size"], vocab_size=c["vocab_size"],
+                   tie_word_embeddings=c.get("tie_word_embeddings", True))
+
+    def num_params(self) -> int:
+        D, H, KVH, hd, I, V = (self.head_dim, self.num_heads, self.num_key_value_heads,
+                               self.hidden_size, self.intermediate_size, self.vocab_size)
+        per_layer = (H + 2 * KVH) * D * hd + (H + 2 * KVH) * D + hd * H * D + 3 * I * hd + 2 * hd
+        return self.layer_nums * per_layer + V * hd * (1 if self.tie_word_embeddings else 2) + hd
+
+
+# The BASELINE configurations
+def tiny_config() -> Qwen2Config:
+    return Qwen2Config(layer_nums=2, hidden_size=256, num_heads=4, num_key_value_heads=2,
+                       intermediate_size=688, vocab_size=1024)
+
+
+def qwen2_1p5b_config() -> Qwen2Config:
+    return Qwen2Config(layer_nums=28, hidden_size=1536, num_heads=12, num_key_value_heads=2,
+                       intermediate_size=8960, vocab_size=151936)
+
+
+def qwen25_3b_config() -> Qwen2Config:
+    return Qwen2Config(layer_nums=36, hidden_size=2048, num_heads=16, num_key_value_heads=2,
+                       intermediate_size=11008, vocab_size=151936)
+
+
+def state_dict_shapes(cfg: Qwen2Config):
+    """(name, shape, kind) in the canonical generation order; kind is 'w'
+    (N(0, std)) or 'norm' (ones)."""
+    D, H, KVH, hd, I, V = (cfg.head_dim, cfg.num_heads, cfg.num_key_value_heads,
+                           cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size)
+    out = [("model.embed_tokens.weight", (V, hd), "w")]
+    for i in range(cfg.layer_nums):
+        p = f"model.layers.{i}."
+        out += [
+            (p + "self_attn.q_proj.weight", (H * D, hd), "w"),
+            (p + "self_attn.q_proj.bias", (H * D,), "w"),
+            (p + "self_attn.k_proj.weight", (KVH * D, hd), "w"),
+            (p + "self_attn.k_proj.bias", (KVH * D,), "w"),
+            (p + "self_attn.v_proj.weight", (KVH * D, hd), "w"),
+            (p + "self_attn.v_proj.bias", (KVH * D,), "w"),
+            (p + "self_attn.o_proj.weight", (hd, H * D), "w"),
+            (p + "mlp.gate_proj.weight", (I, hd), "w"),
+            (p + "mlp.up_proj.weight", (I, hd), "w"),
+            (p + "mlp.down_proj.weight", (hd, I), "w"),
+            (p + "input_layernorm.weight", (hd,), "norm"),
+            (p + "post_attention_layernorm.weight", (hd,), "norm"),
+        ]
+    out.append(("model.norm.weight", (hd,), "norm"))
+    if not cfg.tie_word_embeddings:
+        out.append(("lm_head.weight", (V, hd), "w"))
+    return out
+
+
+def random_state_dict(cfg: Qwen2Config, seed: int = 0, std: float = 0.02, device="cpu",
+                      dtype=torch.float32):
+    """Random-init weights: linear/embedding weights and q/k/v biases drawn
+    N(0, std) from one torch.Generator seeded `seed`, in the order of
+    state_dict_shapes; RMSNorm gammas = 1 (the Hugging Face init)."""
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    sd = {}
+    for name, shape, kind in state_dict_shapes(cfg):
+        if kind == "norm":
+            sd[name] = torch.ones(shape, device=device, dtype=dtype)
+        else:
+            t = torch.randn(shape, generator=g, device=device, dtype=torch.float32)
+            sd[name] = (t * std).to(dtype)
+    return sd
+
+
+def load_state_dict(model_path: str):
+    """Read every tensor of a (possibly sharded) safetensors checkpoint on the
+    CPU (model.py:61-97)."""
+    from safetensors import safe_open
+
+    index = None
+    for name in ("model.safetensors.index.json", "pytorch_model.safetensors.index.json"):
+        if os.path.exists(os.path.join(model_path, name)):
+            index = os.path.join(model_path, name)
+    files = []
+    if index is not None:
+        with open(index) as f:
+            files = sorted(set(json.load(f)["weight_map"].values()))
+    else:
+        files = ["model.safetensors"]
+    sd = {}
+    for fn in files:
+        with safe_open(os.path.join(model_path, fn), framework="pt") as f:
+            for k in f.keys():
+                sd[k] = f.get_tensor(k)
+    return sd
+
+
+class DeviceWeights:
+    """Packed device copy of a state dict (layout in the module docstring)."""
+
+    def __init__(self, cfg: Qwen2Config, sd: dict, dtype: torch.dtype, device):
+        def dev(t):
+            return t.to(device=device, dtype=dtype).contiguous()
+
+        self.embed = dev(sd["model.embed_tokens.weight"])
+        self.norm = dev(sd["model.norm.weight"])
+        self.lm_head = self.embed if cfg.tie_word_embeddings else dev(sd["lm_head.weight"])
+        self.layers = []
+        for i in range(cfg.layer_nums):
+            p = f"model.layers.{i}."
+            lw = {}
+            lw["wqkv"] = dev(torch.cat([sd[p + "self_attn.q_proj.weight"],
+                                        sd[p + "self_attn.k_proj.weight"],
+                                        sd[p + "self_attn.v_proj.weight"]], 0))
+            bq = sd.get(p + "self_attn.q_proj.bias")
+            lw["bqkv"] = None if bq is None else dev(torch.cat([
+                bq, sd[p + "self_attn.k_proj.bias"], sd[p + "self_attn.v_proj.bias"]], 0))
+            lw["wo"] = dev(sd[p + "self_attn.o_proj.weight"])
+            lw["wgu"] = dev(torch.cat([sd[p + "mlp.gate_proj.weight"],
+                                       sd[p + "mlp.up_proj.weight"]], 0))
+            lw["wdown"] = dev(sd[p + "mlp.down_proj.weight"])
+            lw["ln1"] = dev(sd[p + "input_layernorm.weight"])
+            lw["ln2"] = dev(sd[p + "post_attention_layernorm.weight"])
+            self.layers.append(lw)
+
+    def nbytes_streamed_per_decode(self) -> int:
+        """Weight bytes one decode forward reads (embedding rows excluded)."""
+        n = self.norm.numel() + self.lm_head.numel()
+        for lw in self.layers:
+            for v in lw.values():
+                if v is not None:
+                    n += v.numel()
+        return n * self.embed.element_size()

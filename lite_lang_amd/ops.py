@@ -1,0 +1,265 @@
+"""Torch-tensor front end of the C ABI.
+
+Every function here takes torch tensors that live on a HIP device, checks
+shapes the way the reference does (Python ``assert``), and launches the
+matching ``ll_*`` entry point on torch's current stream. Nothing here
+computes on the host; a missing library raises at import.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+_L = _lib.load()
+
+_DTYPES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+_IDX = {torch.int32: 0, torch.int64: 1}
+
+
+def dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DTYPES[t.dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {t.dtype}") from None
+
+
+def _idx(t: torch.Tensor, name: str) -> int:
+    try:
+        return _IDX[t.dtype]
+    except KeyError:
+        raise TypeError(f"{name}: index tensor must be int32 or int64, got {t.dtype}") from None
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _dev(*ts: torch.Tensor) -> None:
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("lite_lang_amd ops need device tensors (got a CPU tensor)")
+
+
+# ------------------------------------------------------------------ workspaces
+# Persistent, zero-initialised device buffers keyed by (device, name). Tickets
+# inside them are left at zero by the kernels, so they are zeroed only when a
+# buffer is (re)allocated. Calls on one device that share a buffer must not
+# overlap in time (the reference's single scheduler thread never does).
+_WS: dict[tuple[int, str], torch.Tensor] = {}
+
+
+def workspace(device: torch.device, name: str, nbytes: int) -> torch.Tensor:
+    key = (device.index if device.index is not None else torch.cuda.current_device(), name)
+    buf = _WS.get(key)
+    if buf is None or buf.numel() < nbytes:
+        if buf is not None and torch.cuda.is_current_stream_capturing():
+            raise RuntimeError(f"workspace '{name}' must be sized before graph capture")
+        buf = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
+        _WS[key] = buf
+    return buf
+
+
+def reserve_workspace(device: torch.device, name: str, nbytes: int) -> None:
+    workspace(device, name, nbytes)
+
+
+# ------------------------------------------------------------------ attention
+def decode_attention(q, req_to_tokens, b_req_idx, b_seq_len, max_len_in_batch, cache_k, cache_v,
+                     out, sm_scale=None):
+    """out[b, h] = softmax(q[b,h] K^T / sqrt(D)) V over the slot-table rows."""
+    _dev(q, req_to_tokens, b_req_idx, b_seq_len, cache_k, cache_v, out)
+    B, H, D = q.shape
+    KVH = cache_k.shape[1]
+    assert cache_k.shape[-1] == D and cache_v.shape[-1] == D
+    assert q.stride(-1) == 1 and cache_k.stride(-1) == 1 and cache_v.stride(-1) == 1
+    assert out.shape == q.shape and out.stride(-1) == 1
+    assert H % KVH == 0
+    if req_to_tokens.dtype != torch.int32:
+        req_to_tokens = req_to_tokens.to(torch.int32)
+    assert req_to_tokens.stride(-1) == 1
+    if sm_scale is None:
+        sm_scale = 1.0 / (D ** 0.5)
+    max_len = int(max_len_in_batch)
+    nbytes = _L.ll_decode_attention_workspace_size(B, H, KVH, D, max_len)
+    ws = workspace(q.device, "decode_attention", nbytes)
+    rc = _L.ll_decode_attention(
+        q.data_ptr(), q.stride(0), q.stride(1),
+        cache_k.data_ptr(), cache_k.stride(0), cache_k.stride(1),
+        cache_v.data_ptr(), cache_v.stride(0), cache_v.stride(1),
+        req_to_tokens.data_ptr(), req_to_tokens.stride(0),
+        b_req_idx.data_ptr(), _idx(b_req_idx, "b_req_idx"),
+        b_seq_len.data_ptr(), _idx(b_seq_len, "b_seq_len"),
+        out.data_ptr(), out.stride(0), out.stride(1),
+        B, H, KVH, D, max_len, float(sm_scale), dtype_code(q),
+        ws.data_ptr(), ws.numel(), _stream(q))
+    _lib.check(rc, "ll_decode_attention")
+    return out
+
+
+def prefill_attention(q, k, v, o, b_req_idx, b_start_loc, b_seq_len, max_input_len,
+                      req_to_tokens, b_shared_seq_len=None, sm_scale=None):
+    """NoPad causal prefill over the slot table (optionally with shared prefixes)."""
+    _dev(q, k, v, o, b_req_idx, b_start_loc, b_seq_len, req_to_tokens)
+    T, H, D = q.shape
+    KVH = k.shape[1]
+    assert k.shape[-1] == D and v.shape[-1] == D
+    assert q.stride(-1) == 1 and k.stride(-1) == 1 and v.stride(-1) == 1 and o.stride(-1) == 1
+    assert H % KVH == 0
+    if req_to_tokens.dtype != torch.int32:
+        req_to_tokens = req_to_tokens.to(torch.int32)
+    if sm_scale is None:
+        sm_scale = 1.0 / (D ** 0.5)
+    B = b_seq_len.shape[0]
+    sh_ptr, sh64 = (0, 0)
+    if b_shared_seq_len is not None:
+        _dev(b_shared_seq_len)
+        sh_ptr, sh64 = b_shared_seq_len.data_ptr(), _idx(b_shared_seq_len, "b_shared_seq_len")
+    rc = _L.ll_prefill_attention(
+        q.data_ptr(), q.stride(0), q.stride(1),
+        k.data_ptr(), k.stride(0), k.stride(1),
+        v.data_ptr(), v.stride(0), v.stride(1),
+        o.data_ptr(), o.stride(0), o.stride(1),
+        req_to_tokens.data_ptr(), req_to_tokens.stride(0),
+        b_req_idx.data_ptr(), _idx(b_req_idx, "b_req_idx"),
+        b_start_loc.data_ptr(), _idx(b_start_loc, "b_start_loc"),
+        b_seq_len.data_ptr(), _idx(b_seq_len, "b_seq_len"),
+        sh_ptr or None, sh64,
+        B, H, KVH, D, int(max_input_len), float(sm_scale), dtype_code(q), _stream(q))
+    _lib.check(rc, "ll_prefill_attention")
+    return o
+
+
+# ------------------------------------------------------------------ elementwise
+def rmsnorm(x, gamma, eps, residual=None, out=None):
+    """out = rmsnorm(x [+ residual]) * gamma; with residual, x is updated in place."""
+    _dev(x, gamma, residual, out)
+    assert x.ndim == 2 and x.shape[1] == gamma.shape[0]
+    assert x.stride(1) == 1 and gamma.stride(0) == 1
+    if out is None:
+        out = torch.empty_like(x)
+    assert out.shape == x.shape and out.stride(1) == 1
+    r_ptr, r_rs = (None, 0)
+    if residual is not None:
+        assert residual.shape == x.shape and residual.stride(1) == 1
+        r_ptr, r_rs = residual.data_ptr(), residual.stride(0)
+    rc = _L.ll_rmsnorm(x.data_ptr(), x.stride(0), r_ptr, r_rs, gamma.data_ptr(), out.data_ptr(),
+                       out.stride(0), x.shape[0], x.shape[1], float(eps), dtype_code(x),
+                       _stream(x))
+    _lib.check(rc, "ll_rmsnorm")
+    return out
+
+
+def rotary_emb(q, k, cos, sin):
+    _dev(q, k, cos, sin)
+    T, Hq, D = q.shape
+    Hk = k.shape[1]
+    assert q.stride(2) == 1 and k.stride(2) == 1 and cos.stride(1) == 1 and sin.stride(1) == 1
+    assert cos.dtype == sin.dtype
+    rc = _L.ll_rotary_emb(q.data_ptr(), q.stride(0), q.stride(1), Hq,
+                          k.data_ptr(), k.stride(0), k.stride(1), Hk,
+                          cos.data_ptr(), cos.stride(0), sin.data_ptr(), sin.stride(0),
+                          T, D, dtype_code(q), dtype_code(cos), _stream(q))
+    _lib.check(rc, "ll_rotary_emb")
+
+
+def rope_kv_scatter(qkv, q_heads, kv_heads, head_dim, positions, cos_table, sin_table, slots,
+                    pool_layer):
+    """Rotate q in place inside qkv; write rotated K and V to pool_layer[slots]."""
+    _dev(qkv, positions, cos_table, sin_table, slots, pool_layer)
+    T = qkv.shape[0]
+    assert qkv.stride(1) == 1 and qkv.shape[1] == (q_heads + 2 * kv_heads) * head_dim
+    assert slots.dtype == torch.int32 and pool_layer.stride(-1) == 1
+    assert cos_table.stride(1) == 1 and cos_table.stride(0) == sin_table.stride(0)
+    rc = _L.ll_rope_kv_scatter(qkv.data_ptr(), qkv.stride(0), T, q_heads, kv_heads, head_dim,
+                               positions.data_ptr(), _idx(positions, "positions"),
+                               cos_table.data_ptr(), sin_table.data_ptr(), cos_table.stride(0),
+                               dtype_code(cos_table), slots.data_ptr(), pool_layer.data_ptr(),
+                               pool_layer.stride(0), pool_layer.stride(1), dtype_code(qkv),
+                               _stream(qkv))
+    _lib.check(rc, "ll_rope_kv_scatter")
+
+
+def kv_store(src, slots, pool):
+    _dev(src, slots, pool)
+    T, Hs, D = src.shape
+    assert slots.dtype == torch.int32 and src.stride(2) == 1 and pool.stride(-1) == 1
+    rc = _L.ll_kv_store(src.data_ptr(), src.stride(0), src.stride(1), Hs, D, slots.data_ptr(),
+                        pool.data_ptr(), pool.stride(0), pool.stride(1), T, dtype_code(src),
+                        _stream(src))
+    _lib.check(rc, "ll_kv_store")
+
+
+def silu_and_mul(x, out=None):
+    _dev(x, out)
+    M, N2 = x.shape
+    N = N2 // 2
+    assert x.stride(1) == 1
+    if out is None:
+        out = x[:, :N]
+    assert out.stride(1) == 1
+    rc = _L.ll_silu_and_mul(x.data_ptr(), x.stride(0), out.data_ptr(), out.stride(0), M, N,
+                            dtype_code(x), _stream(x))
+    _lib.check(rc, "ll_silu_and_mul")
+    return out
+
+
+def embedding(table, ids, out=None):
+    _dev(table, ids, out)
+    V, Hd = table.shape
+    T = ids.shape[0]
+    assert table.stride(1) == 1
+    if out is None:
+        out = torch.empty((T, Hd), dtype=table.dtype, device=table.device)
+    rc = _L.ll_embedding(table.data_ptr(), table.stride(0), V, ids.data_ptr(), _idx(ids, "ids"),
+                         out.data_ptr(), out.stride(0), T, Hd, dtype_code(table), _stream(table))
+    _lib.check(rc, "ll_embedding")
+    return out
+
+
+def argmax(x, out=None):
+    _dev(x, out)
+    M, N = x.shape
+    assert x.stride(1) == 1
+    if out is None:
+        out = torch.empty((M,), dtype=torch.int64, device=x.device)
+    nbytes = _L.ll_argmax_workspace_size(M, N)
+    ws = workspace(x.device, "argmax", nbytes)
+    rc = _L.ll_argmax(x.data_ptr(), x.stride(0), M, N, out.data_ptr(), ws.data_ptr(), ws.numel(),
+                      dtype_code(x), _stream(x))
+    _lib.check(rc, "ll_argmax")
+    return out
+
+
+# ------------------------------------------------------------------ GEMM
+def gemm(x, w, bias=None, out=None):
+    """out[M, N] = x[M, K] @ w[N, K]^T (+ bias); w in nn.Linear [out, in] layout."""
+    _dev(x, w, bias, out)
+    M, K = x.shape
+    N, K2 = w.shape
+    assert K == K2, f"gemm: K mismatch {K} vs {K2}"
+    assert x.stride(1) == 1 and w.stride(1) == 1 and x.dtype == w.dtype
+    if out is None:
+        out = torch.empty((M, N), dtype=x.dtype, device=x.device)
+    assert out.shape == (M, N) and out.stride(1) == 1
+    nbytes = _L.ll_gemm_workspace_size(M, N, K)
+    ws_ptr, ws_n = (None, 0)
+    if nbytes > 0:
+        ws = workspace(x.device, "gemm", nbytes)
+        ws_ptr, ws_n = ws.data_ptr(), ws.numel()
+    rc = _L.ll_gemm(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0),
+                    bias.data_ptr() if bias is not None else None, out.data_ptr(), out.stride(0),
+                    M, N, K, dtype_code(x), ws_ptr, ws_n, _stream(x))
+    _lib.check(rc, "ll_gemm")
+    return out
+
+
+# ------------------------------------------------------------------ slot table
+def assign_slots(req_to_tokens, packed, n):
+    """req_to_tokens[rows, cols] = slots with packed = int32 [3, n] (slots, rows, cols)."""
+    _dev(req_to_tokens, packed)
+    assert req_to_tokens.dtype == torch.int32 and packed.dtype == torch.int32
+    assert packed.is_contiguous() and packed.shape[0] == 3
+    rc = _L.ll_assign_slots(req_to_tokens.data_ptr(), req_to_tokens.stride(0), packed[0].data_ptr(),
+                            packed[1].data_ptr(), packed[2].data_ptr(), n, _stream(req_to_tokens))
+    _lib.check(rc, "ll_assign_slots")

@@ -1,0 +1,140 @@
+"""CPU restatement of the Qwen2 token loop (test infrastructure only).
+
+Dataflow follows litelang/models/qwen2/model.py:48-59 (Qwen2Model.forward),
+layer/pre_layer.py:15-30, layer/transformer_layer.py:46-194 and
+layer/post_layer.py:44-107, with the reference quirks kept:
+  * per-layer RMSNorm eps 1e-6 (transformer_layer.py:41), final norm eps 1e-5
+    (post_layer.py:42);
+  * RoPE theta 1e6, cos/sin table built in fp32 and stored fp16
+    (pre_layer.py:21-30);
+  * K rotated before it is written to the pool (transformer_layer.py:115,143);
+  * o_proj bias ignored (transformer_layer.py:193);
+  * residual adds stored in the model dtype (transformer_layer.py:69,76);
+  * greedy argmax on the stored logits, first index on ties (post_layer.py:105-107).
+Compute is float64; `rnd` stores an intermediate in the model dtype wherever
+the reference stores a tensor.
+
+Weights come in as a Hugging Face style state dict (the names read by
+layer_weights/load_weights.py:86-172 and pre/post_layer_weights.py).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import ops
+from .cache import PageCache
+from .runner_batch import Req, no_padding_messages
+
+
+@dataclass
+class Qwen2Cfg:
+    num_layers: int
+    hidden: int
+    heads: int
+    kv_heads: int
+    intermediate: int
+    vocab: int
+    tie_word_embeddings: bool = True
+    eps: float = 1e-6
+    final_eps: float = 1e-5
+    theta: float = 1e6
+
+    @property
+    def head_dim(self) -> int:
+        return self.hidden // self.heads  # model.py:19
+
+
+class Qwen2Oracle:
+    def __init__(self, cfg: Qwen2Cfg, sd: dict, dtype: torch.dtype, max_batch: int,
+                 max_length: int, kv_slots: int):
+        self.cfg, self.dtype = cfg, dtype
+        r = lambda t: ops.rnd(t.detach().cpu(), dtype)  # noqa: E731
+        self.embed = r(sd["model.embed_tokens.weight"])
+        self.lm_head = self.embed if cfg.tie_word_embeddings else r(sd["lm_head.weight"])
+        self.norm = r(sd["model.norm.weight"])
+        self.layers = []
+        for i in range(cfg.num_layers):
+            p = f"model.layers.{i}."
+            self.layers.append(dict(
+                wq=r(sd[p + "self_attn.q_proj.weight"]), bq=r(sd[p + "self_attn.q_proj.bias"]),
+                wk=r(sd[p + "self_attn.k_proj.weight"]), bk=r(sd[p + "self_attn.k_proj.bias"]),
+                wv=r(sd[p + "self_attn.v_proj.weight"]), bv=r(sd[p + "self_attn.v_proj.bias"]),
+                wo=r(sd[p + "self_attn.o_proj.weight"]),
+                wg=r(sd[p + "mlp.gate_proj.weight"]), wu=r(sd[p + "mlp.up_proj.weight"]),
+                wd=r(sd[p + "mlp.down_proj.weight"]),
+                ln1=r(sd[p + "input_layernorm.weight"]),
+                ln2=r(sd[p + "post_attention_layernorm.weight"]),
+            ))
+        D, KVH = cfg.head_dim, cfg.kv_heads
+        self.pool = torch.zeros((cfg.num_layers, kv_slots, 2 * KVH, D), dtype=torch.float64)
+        self.cache = PageCache(max_batch, max_length, kv_slots)
+        cos, sin = ops.rope_table(max_length, D, cfg.theta)
+        self.cos, self.sin = cos.to(torch.float64), sin.to(torch.float64)
+
+    # ------------------------------------------------------------ one forward
+    def forward(self, reqs, is_prefill: bool, ids):
+        cfg, dt = self.cfg, self.dtype
+        H, KVH, D = cfg.heads, cfg.kv_heads, cfg.head_dim
+        _, pos, start, lens, shared, rids = no_padding_messages(reqs, is_prefill)
+        if is_prefill:
+            mem = self.cache.alloc_token_idxs(rids, shared, [l - s for l, s in zip(lens, shared)])
+        else:
+            mem = self.cache.alloc_token_idxs(rids, [l - 1 for l in lens], [1] * len(reqs))
+        mem = torch.as_tensor(mem).long()
+        r2t = torch.as_tensor(self.cache.req_to_tokens_)
+        pos_t = torch.as_tensor(pos).long()
+        cos, sin = self.cos[pos_t], self.sin[pos_t]
+        T = len(ids)
+        h = self.embed[torch.as_tensor(ids).long()]
+        for li, w in enumerate(self.layers):
+            x = ops.rnd(ops.rmsnorm(h, w["ln1"], cfg.eps), dt)
+            q = ops.rnd(ops.linear(x, w["wq"], w["bq"]), dt).view(T, H, D)
+            k = ops.rnd(ops.linear(x, w["wk"], w["bk"]), dt).view(T, KVH, D)
+            v = ops.rnd(ops.linear(x, w["wv"], w["bv"]), dt).view(T, KVH, D)
+            q = ops.rnd(ops.rotary(q, cos, sin), dt)
+            k = ops.rnd(ops.rotary(k, cos, sin), dt)
+            self.pool[li, mem, :KVH] = k
+            self.pool[li, mem, KVH:] = v
+            kp, vp = self.pool[li, :, :KVH], self.pool[li, :, KVH:]
+            if is_prefill:
+                a = ops.prefill_attention(q, kp, vp, rids, start, lens, r2t,
+                                          b_shared_seq_len=shared, p_dtype=dt)
+            else:
+                a = ops.decode_attention(q, r2t, rids, lens, kp, vp)
+            a = ops.rnd(a, dt).view(T, H * D)
+            o = ops.rnd(ops.linear(a, w["wo"]), dt)
+            h = ops.rnd(h + o, dt)
+            x2 = ops.rnd(ops.rmsnorm(h, w["ln2"], cfg.eps), dt)
+            gu = ops.rnd(ops.linear(x2, torch.cat([w["wg"], w["wu"]], 0)), dt)
+            act = ops.rnd(ops.silu_and_mul(gu, dt), dt)
+            f = ops.rnd(ops.linear(act, w["wd"]), dt)
+            h = ops.rnd(h + f, dt)
+        if is_prefill:  # last row of each request (post_layer.py:56-71)
+            rows = [st + (l - s) - 1 for st, l, s in zip(start, lens, shared)]
+        else:
+            rows = list(start)
+        hs = ops.rnd(ops.rmsnorm(h[torch.as_tensor(rows)], self.norm, cfg.final_eps), dt)
+        logits = ops.rnd(ops.linear(hs, self.lm_head), dt)
+        return ops.argmax_first(logits), logits
+
+    # ------------------------------------------------------------ greedy loop
+    def generate(self, prompts, n_new: int, return_logits: bool = False):
+        """Prefill all prompts as one NoPad batch, then n_new-1 decode steps
+        (the loop of test/generate_token.py:61-63). Returns [B, n_new] tokens."""
+        reqs = []
+        for p in prompts:
+            rid = self.cache.alloc_req()
+            reqs.append(Req(rid=rid, input_tokens=list(p)))
+        ids = [t for p in prompts for t in p]
+        toks, logits = self.forward(reqs, True, ids)
+        out, all_logits = [toks], [logits]
+        for _ in range(n_new - 1):
+            for r, t in zip(reqs, toks.tolist()):
+                r.output_tokens.append(t)
+            toks, logits = self.forward(reqs, False, toks.tolist())
+            out.append(toks)
+            all_logits.append(logits)
+        res = torch.stack(out, 1)
+        return (res, torch.stack(all_logits, 1)) if return_logits else res

@@ -1,0 +1,309 @@
+"""GPU parity of every kernel against the CPU oracle (oracle/ops.py).
+
+Tolerances: outputs stored in bf16/fp16 are compared with the float64
+oracle evaluated on the same (rounded) inputs at max-abs 2e-2 (the bar the
+north star sets for bf16 attention, norm and logits); fp32 outputs at 1e-4.
+Integer / index outputs are compared exactly.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import ops as O
+
+pytestmark = pytest.mark.gpu
+
+BF16_ATOL = 2e-2
+F32_ATOL = 1e-4
+
+
+def _ops():
+    from lite_lang_amd import ops
+    return ops
+
+
+def _tol(dtype):
+    return F32_ATOL if dtype == torch.float32 else BF16_ATOL
+
+
+def _maxdiff(a, b):
+    return float((a.detach().cpu().to(torch.float64) - b.to(torch.float64)).abs().max())
+
+
+# ------------------------------------------------------------ decode attention
+def _decode_case(cuda, B, H, KVH, D, lens, dtype, seed, pool_slots=None, rids=None):
+    g = torch.Generator().manual_seed(seed)
+    max_len = max(lens)
+    P = pool_slots or B * max_len
+    q = torch.randn(B, H, D, generator=g).to(dtype)
+    pool = torch.randn(P, 2 * KVH, D, generator=g).to(dtype)
+    perm = torch.from_numpy(np.random.RandomState(seed).permutation(P)[: B * max_len]
+                            .astype(np.int32)).view(B, max_len)
+    r2t = torch.zeros(B + 3, max_len, dtype=torch.int32)
+    rids = rids if rids is not None else list(range(B))
+    for b, r in enumerate(rids):
+        r2t[r] = perm[b]
+    ref = O.decode_attention(q, r2t, rids, lens, pool[:, :KVH], pool[:, KVH:])
+    qd, pd, r2td = q.to(cuda), pool.to(cuda), r2t.to(cuda)
+    out = torch.empty_like(qd)
+    _ops().decode_attention(qd, r2td, torch.tensor(rids, dtype=torch.int32, device=cuda),
+                            torch.tensor(lens, dtype=torch.int64, device=cuda), max_len,
+                            pd[:, :KVH], pd[:, KVH:], out)
+    torch.cuda.synchronize()
+    return out, ref
+
+
+def test_decode_attention_config2_uniform(cuda):
+    print("case: decode config2 B=40 ctx=600 H=12 KVH=2 D=128 bf16", flush=True)
+    out, ref = _decode_case(cuda, 40, 12, 2, 128, [600] * 40, torch.bfloat16, 0)
+    assert _maxdiff(out, ref) <= BF16_ATOL
+
+
+def test_decode_attention_config2_varlen(cuda):
+    lens = np.random.RandomState(1).randint(1, 601, size=40).tolist()
+    print(f"case: decode config2b varlen lens[:5]={lens[:5]}", flush=True)
+    out, ref = _decode_case(cuda, 40, 12, 2, 128, lens, torch.bfloat16, 1)
+    assert _maxdiff(out, ref) <= BF16_ATOL
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("H,KVH,D", [(16, 2, 128), (8, 8, 64), (4, 2, 64), (6, 1, 128)])
+def test_decode_attention_shapes(cuda, dtype, H, KVH, D):
+    lens = [1, 33, 100, 257, 31, 64]
+    print(f"case: decode H={H} KVH={KVH} D={D} {dtype}", flush=True)
+    out, ref = _decode_case(cuda, len(lens), H, KVH, D, lens, dtype, 2, rids=[4, 0, 2, 1, 3, 5])
+    assert _maxdiff(out, ref) <= _tol(dtype)
+
+
+def test_decode_attention_repeat_calls_are_identical(cuda):
+    # the split combine uses self-resetting tickets: calls must not interfere
+    print("case: decode repeat x3", flush=True)
+    a, ref = _decode_case(cuda, 40, 16, 2, 128, [700] * 40, torch.bfloat16, 3)
+    b, _ = _decode_case(cuda, 40, 16, 2, 128, [700] * 40, torch.bfloat16, 3)
+    c, _ = _decode_case(cuda, 2, 16, 2, 128, [40, 2000], torch.bfloat16, 4)
+    assert torch.equal(a, b)
+    assert _maxdiff(a, ref) <= BF16_ATOL
+
+
+def test_decode_attention_reference_wrapper(cuda):
+    from lite_lang_amd.kernel.develop_flash_attn.flash_decoding import (
+        token_decode_attention_flash_decoding)
+    g = torch.Generator().manual_seed(5)
+    B, H, KVH, D = 3, 8, 2, 64
+    lens = [1000, 2000, 3000]  # test_flash_decoding shape (flash_decoding.py:315-345)
+    P = sum(lens)
+    q = torch.randn(B, H, D, generator=g).half()
+    k = torch.randn(P, KVH, D, generator=g).half()
+    v = torch.randn(P, KVH, D, generator=g).half()
+    r2t = torch.zeros(B, max(lens), dtype=torch.int32)
+    s = 0
+    for i, l in enumerate(lens):
+        r2t[i, :l] = torch.arange(s, s + l)
+        s += l
+    ref = O.decode_attention(q, r2t, list(range(B)), lens, k, v)
+    out = torch.empty(B, H, D, dtype=torch.float16, device=cuda)
+    token_decode_attention_flash_decoding(q.to(cuda), r2t.to(cuda), torch.arange(B, device=cuda),
+                                          torch.tensor(lens, device=cuda), max(lens), H, D,
+                                          k.to(cuda), v.to(cuda), out)
+    torch.cuda.synchronize()
+    assert _maxdiff(out, ref) <= 1e-2  # the reference test's own atol
+
+
+# ------------------------------------------------------------ prefill attention
+def _prefill_case(cuda, H, KVH, D, lens, shared, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    B = len(lens)
+    qlens = [l - s for l, s in zip(lens, shared)]
+    T = sum(qlens)
+    starts = np.concatenate([[0], np.cumsum(qlens)[:-1]]).tolist()
+    P = sum(lens) + 17
+    q = torch.randn(T, H, D, generator=g).to(dtype)
+    pool = torch.randn(P, 2 * KVH, D, generator=g).to(dtype)
+    perm = np.random.RandomState(seed).permutation(P).astype(np.int32)
+    r2t = torch.zeros(B + 1, max(lens), dtype=torch.int32)
+    rids = list(range(1, B + 1))
+    o = 0
+    for b, r in enumerate(rids):
+        r2t[r, :lens[b]] = torch.from_numpy(perm[o:o + lens[b]])
+        o += lens[b]
+    ref = O.prefill_attention(q, pool[:, :KVH], pool[:, KVH:], rids, starts, lens, r2t,
+                              b_shared_seq_len=shared,
+                              p_dtype=None if dtype == torch.float32 else dtype)
+    pd = pool.to(cuda)
+    out = torch.empty(T, H, D, dtype=dtype, device=cuda)
+    _ops().prefill_attention(q.to(cuda), pd[:, :KVH], pd[:, KVH:], out,
+                             torch.tensor(rids, dtype=torch.int32, device=cuda),
+                             torch.tensor(starts, dtype=torch.int64, device=cuda),
+                             torch.tensor(lens, dtype=torch.int64, device=cuda), max(lens),
+                             r2t.to(cuda),
+                             b_shared_seq_len=torch.tensor(shared, device=cuda) if any(shared) else None)
+    torch.cuda.synchronize()
+    return out, ref
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("H,KVH,D", [(16, 2, 128), (4, 4, 64)])
+def test_prefill_attention_varlen(cuda, dtype, H, KVH, D):
+    lens = [1, 70, 200, 64, 129]
+    print(f"case: prefill H={H} KVH={KVH} D={D} {dtype}", flush=True)
+    out, ref = _prefill_case(cuda, H, KVH, D, lens, [0] * len(lens), dtype, 10)
+    assert _maxdiff(out, ref) <= _tol(dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_prefill_attention_prompt_cache(cuda, dtype):
+    # shapes of test_context_attention_with_kv_cache_and_prompt_cache
+    # (flash_attn_v2.py:765-800) plus a long-prefix case
+    lens, shared = [16, 32, 300], [8, 11, 260]
+    print(f"case: prefill prompt cache {dtype}", flush=True)
+    out, ref = _prefill_case(cuda, 8, 2, 64, lens, shared, dtype, 11)
+    assert _maxdiff(out, ref) <= _tol(dtype)
+
+
+# ------------------------------------------------------------ elementwise
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_rmsnorm_and_residual(cuda, dtype):
+    g = torch.Generator().manual_seed(20)
+    x = (torch.randn(37, 2048, generator=g) * 0.5 + 0.3).to(dtype)
+    r = torch.randn(37, 2048, generator=g).to(dtype)
+    gamma = (torch.rand(2048, generator=g) + 0.5).to(dtype)
+    ops = _ops()
+    out = ops.rmsnorm(x.to(cuda), gamma.to(cuda), 1e-6)
+    assert _maxdiff(out, O.rmsnorm(x, gamma, 1e-6)) <= _tol(dtype)
+    xd = x.to(cuda)
+    out2 = ops.rmsnorm(xd, gamma.to(cuda), 1e-5, residual=r.to(cuda))
+    h = O.rnd(x.double() + r.double(), dtype)
+    assert torch.equal(xd.cpu(), h.to(dtype))  # residual stored exactly as dtype(x + r)
+    assert _maxdiff(out2, O.rmsnorm(h, gamma, 1e-5)) <= _tol(dtype)
+
+
+def test_rmsnorm_reference_wrapper(cuda):
+    from lite_lang_amd.kernel.develop_rmsnorm.rms_norm import rmsnorm
+    g = torch.Generator().manual_seed(21)
+    # test_rmsnorm shape and distribution (rms_norm.py:101-113)
+    x = torch.normal(0.3, 0.5, size=(100, 2048), generator=g)
+    gamma = torch.normal(0.3, 0.5, size=(2048,), generator=g)
+    out = rmsnorm(x.to(cuda), gamma.to(cuda), 1e-5)
+    assert _maxdiff(out, O.rmsnorm(x, gamma, 1e-5)) <= 1e-3
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_rotary_emb_wrapper_on_pool_view(cuda, dtype):
+    from lite_lang_amd.kernel.develop_rope.rope import rotary_emb_fwd
+    g = torch.Generator().manual_seed(22)
+    T, H, KVH, D = 50, 16, 2, 128
+    q = (torch.randn(T, H, D, generator=g) * 0.3).to(dtype)
+    kv = (torch.randn(T, 2 * KVH, D, generator=g) * 0.3).to(dtype)
+    cos = torch.randn(T, D // 2, generator=g).clamp(-1, 1).to(dtype)
+    sin = torch.randn(T, D // 2, generator=g).clamp(-1, 1).to(dtype)
+    qd, kvd = q.to(cuda), kv.to(cuda)
+    rotary_emb_fwd(qd, kvd[:, :KVH], cos.to(cuda), sin.to(cuda))
+    torch.cuda.synchronize()
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    assert _maxdiff(qd, O.rotary(q, cos, sin)) <= tol
+    assert _maxdiff(kvd[:, :KVH], O.rotary(kv[:, :KVH], cos, sin)) <= tol
+    assert torch.equal(kvd[:, KVH:].cpu(), kv[:, KVH:])  # V heads untouched
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_rope_kv_scatter(cuda, dtype):
+    g = torch.Generator().manual_seed(23)
+    T, H, KVH, D, P = 19, 4, 2, 64, 64
+    qkv = torch.randn(T, (H + 2 * KVH) * D, generator=g).to(dtype)
+    pos = torch.randint(0, 100, (T,), generator=g)
+    cos, sin = O.rope_table(128, D)
+    slots = torch.from_numpy(np.random.RandomState(3).permutation(P)[:T].astype(np.int32))
+    pool = torch.zeros(P, 2 * KVH, D, dtype=dtype)
+    qkvd, poold = qkv.to(cuda), pool.to(cuda)
+    _ops().rope_kv_scatter(qkvd, H, KVH, D, pos.to(cuda), cos.float().to(cuda),
+                           sin.float().to(cuda), slots.to(cuda), poold)
+    torch.cuda.synchronize()
+    c, s = cos[pos], sin[pos]
+    q_ref = O.rotary(qkv[:, :H * D].view(T, H, D), c, s)
+    k_ref = O.rotary(qkv[:, H * D:(H + KVH) * D].view(T, KVH, D), c, s)
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    assert _maxdiff(qkvd[:, :H * D].view(T, H, D), q_ref) <= tol
+    assert _maxdiff(poold[slots.long(), :KVH], k_ref) <= tol
+    assert torch.equal(poold[slots.long(), KVH:].cpu(), qkv[:, (H + KVH) * D:].view(T, KVH, D))
+    untouched = torch.ones(P, dtype=torch.bool)
+    untouched[slots.long()] = False
+    assert float(poold[untouched.to(cuda)].abs().max()) == 0.0
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_silu_and_mul_in_place(cuda, dtype):
+    from lite_lang_amd.kernel.develop_silu_and_mul.silu_and_mul import silu_and_mul_fwd
+    g = torch.Generator().manual_seed(24)
+    x = torch.randn(40, 2 * 1376, generator=g).to(dtype)
+    xd = x.to(cuda)
+    out = silu_and_mul_fwd(xd)
+    assert out.data_ptr() == xd.data_ptr() and out.stride(0) == 2 * 1376
+    ref = O.silu_and_mul(x, dtype)
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    assert _maxdiff(out, ref) <= tol
+
+
+def test_embedding_and_argmax(cuda):
+    g = torch.Generator().manual_seed(25)
+    table = torch.randn(1000, 64, generator=g).bfloat16()
+    ids = torch.randint(0, 1000, (33,), generator=g)
+    out = _ops().embedding(table.to(cuda), ids.to(cuda))
+    assert torch.equal(out.cpu(), table[ids])
+    logits = torch.randn(40, 151936, generator=g).bfloat16()
+    logits[3, 100] = 50.0
+    logits[3, 90000] = 50.0  # tie across chunks: first index wins
+    logits[7, :] = 1.0       # all equal
+    got = _ops().argmax(logits.to(cuda)).cpu()
+    assert torch.equal(got, O.argmax_first(logits.float()))
+    assert got[3] == 100 and got[7] == 0
+    got2 = _ops().argmax(logits[:, :5000].contiguous().to(cuda)).cpu()  # single-chunk path
+    assert torch.equal(got2, O.argmax_first(logits[:, :5000].float()))
+
+
+# ------------------------------------------------------------ GEMM
+@pytest.mark.parametrize("M,N,K", [(1, 2560, 2048), (40, 2560, 2048), (40, 2048, 11008),
+                                   (64, 300, 688), (40, 22016, 2048), (300, 520, 264),
+                                   (129, 256, 64)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_gemm_mfma(cuda, M, N, K, dtype):
+    g = torch.Generator().manual_seed(30)
+    x = torch.randn(M, K, generator=g).to(dtype)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(dtype)
+    b = (torch.randn(N, generator=g) * 0.1).to(dtype)
+    print(f"case: gemm M={M} N={N} K={K} {dtype}", flush=True)
+    y = _ops().gemm(x.to(cuda), w.to(cuda), b.to(cuda))
+    torch.cuda.synchronize()
+    ref = O.linear(x, w, b)
+    assert _maxdiff(y, ref) <= BF16_ATOL
+
+
+def test_gemm_fp32_and_strided_input(cuda):
+    g = torch.Generator().manual_seed(31)
+    x = torch.randn(17, 2 * 96, generator=g)
+    w = torch.randn(70, 96, generator=g)
+    y = _ops().gemm(x.to(cuda)[:, :96], w.to(cuda))
+    assert _maxdiff(y, O.linear(x[:, :96], w)) <= 1e-4
+    xb = x.bfloat16().to(cuda)
+    yb = _ops().gemm(xb[:, 96:], w.bfloat16().to(cuda))
+    assert _maxdiff(yb, O.linear(x[:, 96:].bfloat16(), w.bfloat16())) <= BF16_ATOL
+
+
+# ------------------------------------------------------------ slot table on device
+def test_page_cache_kat_on_device(cuda):
+    import json, os
+    from lite_lang_amd.models.cache import PageCache
+    kat = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "page_cache_kat.json")))
+    pc = PageCache(kat["max_batch_size"], kat["max_length"], 0.0, 1, 128, 2,
+                   torch_dtype=torch.bfloat16, kv_max_size=4096, device=cuda)
+    rids = [pc.alloc_req(), pc.alloc_req()]
+    lens = kat["prefill"]["seq_lens"]
+    got = pc.alloc_token_idxs(rids, [0, 0], lens)
+    r2t = pc.req_to_tokens_.cpu()
+    assert torch.cat([r2t[r, :l] for r, l in zip(rids, lens)]).tolist() == \
+        kat["prefill"]["expected_rows_concat"]
+    assert got.cpu().tolist() == list(range(7))
+    pc.alloc_token_idxs(rids, lens, kat["decode"]["new_tokens"])
+    r2t = pc.req_to_tokens_.cpu()
+    assert torch.cat([r2t[0, :3], r2t[1, :6]]).tolist() == kat["decode"]["expected_rows_concat"]
