@@ -11,10 +11,9 @@
  *   - every call is asynchronous on `stream` and returns LL_OK (0) or a
  *     negative LL_ERR_* code; ll_last_error() then holds the reason. Argument
  *     errors are raised before anything is launched.
- *   - workspaces are caller-owned device buffers. Where a workspace holds
- *     tickets (decode attention, argmax) it must be zero-filled once when it
- *     is allocated; the kernels leave the tickets at zero again. Calls that
- *     share one workspace must not overlap in time.
+ *   - workspaces are caller-owned device buffers of the size the matching
+ *     *_workspace_size query returns (their contents need no initialisation);
+ *     calls that share one workspace must not overlap in time.
  */
 #ifndef LITELANG_AMD_H
 #define LITELANG_AMD_H
@@ -44,7 +43,7 @@ const char* ll_last_error(void);
 
 /* ---------------------------------------------------------------- attention */
 
-/* Paged GQA decode attention, split-K with in-launch combine.
+/* Paged GQA decode attention, split-K (partials merged by a second kernel).
  * Replaces token_decode_attention_flash_decoding
  *   (litelang/kernel/develop_flash_attn/flash_decoding.py:262-312).
  * q [batch, q_heads, head_dim]; k_cache / v_cache [P, kv_heads, head_dim]
@@ -162,6 +161,35 @@ int64_t ll_gemm_workspace_size(int64_t M, int64_t N, int64_t K);
 int ll_gemm(const void* X, int64_t ldx, const void* W, int64_t ldw, const void* bias, void* Y,
             int64_t ldy, int64_t M, int64_t N, int64_t K, int dtype, void* workspace,
             int64_t workspace_bytes, hipStream_t stream);
+
+/* ------------------------------------------------- decode-step split-K path
+ * The M <= 64 projections of a decode step write fp32 partial sums
+ * part[s][m][n] (s < ll_gemm_splitk_count(M, N, K)); the consumer kernels
+ * below sum them in a fixed order, store the projection output in `dtype`
+ * (bit-identical to the unfused product's rounding) and fuse the next op of
+ * the layer. They replace the same reference operations as the entry points
+ * they are named after: the projections of transformer_layer.py:80,82,95-109,193
+ * followed by, respectively, the residual add_ + rmsnorm (:69-71,76,61),
+ * silu_and_mul_fwd (:81) and rotary_emb_fwd + KV-cache write (:112-115,142-143). */
+int ll_gemm_splitk_count(int64_t M, int64_t N, int64_t K);
+int ll_gemm_splitk(const void* X, int64_t ldx, const void* W, int64_t ldw, int64_t M, int64_t N,
+                   int64_t K, int dtype, float* part, int64_t part_bytes, hipStream_t stream);
+/* h = dtype(h + dtype(sum part)); out = rmsnorm(h) * gamma (h updated in place) */
+int ll_add_rmsnorm_splitk(void* h, int64_t h_row_stride, const float* part, int splits,
+                          const void* gamma, void* out, int64_t out_row_stride, int64_t M,
+                          int64_t N, float eps, int dtype, hipStream_t stream);
+/* part covers [M, 2N] (gate then up); out[m, n] = up * dtype(silu(gate)) */
+int ll_silu_and_mul_splitk(const float* part, int splits, void* out, int64_t out_row_stride,
+                           int64_t M, int64_t N, int dtype, hipStream_t stream);
+/* part covers [T, (q_heads + 2*kv_heads)*D]; adds bias, rotates q into q_out
+ * [T, q_heads*D] and writes rotated K and V to pool_layer[slots[t]] */
+int ll_rope_kv_scatter_splitk(const float* part, int splits, const void* bias, void* q_out,
+                              int64_t q_row_stride, int64_t ntok, int64_t q_heads,
+                              int64_t kv_heads, int64_t head_dim, const void* positions,
+                              int positions_i64, const void* cos_table, const void* sin_table,
+                              int64_t table_row_stride, int cs_dtype, const int32_t* slots,
+                              void* pool_layer, int64_t pool_slot_stride,
+                              int64_t pool_head_stride, int dtype, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -18,8 +18,11 @@
 //     length into that many tile-aligned chunks, so short and long sequences
 //     are balanced and the grid does not depend on the lengths (graph safe);
 //   * the 4 waves of a workgroup merge in LDS; the splits of a (sequence, KV
-//     head) merge in the same launch: the last workgroup to finish (atomic
-//     ticket, self-resetting) performs the log-sum-exp combine.
+//     head) are merged by a second, small kernel (log-sum-exp combine of the
+//     fp32 partials). An in-launch "last workgroup combines" scheme needs a
+//     device-scope release/acquire per workgroup, which on gfx950 writes back
+//     and invalidates the whole L2 of the XCD and costs far more than the
+//     extra launch.
 // A generic VALU path covers fp32 and head dims other than 64/128.
 #include "ll_common.h"
 
@@ -55,12 +58,10 @@ struct DecodeArgs {
   float scale_log2;   // sm_scale * log2(e)
   float* part_acc;    // [B*H*nsplit, D] unnormalised partial outputs
   float* part_ml;     // [B*H*nsplit, 2] running max (log2 domain) and sum
-  int* tickets;       // [B*KVH], zero between launches
 };
 
 // XCD-aware unit mapping: workgroups are dispatched round-robin over the 8
-// XCDs, so all splits of one (sequence, KV head) are placed on the same XCD
-// and their partials stay in that XCD's L2 for the combine.
+// XCDs, so all splits of one (sequence, KV head) land on the same XCD.
 __device__ __forceinline__ void map_block(int bid, int nsplit, int& unit, int& split) {
   const int xcd = bid & 7;
   const int slot = bid >> 3;
@@ -77,7 +78,6 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_mfma_kernel(DecodeArg
   constexpr int kVtBytes = kWaves * kTile * kVStride * (int)sizeof(T);
   constexpr int kCombBytes = kWaves * 16 * (D + 1) * 4 + 2 * kWaves * 16 * 4;
   __shared__ __attribute__((aligned(16))) char smem[kVtBytes > kCombBytes ? kVtBytes : kCombBytes];
-  __shared__ int s_last;
   typedef float CombAcc[16][D + 1];
   CombAcc* comb_acc = (CombAcc*)smem;
   float (*comb_m)[16] = (float (*)[16])(smem + kWaves * 16 * (D + 1) * 4);
@@ -268,37 +268,28 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_mfma_kernel(DecodeArg
       }
     }
   }
-  if (direct) return;
+}
 
-  // ---- cross-split combine by the last workgroup of this unit
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const int t = atomicAdd(&a.tickets[unit], 1);
-    s_last = (t == a.nsplit - 1);
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  const int64_t p0 = ((int64_t)b * a.H + (int64_t)kvh * G) * a.nsplit;
-  for (int e = threadIdx.x; e < G * D; e += kWaves * 64) {
-    const int g = e / D, d = e - g * D;
-    const int64_t pg = p0 + (int64_t)g * a.nsplit;
-    float M = -INFINITY;
-    for (int s = 0; s < a.nsplit; ++s) M = fmaxf(M, __builtin_nontemporal_load(&a.part_ml[(pg + s) * 2]));
+// Log-sum-exp merge of the split partials: one workgroup per (sequence, head).
+template <typename T>
+__global__ __launch_bounds__(128) void decode_attn_combine_kernel(DecodeArgs a, int D) {
+  const int bh = blockIdx.x;
+  const int b = bh / a.H, h = bh - b * a.H;
+  const int64_t p0 = (int64_t)bh * a.nsplit;
+  float M = -INFINITY;
+  for (int s = 0; s < a.nsplit; ++s) M = fmaxf(M, a.part_ml[(p0 + s) * 2]);
+  T* op = (T*)a.out + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh;
+  for (int d = threadIdx.x; d < D; d += 128) {
     float L = 0.f, A = 0.f;
     if (M != -INFINITY) {
       for (int s = 0; s < a.nsplit; ++s) {
-        const float ms = __builtin_nontemporal_load(&a.part_ml[(pg + s) * 2]);
-        const float sc = exp2f(ms - M);
-        L += __builtin_nontemporal_load(&a.part_ml[(pg + s) * 2 + 1]) * sc;
-        A += __builtin_nontemporal_load(&a.part_acc[(pg + s) * D + d]) * sc;
+        const float sc = exp2f(a.part_ml[(p0 + s) * 2] - M);
+        L += a.part_ml[(p0 + s) * 2 + 1] * sc;
+        A += a.part_acc[(p0 + s) * D + d] * sc;
       }
     }
-    T* op = (T*)a.out + (int64_t)b * a.o_sb + (int64_t)(kvh * G + g) * a.o_sh;
     op[d] = ll_from_f32<T>(L > 0.f ? A / L : 0.f);
   }
-  if (threadIdx.x == 0) a.tickets[unit] = 0;
 }
 
 // ---------------------------------------------------------------- generic path
@@ -381,8 +372,7 @@ extern "C" int64_t ll_decode_attention_workspace_size(int64_t batch, int64_t q_h
                                                       int64_t max_len_in_batch) {
   const int ns = choose_nsplit((int)batch, (int)kv_heads, max_len_in_batch);
   const int64_t parts = batch * q_heads * ns;
-  int64_t bytes = ((batch * kv_heads * 4 + 255) / 256) * 256;  // tickets
-  bytes += ((parts * head_dim * 4 + 255) / 256) * 256;           // partial acc
+  int64_t bytes = ((parts * head_dim * 4 + 255) / 256) * 256;    // partial acc
   bytes += ((parts * 2 * 4 + 255) / 256) * 256;                  // partial (m, l)
   return bytes;
 }
@@ -416,7 +406,7 @@ extern "C" int ll_decode_attention(const void* q, int64_t q_stride_b, int64_t q_
   a.B = (int)batch; a.H = (int)q_heads; a.KVH = (int)kv_heads; a.G = (int)(q_heads / kv_heads);
   a.units = a.B * a.KVH;
   a.scale_log2 = sm_scale * 1.4426950408889634f;
-  a.part_acc = nullptr; a.part_ml = nullptr; a.tickets = nullptr;
+  a.part_acc = nullptr; a.part_ml = nullptr;
 
   const bool mfma_ok = (dtype == LL_BF16 || dtype == LL_F16) && (head_dim == 128 || head_dim == 64) &&
                        a.G <= 16 && (q_stride_h % 8 == 0) && (q_stride_b % 8 == 0) &&
@@ -442,8 +432,6 @@ extern "C" int ll_decode_attention(const void* q, int64_t q_stride_b, int64_t q_
                  (long long)need, (long long)workspace_bytes);
     char* w = (char*)workspace;
     const int64_t parts = batch * q_heads * a.nsplit;
-    a.tickets = (int*)w;
-    w += ((batch * kv_heads * 4 + 255) / 256) * 256;
     a.part_acc = (float*)w;
     w += ((parts * head_dim * 4 + 255) / 256) * 256;
     a.part_ml = (float*)w;
@@ -460,6 +448,13 @@ extern "C" int ll_decode_attention(const void* q, int64_t q_stride_b, int64_t q_
       hipLaunchKernelGGL((decode_attn_mfma_kernel<_Float16, 128>), dim3(grid), dim3(kWaves * 64), 0, stream, a);
     else
       hipLaunchKernelGGL((decode_attn_mfma_kernel<_Float16, 64>), dim3(grid), dim3(kWaves * 64), 0, stream, a);
+  }
+  if (a.nsplit > 1) {
+    const unsigned cgrid = (unsigned)(batch * q_heads);
+    if (dtype == LL_BF16)
+      hipLaunchKernelGGL((decode_attn_combine_kernel<__bf16>), dim3(cgrid), dim3(128), 0, stream, a, (int)head_dim);
+    else
+      hipLaunchKernelGGL((decode_attn_combine_kernel<_Float16>), dim3(cgrid), dim3(128), 0, stream, a, (int)head_dim);
   }
   LL_RETURN_LAUNCH();
 }

@@ -297,88 +297,72 @@ extern "C" int ll_embedding(const void* table, int64_t table_row_stride, int64_t
 
 // ============================================================== argmax
 // out[m] = first index of the maximum of row m (torch.argmax tie rule).
-// Two-level: each workgroup reduces a chunk of the row into (value, index)
-// partials, and the last workgroup of the row (atomic ticket) reduces those.
-template <typename T>
-__global__ __launch_bounds__(256) void argmax_kernel(const T* __restrict__ x, int64_t x_rs, int N,
-                                                     int chunk, float* __restrict__ pval,
-                                                     int* __restrict__ pidx,
-                                                     int* __restrict__ tickets,
-                                                     int64_t* __restrict__ out) {
-  const int row = blockIdx.y;
-  const int nchunk = gridDim.x;
-  const int c = blockIdx.x;
-  const T* xr = x + (int64_t)row * x_rs;
-  const int beg = c * chunk;
-  const int end = min(N, beg + chunk);
-  float best = -INFINITY;
-  int bi = 0x7fffffff;
-  for (int i = beg + threadIdx.x; i < end; i += 256) {
-    float v = ll_to_f32(xr[i]);
-    if (v > best || (v == best && i < bi)) { best = v; bi = i; }
+// Pass 1: every workgroup reduces an 8192-wide chunk of a row to a
+// (value, index) partial; pass 2 reduces the partials of each row. (Two
+// launches: an in-launch last-workgroup merge would need a device-scope
+// fence per workgroup, which flushes the XCD's whole L2 on gfx950.)
+__device__ __forceinline__ void argmax_merge(float& v, int& i, float ov, int oi) {
+  if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
+}
+
+__device__ __forceinline__ void argmax_block_reduce(float& v, int& i, float* sv, int* si) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(v, o, 64);
+    const int oi = __shfl_xor(i, o, 64);
+    argmax_merge(v, i, ov, oi);
   }
-  __shared__ float sv[256];
-  __shared__ int si[256];
-  __shared__ int last;
-  sv[threadIdx.x] = best;
-  si[threadIdx.x] = bi;
+  if ((threadIdx.x & 63) == 0) { sv[threadIdx.x >> 6] = v; si[threadIdx.x >> 6] = i; }
   __syncthreads();
-  for (int s = 128; s > 0; s >>= 1) {
-    if (threadIdx.x < s) {
-      float ov = sv[threadIdx.x + s];
-      int oi = si[threadIdx.x + s];
-      if (ov > sv[threadIdx.x] || (ov == sv[threadIdx.x] && oi < si[threadIdx.x])) {
-        sv[threadIdx.x] = ov;
-        si[threadIdx.x] = oi;
-      }
-    }
-    __syncthreads();
-  }
-  if (nchunk == 1) {
-    if (threadIdx.x == 0) out[row] = (int64_t)(si[0] == 0x7fffffff ? 0 : si[0]);
-    return;
-  }
   if (threadIdx.x == 0) {
-    pval[row * nchunk + c] = sv[0];
-    pidx[row * nchunk + c] = si[0];
-    __threadfence();
-    int t = atomicAdd(&tickets[row], 1);
-    last = (t == nchunk - 1);
-  }
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-  best = -INFINITY;
-  bi = 0x7fffffff;
-  for (int i = threadIdx.x; i < nchunk; i += 256) {
-    float v = __builtin_nontemporal_load(&pval[row * nchunk + i]);
-    int ix = __builtin_nontemporal_load(&pidx[row * nchunk + i]);
-    if (v > best || (v == best && ix < bi)) { best = v; bi = ix; }
-  }
-  sv[threadIdx.x] = best;
-  si[threadIdx.x] = bi;
-  __syncthreads();
-  for (int s = 128; s > 0; s >>= 1) {
-    if (threadIdx.x < s) {
-      float ov = sv[threadIdx.x + s];
-      int oi = si[threadIdx.x + s];
-      if (ov > sv[threadIdx.x] || (ov == sv[threadIdx.x] && oi < si[threadIdx.x])) {
-        sv[threadIdx.x] = ov;
-        si[threadIdx.x] = oi;
-      }
-    }
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) {
-    out[row] = (int64_t)(si[0] == 0x7fffffff ? 0 : si[0]);
-    tickets[row] = 0;  // self-reset for the next call
+    for (int w = 1; w < (int)(blockDim.x >> 6); ++w) argmax_merge(v, i, sv[w], si[w]);
   }
 }
 
+template <typename T>
+__global__ __launch_bounds__(256) void argmax_partial_kernel(const T* __restrict__ x, int64_t x_rs,
+                                                             int N, int chunk,
+                                                             float* __restrict__ pval,
+                                                             int* __restrict__ pidx,
+                                                             int64_t* __restrict__ out) {
+  __shared__ float sv[4];
+  __shared__ int si[4];
+  const int row = blockIdx.y, c = blockIdx.x, nchunk = gridDim.x;
+  const T* xr = x + (int64_t)row * x_rs;
+  const int beg = c * chunk, end = min(N, beg + chunk);
+  float best = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int i = beg + threadIdx.x; i < end; i += 256) argmax_merge(best, bi, ll_to_f32(xr[i]), i);
+  argmax_block_reduce(best, bi, sv, si);
+  if (threadIdx.x == 0) {
+    if (nchunk == 1) {
+      out[row] = (int64_t)(bi == 0x7fffffff ? 0 : bi);
+    } else {
+      pval[row * nchunk + c] = best;
+      pidx[row * nchunk + c] = bi;
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void argmax_final_kernel(const float* __restrict__ pval,
+                                                           const int* __restrict__ pidx,
+                                                           int nchunk, int64_t* __restrict__ out) {
+  __shared__ float sv[4];
+  __shared__ int si[4];
+  const int row = blockIdx.x;
+  float best = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int i = threadIdx.x; i < nchunk; i += 256)
+    argmax_merge(best, bi, pval[row * nchunk + i], pidx[row * nchunk + i]);
+  argmax_block_reduce(best, bi, sv, si);
+  if (threadIdx.x == 0) out[row] = (int64_t)(bi == 0x7fffffff ? 0 : bi);
+}
+
+static const int kArgmaxChunk = 8192;
+
 extern "C" int64_t ll_argmax_workspace_size(int64_t M, int64_t N) {
-  const int64_t chunk = 8192;
-  const int64_t nchunk = (N + chunk - 1) / chunk;
-  return M * nchunk * 8 + M * 4 + 256;
+  const int64_t nchunk = (N + kArgmaxChunk - 1) / kArgmaxChunk;
+  return nchunk > 1 ? M * nchunk * 8 : 0;
 }
 
 extern "C" int ll_argmax(const void* x, int64_t x_row_stride, int64_t M, int64_t N, int64_t* out,
@@ -386,23 +370,22 @@ extern "C" int ll_argmax(const void* x, int64_t x_row_stride, int64_t M, int64_t
   LL_CHECK_ARG(x && out, "ll_argmax: null pointer");
   LL_CHECK_ARG(N > 0, "ll_argmax: empty rows");
   if (M == 0) return LL_OK;
-  const int chunk = 8192;
-  const int nchunk = ll_cdiv(N, chunk);
+  const int nchunk = ll_cdiv(N, kArgmaxChunk);
   float* pval = nullptr;
   int* pidx = nullptr;
-  int* tickets = nullptr;
   if (nchunk > 1) {
     LL_CHECK_ARG(workspace != nullptr && workspace_bytes >= ll_argmax_workspace_size(M, N),
                  "ll_argmax: workspace too small (need %lld bytes)",
                  (long long)ll_argmax_workspace_size(M, N));
-    char* w = (char*)workspace;
-    tickets = (int*)w;  // must be zero on first use; the kernel keeps it zero
-    pval = (float*)(w + ((M * 4 + 255) / 256) * 256);
+    pval = (float*)workspace;
     pidx = (int*)(pval + M * nchunk);
   }
   return LL_DISPATCH_DTYPE(dtype, T, [&]() -> int {
-    hipLaunchKernelGGL((argmax_kernel<T>), dim3(nchunk, (unsigned)M), dim3(256), 0, stream,
-                       (const T*)x, x_row_stride, (int)N, chunk, pval, pidx, tickets, out);
+    hipLaunchKernelGGL((argmax_partial_kernel<T>), dim3(nchunk, (unsigned)M), dim3(256), 0, stream,
+                       (const T*)x, x_row_stride, (int)N, kArgmaxChunk, pval, pidx, out);
+    if (nchunk > 1)
+      hipLaunchKernelGGL(argmax_final_kernel, dim3((unsigned)M), dim3(256), 0, stream, pval, pidx,
+                         nchunk, out);
     LL_RETURN_LAUNCH();
   });
 }
@@ -427,4 +410,225 @@ extern "C" int ll_assign_slots(int32_t* req_to_tokens, int64_t req_to_tokens_str
   hipLaunchKernelGGL(assign_slots_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
                      req_to_tokens, req_to_tokens_stride, slots, rows, cols, n);
   LL_RETURN_LAUNCH();
+}
+
+// ============================================================== split-K consumers
+// The decode-step projections leave fp32 partial sums part[s][m][n]
+// (ll_gemm_splitk). The kernels below finish those sums in a fixed split
+// order, store the projection output in the model dtype exactly as the
+// unfused GEMM epilogue would (T(sum [+ bias])), and fuse the next op.
+
+__device__ __forceinline__ float ll_sum_splits(const float* __restrict__ part, int splits,
+                                               int64_t split_stride, int64_t idx) {
+  float s = 0.f;
+  for (int sp = 0; sp < splits; ++sp) s += part[sp * split_stride + idx];
+  return s;
+}
+
+// Sum of 4 consecutive partial columns over all splits, loads batched 4 at a
+// time (the additions still run in split order 0, 1, 2, ...).
+__device__ __forceinline__ f32x4 ll_sum_splits4(const float* __restrict__ part, int splits,
+                                                int64_t split_stride, int64_t idx) {
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  int sp = 0;
+  for (; sp + 4 <= splits; sp += 4) {
+    const f32x4 a = *(const f32x4*)(part + (sp + 0) * split_stride + idx);
+    const f32x4 b = *(const f32x4*)(part + (sp + 1) * split_stride + idx);
+    const f32x4 c = *(const f32x4*)(part + (sp + 2) * split_stride + idx);
+    const f32x4 d = *(const f32x4*)(part + (sp + 3) * split_stride + idx);
+    acc += a;
+    acc += b;
+    acc += c;
+    acc += d;
+  }
+  for (; sp < splits; ++sp) acc += *(const f32x4*)(part + sp * split_stride + idx);
+  return acc;
+}
+
+// h[m] = T(h[m] + T(sum_s part[s][m])); out[m] = rmsnorm(h[m]) * gamma.
+// One workgroup per row, 4 consecutive columns per thread (N % 4 == 0).
+template <typename T, int BLOCK>
+__global__ __launch_bounds__(BLOCK) void add_rmsnorm_splitk_kernel(
+    T* __restrict__ h, int64_t h_rs, const float* __restrict__ part, int splits,
+    const T* __restrict__ gamma, T* __restrict__ out, int64_t o_rs, int M, int N, float eps) {
+  const int row = blockIdx.x;
+  T* hr = h + (int64_t)row * h_rs;
+  const int64_t sstride = (int64_t)M * N;
+  constexpr int PER = 4;  // columns per thread per pass
+  constexpr int MAXP = 4; // passes kept in registers (N <= 4 * BLOCK * MAXP)
+  float hv[MAXP][PER];
+  float ss = 0.f;
+#pragma unroll
+  for (int ps = 0; ps < MAXP; ++ps) {
+    const int c = (ps * BLOCK + threadIdx.x) * PER;
+    if (c < N) {
+      const f32x4 o = ll_sum_splits4(part, splits, sstride, (int64_t)row * N + c);
+#pragma unroll
+      for (int e = 0; e < PER; ++e) {
+        const T nh = ll_from_f32<T>(ll_to_f32(hr[c + e]) + ll_to_f32(ll_from_f32<T>(o[e])));
+        hr[c + e] = nh;
+        hv[ps][e] = ll_to_f32(nh);
+        ss += hv[ps][e] * hv[ps][e];
+      }
+    }
+  }
+  __shared__ float red[BLOCK / 64];
+  ss = ll_wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int w = 0; w < BLOCK / 64; ++w) tot += red[w];
+  const float denom = sqrtf(tot / (float)N + eps);
+  T* orow = out + (int64_t)row * o_rs;
+#pragma unroll
+  for (int ps = 0; ps < MAXP; ++ps) {
+    const int c = (ps * BLOCK + threadIdx.x) * PER;
+    if (c < N) {
+#pragma unroll
+      for (int e = 0; e < PER; ++e)
+        orow[c + e] = ll_from_f32<T>(hv[ps][e] / denom * ll_to_f32(gamma[c + e]));
+    }
+  }
+}
+
+extern "C" int ll_add_rmsnorm_splitk(void* h, int64_t h_row_stride, const float* part, int splits,
+                                     const void* gamma, void* out, int64_t out_row_stride,
+                                     int64_t M, int64_t N, float eps, int dtype,
+                                     hipStream_t stream) {
+  LL_CHECK_ARG(h && part && gamma && out, "ll_add_rmsnorm_splitk: null pointer");
+  LL_CHECK_ARG(splits >= 1 && N > 0 && N % 4 == 0 && N <= 4 * 512 * 4,
+               "ll_add_rmsnorm_splitk: N must be a multiple of 4 and <= 8192 (N=%lld)",
+               (long long)N);
+  LL_CHECK_ARG(((uintptr_t)part) % 16 == 0, "ll_add_rmsnorm_splitk: partials must be 16 B aligned");
+  if (M == 0) return LL_OK;
+  return LL_DISPATCH_DTYPE(dtype, T, [&]() -> int {
+    hipLaunchKernelGGL((add_rmsnorm_splitk_kernel<T, 512>), dim3((unsigned)M), dim3(512), 0, stream,
+                       (T*)h, h_row_stride, part, splits, (const T*)gamma, (T*)out, out_row_stride,
+                       (int)M, (int)N, eps);
+    LL_RETURN_LAUNCH();
+  });
+}
+
+// out[m][n] = T(u * T(silu(g))), g = T(sum part[.][m][n]), u = T(sum part[.][m][N + n]);
+// 4 consecutive columns per thread (N % 4 == 0).
+template <typename T>
+__global__ void silu_and_mul_splitk_kernel(const float* __restrict__ part, int splits,
+                                           T* __restrict__ out, int64_t o_rs, int M, int N) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int q = N / 4;
+  const int m = (int)(gid / q);
+  if (m >= M) return;
+  const int n = (int)(gid - (int64_t)m * q) * 4;
+  const int64_t sstride = (int64_t)M * 2 * N;
+  const int64_t base = (int64_t)m * 2 * N;
+  const f32x4 g4 = ll_sum_splits4(part, splits, sstride, base + n);
+  const f32x4 u4 = ll_sum_splits4(part, splits, sstride, base + N + n);
+  T* op = out + (int64_t)m * o_rs + n;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float g = ll_to_f32(ll_from_f32<T>(g4[e]));
+    const float u = ll_to_f32(ll_from_f32<T>(u4[e]));
+    const T sv = ll_from_f32<T>(g / (1.0f + __expf(-g)));
+    op[e] = ll_from_f32<T>(u * ll_to_f32(sv));
+  }
+}
+
+extern "C" int ll_silu_and_mul_splitk(const float* part, int splits, void* out,
+                                      int64_t out_row_stride, int64_t M, int64_t N, int dtype,
+                                      hipStream_t stream) {
+  LL_CHECK_ARG(part && out, "ll_silu_and_mul_splitk: null pointer");
+  LL_CHECK_ARG(N % 4 == 0 && ((uintptr_t)part) % 16 == 0,
+               "ll_silu_and_mul_splitk: N must be a multiple of 4, partials 16 B aligned");
+  if (M == 0 || N == 0) return LL_OK;
+  const int64_t total = M * N / 4;
+  return LL_DISPATCH_DTYPE(dtype, T, [&]() -> int {
+    hipLaunchKernelGGL((silu_and_mul_splitk_kernel<T>), dim3((unsigned)((total + 255) / 256)),
+                       dim3(256), 0, stream, part, splits, (T*)out, out_row_stride, (int)M, (int)N);
+    LL_RETURN_LAUNCH();
+  });
+}
+
+// qkv = T(sum part + bias); q heads rotated -> q_out [T, H*D]; k rotated and
+// v copied into pool_layer[slots[t]] (K heads then V heads). Each thread
+// handles 4 consecutive rotation pairs (i..i+3, i+half..i+half+3); D % 8 == 0.
+template <typename T, typename C>
+__global__ void rope_kv_scatter_splitk_kernel(const float* __restrict__ part, int splits,
+                                              const T* __restrict__ bias, T* __restrict__ q_out,
+                                              int64_t q_rs, int H, int KVH, int D,
+                                              const void* __restrict__ pos, int pos64,
+                                              const C* __restrict__ cos_tab,
+                                              const C* __restrict__ sin_tab, int64_t tab_stride,
+                                              const int32_t* __restrict__ slots,
+                                              T* __restrict__ pool, int64_t pool_slot_stride,
+                                              int64_t pool_head_stride, int ntok) {
+  const int half = D / 2;
+  const int qd = half / 4;
+  const int width = (H + 2 * KVH) * D;
+  const int64_t per_tok = (int64_t)(H + 2 * KVH) * qd;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int t = (int)(gid / per_tok);
+  if (t >= ntok) return;
+  const int rem = (int)(gid - (int64_t)t * per_tok);
+  const int h = rem / qd;
+  const int i = (rem - h * qd) * 4;
+  const int64_t sstride = (int64_t)ntok * width;
+  const int c0 = h * D + i, c1 = c0 + half;
+  f32x4 x0 = ll_sum_splits4(part, splits, sstride, (int64_t)t * width + c0);
+  f32x4 x1 = ll_sum_splits4(part, splits, sstride, (int64_t)t * width + c1);
+  if (bias != nullptr) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x0[e] += ll_to_f32(bias[c0 + e]);
+      x1[e] += ll_to_f32(bias[c1 + e]);
+    }
+  }
+  T* dst;
+  if (h < H) dst = q_out + (int64_t)t * q_rs + (int64_t)h * D;
+  else dst = pool + (int64_t)slots[t] * pool_slot_stride + (int64_t)(h - H) * pool_head_stride;
+  if (h < H + KVH) {
+    const int64_t p = ll_load_idx(pos, t, pos64);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float c = ll_to_f32(cos_tab[p * tab_stride + i + e]);
+      const float s = ll_to_f32(sin_tab[p * tab_stride + i + e]);
+      const float a = ll_to_f32(ll_from_f32<T>(x0[e])), b = ll_to_f32(ll_from_f32<T>(x1[e]));
+      dst[i + e] = ll_from_f32<T>(a * c - b * s);
+      dst[i + half + e] = ll_from_f32<T>(a * s + b * c);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      dst[i + e] = ll_from_f32<T>(x0[e]);
+      dst[i + half + e] = ll_from_f32<T>(x1[e]);
+    }
+  }
+}
+
+extern "C" int ll_rope_kv_scatter_splitk(const float* part, int splits, const void* bias,
+                                         void* q_out, int64_t q_row_stride, int64_t ntok,
+                                         int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                                         const void* positions, int positions_i64,
+                                         const void* cos_table, const void* sin_table,
+                                         int64_t table_row_stride, int cs_dtype,
+                                         const int32_t* slots, void* pool_layer,
+                                         int64_t pool_slot_stride, int64_t pool_head_stride,
+                                         int dtype, hipStream_t stream) {
+  LL_CHECK_ARG(part && q_out && positions && cos_table && sin_table && slots && pool_layer,
+               "ll_rope_kv_scatter_splitk: null pointer");
+  LL_CHECK_ARG(head_dim % 8 == 0 && ((uintptr_t)part) % 16 == 0,
+               "ll_rope_kv_scatter_splitk: head_dim must be a multiple of 8, partials 16 B aligned");
+  if (ntok == 0) return LL_OK;
+  const int64_t total = ntok * (q_heads + 2 * kv_heads) * (head_dim / 8);
+  const unsigned grid = (unsigned)((total + 255) / 256);
+  return LL_DISPATCH_DTYPE(dtype, T, [&]() -> int {
+    return LL_DISPATCH_DTYPE(cs_dtype, C, [&]() -> int {
+      hipLaunchKernelGGL((rope_kv_scatter_splitk_kernel<T, C>), dim3(grid), dim3(256), 0, stream,
+                         part, splits, (const T*)bias, (T*)q_out, q_row_stride, (int)q_heads,
+                         (int)kv_heads, (int)head_dim, positions, positions_i64,
+                         (const C*)cos_table, (const C*)sin_table, table_row_stride, slots,
+                         (T*)pool_layer, pool_slot_stride, pool_head_stride, (int)ntok);
+      LL_RETURN_LAUNCH();
+    });
+  });
 }

@@ -5,13 +5,13 @@
 // post_layer.py:50-52). W keeps the nn.Linear [out, in] layout so that both
 // MFMA operands are 16-byte k-contiguous loads.
 //
-// Three kernels:
-//   * skinny (M <= 64, the decode step): weight-streaming. A workgroup owns
-//     16*WR output channels and a K range; its 4 waves interleave over the
-//     32-wide k-steps with 4 steps in flight, multiply on MFMA
-//     (v_mfma_f32_16x16x32) with the tokens as the 16-wide N side, and merge
-//     in LDS. Narrow N is split over K across workgroups (fp32 partials,
-//     reduced by a second kernel that also adds the bias);
+// Kernels:
+//   * M <= 64 (the decode step) is weight streaming: two kernels (LDS-staged
+//     for wide/deep weights, direct for the small projections, below), MFMA
+//     v_mfma_f32_16x16x32 with the tokens as the 16-wide N side. Narrow N is
+//     split over K across workgroups into fp32 partials, which either a
+//     reduce kernel (ll_gemm) or the consumer kernel of the model
+//     (ll_gemm_splitk + the *_splitk entry points) sums in a fixed order;
 //   * tiled (M > 64, prefill): 128x128x64 LDS tiles, 2x2 waves of 64x64,
 //     register-staged prefetch of the next k tile;
 //   * fp32: plain FMA tiles for the fp32 parity path.
@@ -38,73 +38,198 @@ template <typename V8> __device__ __forceinline__ V8 zero8() {
 }
 
 // ---------------------------------------------------------------- skinny
-constexpr int kSkWaves = 4;
-constexpr int kSkUnroll = 4;
+// Output of the M <= 64 kernels: if `part` is non-null, fp32 partial sums
+// part[split][m][n] (N contiguous, no bias); else Y[m][n] = T(sum + bias[n]).
 
-// grid.x = ceil(N / (16*WR)), grid.y = splits. Each split covers
-// `ksteps_per_split` 32-wide k-steps.
-template <typename T, int MB, int WR>
-__global__ __launch_bounds__(kSkWaves * 64) void gemm_skinny_kernel(
-    const T* __restrict__ X, int64_t ldx, const T* __restrict__ W, int64_t ldw,
-    const T* __restrict__ bias, T* __restrict__ Y, int64_t ldy, float* __restrict__ part,
-    int M, int N, int K, int ksteps_per_split) {
+template <int N_> __device__ __forceinline__ void vm_wait();
+#define LL_VMWAIT(n) \
+  template <> __device__ __forceinline__ void vm_wait<n>() { asm volatile("s_waitcnt vmcnt(" #n ")" ::: "memory"); }
+LL_VMWAIT(0) LL_VMWAIT(5) LL_VMWAIT(6) LL_VMWAIT(7) LL_VMWAIT(8)
+#undef LL_VMWAIT
+
+// 16 B global -> LDS DMA of one lane (lane i of the wave lands at lds + 16 i).
+// Kept out of the kernel templates: a dependent call of this device-only
+// builtin makes the host pass drop the template's launch stub.
+__device__ __forceinline__ void dma16(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0);
+}
+
+// (1) Wide N: weight rows streamed through LDS. A workgroup (4 waves) owns 64
+// rows; every stage DMA's (global_load_lds_dwordx4, no VGPR staging) a
+// 64-row x 128-k weight tile and the matching 16*MB-row activation tile into
+// LDS, with 256 contiguous bytes per row per wave instruction. The 16 B chunk
+// index of every row is XOR-swizzled by (row & 15) so the MFMA operand reads
+// (16 rows x 16 B per 16 lanes) are bank-conflict free. Two stages in flight.
+constexpr int kDmaKC = 128, kDmaNST = 2, kDmaTR = 64;
+
+template <typename T, int MB>
+__global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, int64_t ldx,
+                                                       const T* __restrict__ W, int64_t ldw,
+                                                       const T* __restrict__ bias,
+                                                       T* __restrict__ Y, int64_t ldy,
+                                                       float* __restrict__ part, int M, int N,
+                                                       int K, int ksps) {
   typedef typename Vec8<T>::type V8;
-  const int wave = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
+  constexpr int TR = kDmaTR, XR = 16 * MB, KC = kDmaKC, NST = kDmaNST;
+  constexpr int ROWB = KC * 2, CH = ROWB / 16, RPI = 64 / CH;  // 16 chunks, 4 rows/instr
+  constexpr int W_PER_WAVE = (TR / RPI) / 4;
+  constexpr int X_PER_WAVE = (XR / RPI) / 4;
+  constexpr int C = W_PER_WAVE + X_PER_WAVE;
+  constexpr int STAGE_B = (TR + XR) * ROWB;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int n = lane & 15, j = lane >> 4;
+  const int row0 = blockIdx.x * TR;
+  const int split = blockIdx.y;
+  const int k_beg = split * ksps * 32;
+  const int k_end = min(K, k_beg + ksps * 32);
+  const int nst = (k_end - k_beg) / KC;
+  const int lr_in = lane / CH, p = lane % CH;
+  auto issue = [&](int st) {
+    char* base = smem + (st % NST) * STAGE_B;
+    const int k0 = k_beg + st * KC;
+#pragma unroll
+    for (int q = 0; q < W_PER_WAVE; ++q) {
+      const int ii = wave * W_PER_WAVE + q;
+      const int r = ii * RPI + lr_in;
+      const T* g = W + (int64_t)min(row0 + r, N - 1) * ldw + k0 + (p ^ (r & 15)) * 8;
+      dma16(g, base + ii * 1024);
+    }
+#pragma unroll
+    for (int q = 0; q < X_PER_WAVE; ++q) {
+      const int ii = wave + q * 4;
+      const int r = ii * RPI + lr_in;
+      const T* g = X + (int64_t)min(r, M - 1) * ldx + k0 + (p ^ (r & 15)) * 8;
+      dma16(g, base + TR * ROWB + ii * 1024);
+    }
+  };
+  f32x4 acc[MB];
+#pragma unroll
+  for (int t = 0; t < MB; ++t) acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  if (nst > 0) issue(0);
+  const int lr = wave * 16 + n;
+  for (int st = 0; st < nst; ++st) {
+    if (st + 1 < nst) {
+      issue(st + 1);
+      vm_wait<C>();
+    } else {
+      vm_wait<0>();
+    }
+    __syncthreads();
+    const char* wb = smem + (st % NST) * STAGE_B;
+    const char* xb = wb + TR * ROWB;
+#pragma unroll
+    for (int s = 0; s < KC / 32; ++s) {
+      const V8 a = *(const V8*)(wb + lr * ROWB + (((4 * s + j) ^ (lr & 15)) * 16));
+#pragma unroll
+      for (int t = 0; t < MB; ++t) {
+        const int xr = 16 * t + n;
+        const V8 b = *(const V8*)(xb + xr * ROWB + (((4 * s + j) ^ (xr & 15)) * 16));
+        acc[t] = mfma16x16x32(a, b, acc[t]);
+      }
+    }
+    __syncthreads();
+  }
+  // acc[t][i] = Y[token 16t + n][channel row0 + 16*wave + 4j + i]
+  const int ch = row0 + wave * 16 + 4 * j;
+#pragma unroll
+  for (int t = 0; t < MB; ++t) {
+    const int tok = 16 * t + n;
+    if (tok >= M || ch >= N) continue;
+    if (part != nullptr) {
+      float* pp = part + ((int64_t)split * M + tok) * N + ch;
+      if (ch + 3 < N && (N & 3) == 0) {
+        *(f32x4*)pp = acc[t];
+      } else {
+        for (int i = 0; i < 4 && ch + i < N; ++i) pp[i] = acc[t][i];
+      }
+    } else {
+      T* yp = Y + (int64_t)tok * ldy + ch;
+      for (int i = 0; i < 4 && ch + i < N; ++i)
+        yp[i] = ll_from_f32<T>(acc[t][i] + (bias != nullptr ? ll_to_f32(bias[ch + i]) : 0.f));
+    }
+  }
+}
+
+// (2) Narrow N: direct operand loads. A workgroup owns 16*WR rows; its KW
+// waves interleave over the 32-wide k-steps with U steps per group, loads of
+// group g+1 in flight while group g is multiplied (register double buffer).
+// Row and token indices are clamped into the tensors (their results are
+// discarded), so the steady loop has no divergent branches; a masked tail
+// handles K % 32 != 0.
+template <typename T, int MB, int WR, int KW, int U>
+__global__ __launch_bounds__(64 * KW) void gemm_direct_kernel(
+    const T* __restrict__ X, int64_t ldx, const T* __restrict__ W, int64_t ldw,
+    const T* __restrict__ bias, T* __restrict__ Y, int64_t ldy, float* __restrict__ part, int M,
+    int N, int K, int ksps) {
+  typedef typename Vec8<T>::type V8;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int n = lane & 15, j = lane >> 4;
   const int row0 = blockIdx.x * (16 * WR);
   const int split = blockIdx.y;
   const int ksteps = (K + 31) / 32;
-  const int kb = split * ksteps_per_split;
-  const int ke = min(ksteps, kb + ksteps_per_split);
-
+  const int full = K / 32;  // k-steps with all 32 columns inside K
+  const int kb = split * ksps, ke = min(ksteps, kb + ksps);
   const T* wrow[WR];
-  bool wok[WR];
 #pragma unroll
-  for (int r = 0; r < WR; ++r) {
-    const int row = row0 + 16 * r + n;
-    wok[r] = row < N;
-    wrow[r] = W + (int64_t)(wok[r] ? row : 0) * ldw + 8 * j;
-  }
+  for (int r = 0; r < WR; ++r) wrow[r] = W + (int64_t)min(row0 + 16 * r + n, N - 1) * ldw + 8 * j;
   const T* xrow[MB];
-  bool xok[MB];
 #pragma unroll
-  for (int t = 0; t < MB; ++t) {
-    const int tok = 16 * t + n;
-    xok[t] = tok < M;
-    xrow[t] = X + (int64_t)(xok[t] ? tok : 0) * ldx + 8 * j;
-  }
-
+  for (int t = 0; t < MB; ++t) xrow[t] = X + (int64_t)min(16 * t + n, M - 1) * ldx + 8 * j;
   f32x4 acc[WR][MB];
 #pragma unroll
   for (int r = 0; r < WR; ++r)
 #pragma unroll
     for (int t = 0; t < MB; ++t) acc[r][t] = (f32x4){0.f, 0.f, 0.f, 0.f};
-
-  for (int ks0 = kb + wave; ks0 < ke; ks0 += kSkWaves * kSkUnroll) {
-    V8 wv[kSkUnroll][WR], xv[kSkUnroll][MB];
+  // this wave's k-steps: kb + wave + KW*i, i < per_wave; the first `safe` are full
+  const int per_wave = max(0, (ke - kb - wave + KW - 1) / KW);
+  const int safe = max(0, min(per_wave, (min(ke, full) - kb - wave + KW - 1) / KW));
+  const int groups = safe / U;
+  V8 wv[2][U][WR], xv[2][U][MB];
+  auto load = [&](int buf, int g) {
 #pragma unroll
-    for (int u = 0; u < kSkUnroll; ++u) {
-      const int ks = ks0 + u * kSkWaves;
-      const int k = ks * 32 + 8 * j;
-      const bool kok = (ks < ke) && (k < K);
+    for (int u = 0; u < U; ++u) {
+      const int ks = kb + wave + KW * (g * U + u);
 #pragma unroll
-      for (int r = 0; r < WR; ++r)
-        wv[u][r] = (kok && wok[r]) ? *(const V8*)(wrow[r] + ks * 32) : zero8<V8>();
+      for (int r = 0; r < WR; ++r) wv[buf][u][r] = *(const V8*)(wrow[r] + ks * 32);
 #pragma unroll
-      for (int t = 0; t < MB; ++t)
-        xv[u][t] = (kok && xok[t]) ? *(const V8*)(xrow[t] + ks * 32) : zero8<V8>();
+      for (int t = 0; t < MB; ++t) xv[buf][u][t] = *(const V8*)(xrow[t] + ks * 32);
     }
+  };
+  auto compute = [&](int buf) {
 #pragma unroll
-    for (int u = 0; u < kSkUnroll; ++u)
+    for (int u = 0; u < U; ++u)
 #pragma unroll
       for (int r = 0; r < WR; ++r)
 #pragma unroll
-        for (int t = 0; t < MB; ++t) acc[r][t] = mfma16x16x32(wv[u][r], xv[u][t], acc[r][t]);
+        for (int t = 0; t < MB; ++t) acc[r][t] = mfma16x16x32(wv[buf][u][r], xv[buf][u][t], acc[r][t]);
+  };
+  if (groups > 0) {
+    load(0, 0);
+    int g = 0;
+    for (; g + 1 < groups; g += 2) {
+      load(1, g + 1);
+      compute(0);
+      if (g + 2 < groups) load(0, g + 2);
+      compute(1);
+    }
+    if (g < groups) compute(0);
   }
-
-  // acc[r][t][i] = Y[token 16t + n][channel row0 + 16r + 4j + i]
-  __shared__ float red[kSkWaves][WR * 16][MB * 16 + 1];
+  for (int i = groups * U; i < per_wave; ++i) {
+    const int ks = kb + wave + KW * i;
+    const bool kok = ks * 32 + 8 * j < K;
+    V8 w1[WR], x1[MB];
+#pragma unroll
+    for (int r = 0; r < WR; ++r) w1[r] = kok ? *(const V8*)(wrow[r] + ks * 32) : zero8<V8>();
+#pragma unroll
+    for (int t = 0; t < MB; ++t) x1[t] = kok ? *(const V8*)(xrow[t] + ks * 32) : zero8<V8>();
+#pragma unroll
+    for (int r = 0; r < WR; ++r)
+#pragma unroll
+      for (int t = 0; t < MB; ++t) acc[r][t] = mfma16x16x32(w1[r], x1[t], acc[r][t]);
+  }
+  // acc[r][t][i] = Y[token 16t + n][channel row0 + 16r + 4j + i]; merge the KW waves
+  __shared__ float red[KW][WR * 16][MB * 16 + 1];
 #pragma unroll
   for (int r = 0; r < WR; ++r)
 #pragma unroll
@@ -112,14 +237,14 @@ __global__ __launch_bounds__(kSkWaves * 64) void gemm_skinny_kernel(
 #pragma unroll
       for (int i = 0; i < 4; ++i) red[wave][16 * r + 4 * j + i][16 * t + n] = acc[r][t][i];
   __syncthreads();
-  for (int e = threadIdx.x; e < WR * 16 * MB * 16; e += kSkWaves * 64) {
+  for (int e = threadIdx.x; e < WR * 16 * MB * 16; e += KW * 64) {
     const int tok = e / (WR * 16);
     const int cr = e - tok * (WR * 16);
     const int ch = row0 + cr;
     if (tok >= M || ch >= N) continue;
     float s = 0.f;
 #pragma unroll
-    for (int w = 0; w < kSkWaves; ++w) s += red[w][cr][tok];
+    for (int w = 0; w < KW; ++w) s += red[w][cr][tok];
     if (part != nullptr) {
       part[((int64_t)split * M + tok) * N + ch] = s;
     } else {
@@ -281,38 +406,67 @@ __global__ __launch_bounds__(256) void gemm_fp32_kernel(const T* __restrict__ X,
     }
 }
 
+// Kernel choice and split count for M <= 64, from sweeps on MI355X at the
+// Qwen2 decode shapes (M = 40): the LDS kernel wins when the weight matrix is
+// wide or deep, the direct kernel on the small 2k x 2k projections.
 struct SkinnyPlan {
-  int wr;       // 16-row blocks per wave
-  int splits;   // K splits across workgroups
-  int ksps;     // k-steps per split
+  bool dma;
+  int splits;  // K splits across workgroups (all non-empty)
+  int ksps;    // 32-wide k-steps per split
+  int tiles;   // row tiles
 };
+
+constexpr int kDirWR = 2, kDirKW = 4, kDirU = 2;
 
 SkinnyPlan plan_skinny(int64_t N, int64_t K) {
   SkinnyPlan p;
   const int ksteps = (int)((K + 31) / 32);
-  p.wr = (N >= 16 * 2 * 512) ? 2 : 1;  // wide N: 32 channels per workgroup
-  const int64_t tiles = (N + 16 * p.wr - 1) / (16 * p.wr);
-  // aim for >= 512 workgroups; each split keeps >= 4 k-steps per wave
-  int splits = 1;
-  while (tiles * splits < 512 && (ksteps / (splits * 2)) >= kSkWaves * 4) splits *= 2;
-  p.splits = splits;
-  p.ksps = (ksteps + splits - 1) / splits;
-  p.splits = (ksteps + p.ksps - 1) / p.ksps;
+  p.dma = (K % kDmaKC == 0) && (N >= 4096 || K >= 8192);
+  if (p.dma) {
+    const int chunks = (int)(K / kDmaKC);
+    p.tiles = (int)((N + kDmaTR - 1) / kDmaTR);
+    int sp = 1;
+    while ((int64_t)p.tiles * sp < 640 && chunks / (sp * 2) >= 2) sp *= 2;
+    const int per = (chunks + sp - 1) / sp;
+    p.splits = (chunks + per - 1) / per;
+    p.ksps = per * (kDmaKC / 32);
+  } else {
+    p.tiles = (int)((N + 16 * kDirWR - 1) / (16 * kDirWR));
+    int sp = 1;
+    while ((int64_t)p.tiles * sp < 512 && ksteps / (sp * 2) >= kDirKW * 2) sp *= 2;
+    const int per = (ksteps + sp - 1) / sp;
+    p.splits = (ksteps + per - 1) / per;
+    p.ksps = per;
+  }
   return p;
 }
 
 template <typename T, int MB>
-int launch_skinny_mb(const SkinnyPlan& p, const T* X, int64_t ldx, const T* W, int64_t ldw,
-                     const T* bias, T* Y, int64_t ldy, float* part, int M, int N, int K,
-                     hipStream_t stream) {
-  const dim3 grid((unsigned)ll_cdiv(N, 16 * p.wr), (unsigned)p.splits);
-  if (p.wr == 2)
-    hipLaunchKernelGGL((gemm_skinny_kernel<T, MB, 2>), grid, dim3(kSkWaves * 64), 0, stream, X,
-                       ldx, W, ldw, bias, Y, ldy, part, M, N, K, p.ksps);
-  else
-    hipLaunchKernelGGL((gemm_skinny_kernel<T, MB, 1>), grid, dim3(kSkWaves * 64), 0, stream, X,
-                       ldx, W, ldw, bias, Y, ldy, part, M, N, K, p.ksps);
-  return 0;
+void launch_skinny_mb(const SkinnyPlan& p, const T* X, int64_t ldx, const T* W, int64_t ldw,
+                      const T* bias, T* Y, int64_t ldy, float* part, int M, int N, int K,
+                      hipStream_t stream) {
+  const dim3 grid((unsigned)p.tiles, (unsigned)p.splits);
+  if (p.dma) {
+    const size_t lds = (size_t)kDmaNST * (kDmaTR + 16 * MB) * kDmaKC * 2;
+    hipLaunchKernelGGL((gemm_dma_kernel<T, MB>), grid, dim3(256), lds, stream, X, ldx, W, ldw,
+                       bias, Y, ldy, part, M, N, K, p.ksps);
+  } else {
+    hipLaunchKernelGGL((gemm_direct_kernel<T, MB, kDirWR, kDirKW, kDirU>), grid,
+                       dim3(64 * kDirKW), 0, stream, X, ldx, W, ldw, bias, Y, ldy, part, M, N, K,
+                       p.ksps);
+  }
+}
+
+template <typename T>
+void launch_skinny(const SkinnyPlan& p, const T* X, int64_t ldx, const T* W, int64_t ldw,
+                   const T* bias, T* Y, int64_t ldy, float* part, int M, int N, int K,
+                   hipStream_t stream) {
+  switch ((M + 15) / 16) {
+    case 1: launch_skinny_mb<T, 1>(p, X, ldx, W, ldw, bias, Y, ldy, part, M, N, K, stream); break;
+    case 2: launch_skinny_mb<T, 2>(p, X, ldx, W, ldw, bias, Y, ldy, part, M, N, K, stream); break;
+    case 3: launch_skinny_mb<T, 3>(p, X, ldx, W, ldw, bias, Y, ldy, part, M, N, K, stream); break;
+    default: launch_skinny_mb<T, 4>(p, X, ldx, W, ldw, bias, Y, ldy, part, M, N, K, stream); break;
+  }
 }
 
 template <typename T>
@@ -327,13 +481,7 @@ int launch_gemm(const T* X, int64_t ldx, const T* W, int64_t ldw, const T* bias,
                    "ll_gemm: workspace too small (need %lld bytes)", (long long)need);
       part = (float*)ws;
     }
-    const int mb = (int)((M + 15) / 16);
-    switch (mb) {
-      case 1: launch_skinny_mb<T, 1>(p, X, ldx, W, ldw, bias, Y, ldy, part, (int)M, (int)N, (int)K, stream); break;
-      case 2: launch_skinny_mb<T, 2>(p, X, ldx, W, ldw, bias, Y, ldy, part, (int)M, (int)N, (int)K, stream); break;
-      case 3: launch_skinny_mb<T, 3>(p, X, ldx, W, ldw, bias, Y, ldy, part, (int)M, (int)N, (int)K, stream); break;
-      default: launch_skinny_mb<T, 4>(p, X, ldx, W, ldw, bias, Y, ldy, part, (int)M, (int)N, (int)K, stream); break;
-    }
+    launch_skinny<T>(p, X, ldx, W, ldw, bias, Y, ldy, part, (int)M, (int)N, (int)K, stream);
     if (p.splits > 1) {
       const int64_t total = M * N;
       hipLaunchKernelGGL((splitk_reduce_kernel<T>), dim3((unsigned)((total + 255) / 256)), dim3(256),
@@ -353,6 +501,34 @@ extern "C" int64_t ll_gemm_workspace_size(int64_t M, int64_t N, int64_t K) {
   if (M > 64) return 0;
   const SkinnyPlan p = plan_skinny(N, K);
   return p.splits > 1 ? (int64_t)p.splits * M * N * 4 : 0;
+}
+
+extern "C" int ll_gemm_splitk_count(int64_t M, int64_t N, int64_t K) {
+  if (M > 64 || M <= 0) return 0;
+  return plan_skinny(N, K).splits;
+}
+
+extern "C" int ll_gemm_splitk(const void* X, int64_t ldx, const void* W, int64_t ldw, int64_t M,
+                              int64_t N, int64_t K, int dtype, float* part, int64_t part_bytes,
+                              hipStream_t stream) {
+  LL_CHECK_ARG(X && W && part, "ll_gemm_splitk: null pointer");
+  LL_CHECK_ARG(M > 0 && M <= 64 && N > 0 && K > 0, "ll_gemm_splitk: needs 0 < M <= 64 (M=%lld)",
+               (long long)M);
+  LL_CHECK_ARG(dtype == LL_BF16 || dtype == LL_F16, "ll_gemm_splitk: bf16/fp16 only");
+  LL_CHECK_ARG(K % 8 == 0 && ldx % 8 == 0 && ldw % 8 == 0,
+               "ll_gemm_splitk: K and leading dims must be multiples of 8");
+  LL_CHECK_ARG((((uintptr_t)X | (uintptr_t)W) % 16) == 0, "ll_gemm_splitk: X and W must be 16 B aligned");
+  const SkinnyPlan p = plan_skinny(N, K);
+  LL_CHECK_ARG(part_bytes >= (int64_t)p.splits * M * N * 4,
+               "ll_gemm_splitk: partial buffer too small (need %lld bytes)",
+               (long long)((int64_t)p.splits * M * N * 4));
+  if (dtype == LL_BF16)
+    launch_skinny<__bf16>(p, (const __bf16*)X, ldx, (const __bf16*)W, ldw, nullptr, nullptr, 0,
+                          part, (int)M, (int)N, (int)K, stream);
+  else
+    launch_skinny<_Float16>(p, (const _Float16*)X, ldx, (const _Float16*)W, ldw, nullptr, nullptr,
+                            0, part, (int)M, (int)N, (int)K, stream);
+  LL_RETURN_LAUNCH();
 }
 
 extern "C" int ll_gemm(const void* X, int64_t ldx, const void* W, int64_t ldw, const void* bias,

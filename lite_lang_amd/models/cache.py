@@ -94,16 +94,20 @@ class PageCache:
         self._r2t_host = np.zeros((max_batch_size, max_length), dtype=np.int32)
 
     # ------------------------------------------------------------ slots
-    def _upload_assign(self, slots: np.ndarray, rows: np.ndarray, cols: np.ndarray):
-        n = slots.shape[0]
-        if n == 0:
-            return torch.empty((0,), dtype=torch.int32, device=self.device)
+    def _check_and_mirror(self, slots, rows, cols):
+        if slots.shape[0] == 0:
+            return
         if rows.min() < 0 or rows.max() >= self.max_batch_size_ or cols.min() < 0 \
                 or cols.max() >= self.max_length_:
             raise IndexError(f"slot-table write outside [{self.max_batch_size_}, "
                              f"{self.max_length_}] (request longer than max_length?)")
-        packed = np.stack([slots, rows, cols]).astype(np.int32)
         self._r2t_host[rows, cols] = slots
+
+    def _upload_assign(self, slots: np.ndarray, rows: np.ndarray, cols: np.ndarray):
+        n = slots.shape[0]
+        if n == 0:
+            return torch.empty((0,), dtype=torch.int32, device=self.device)
+        packed = np.stack([slots, rows, cols]).astype(np.int32)
         dev = torch.from_numpy(packed).pin_memory().to(self.device, non_blocking=True)
         ops.assign_slots(self.req_to_tokens_, dev, n)
         return dev[0]
@@ -112,6 +116,13 @@ class PageCache:
         """Pop sum(b_new) slots; request r gets the next b_new[r] of them at
         columns b_length[r] .. of its row (cache.py:225-249). Returns the
         device int32 slot ids in batch order."""
+        slots, rows, cols = self.plan_token_idxs(b_rids, b_length, b_new_add_token_length)
+        return self._upload_assign(slots, rows, cols)
+
+    def plan_token_idxs(self, b_rids, b_length, b_new_add_token_length):
+        """Host half of alloc_token_idxs: pops the slots, updates the host
+        mirror of the slot table and returns (slots, rows, cols) int32 arrays;
+        the caller writes them to the device table (ll_assign_slots)."""
         rids = _host_ints(b_rids)
         lens = _host_ints(b_length)
         new = _host_ints(b_new_add_token_length)
@@ -125,7 +136,8 @@ class PageCache:
         offs = np.arange(total, dtype=np.int32) - np.repeat(
             np.cumsum([0] + new[:-1], dtype=np.int64).astype(np.int32), new)
         cols = np.repeat(np.asarray(lens, dtype=np.int32), new) + offs
-        return self._upload_assign(slots, rows, cols)
+        self._check_and_mirror(slots, rows, cols)
+        return slots, rows, cols
 
     def alloc_req(self):
         return self.free_req_.alloc_new_req()
@@ -144,7 +156,9 @@ class PageCache:
         """req_to_tokens[rid, :n] = token_idxs (cache.py:284-285)."""
         t = np.asarray(_host_ints(token_idxs), dtype=np.int32)
         n = t.shape[0]
-        self._upload_assign(t, np.full(n, rid, dtype=np.int32), np.arange(n, dtype=np.int32))
+        rows, cols = np.full(n, rid, dtype=np.int32), np.arange(n, dtype=np.int32)
+        self._check_and_mirror(t, rows, cols)
+        self._upload_assign(t, rows, cols)
 
     def free_token_idxs(self, token_idxs):
         """Push slots back just below the stack window (cache.py:287-295)."""

@@ -1,0 +1,89 @@
+"""HIP-graph replay of the decode step.
+
+The reference rebuilds six metadata tensors on the host, reads 2*B scalars
+back and launches every kernel from Python on each decode step
+(runner_batch.py:227-243, transformer_layer.py:154); its README names the
+resulting timeline gaps as the bottleneck (README.md:108-116). Here one
+decode forward for a fixed batch size is captured once into a HIP graph:
+
+  * per-step metadata (new slot ids, request rows, slot-table columns,
+    positions, lengths) lives in one static int32 device buffer [5, B] that
+    the host refreshes with a single pinned upload before each replay;
+  * the slot-table write (ll_assign_slots) is the first node of the graph;
+  * the argmax writes the next tokens straight into the static token buffer
+    the embedding of the next replay reads, so consecutive steps chain on the
+    device without a host round trip;
+  * decode attention is captured with the runner's max_length as the length
+    bound: its split count and workspace are fixed, and every sequence
+    divides its own current length among the splits (ll_decode_attention).
+Workspaces are reserved before capture, so nothing is allocated by the
+library inside the graph; activations come from the graph's private pool.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from lite_lang_amd import _lib, ops
+
+
+def reserve_decode_workspaces(cfg, batch, max_len, device):
+    L = _lib.load()
+    D, H, KVH = cfg.head_dim, cfg.num_heads, cfg.num_key_value_heads
+    ops.reserve_workspace(device, "decode_attention",
+                          L.ll_decode_attention_workspace_size(batch, H, KVH, D, max_len))
+    shapes = [((H + 2 * KVH) * D, cfg.hidden_size), (cfg.hidden_size, H * D),
+              (2 * cfg.intermediate_size, cfg.hidden_size),
+              (cfg.hidden_size, cfg.intermediate_size), (cfg.vocab_size, cfg.hidden_size)]
+    ops.reserve_workspace(device, "gemm",
+                          max(L.ll_gemm_workspace_size(batch, n, k) for n, k in shapes))
+    ops.reserve_workspace(device, "argmax", L.ll_argmax_workspace_size(batch, cfg.vocab_size))
+
+
+def reserve_model_workspaces(model, batch, max_len):
+    reserve_decode_workspaces(model.cfg, batch, max_len, model.device)
+    if model.fused_decode_ok(batch):
+        ops.reserve_workspace(model.device, "splitk_part", model.splitk_part_numel(batch) * 4)
+
+
+class DecodeGraph:
+    META_ROWS = 5  # slots, rids, cols, positions, seq_len
+
+    def __init__(self, model, kv_cache, batch_size: int, max_len: int):
+        self.model, self.kv_cache = model, kv_cache
+        self.B = batch_size
+        self.max_len = max_len
+        dev = model.device
+        self.meta = torch.zeros((self.META_ROWS, batch_size), dtype=torch.int32, device=dev)
+        self.ids = torch.zeros((batch_size,), dtype=torch.int64, device=dev)
+        self._host = [torch.zeros((self.META_ROWS, batch_size), dtype=torch.int32,
+                                  pin_memory=True) for _ in range(2)]
+        self._host_ev = [None, None]
+        self._k = 0
+        reserve_model_workspaces(model, batch_size, max_len)
+        # the slot table must never be written by the capture itself
+        torch.cuda.synchronize(dev)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            ops.assign_slots(kv_cache.req_to_tokens_, self.meta[0:3], batch_size)
+            model.decode_tokens(self.ids, self.meta[3], self.meta[4], self.meta[1], self.meta[0],
+                                kv_cache, max_len, out=self.ids)
+        torch.cuda.synchronize(dev)
+
+    def run(self, in_ids: torch.Tensor, slots, rids, cols, positions, seq_len) -> torch.Tensor:
+        """Upload this step's metadata, replay, return the token buffer [B]
+        (valid until the next replay)."""
+        i = self._k & 1
+        self._k += 1
+        if self._host_ev[i] is not None:
+            self._host_ev[i].synchronize()
+        hm = self._host[i].numpy()
+        hm[0], hm[1], hm[2], hm[3], hm[4] = slots, rids, cols, positions, seq_len
+        self.meta.copy_(self._host[i], non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record()
+        self._host_ev[i] = ev
+        if in_ids.data_ptr() != self.ids.data_ptr():
+            self.ids.copy_(in_ids.view(-1))
+        self.graph.replay()
+        return self.ids

@@ -20,6 +20,7 @@ import torch
 from lite_lang_amd import ops
 from lite_lang_amd.models.cache import PageCache
 from lite_lang_amd.models.radix_cache import RadixTree
+from .decode_graph import DecodeGraph
 from .weights import DeviceWeights, Qwen2Config, load_state_dict, random_state_dict
 
 
@@ -51,54 +52,128 @@ class Qwen2Model:
     def load_state_dict(self, sd):
         self.w = DeviceWeights(self.cfg, sd, self.dtype, self.device)
 
-    # ------------------------------------------------------------ forward
-    def forward(self, model_inputs, kv_cache: PageCache, mem_idxs: torch.Tensor):
-        """One forward of the NoPad batch; returns next tokens [B, 1] int64."""
+    # ------------------------------------------------------------ layer stack
+    def _layers(self, h, T, slots, positions, pool, attention):
+        """The L transformer layers (transformer_layer.py:46-77) over hidden
+        rows h [T, hidden] (updated in place with the attention residual and
+        all but the last FFN residual). Returns the last FFN output."""
         cfg, w = self.cfg, self.w
         H, KVH, D = cfg.num_heads, cfg.num_key_value_heads, cfg.head_dim
-        is_prefill = model_inputs.is_prefill
-        ids_h, pos_h, start_h, lens_h, shared_h, rids_h = model_inputs.host
-        ids = model_inputs.input_tokens if is_prefill else model_inputs.output_token_ids
-        T = ids.shape[0]
-        pool = kv_cache.kv_cache_
-        r2t = kv_cache.req_to_tokens_
-        max_len = max(lens_h)
-
-        h = ops.embedding(w.embed, ids)
         attn = torch.empty((T, H, D), dtype=self.dtype, device=self.device)
         f = None
         for li, lw in enumerate(w.layers):
             x = ops.rmsnorm(h, lw["ln1"], cfg.rms_norm_eps, residual=f)
             qkv = ops.gemm(x, lw["wqkv"], lw["bqkv"])
-            ops.rope_kv_scatter(qkv, H, KVH, D, model_inputs.position_ids, self.cos, self.sin,
-                                mem_idxs, pool[li])
+            ops.rope_kv_scatter(qkv, H, KVH, D, positions, self.cos, self.sin, slots, pool[li])
             q = qkv[:, : H * D].view(T, H, D)
-            kc, vc = pool[li, :, :KVH], pool[li, :, KVH:]
-            if not is_prefill:
-                ops.decode_attention(q, r2t, model_inputs.b_rids, model_inputs.b_seq_len, max_len,
-                                     kc, vc, attn)
-            else:
-                shared = model_inputs.b_shared_seq_len if model_inputs.radix_cache is not None else None
-                ops.prefill_attention(q, kc, vc, attn, model_inputs.b_rids, model_inputs.b_start_idx,
-                                      model_inputs.b_seq_len, max_len, r2t, b_shared_seq_len=shared)
+            attention(li, q, attn)
             o = ops.gemm(attn.view(T, H * D), lw["wo"])
             x2 = ops.rmsnorm(h, lw["ln2"], cfg.rms_norm_eps, residual=o)
             gu = ops.gemm(x2, lw["wgu"])
             act = ops.silu_and_mul(gu)
             f = ops.gemm(act, lw["wdown"])
+        return f
 
-        if is_prefill:  # last row of each request (post_layer.py:56-71)
-            rows = [s + (l - sh) - 1 for s, l, sh in zip(start_h, lens_h, shared_h)]
-            rows_d = torch.from_numpy(np.asarray(rows, dtype=np.int64)).pin_memory().to(
-                self.device, non_blocking=True)
-            hs = ops.embedding(h, rows_d)
-            fs = ops.embedding(f, rows_d)
-        else:
-            hs, fs = h, f
-        y = ops.rmsnorm(hs, w.norm, cfg.final_norm_eps, residual=fs)
-        logits = ops.gemm(y, w.lm_head)
+    def _post(self, hs, fs, out=None):
+        """Final residual add + RMSNorm (eps 1e-5), lm_head, greedy argmax
+        (post_layer.py:44-54,105-107)."""
+        y = ops.rmsnorm(hs, self.w.norm, self.cfg.final_norm_eps, residual=fs)
+        logits = ops.gemm(y, self.w.lm_head)
         self.last_logits = logits
-        return ops.argmax(logits).view(-1, 1)
+        return ops.argmax(logits, out=out)
+
+    # ------------------------------------------------------------ decode
+    def splitk_part_numel(self, batch):
+        """fp32 elements of the partial-sum buffer the fused decode path needs."""
+        cfg = self.cfg
+        H, KVH, D, hd, I = (cfg.num_heads, cfg.num_key_value_heads, cfg.head_dim,
+                            cfg.hidden_size, cfg.intermediate_size)
+        shapes = [((H + 2 * KVH) * D, hd), (hd, H * D), (2 * I, hd), (hd, I)]
+        return max(ops.gemm_splitk_count(batch, n, k) * batch * n for n, k in shapes)
+
+    def fused_decode_ok(self, batch):
+        return self.dtype in (torch.bfloat16, torch.float16) and 0 < batch <= 64
+
+    def decode_tokens(self, ids, positions, seq_len, rids, slots, kv_cache: PageCache, max_len,
+                      out=None):
+        """One decode forward from device-resident metadata only (no host
+        reads, so it can be captured in a HIP graph). ids/positions/seq_len
+        [B] int32 or int64, rids/slots [B] int32; max_len bounds seq_len.
+        Writes the next tokens [B] int64 into `out` (may alias ids).
+
+        bf16/fp16 with B <= 64 runs the fused split-K layer: every projection
+        leaves fp32 partials that the next kernel finishes (RoPE + KV scatter,
+        residual + RMSNorm, SiLU_and_Mul), 9 launches per layer; other cases
+        run the generic layer."""
+        cfg = self.cfg
+        H, KVH, D = cfg.num_heads, cfg.num_key_value_heads, cfg.head_dim
+        B = ids.shape[0]
+        pool, r2t = kv_cache.kv_cache_, kv_cache.req_to_tokens_
+        h = ops.embedding(self.w.embed, ids)
+        if not self.fused_decode_ok(B):
+            def attention(li, q, attn):
+                ops.decode_attention(q, r2t, rids, seq_len, max_len, pool[li, :, :KVH],
+                                     pool[li, :, KVH:], attn)
+
+            f = self._layers(h, B, slots, positions, pool, attention)
+            return self._post(h, f, out=out)
+
+        w = self.w
+        dev, dt = self.device, self.dtype
+        part = ops.workspace(dev, "splitk_part", self.splitk_part_numel(B) * 4).view(torch.float32)
+        q = torch.empty((B, H * D), dtype=dt, device=dev)
+        attn = torch.empty((B, H, D), dtype=dt, device=dev)
+        act = torch.empty((B, cfg.intermediate_size), dtype=dt, device=dev)
+        x = ops.rmsnorm(h, w.layers[0]["ln1"], cfg.rms_norm_eps)
+        nl = len(w.layers)
+        for li, lw in enumerate(w.layers):
+            s = ops.gemm_splitk(x, lw["wqkv"], part)
+            ops.rope_kv_scatter_splitk(part, s, lw["bqkv"], q, H, KVH, D, positions, self.cos,
+                                       self.sin, slots, pool[li])
+            ops.decode_attention(q.view(B, H, D), r2t, rids, seq_len, max_len, pool[li, :, :KVH],
+                                 pool[li, :, KVH:], attn)
+            s = ops.gemm_splitk(attn.view(B, H * D), lw["wo"], part)
+            x2 = ops.add_rmsnorm_splitk(h, part, s, lw["ln2"], cfg.rms_norm_eps)
+            s = ops.gemm_splitk(x2, lw["wgu"], part)
+            ops.silu_and_mul_splitk(part, s, act)
+            s = ops.gemm_splitk(act, lw["wdown"], part)
+            if li + 1 < nl:
+                x = ops.add_rmsnorm_splitk(h, part, s, w.layers[li + 1]["ln1"], cfg.rms_norm_eps)
+            else:
+                x = ops.add_rmsnorm_splitk(h, part, s, w.norm, cfg.final_norm_eps)
+        logits = ops.gemm(x, w.lm_head)
+        self.last_logits = logits
+        return ops.argmax(logits, out=out)
+
+    # ------------------------------------------------------------ forward
+    def forward(self, model_inputs, kv_cache: PageCache, mem_idxs: torch.Tensor):
+        """One forward of the NoPad batch; returns next tokens [B, 1] int64."""
+        if not model_inputs.is_prefill:
+            lens = model_inputs.host[3]
+            return self.decode_tokens(model_inputs.output_token_ids, model_inputs.position_ids,
+                                      model_inputs.b_seq_len, model_inputs.b_rids, mem_idxs,
+                                      kv_cache, max(lens)).view(-1, 1)
+        cfg = self.cfg
+        KVH = cfg.num_key_value_heads
+        _, _, start_h, lens_h, shared_h, _ = model_inputs.host
+        ids = model_inputs.input_tokens
+        T = ids.shape[0]
+        pool, r2t = kv_cache.kv_cache_, kv_cache.req_to_tokens_
+        max_len = max(lens_h)
+        shared = model_inputs.b_shared_seq_len if model_inputs.radix_cache is not None else None
+        h = ops.embedding(self.w.embed, ids)
+
+        def attention(li, q, attn):
+            ops.prefill_attention(q, pool[li, :, :KVH], pool[li, :, KVH:], attn,
+                                  model_inputs.b_rids, model_inputs.b_start_idx,
+                                  model_inputs.b_seq_len, max_len, r2t, b_shared_seq_len=shared)
+
+        f = self._layers(h, T, mem_idxs, model_inputs.position_ids, pool, attention)
+        # last row of each request (post_layer.py:56-71)
+        rows = [s + (l - sh) - 1 for s, l, sh in zip(start_h, lens_h, shared_h)]
+        rows_d = torch.from_numpy(np.asarray(rows, dtype=np.int64)).pin_memory().to(
+            self.device, non_blocking=True)
+        return self._post(ops.embedding(h, rows_d), ops.embedding(f, rows_d)).view(-1, 1)
 
 
 class Qwen2ModelRunner:
@@ -107,7 +182,10 @@ class Qwen2ModelRunner:
     Extra keyword arguments (all optional): dtype (default bfloat16),
     kv_max_size (token slots; default sized from free memory x mem_usage as
     the reference), state_dict (weights as a HF-style dict), seed (random
-    init when neither model_path nor state_dict is given), device.
+    init when neither model_path nor state_dict is given), device,
+    use_cuda_graph (default True: decode steps replay a HIP graph captured
+    once per batch size; the returned token tensor is then valid until the
+    next forward).
     """
 
     def __init__(self, layer_nums, max_batch_size, config: Qwen2Config, **runner_kwargs):
@@ -130,6 +208,8 @@ class Qwen2ModelRunner:
         self.kv_cache = None
         self.layer_nums_ = layer_nums
         self.config_ = config
+        self.use_cuda_graph_ = runner_kwargs.get("use_cuda_graph", True)
+        self._graphs = {}
 
     def init_model(self):
         if self.state_dict_ is not None:
@@ -161,8 +241,21 @@ class Qwen2ModelRunner:
     def forward(self, model_inputs):
         if self.radix_cache is not None:
             self._compute_if_need_free_radix_tree(model_inputs)
+        if not model_inputs.is_prefill and self.use_cuda_graph_:
+            return self._graph_decode(model_inputs)
         mem_idxs = self._alloc_for_forward(model_inputs)
         return self.model_ins_.forward(model_inputs, self.kv_cache, mem_idxs)
+
+    def _graph_decode(self, model_inputs):
+        _, pos, _, lens, _, rids = model_inputs.host
+        B = len(lens)
+        g = self._graphs.get(B)
+        if g is None:
+            g = DecodeGraph(self.model_ins_, self.kv_cache, B, self.max_length_)
+            self._graphs[B] = g
+        slots, rows, cols = self.kv_cache.plan_token_idxs(rids, [l - 1 for l in lens], [1] * B)
+        out = g.run(model_inputs.output_token_ids, slots, rows, cols, pos, lens)
+        return out.view(-1, 1)
 
     def _compute_if_need_free_radix_tree(self, model_inputs):
         """Evict LRU radix leaves when the next forward needs more slots than

@@ -1,14 +1,20 @@
 """NoPad batch metadata and request bookkeeping.
 
 Counterpart of litelang/models/runner_batch.py (get_no_padding_messages
-:8-35, RunnerReq :38-85, RunnerBatch :88-265) with the same public API. The
-metadata is built on the host from the request lists and uploaded in one
-pinned copy (the reference makes six separate torch.tensor(...).cuda() calls
-and 2*B .item() reads per step).
+:8-35, RunnerReq :38-85, RunnerBatch :88-265) with the same public API and
+field names. Differences in mechanism, not in results:
+  * the metadata lists are kept on the host and the device tensors
+    (input_tokens, position_ids, b_start_idx, b_seq_len, b_shared_seq_len,
+    b_rids) are built lazily, in one pinned upload, only when a forward that
+    needs them reads them;
+  * generated tokens are copied to a pinned host ring asynchronously; a
+    request's `output_tokens` list is completed on first read (and at
+    filter / merge / radix insert), so a decode loop does not wait on the
+    device every step (the reference reads 2*B scalars per step,
+    runner_batch.py:231-234).
 """
 from __future__ import annotations
 
-from dataclasses import dataclass
 from typing import Dict
 
 import numpy as np
@@ -23,16 +29,15 @@ def get_no_padding_messages_host(input_reqs, is_prefill=True):
     position_ids, input_ids, req_lengths, start_idx, shared_seq_len, rids = [], [], [], [], [], []
     for idx, req in enumerate(input_reqs):
         rids.append(req.rid)
+        ns = len(req.shared_tokens)
+        shared_seq_len.append(ns)
         if is_prefill:
-            ns = len(req.shared_tokens)
-            shared_seq_len.append(ns)
             position_ids.extend(range(ns, ns + len(req.input_tokens)))
             start_idx.append(len(input_ids))
             input_ids.extend(req.input_tokens)
         else:
             position_ids.append(req.length - 1)
             start_idx.append(idx)
-            shared_seq_len.append(len(req.shared_tokens))
         req_lengths.append(req.length)
     return input_ids, position_ids, start_idx, req_lengths, shared_seq_len, rids
 
@@ -40,12 +45,13 @@ def get_no_padding_messages_host(input_reqs, is_prefill=True):
 def _upload(lists, device):
     """One pinned host buffer -> device; returns int64 device tensors, one per list."""
     sizes = [len(x) for x in lists]
-    flat = np.zeros(max(1, sum(sizes)), dtype=np.int64)
+    flat = torch.empty(max(1, sum(sizes)), dtype=torch.int64, pin_memory=True)
+    fn = flat.numpy()
     o = 0
     for x, n in zip(lists, sizes):
-        flat[o:o + n] = x
+        fn[o:o + n] = x
         o += n
-    dev = torch.from_numpy(flat).pin_memory().to(device, non_blocking=True)
+    dev = flat.to(device, non_blocking=True)
     out, o = [], 0
     for n in sizes:
         out.append(dev[o:o + n])
@@ -56,25 +62,25 @@ def _upload(lists, device):
 def get_no_padding_messages(input_reqs, is_prefill=True, device="cuda"):
     """Device tensors (input_ids, position_ids, b_start_idx, b_seq_len,
     b_shared_seq_len, b_rids) as in runner_batch.py:8-35 (b_rids int32)."""
-    ids, pos, st, lens, shared, rids = get_no_padding_messages_host(input_reqs, is_prefill)
-    t_ids, t_pos, t_st, t_len, t_sh, t_rid = _upload([ids, pos, st, lens, shared, rids], device)
-    return t_ids, t_pos, t_st, t_len, t_sh, t_rid.to(torch.int32)
+    h = get_no_padding_messages_host(input_reqs, is_prefill)
+    t = _upload(list(h), device)
+    return t[0], t[1], t[2], t[3], t[4], t[5].to(torch.int32)
 
 
-@dataclass
 class RunnerReq:
-    id: int
-    rid: int
-    input_length: int
-    output_length: int = 0
-    shared_tokens: list = None
-    match_token_idxs: object = None
-    input_tokens: list = None
-    output_tokens: list = None
-    temperature: float = 0.0
-    top_p: float = 0.0
-    top_k: float = 0.0
-    do_sample: bool = False
+    """One admitted request (runner_batch.py:38-85)."""
+
+    def __init__(self, id, rid, input_length, output_length=0, shared_tokens=None,
+                 match_token_idxs=None, input_tokens=None, output_tokens=None,
+                 temperature=0.0, top_p=0.0, top_k=0.0, do_sample=False):
+        self.id, self.rid = id, rid
+        self.input_length, self.output_length = input_length, output_length
+        self.shared_tokens = shared_tokens if shared_tokens is not None else []
+        self.match_token_idxs = match_token_idxs
+        self.input_tokens = input_tokens
+        self._output_tokens = output_tokens
+        self.temperature, self.top_p, self.top_k, self.do_sample = temperature, top_p, top_k, do_sample
+        self._batch = None  # batch holding not-yet-fetched tokens of this request
 
     @staticmethod
     def create_runner_req(id, input_tokens, shared_tokens, match_token_idxs, temperature, top_p,
@@ -85,40 +91,64 @@ class RunnerReq:
                          top_k=top_k, do_sample=do_sample)
 
     @property
+    def output_tokens(self):
+        if self._batch is not None:
+            self._batch.flush()
+        return self._output_tokens
+
+    @output_tokens.setter
+    def output_tokens(self, v):
+        self._output_tokens = v
+
+    @property
     def length(self):
         return len(self.shared_tokens) + self.input_length + self.output_length
 
     def update_forward_message(self, token_id):
         self.output_length += 1
-        if self.output_tokens is None:
-            self.output_tokens = []
-        self.output_tokens.append(int(token_id))
+        if self._output_tokens is None:
+            self._output_tokens = []
+        self._output_tokens.append(int(token_id))
 
 
-@dataclass
 class RunnerBatch:
-    id: object
-    request_mapping: Dict[int, RunnerReq]
-    input_tokens: torch.Tensor
-    position_ids: torch.Tensor
-    b_start_idx: torch.Tensor
-    b_seq_len: torch.Tensor
-    b_shared_seq_len: torch.Tensor
-    b_rids: torch.Tensor
-    output_token_ids: torch.Tensor
-    is_prefill: bool
-    radix_cache: RadixTree
-    kv_cache: PageCache
-    host: tuple = None  # host lists of the current metadata
+    """A NoPad batch of admitted requests (runner_batch.py:88-265)."""
 
-    def _refresh(self, is_prefill):
-        device = self.kv_cache.device
-        h = get_no_padding_messages_host(self.request_mapping.values(), is_prefill)
-        t_ids, t_pos, t_st, t_len, t_sh, t_rid = _upload(list(h), device)
-        self.input_tokens, self.position_ids, self.b_start_idx = t_ids, t_pos, t_st
-        self.b_seq_len, self.b_shared_seq_len, self.b_rids = t_len, t_sh, t_rid.to(torch.int32)
-        self.host = h
+    TOKEN_RING = 64  # decode steps whose tokens may be in flight to the host
 
+    def __init__(self, id, request_mapping: Dict[int, RunnerReq], is_prefill: bool,
+                 radix_cache: RadixTree, kv_cache: PageCache):
+        self.id = id
+        self.request_mapping = request_mapping
+        self.is_prefill = is_prefill
+        self.radix_cache = radix_cache
+        self.kv_cache = kv_cache
+        self.output_token_ids = None
+        self.host = None
+        self._dev = None
+        self._ring = None
+        self._pending = []  # (ring row, requests, event)
+        self._refresh_host()
+
+    # ------------------------------------------------------------ metadata
+    def _refresh_host(self):
+        self.host = get_no_padding_messages_host(self.request_mapping.values(), self.is_prefill)
+        self._dev = None
+
+    def _device(self):
+        if self._dev is None:
+            t = _upload(list(self.host), self.kv_cache.device)
+            self._dev = (t[0], t[1], t[2], t[3], t[4], t[5].to(torch.int32))
+        return self._dev
+
+    input_tokens = property(lambda self: self._device()[0])
+    position_ids = property(lambda self: self._device()[1])
+    b_start_idx = property(lambda self: self._device()[2])
+    b_seq_len = property(lambda self: self._device()[3])
+    b_shared_seq_len = property(lambda self: self._device()[4])
+    b_rids = property(lambda self: self._device()[5])
+
+    # ------------------------------------------------------------ admission
     @classmethod
     def create_batch(cls, req_messages, batch_id, is_prefill: bool = True, model_runner=None):
         """Admit requests (runner_batch.py:103-167): radix prefix match on all
@@ -128,7 +158,7 @@ class RunnerBatch:
             request_id = message["id"]
             input_tokens = list(message["input_tokens"])
             shared_tokens = []
-            match_token_idxs, has_match_len = None, 0
+            match_token_idxs = None
             if model_runner.radix_cache is not None:
                 match_token_idxs, has_match_len = model_runner.radix_cache.match_prefix(
                     torch.tensor(input_tokens[:-1], dtype=torch.int64))
@@ -144,12 +174,8 @@ class RunnerBatch:
             if model_runner.radix_cache is not None and new_req.match_token_idxs is not None:
                 model_runner.kv_cache.add_refs(new_req.rid, new_req.match_token_idxs)
             request_mapping[request_id] = new_req
-        batch = cls(id=batch_id, request_mapping=request_mapping, input_tokens=None,
-                    position_ids=None, b_start_idx=None, b_seq_len=None, b_shared_seq_len=None,
-                    b_rids=None, output_token_ids=None, is_prefill=is_prefill,
-                    radix_cache=model_runner.radix_cache, kv_cache=model_runner.kv_cache)
-        batch._refresh(is_prefill)
-        return batch
+        return cls(batch_id, request_mapping, is_prefill, model_runner.radix_cache,
+                   model_runner.kv_cache)
 
     def get_post_sample_para(self):
         reqs = list(self.request_mapping.values())
@@ -159,6 +185,49 @@ class RunnerBatch:
                 torch.tensor([r.top_k for r in reqs], device=dev),
                 torch.tensor([r.do_sample for r in reqs], device=dev))
 
+    # ------------------------------------------------------------ tokens
+    def flush(self):
+        """Complete every request's output_tokens with the fetched tokens."""
+        if not self._pending:
+            return
+        self._pending[-1][2].synchronize()
+        ring = self._ring.numpy()
+        for row, reqs, _ in self._pending:
+            for j, req in enumerate(reqs):
+                if req._output_tokens is None:
+                    req._output_tokens = []
+                req._output_tokens.append(int(ring[row, j]))
+                req._batch = None
+        self._pending = []
+
+    def update_forward_message(self, output_token_ids):
+        """Record one generated token per request and move to decode metadata
+        (runner_batch.py:227-243). The tokens reach the host asynchronously."""
+        self.is_prefill = False
+        out = output_token_ids.view(-1)
+        self.output_token_ids = out
+        reqs = list(self.request_mapping.values())
+        B = len(reqs)
+        if self._ring is None or self._ring.shape[1] < B:
+            self.flush()
+            self._ring = torch.empty((self.TOKEN_RING, max(B, 1)), dtype=torch.int64,
+                                     pin_memory=True)
+        if len(self._pending) == self.TOKEN_RING:
+            self.flush()
+        row = len(self._pending)
+        self._ring[row, :B].copy_(out, non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record()
+        self._pending.append((row, reqs, ev))
+        req_ids = []
+        for req in reqs:
+            req.output_length += 1
+            req._batch = self
+            req_ids.append(req.id)
+        self._refresh_host()
+        return req_ids
+
+    # ------------------------------------------------------------ membership
     def _free_req_cache(self, req_id):
         """Insert the finished request into the radix tree and release the
         duplicate slots and the request row (runner_batch.py:184-204)."""
@@ -174,36 +243,27 @@ class RunnerBatch:
         return True
 
     def filter(self, req_ids):
+        """Drop finished requests (runner_batch.py:206-225)."""
+        self.flush()
         should_free_reqs = []
         for req_id in req_ids:
             if self.radix_cache is not None:
                 self._free_req_cache(req_id)
             should_free_reqs.append(self.request_mapping.pop(req_id))
         last = [req.output_tokens[-1] for req in self.request_mapping.values()]
-        self._refresh(False)
         self.is_prefill = False
+        self._refresh_host()
         self.output_token_ids = torch.tensor(last, dtype=torch.int64, device=self.kv_cache.device)
         return should_free_reqs
-
-    def update_forward_message(self, output_token_ids):
-        """Record one generated token per request (one device->host read for
-        the whole batch) and rebuild the decode metadata (runner_batch.py:227-243)."""
-        self.is_prefill = False
-        self.output_token_ids = output_token_ids.view(-1)
-        toks = self.output_token_ids.tolist()
-        req_ids = []
-        for tok, req in zip(toks, self.request_mapping.values()):
-            req_ids.append(req.id)
-            req.update_forward_message(tok)
-        self._refresh(False)
-        return req_ids
 
     def update(self, new_runner_batch):
         """Merge another decode batch into this one (runner_batch.py:245-265)."""
         assert self.is_prefill is False and new_runner_batch.is_prefill is False, (
             "only decode batch can be merged")
+        self.flush()
+        new_runner_batch.flush()
         self.request_mapping.update(new_runner_batch.request_mapping)
         last = [req.output_tokens[-1] for req in self.request_mapping.values()]
-        self._refresh(False)
+        self._refresh_host()
         self.output_token_ids = torch.tensor(last, dtype=torch.int64, device=self.kv_cache.device)
         return True

@@ -263,3 +263,59 @@ def assign_slots(req_to_tokens, packed, n):
     rc = _L.ll_assign_slots(req_to_tokens.data_ptr(), req_to_tokens.stride(0), packed[0].data_ptr(),
                             packed[1].data_ptr(), packed[2].data_ptr(), n, _stream(req_to_tokens))
     _lib.check(rc, "ll_assign_slots")
+
+
+# ------------------------------------------------------------------ decode split-K path
+def gemm_splitk_count(M, N, K) -> int:
+    return _L.ll_gemm_splitk_count(M, N, K)
+
+
+def gemm_splitk(x, w, part):
+    """fp32 partial sums of x[M, K] @ w[N, K]^T into part (flat fp32 buffer);
+    returns the split count s (part[:s*M*N] holds [s, M, N])."""
+    _dev(x, w, part)
+    M, K = x.shape
+    N = w.shape[0]
+    assert w.shape[1] == K and x.stride(1) == 1 and w.stride(1) == 1 and part.dtype == torch.float32
+    s = _L.ll_gemm_splitk_count(M, N, K)
+    rc = _L.ll_gemm_splitk(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), M, N, K,
+                           dtype_code(x), part.data_ptr(), part.numel() * 4, _stream(x))
+    _lib.check(rc, "ll_gemm_splitk")
+    return s
+
+
+def add_rmsnorm_splitk(h, part, splits, gamma, eps, out=None):
+    """h = dtype(h + dtype(sum part)); returns rmsnorm(h) * gamma."""
+    _dev(h, part, gamma, out)
+    M, N = h.shape
+    if out is None:
+        out = torch.empty_like(h)
+    rc = _L.ll_add_rmsnorm_splitk(h.data_ptr(), h.stride(0), part.data_ptr(), splits,
+                                  gamma.data_ptr(), out.data_ptr(), out.stride(0), M, N, float(eps),
+                                  dtype_code(h), _stream(h))
+    _lib.check(rc, "ll_add_rmsnorm_splitk")
+    return out
+
+
+def silu_and_mul_splitk(part, splits, out):
+    """out[M, N] = up * dtype(silu(gate)) from partials of the [M, 2N] product."""
+    _dev(part, out)
+    M, N = out.shape
+    rc = _L.ll_silu_and_mul_splitk(part.data_ptr(), splits, out.data_ptr(), out.stride(0), M, N,
+                                   dtype_code(out), _stream(out))
+    _lib.check(rc, "ll_silu_and_mul_splitk")
+    return out
+
+
+def rope_kv_scatter_splitk(part, splits, bias, q_out, q_heads, kv_heads, head_dim, positions,
+                           cos_table, sin_table, slots, pool_layer):
+    _dev(part, q_out, positions, cos_table, sin_table, slots, pool_layer)
+    T = q_out.shape[0]
+    assert slots.dtype == torch.int32 and q_out.stride(1) == 1 and pool_layer.stride(-1) == 1
+    rc = _L.ll_rope_kv_scatter_splitk(
+        part.data_ptr(), splits, bias.data_ptr() if bias is not None else None, q_out.data_ptr(),
+        q_out.stride(0), T, q_heads, kv_heads, head_dim, positions.data_ptr(),
+        _idx(positions, "positions"), cos_table.data_ptr(), sin_table.data_ptr(),
+        cos_table.stride(0), dtype_code(cos_table), slots.data_ptr(), pool_layer.data_ptr(),
+        pool_layer.stride(0), pool_layer.stride(1), dtype_code(q_out), _stream(q_out))
+    _lib.check(rc, "ll_rope_kv_scatter_splitk")

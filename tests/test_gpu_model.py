@@ -26,12 +26,13 @@ def _cfgs():
     return c, oc
 
 
-def _run_product(cfg, sd, prompts, n_new, dtype, cuda, max_length=128):
+def _run_product(cfg, sd, prompts, n_new, dtype, cuda, max_length=128, graph=True):
     from lite_lang_amd.models.qwen2 import Qwen2ModelRunner
     from lite_lang_amd.models.runner_batch import RunnerBatch
     runner = Qwen2ModelRunner(cfg.layer_nums, 8, cfg, tp_rank=0, world_size=1, model_path=None,
                               max_length=max_length, mem_usage=0.5, use_radix_cache=False,
-                              dtype=dtype, state_dict=sd, kv_max_size=1024, device=cuda)
+                              dtype=dtype, state_dict=sd, kv_max_size=1024, device=cuda,
+                              use_cuda_graph=graph)
     runner.init_model()
     msgs = [{"id": i, "input_tokens": list(p), "temperature": 0.0, "top_p": 1.0, "top_k": 1,
              "do_sample": False} for i, p in enumerate(prompts)]
@@ -45,18 +46,20 @@ def _run_product(cfg, sd, prompts, n_new, dtype, cuda, max_length=128):
     return toks, torch.stack(logits, 1)
 
 
-def test_config1_fp32_greedy_tokens_identical(cuda):
+@pytest.mark.parametrize("graph", [True, False])
+def test_config1_fp32_greedy_tokens_identical(cuda, graph):
     from lite_lang_amd.models.qwen2.weights import random_state_dict
     cfg, ocfg = _cfgs()
     sd = random_state_dict(cfg, seed=0)
     prompt = torch.randint(0, 1024, (16,), generator=torch.Generator().manual_seed(0)).tolist()
-    print("case: config1 fp32 greedy 32", flush=True)
+    print(f"case: config1 fp32 greedy 32 graph={graph}", flush=True)
     ref = Qwen2Oracle(ocfg, sd, torch.float32, 8, 128, 1024).generate([prompt], 32)
-    got, _ = _run_product(cfg, sd, [prompt], 32, torch.float32, cuda)
+    got, _ = _run_product(cfg, sd, [prompt], 32, torch.float32, cuda, graph=graph)
     assert got.tolist() == ref.tolist()
 
 
-def test_tiny_bf16_ragged_batch_logits(cuda):
+@pytest.mark.parametrize("graph", [True, False])
+def test_tiny_bf16_ragged_batch_logits(cuda, graph):
     from lite_lang_amd.models.qwen2.weights import random_state_dict
     cfg, ocfg = _cfgs()
     sd = random_state_dict(cfg, seed=1)
@@ -65,7 +68,7 @@ def test_tiny_bf16_ragged_batch_logits(cuda):
     print("case: tiny bf16 ragged batch", flush=True)
     ref, ref_logits = Qwen2Oracle(ocfg, sd, torch.bfloat16, 8, 128, 1024).generate(
         prompts, 8, return_logits=True)
-    got, got_logits = _run_product(cfg, sd, prompts, 8, torch.bfloat16, cuda)
+    got, got_logits = _run_product(cfg, sd, prompts, 8, torch.bfloat16, cuda, graph=graph)
     for b in range(len(prompts)):
         for s in range(8):
             d = float((got_logits[b, s].double() - ref_logits[b, s]).abs().max())
@@ -74,3 +77,54 @@ def test_tiny_bf16_ragged_batch_logits(cuda):
                 top2 = ref_logits[b, s].topk(2).values
                 assert float(top2[0] - top2[1]) <= 2e-2, "token divergence without a near tie"
                 break
+
+
+def test_qwen25_3b_geometry_two_layers_batch40(cuda):
+    """Qwen2.5-3B layer geometry (hidden 2048, 16/2 heads, D 128, I 11008,
+    vocab 151936) with 2 layers, batch 40: exercises the wide-N LDS GEMM, the
+    split-K fused decode layer and the graph path at the real shapes.
+
+    At this width the logits are O(5) and carry bf16 noise: an exact bf16
+    execution of the reference algorithm (the bf16-emulating oracle) is itself
+    ~6e-2 away from the fp32 oracle, so a fixed max-abs bar cannot separate a
+    bug from rounding. The check is instead that the GPU path is no less
+    accurate than that exact bf16 execution, measured against the fp32
+    oracle, for 3 steps; tokens must match the bf16 oracle except at near ties.
+    """
+    from lite_lang_amd.models.qwen2.weights import Qwen2Config, random_state_dict
+    cfg = Qwen2Config(layer_nums=2, hidden_size=2048, num_heads=16, num_key_value_heads=2,
+                      intermediate_size=11008, vocab_size=151936)
+    ocfg = Qwen2Cfg(num_layers=2, hidden=2048, heads=16, kv_heads=2, intermediate=11008,
+                    vocab=151936)
+    sd = random_state_dict(cfg, seed=3)
+    g = torch.Generator().manual_seed(3)
+    prompts = [torch.randint(0, 151936, (int(n),), generator=g).tolist()
+               for n in torch.randint(1, 24, (40,), generator=g)]
+    print("case: 3B geometry 2 layers batch 40", flush=True)
+    tb, lb = Qwen2Oracle(ocfg, sd, torch.bfloat16, 48, 64, 2048).generate(
+        prompts, 3, return_logits=True)
+    tf, lf = Qwen2Oracle(ocfg, sd, torch.float32, 48, 64, 2048).generate(
+        prompts, 3, return_logits=True)
+    from lite_lang_amd.models.qwen2 import Qwen2ModelRunner
+    from lite_lang_amd.models.runner_batch import RunnerBatch
+    runner = Qwen2ModelRunner(2, 48, cfg, max_length=64, dtype=torch.bfloat16, state_dict=sd,
+                              kv_max_size=2048, device=cuda)
+    runner.init_model()
+    msgs = [{"id": i, "input_tokens": p} for i, p in enumerate(prompts)]
+    batch = RunnerBatch.create_batch(msgs, "b", True, runner)
+    alive = torch.ones(40, dtype=torch.bool)  # requests whose history equals both oracles'
+    for step in range(3):
+        out = runner.forward(batch)
+        lg = runner.model_ins_.last_logits.double().cpu()
+        got = out.view(-1).cpu()
+        batch.update_forward_message(out)
+        err_gpu = float((lg[alive] - lf[alive, step]).abs().max())
+        err_bf16 = float((lb[alive, step] - lf[alive, step]).abs().max())
+        print(f"step {step}: |gpu - fp32| {err_gpu:.4f}  |bf16 exact - fp32| {err_bf16:.4f}")
+        assert err_gpu <= 1.25 * err_bf16 + 1e-3, f"step {step}: gpu {err_gpu} vs bf16 {err_bf16}"
+        mism = (got != tb[:, step]) & alive
+        for b in mism.nonzero().view(-1).tolist():
+            top2 = lb[b, step].topk(2).values
+            assert float(top2[0] - top2[1]) <= 2 * err_bf16, f"request {b} diverged without a near tie"
+        alive &= ~mism & (tb[:, step] == tf[:, step])
+    assert int(alive.sum()) >= 30
