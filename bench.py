@@ -33,6 +33,11 @@ import torch
 
 HBM_PEAK_GBS = 8000.0
 B, PROMPT = 40, 600
+# HBM bytes per config-2 attention op (split stage + combine), from
+# rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of `bench.py --attention-only`,
+# scaled by what the counters read for a 256 MiB copy (fetch x2.0, write x1.0).
+# Measured on the current kernels; re-measure when they change.
+ATTN_TRAFFIC_BYTES = 27120 * 1024
 
 
 def log(msg):
@@ -167,6 +172,9 @@ def main():
     ap.add_argument("--steps", type=int, default=600)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--attention-only", action="store_true",
+                    help="run only the config-2 decode attention launches plus a 256 MiB "
+                         "device copy of known size (for rocprofv3 --pmc traffic runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU (tp=1, no collectives); "
@@ -179,6 +187,15 @@ def main():
     from lite_lang_amd.models.qwen2.weights import qwen25_3b_config
     cfg = qwen25_3b_config()
     K, W = args.steps, args.warmup
+
+    if args.attention_only:
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)  # reference copy: 256 MiB read + 256 MiB written
+        torch.cuda.synchronize()
+        attn_sec, attn_bytes = bench_decode_attention(dev, iters=50)
+        print(json.dumps({"attention_us": attn_sec * 1e6, "bytes_per_launch": attn_bytes}))
+        return
 
     log("decode attention microbench (config 2)")
     attn_sec, attn_bytes = bench_decode_attention(dev)
@@ -233,7 +250,7 @@ def main():
                         "hbm_frac": round(step_bytes / step_sec / 1e9 / HBM_PEAK_GBS, 4)},
         "roofline": {"kernel": "decode_attn_mfma_kernel (config 2)", "bound": "hbm",
                      "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "traffic": ATTN_TRAFFIC_BYTES,
                      "avg_us": round(attn_sec * 1e6, 3), "bytes_per_launch": attn_bytes},
         "cpu_baseline": cpu,
     }
