@@ -41,11 +41,20 @@ template <typename V8> __device__ __forceinline__ V8 zero8() {
 // Output of the M <= 64 kernels: if `part` is non-null, fp32 partial sums
 // part[split][m][n] (N contiguous, no bias); else Y[m][n] = T(sum + bias[n]).
 
-template <int N_> __device__ __forceinline__ void vm_wait();
-#define LL_VMWAIT(n) \
-  template <> __device__ __forceinline__ void vm_wait<n>() { asm volatile("s_waitcnt vmcnt(" #n ")" ::: "memory"); }
-LL_VMWAIT(0) LL_VMWAIT(5) LL_VMWAIT(6) LL_VMWAIT(7) LL_VMWAIT(8)
-#undef LL_VMWAIT
+// Wait until at most N of this wave's vector memory operations are in flight.
+template <int N_> __device__ __forceinline__ void vm_wait() {
+  static_assert(N_ >= 0 && N_ < 64, "vmcnt is a 6-bit counter");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N_) : "memory");
+}
+
+// Workgroup barrier that waits for nothing but this wave's LDS reads. The
+// caller has already waited (vm_wait) for its own LDS DMA of the stage the
+// other waves will read. __syncthreads() would also drain every outstanding
+// global load, including the DMA of the stage being prefetched, and so
+// serialise the pipeline.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
 
 // 16 B global -> LDS DMA of one lane (lane i of the wave lands at lds + 16 i).
 // Kept out of the kernel templates: a dependent call of this device-only
@@ -59,22 +68,39 @@ __device__ __forceinline__ void dma16(const void* g, void* lds) {
 // 64-row x 128-k weight tile and the matching 16*MB-row activation tile into
 // LDS, with 256 contiguous bytes per row per wave instruction. The 16 B chunk
 // index of every row is XOR-swizzled by (row & 15) so the MFMA operand reads
-// (16 rows x 16 B per 16 lanes) are bank-conflict free. Two stages in flight.
-constexpr int kDmaKC = 128, kDmaNST = 2, kDmaTR = 64;
+// (16 rows x 16 B per 16 lanes) are bank-conflict free. NST stage buffers
+// form a ring: while stage st is multiplied, stages st+1 .. st+NST-1 are in
+// flight. One barrier per stage: after it, every wave has finished stage
+// st-1, so its buffer is refilled with stage st+NST-1.
+constexpr int kDmaKC = 128, kDmaTR = 64;
 
-template <typename T, int MB>
+// Wait for the oldest in-flight stage when `later` younger stages of C
+// operations each may stay in flight (later <= NST - 2).
+template <int C, int NST>
+__device__ __forceinline__ void wait_stage(int later) {
+  if constexpr (NST >= 4) {
+    if (later >= 2) { vm_wait<2 * C>(); return; }
+  }
+  if constexpr (NST >= 3) {
+    if (later >= 1) { vm_wait<C>(); return; }
+  }
+  vm_wait<0>();
+}
+
+template <typename T, int MB, int NST>
 __global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, int64_t ldx,
                                                        const T* __restrict__ W, int64_t ldw,
                                                        const T* __restrict__ bias,
                                                        T* __restrict__ Y, int64_t ldy,
                                                        float* __restrict__ part, int M, int N,
-                                                       int K, int ksps) {
+                                                       int K, int ksps, int rotate) {
+  static_assert(NST >= 2 && NST <= 4, "2 to 4 stage buffers");
   typedef typename Vec8<T>::type V8;
-  constexpr int TR = kDmaTR, XR = 16 * MB, KC = kDmaKC, NST = kDmaNST;
+  constexpr int TR = kDmaTR, XR = 16 * MB, KC = kDmaKC;
   constexpr int ROWB = KC * 2, CH = ROWB / 16, RPI = 64 / CH;  // 16 chunks, 4 rows/instr
   constexpr int W_PER_WAVE = (TR / RPI) / 4;
   constexpr int X_PER_WAVE = (XR / RPI) / 4;
-  constexpr int C = W_PER_WAVE + X_PER_WAVE;
+  constexpr int C = W_PER_WAVE + X_PER_WAVE;  // DMA instructions per wave per stage
   constexpr int STAGE_B = (TR + XR) * ROWB;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -85,9 +111,14 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, 
   const int k_end = min(K, k_beg + ksps * 32);
   const int nst = (k_end - k_beg) / KC;
   const int lr_in = lane / CH, p = lane % CH;
+  // optional per-workgroup rotation of the k-chunk order, so that concurrent
+  // workgroups read different column ranges of their rows
+  const int rot = (rotate && nst > 0) ? (int)(blockIdx.x % nst) : 0;
   auto issue = [&](int st) {
     char* base = smem + (st % NST) * STAGE_B;
-    const int k0 = k_beg + st * KC;
+    int kc = st + rot;
+    if (kc >= nst) kc -= nst;
+    const int k0 = k_beg + kc * KC;
 #pragma unroll
     for (int q = 0; q < W_PER_WAVE; ++q) {
       const int ii = wave * W_PER_WAVE + q;
@@ -106,16 +137,15 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, 
   f32x4 acc[MB];
 #pragma unroll
   for (int t = 0; t < MB; ++t) acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
-  if (nst > 0) issue(0);
+#pragma unroll
+  for (int st = 0; st < NST - 1; ++st)
+    if (st < nst) issue(st);
   const int lr = wave * 16 + n;
   for (int st = 0; st < nst; ++st) {
-    if (st + 1 < nst) {
-      issue(st + 1);
-      vm_wait<C>();
-    } else {
-      vm_wait<0>();
-    }
-    __syncthreads();
+    // issued so far: stages 0 .. min(nst, st + NST - 1) - 1
+    wait_stage<C, NST>(min(NST - 2, nst - 1 - st));
+    lds_barrier();
+    if (st + NST - 1 < nst) issue(st + NST - 1);  // into the buffer of stage st-1
     const char* wb = smem + (st % NST) * STAGE_B;
     const char* xb = wb + TR * ROWB;
 #pragma unroll
@@ -128,7 +158,6 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, 
         acc[t] = mfma16x16x32(a, b, acc[t]);
       }
     }
-    __syncthreads();
   }
   // acc[t][i] = Y[token 16t + n][channel row0 + 16*wave + 4j + i]
   const int ch = row0 + wave * 16 + 4 * j;
@@ -414,22 +443,35 @@ struct SkinnyPlan {
   int splits;  // K splits across workgroups (all non-empty)
   int ksps;    // 32-wide k-steps per split
   int tiles;   // row tiles
+  int nst;     // LDS stage buffers of the DMA kernel
+  int rotate;  // DMA kernel: rotate the k-chunk order per workgroup
 };
 
 constexpr int kDirWR = 2, kDirKW = 4, kDirU = 2;
 
 SkinnyPlan plan_skinny(int64_t N, int64_t K) {
   SkinnyPlan p;
+  p.nst = 2;
+  p.rotate = 0;
   const int ksteps = (int)((K + 31) / 32);
-  p.dma = (K % kDmaKC == 0) && (N >= 4096 || K >= 8192);
+  p.dma = (K % kDmaKC == 0);
   if (p.dma) {
+    // Measured at the Qwen2.5 decode shapes (M = 40): the weight stream is
+    // fastest with about one workgroup per CU when the row tiles are few
+    // (split K until tiles * splits reaches 256, three stage buffers) and with
+    // one split and two stage buffers (two workgroups per CU) when they are
+    // many; rotating each workgroup's k-chunk order spreads the concurrent
+    // reads over more HBM channels.
     const int chunks = (int)(K / kDmaKC);
     p.tiles = (int)((N + kDmaTR - 1) / kDmaTR);
-    int sp = 1;
-    while ((int64_t)p.tiles * sp < 640 && chunks / (sp * 2) >= 2) sp *= 2;
+    int sp = 256 / p.tiles;
+    if (sp > chunks / 2) sp = chunks / 2;
+    if (sp < 1) sp = 1;
     const int per = (chunks + sp - 1) / sp;
     p.splits = (chunks + per - 1) / per;
     p.ksps = per * (kDmaKC / 32);
+    p.nst = (p.tiles * p.splits <= 256) ? 3 : 2;
+    p.rotate = 1;
   } else {
     p.tiles = (int)((N + 16 * kDirWR - 1) / (16 * kDirWR));
     int sp = 1;
@@ -447,9 +489,16 @@ void launch_skinny_mb(const SkinnyPlan& p, const T* X, int64_t ldx, const T* W, 
                       hipStream_t stream) {
   const dim3 grid((unsigned)p.tiles, (unsigned)p.splits);
   if (p.dma) {
-    const size_t lds = (size_t)kDmaNST * (kDmaTR + 16 * MB) * kDmaKC * 2;
-    hipLaunchKernelGGL((gemm_dma_kernel<T, MB>), grid, dim3(256), lds, stream, X, ldx, W, ldw,
-                       bias, Y, ldy, part, M, N, K, p.ksps);
+    const size_t lds = (size_t)p.nst * (kDmaTR + 16 * MB) * kDmaKC * 2;
+    if (p.nst == 4)
+      hipLaunchKernelGGL((gemm_dma_kernel<T, MB, 4>), grid, dim3(256), lds, stream, X, ldx, W, ldw,
+                         bias, Y, ldy, part, M, N, K, p.ksps, p.rotate);
+    else if (p.nst == 3)
+      hipLaunchKernelGGL((gemm_dma_kernel<T, MB, 3>), grid, dim3(256), lds, stream, X, ldx, W, ldw,
+                         bias, Y, ldy, part, M, N, K, p.ksps, p.rotate);
+    else
+      hipLaunchKernelGGL((gemm_dma_kernel<T, MB, 2>), grid, dim3(256), lds, stream, X, ldx, W, ldw,
+                         bias, Y, ldy, part, M, N, K, p.ksps, p.rotate);
   } else {
     hipLaunchKernelGGL((gemm_direct_kernel<T, MB, kDirWR, kDirKW, kDirU>), grid,
                        dim3(64 * kDirKW), 0, stream, X, ldx, W, ldw, bias, Y, ldy, part, M, N, K,
