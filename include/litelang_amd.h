@@ -48,8 +48,11 @@ const char* ll_last_error(void);
  *   (litelang/kernel/develop_flash_attn/flash_decoding.py:262-312).
  * q [batch, q_heads, head_dim]; k_cache / v_cache [P, kv_heads, head_dim]
  * views of the pool (last dim contiguous); req_to_tokens [max_batch, max_len]
- * int32 slot table; out [batch, q_heads, head_dim]. max_len_in_batch is an
- * upper bound of b_seq_len (it sizes the split count and the workspace). */
+ * int32 slot table; out [batch, q_heads, head_dim]. max_len_in_batch bounds
+ * b_seq_len (it sizes the split count and the workspace; tokens beyond it are
+ * ignored, as the reference's grid ignores them). workspace: at least
+ * ll_decode_attention_workspace_size bytes (0 when no split is needed), any
+ * contents; two calls in flight at once must not share it. */
 int64_t ll_decode_attention_workspace_size(int64_t batch, int64_t q_heads, int64_t kv_heads,
                                            int64_t head_dim, int64_t max_len_in_batch);
 int ll_decode_attention(const void* q, int64_t q_stride_b, int64_t q_stride_h,

@@ -9,39 +9,67 @@
 //   * one workgroup per (sequence, KV head, split) serves all G = H/KVH query
 //     heads of the group, so each K/V row is read from HBM exactly once (the
 //     reference launches one program per query head and re-reads it G times);
-//   * per 32-token tile a wave computes S^T = K . Q^T and O^T += V^T . P^T on
-//     bf16/fp16 MFMA (v_mfma_f32_16x16x32), the G heads padded to 16 columns;
-//     K rows are loaded straight from HBM into the MFMA A operand (16 B per
-//     lane), V rows go through a padded LDS tile that the A operand of the
-//     second product reads transposed;
+//   * the split's slot ids are staged in LDS first; then every wave streams
+//     the K and V rows of its own 16-token tiles straight into LDS with
+//     global_load_lds_dwordx4 (no VGPR staging, 16 B chunks XOR-swizzled per
+//     row), two tiles in flight per wave, with no workgroup barrier in the
+//     token loop -- the kernel is bound by how many bytes are in flight;
+//   * per tile S^T = K . Q^T on v_mfma_f32_16x16x32 (the G heads padded to 16
+//     columns) and O^T += V^T . P^T on v_mfma_f32_16x16x16, whose B operand
+//     is exactly the S^T accumulator layout, so P never leaves registers;
 //   * the split count is fixed per launch and each sequence divides its own
-//     length into that many tile-aligned chunks, so short and long sequences
-//     are balanced and the grid does not depend on the lengths (graph safe);
-//   * the 4 waves of a workgroup merge in LDS; the splits of a (sequence, KV
-//     head) are merged by a second, small kernel (log-sum-exp combine of the
-//     fp32 partials). An in-launch "last workgroup combines" scheme needs a
-//     device-scope release/acquire per workgroup, which on gfx950 writes back
-//     and invalidates the whole L2 of the XCD and costs far more than the
-//     extra launch.
+//     length into that many tile-aligned chunks, so the grid does not depend
+//     on the lengths (graph safe);
+//   * the 4 waves merge in LDS; the splits of a (sequence, KV head) are merged
+//     by a second kernel, one wave per (sequence, head) with the partials of
+//     all splits in flight at once. Merging in the same launch (the last
+//     split to finish merges, signalled through a device-scope counter) was
+//     measured slower: the chain of device-scope store acknowledgement,
+//     counter atomic and coherent reloads costs more than the extra launch.
 // A generic VALU path covers fp32 and head dims other than 64/128.
 #include "ll_common.h"
 
 namespace {
 
-constexpr int kTile = 32;   // tokens per wave iteration
+constexpr int kTT = 16;     // tokens per tile
 constexpr int kWaves = 4;   // waves per workgroup
-constexpr int kVStride = 136;  // LDS row stride (elements) of the V tile: 272 B, 16 B aligned,
-                               // rows 4 apart land 16 banks apart -> conflict-free reads
+constexpr int kRing = 2;    // tile buffers per wave
 
 template <typename T> struct Vec8;
 template <> struct Vec8<__bf16> { typedef bf16x8 type; };
 template <> struct Vec8<_Float16> { typedef f16x8 type; };
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+template <typename T> struct Vec4;
+template <> struct Vec4<__bf16> { typedef s16x4 type; };
+template <> struct Vec4<_Float16> { typedef f16x4 type; };
 
 __device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 __device__ __forceinline__ f32x4 mfma16x16x32(f16x8 a, f16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma16x16x16(s16x4 a, s16x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma16x16x16(f16x4 a, f16x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+// raw 16-bit pattern of an element (the 16x16x16 bf16 operands are short vectors)
+__device__ __forceinline__ short bits16(__bf16 x) { return __builtin_bit_cast(short, x); }
+__device__ __forceinline__ _Float16 bits16(_Float16 x) { return x; }
+
+// 16 B global -> LDS DMA of one lane (lane i of the wave lands at lds + 16 i).
+// Kept out of the kernel templates: a dependent call of this device-only
+// builtin makes the host pass drop the template's launch stub.
+__device__ __forceinline__ void dma16(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0);
+}
+
+template <int N_> __device__ __forceinline__ void vm_wait() {
+  static_assert(N_ >= 0 && N_ < 64, "vmcnt is a 6-bit counter");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N_) : "memory");
 }
 
 struct DecodeArgs {
@@ -55,6 +83,8 @@ struct DecodeArgs {
   int B, H, KVH, G;
   int nsplit;
   int units;          // B * KVH
+  int max_len;        // tokens beyond it are ignored (as the reference's grid does)
+  int slots_cap;      // slot entries the LDS slot table holds (>= tiles per split * 16)
   float scale_log2;   // sm_scale * log2(e)
   float* part_acc;    // [B*H*nsplit, D] unnormalised partial outputs
   float* part_ml;     // [B*H*nsplit, 2] running max (log2 domain) and sum
@@ -69,19 +99,29 @@ __device__ __forceinline__ void map_block(int bid, int nsplit, int& unit, int& s
   split = slot % nsplit;
 }
 
+template <int D> struct TileGeom {
+  static constexpr int ROWB = D * 2;            // bytes of one K or V row
+  static constexpr int CH = ROWB / 16;          // 16 B chunks per row
+  static constexpr int RPI = 64 / CH;           // rows per wave DMA instruction
+  static constexpr int IPT = kTT / RPI;         // DMA instructions per tile, K or V
+  static constexpr int TILE_B = 2 * kTT * ROWB; // K rows then V rows
+  static constexpr int ROWS_PER_BANKS = 256 / ROWB;  // rows sharing one 256 B bank window
+  static constexpr int RING_B = kWaves * kRing * TILE_B;
+  static constexpr int MERGE_B = kWaves * 16 * (D + 1) * 4 + 2 * kWaves * 16 * 4;
+  static constexpr int MAIN_B = RING_B > MERGE_B ? RING_B : MERGE_B;
+  // LDS chunk position of global chunk c of tile row r (an involution)
+  static __device__ __forceinline__ int swz(int c, int r) { return c ^ ((r / ROWS_PER_BANKS) & (CH - 1)); }
+};
+
 template <typename T, int D>
-__global__ __launch_bounds__(kWaves * 64) void decode_attn_mfma_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs a) {
   typedef typename Vec8<T>::type V8;
-  constexpr int DS = D / 32;  // d-steps of 32 for the S^T product
+  typedef typename Vec4<T>::type V4;
+  typedef TileGeom<D> TG;
+  constexpr int DS = D / 32;  // k-steps of the S^T product
   constexpr int DB = D / 16;  // 16-wide d blocks of the output
-  // The V tiles (main loop) and the wave-merge buffers (epilogue) share LDS.
-  constexpr int kVtBytes = kWaves * kTile * kVStride * (int)sizeof(T);
-  constexpr int kCombBytes = kWaves * 16 * (D + 1) * 4 + 2 * kWaves * 16 * 4;
-  __shared__ __attribute__((aligned(16))) char smem[kVtBytes > kCombBytes ? kVtBytes : kCombBytes];
-  typedef float CombAcc[16][D + 1];
-  CombAcc* comb_acc = (CombAcc*)smem;
-  float (*comb_m)[16] = (float (*)[16])(smem + kWaves * 16 * (D + 1) * 4);
-  float (*comb_l)[16] = (float (*)[16])(smem + kWaves * 16 * (D + 1) * 4 + kWaves * 16 * 4);
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  int32_t* s_slots = (int32_t*)(smem + TG::MAIN_B);
 
   int unit, split;
   map_block(blockIdx.x, a.nsplit, unit, split);
@@ -90,16 +130,23 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_mfma_kernel(DecodeArg
   const int kvh = unit - b * a.KVH;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int n = lane & 15;  // MFMA column index (query head within the group)
-  const int j = lane >> 4;  // lane group (k-slot group)
+  const int n = lane & 15;  // MFMA column (query head within the group) / row
+  const int j = lane >> 4;  // lane group
 
-  const int64_t len = ll_load_idx(a.seq_len, b, a.len64);
+  int64_t len = ll_load_idx(a.seq_len, b, a.len64);
+  if (len > a.max_len) len = a.max_len;
   const int64_t rid = ll_load_idx(a.req_idx, b, a.req64);
   const int32_t* slot_row = a.r2t + rid * a.r2t_s;
-  const int ntiles = (int)((len + kTile - 1) / kTile);
-  const int per_split = (ntiles + a.nsplit - 1) / a.nsplit;
-  const int tile_beg = split * per_split;
-  const int tile_end = min(ntiles, tile_beg + per_split);
+  const int ntiles = (int)((len + kTT - 1) / kTT);
+  const int per = (ntiles + a.nsplit - 1) / a.nsplit;
+  const int tb = min(ntiles, split * per);
+  const int te = min(ntiles, tb + per);
+  const int64_t tok0 = (int64_t)tb * kTT;
+  const int ntok = (int)(min(len, (int64_t)te * kTT) - tok0);  // tokens of this split (may be 0)
+
+  // slot ids of the split -> LDS (tail entries point at slot 0, masked later)
+  for (int i = threadIdx.x; i < (te - tb) * kTT; i += kWaves * 64)
+    s_slots[i] = (i < ntok) ? slot_row[tok0 + i] : 0;
 
   // Q^T as the B operand: column n = head kvh*G + n, k-slots = d 32*s + 8*j + 0..7
   V8 qb[DS];
@@ -114,119 +161,104 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_mfma_kernel(DecodeArg
       }
     }
   }
+  __syncthreads();
+
+  const char* kbase = (const char*)((const T*)a.k + (int64_t)kvh * a.k_sh);
+  const char* vbase = (const char*)((const T*)a.v + (int64_t)kvh * a.v_sh);
+  const int64_t kst = a.k_st * (int64_t)sizeof(T), vst = a.v_st * (int64_t)sizeof(T);
+  char* ring = smem + wave * kRing * TG::TILE_B;
+  const int nw = (te - tb - wave + kWaves - 1) / kWaves;  // tiles of this wave (may be <= 0)
+  // DMA lane geometry: lane -> (row within an instruction's rows, LDS chunk position)
+  const int dr = lane / TG::CH, dp = lane % TG::CH;
+  auto issue = [&](int k) {
+    const int t0 = (wave + k * kWaves) * kTT;  // token offset of the tile within the split
+    char* buf = ring + (k % kRing) * TG::TILE_B;
+#pragma unroll
+    for (int i = 0; i < TG::IPT; ++i) {
+      const int r = i * TG::RPI + dr;
+      const int64_t slot = s_slots[t0 + r];
+      const int c = TG::swz(dp, r);
+      dma16(kbase + slot * kst + c * 16, buf + i * 1024);
+      dma16(vbase + slot * vst + c * 16, buf + kTT * TG::ROWB + i * 1024);
+    }
+  };
 
   f32x4 acc[DB];
 #pragma unroll
   for (int c = 0; c < DB; ++c) acc[c] = (f32x4){0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY;  // running max of head n (log2 domain)
   float l_run = 0.f;        // this lane's share of the running sum
-  T* vtile = (T*)smem + wave * kTile * kVStride;
-  const T* kbase = (const T*)a.k + (int64_t)kvh * a.k_sh;
-  const T* vbase = (const T*)a.v + (int64_t)kvh * a.v_sh;
 
-  for (int tile = tile_beg + wave; tile < tile_end; tile += kWaves) {
-    const int t0 = tile * kTile;
-    // slots of the two 16-token blocks this lane feeds as MFMA rows
-    const int tokA = t0 + n, tokB = t0 + 16 + n;
-    const bool okA = tokA < len, okB = tokB < len;
-    const int slotA = okA ? slot_row[tokA] : 0;
-    const int slotB = okB ? slot_row[tokB] : 0;
+#pragma unroll
+  for (int k = 0; k < kRing - 1; ++k)
+    if (k < nw) issue(k);
+  for (int k = 0; k < nw; ++k) {
+    if (k + kRing - 1 < nw) {
+      issue(k + kRing - 1);
+      vm_wait<2 * TG::IPT * (kRing - 1)>();
+    } else {
+      vm_wait<0>();
+    }
+    const char* kb = ring + (k % kRing) * TG::TILE_B;
+    const char* vb = kb + kTT * TG::ROWB;
+    const int t0 = (wave + k * kWaves) * kTT;
 
-    // K rows -> A operand of S^T = K . Q^T
-    V8 ka[DS], kb[DS];
-    const T* kpa = kbase + (int64_t)slotA * a.k_st + 8 * j;
-    const T* kpb = kbase + (int64_t)slotB * a.k_st + 8 * j;
+    // S^T block: rows = tokens 4j+i, column = head n
+    f32x4 s4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < DS; ++s) {
-      if (okA) ka[s] = *(const V8*)(kpa + 32 * s); else for (int e = 0; e < 8; ++e) ka[s][e] = (T)0.f;
-      if (okB) kb[s] = *(const V8*)(kpb + 32 * s); else for (int e = 0; e < 8; ++e) kb[s][e] = (T)0.f;
+      const V8 ka = *(const V8*)(kb + n * TG::ROWB + TG::swz(4 * s + j, n) * 16);
+      s4 = mfma16x16x32(ka, qb[s], s4);
     }
-    // V rows: coalesced 16 B per lane, 16 lanes per row -> LDS tile
-    constexpr int VCH = D / 8;            // 16-byte chunks per row
-    constexpr int ROWS_PER_LOAD = 64 / VCH;
-    V8 vr[kTile / ROWS_PER_LOAD];
-#pragma unroll
-    for (int i = 0; i < kTile / ROWS_PER_LOAD; ++i) {
-      const int r = i * ROWS_PER_LOAD + lane / VCH;
-      const int tok = t0 + r;
-      // r < 16 is uniform across the wave for a given i
-      const int sl = __shfl((r < 16) ? slotA : slotB, r & 15, 64);
-      if (tok < len) {
-        vr[i] = *(const V8*)(vbase + (int64_t)sl * a.v_st + (lane % VCH) * 8);
-      } else {
-        for (int e = 0; e < 8; ++e) vr[i][e] = (T)0.f;
-      }
-    }
-
-    // S^T blocks: rows = tokens 4j+i (block A) and 16+4j+i (block B), column = head n
-    f32x4 sA = {0.f, 0.f, 0.f, 0.f}, sB = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < DS; ++s) {
-      sA = mfma16x16x32(ka[s], qb[s], sA);
-      sB = mfma16x16x32(kb[s], qb[s], sB);
-    }
-
-    // store V tile (after issuing the MFMAs so the loads overlap them)
-#pragma unroll
-    for (int i = 0; i < kTile / ROWS_PER_LOAD; ++i) {
-      const int r = i * ROWS_PER_LOAD + lane / VCH;
-      *(V8*)(vtile + r * kVStride + (lane % VCH) * 8) = vr[i];
-    }
-
-    // online softmax for head n over this tile's 32 tokens
-    float x[8];
+    bool ok[4];
+    float x[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      x[i] = (t0 + 4 * j + i < len) ? sA[i] * a.scale_log2 : -INFINITY;
-      x[4 + i] = (t0 + 16 + 4 * j + i < len) ? sB[i] * a.scale_log2 : -INFINITY;
+      ok[i] = (t0 + 4 * j + i) < ntok;
+      x[i] = ok[i] ? s4[i] * a.scale_log2 : -INFINITY;
     }
-    float tmax = x[0];
-#pragma unroll
-    for (int i = 1; i < 8; ++i) tmax = fmaxf(tmax, x[i]);
+    float tmax = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const float m_new = fmaxf(m_run, tmax);  // finite: token t0 is always valid
+    const float m_new = fmaxf(m_run, tmax);  // finite: the tile's first token is valid
     const float alpha = exp2f(m_run - m_new);
-    V8 pb;
+    V4 pb;
     float psum = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < 4; ++i) {
       const float p = exp2f(x[i] - m_new);
       psum += p;
-      pb[i] = (T)p;
+      pb[i] = bits16((T)p);
     }
     l_run = l_run * alpha + psum;
     m_run = m_new;
-#pragma unroll
-    for (int c = 0; c < DB; ++c) acc[c] *= alpha;
 
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-
-    // O^T[d, head] += V^T[d, tok] . P^T[tok, head]; k-slot i of lane group j
-    // is token 4j+i (i<4) or 16+4j+i-4 (i>=4), matching the S^T layout above.
+    // O^T[d, head] += V^T[d, tok] . P^T[tok, head]; k-slot i of lane group j is token 4j+i
 #pragma unroll
     for (int c = 0; c < DB; ++c) {
-      V8 va;
-      const T* col = vtile + 16 * c + n;
+      const int d = 16 * c + n;
+      V4 va;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        va[i] = col[(4 * j + i) * kVStride];
-        va[4 + i] = col[(16 + 4 * j + i) * kVStride];
+        const int r = 4 * j + i;
+        const T v = *(const T*)(vb + r * TG::ROWB + TG::swz(d >> 3, r) * 16 + (d & 7) * 2);
+        va[i] = bits16(ok[i] ? v : (T)0.f);
       }
-      acc[c] = mfma16x16x32(va, pb, acc[c]);
+      acc[c] = mfma16x16x16(va, pb, acc[c] * alpha);
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    // this buffer is refilled by the next issue: its LDS reads must be done
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   }
 
   // total sum of head n across the 4 lane groups
   l_run += __shfl_xor(l_run, 16, 64);
   l_run += __shfl_xor(l_run, 32, 64);
 
-  // ---- merge the waves of this workgroup (the V tiles are dead from here on)
+  // ---- merge the waves of this workgroup (the tile rings are dead from here on)
+  typedef float CombAcc[16][D + 1];
+  CombAcc* comb_acc = (CombAcc*)smem;
+  float (*comb_m)[16] = (float (*)[16])(smem + kWaves * 16 * (D + 1) * 4);
+  float (*comb_l)[16] = (float (*)[16])(smem + kWaves * 16 * (D + 1) * 4 + kWaves * 16 * 4);
   __syncthreads();
   // acc[c][i] holds O^T[d = 16c + 4j + i][head n]
 #pragma unroll
@@ -240,8 +272,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_mfma_kernel(DecodeArg
   __syncthreads();
 
   const int G = a.G;
-  const bool direct = (a.nsplit == 1);
-  const int64_t pbase = ((int64_t)b * a.H + (int64_t)kvh * G) * a.nsplit + split;
+  const int64_t pbase = ((int64_t)b * a.H + (int64_t)kvh * G) * a.nsplit;
   for (int e = threadIdx.x; e < G * D; e += kWaves * 64) {
     const int g = e / D, d = e - g * D;
     float M = -INFINITY;
@@ -256,11 +287,11 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_mfma_kernel(DecodeArg
         A += comb_acc[w][g][d] * sc;
       }
     }
-    if (direct) {
+    if (a.nsplit == 1) {
       T* op = (T*)a.out + (int64_t)b * a.o_sb + (int64_t)(kvh * G + g) * a.o_sh;
       op[d] = ll_from_f32<T>(L > 0.f ? A / L : 0.f);
     } else {
-      const int64_t p = pbase + (int64_t)g * a.nsplit;
+      const int64_t p = pbase + (int64_t)g * a.nsplit + split;
       a.part_acc[p * D + d] = A;
       if (d == 0) {
         a.part_ml[p * 2] = M;
@@ -270,26 +301,57 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_mfma_kernel(DecodeArg
   }
 }
 
-// Log-sum-exp merge of the split partials: one workgroup per (sequence, head).
-template <typename T>
-__global__ __launch_bounds__(128) void decode_attn_combine_kernel(DecodeArgs a, int D) {
-  const int bh = blockIdx.x;
+// Log-sum-exp merge of the split partials: one wave per (sequence, head),
+// lane l owns d = l + 64 q. Splits are taken 16 at a time with all their
+// loads issued before any is used (one memory round trip per 16 splits).
+template <typename T, int D>
+__global__ __launch_bounds__(256) void decode_attn_combine_kernel(DecodeArgs a) {
+  constexpr int DPL = D / 64;
+  constexpr int SB = 16;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int bh = blockIdx.x * kWaves + wave;
+  if (bh >= a.B * a.H) return;
   const int b = bh / a.H, h = bh - b * a.H;
-  const int64_t p0 = (int64_t)bh * a.nsplit;
-  float M = -INFINITY;
-  for (int s = 0; s < a.nsplit; ++s) M = fmaxf(M, a.part_ml[(p0 + s) * 2]);
-  T* op = (T*)a.out + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh;
-  for (int d = threadIdx.x; d < D; d += 128) {
-    float L = 0.f, A = 0.f;
-    if (M != -INFINITY) {
-      for (int s = 0; s < a.nsplit; ++s) {
-        const float sc = exp2f(a.part_ml[(p0 + s) * 2] - M);
-        L += a.part_ml[(p0 + s) * 2 + 1] * sc;
-        A += a.part_acc[(p0 + s) * D + d] * sc;
+  const int ns = a.nsplit;
+  const int64_t p0 = (int64_t)bh * ns;  // partial rows of (b, h): p0 .. p0 + ns - 1
+  float M = -INFINITY, L = 0.f, A[DPL];
+#pragma unroll
+  for (int q = 0; q < DPL; ++q) A[q] = 0.f;
+  for (int s0 = 0; s0 < ns; s0 += SB) {
+    // lane s < SB holds (m, l) of split s0 + s; rows past the last split are
+    // clamped onto it and weighted 0
+    const int sl = min(s0 + (lane & (SB - 1)), ns - 1);
+    const float m = (lane < SB && s0 + lane < ns) ? a.part_ml[(p0 + sl) * 2] : -INFINITY;
+    const float l = a.part_ml[(p0 + sl) * 2 + 1];
+    float av[SB][DPL];
+#pragma unroll
+    for (int u = 0; u < SB; ++u)
+#pragma unroll
+      for (int q = 0; q < DPL; ++q)
+        av[u][q] = a.part_acc[(p0 + min(s0 + u, ns - 1)) * D + lane + 64 * q];
+    float mc = m;
+#pragma unroll
+    for (int off = SB / 2; off > 0; off >>= 1) mc = fmaxf(mc, __shfl_xor(mc, off, 64));
+    mc = __shfl(mc, 0, 64);
+    const float Mn = fmaxf(M, mc);
+    if (Mn != -INFINITY) {
+      const float r = exp2f(M - Mn);
+      L *= r;
+#pragma unroll
+      for (int q = 0; q < DPL; ++q) A[q] *= r;
+#pragma unroll
+      for (int u = 0; u < SB; ++u) {
+        const float w = exp2f(__shfl(m, u, 64) - Mn);  // 0 for splits past the last
+        L += __shfl(l, u, 64) * w;
+#pragma unroll
+        for (int q = 0; q < DPL; ++q) A[q] += av[u][q] * w;
       }
     }
-    op[d] = ll_from_f32<T>(L > 0.f ? A / L : 0.f);
+    M = Mn;
   }
+  T* op = (T*)a.out + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh;
+#pragma unroll
+  for (int q = 0; q < DPL; ++q) op[lane + 64 * q] = ll_from_f32<T>(L > 0.f ? A[q] / L : 0.f);
 }
 
 // ---------------------------------------------------------------- generic path
@@ -306,7 +368,8 @@ __global__ __launch_bounds__(64) void decode_attn_generic_kernel(DecodeArgs a, i
   float* qs = sh;             // [D]
   float* ps = sh + D;         // [64]
   int64_t* ss = (int64_t*)(ps + 64);  // [64]
-  const int64_t len = ll_load_idx(a.seq_len, b, a.len64);
+  int64_t len = ll_load_idx(a.seq_len, b, a.len64);
+  if (len > a.max_len) len = a.max_len;
   const int64_t rid = ll_load_idx(a.req_idx, b, a.req64);
   const T* qp = (const T*)a.q + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh;
   for (int d = lane; d < D; d += 64) qs[d] = ll_to_f32(qp[d]);
@@ -353,17 +416,24 @@ __global__ __launch_bounds__(64) void decode_attn_generic_kernel(DecodeArgs a, i
   }
 }
 
+constexpr int kMaxSplitTokens = 4096;  // LDS slot table bound per split (16 KB)
+
 int choose_nsplit(int B, int KVH, int64_t max_len) {
   const int units = B * KVH;
-  const int64_t tiles = (max_len + kTile - 1) / kTile;
-  // aim for ~2 workgroups per CU (256 CUs) while giving each wave >= 1 tile
-  int ns = (512 + units - 1) / units;
-  const int64_t max_ns = (tiles + kWaves - 1) / kWaves;
+  const int64_t tiles = (max_len + kTT - 1) / kTT;
+  // Two workgroups fit a CU (256 CUs): fill one dispatch round, never more,
+  // while giving every wave at least one tile and bounding the slot table.
+  int ns = 512 / units;
+  const int64_t max_ns = tiles / kWaves;
   if (ns > max_ns) ns = (int)max_ns;
+  const int64_t min_ns = (tiles * kTT + kMaxSplitTokens - 1) / kMaxSplitTokens;
+  if (ns < min_ns) ns = (int)min_ns;
   if (ns < 1) ns = 1;
-  if (ns > 64) ns = 64;
   return ns;
 }
+
+int64_t align256(int64_t x) { return ((x + 255) / 256) * 256; }
+
 
 }  // namespace
 
@@ -371,10 +441,10 @@ extern "C" int64_t ll_decode_attention_workspace_size(int64_t batch, int64_t q_h
                                                       int64_t kv_heads, int64_t head_dim,
                                                       int64_t max_len_in_batch) {
   const int ns = choose_nsplit((int)batch, (int)kv_heads, max_len_in_batch);
+  if (ns <= 1) return 0;
   const int64_t parts = batch * q_heads * ns;
-  int64_t bytes = ((parts * head_dim * 4 + 255) / 256) * 256;    // partial acc
-  bytes += ((parts * 2 * 4 + 255) / 256) * 256;                  // partial (m, l)
-  return bytes;
+  return align256(parts * head_dim * 4)  // partial acc
+         + align256(parts * 2 * 4);        // partial (m, l)
 }
 
 extern "C" int ll_decode_attention(const void* q, int64_t q_stride_b, int64_t q_stride_h,
@@ -394,6 +464,9 @@ extern "C" int ll_decode_attention(const void* q, int64_t q_stride_b, int64_t q_
                (long long)q_heads, (long long)kv_heads);
   LL_CHECK_ARG(head_dim > 0 && head_dim <= 256, "ll_decode_attention: head_dim %lld unsupported",
                (long long)head_dim);
+  LL_CHECK_ARG(max_len_in_batch >= 0 && max_len_in_batch <= INT32_MAX,
+               "ll_decode_attention: max_len_in_batch %lld out of range",
+               (long long)max_len_in_batch);
   if (batch == 0) return LL_OK;
   DecodeArgs a;
   a.q = q; a.q_sb = q_stride_b; a.q_sh = q_stride_h;
@@ -405,6 +478,8 @@ extern "C" int ll_decode_attention(const void* q, int64_t q_stride_b, int64_t q_
   a.out = out; a.o_sb = out_stride_b; a.o_sh = out_stride_h;
   a.B = (int)batch; a.H = (int)q_heads; a.KVH = (int)kv_heads; a.G = (int)(q_heads / kv_heads);
   a.units = a.B * a.KVH;
+  a.max_len = (int)max_len_in_batch;
+  a.slots_cap = 0;
   a.scale_log2 = sm_scale * 1.4426950408889634f;
   a.part_acc = nullptr; a.part_ml = nullptr;
 
@@ -433,28 +508,40 @@ extern "C" int ll_decode_attention(const void* q, int64_t q_stride_b, int64_t q_
     char* w = (char*)workspace;
     const int64_t parts = batch * q_heads * a.nsplit;
     a.part_acc = (float*)w;
-    w += ((parts * head_dim * 4 + 255) / 256) * 256;
+    w += align256(parts * head_dim * 4);
     a.part_ml = (float*)w;
   }
+  const int64_t tiles = (max_len_in_batch + kTT - 1) / kTT;
+  a.slots_cap = (int)((tiles + a.nsplit - 1) / a.nsplit) * kTT;
   const int groups = (a.units + 7) / 8;
   const unsigned grid = (unsigned)(groups * 8 * a.nsplit);
-  if (dtype == LL_BF16) {
-    if (head_dim == 128)
-      hipLaunchKernelGGL((decode_attn_mfma_kernel<__bf16, 128>), dim3(grid), dim3(kWaves * 64), 0, stream, a);
+  const dim3 block(kWaves * 64);
+  if (head_dim == 128) {
+    const size_t lds = TileGeom<128>::MAIN_B + (size_t)a.slots_cap * 4;
+    if (dtype == LL_BF16)
+      hipLaunchKernelGGL((decode_attn_dma_kernel<__bf16, 128>), dim3(grid), block, lds, stream, a);
     else
-      hipLaunchKernelGGL((decode_attn_mfma_kernel<__bf16, 64>), dim3(grid), dim3(kWaves * 64), 0, stream, a);
+      hipLaunchKernelGGL((decode_attn_dma_kernel<_Float16, 128>), dim3(grid), block, lds, stream, a);
   } else {
-    if (head_dim == 128)
-      hipLaunchKernelGGL((decode_attn_mfma_kernel<_Float16, 128>), dim3(grid), dim3(kWaves * 64), 0, stream, a);
+    const size_t lds = TileGeom<64>::MAIN_B + (size_t)a.slots_cap * 4;
+    if (dtype == LL_BF16)
+      hipLaunchKernelGGL((decode_attn_dma_kernel<__bf16, 64>), dim3(grid), block, lds, stream, a);
     else
-      hipLaunchKernelGGL((decode_attn_mfma_kernel<_Float16, 64>), dim3(grid), dim3(kWaves * 64), 0, stream, a);
+      hipLaunchKernelGGL((decode_attn_dma_kernel<_Float16, 64>), dim3(grid), block, lds, stream, a);
   }
   if (a.nsplit > 1) {
-    const unsigned cgrid = (unsigned)(batch * q_heads);
-    if (dtype == LL_BF16)
-      hipLaunchKernelGGL((decode_attn_combine_kernel<__bf16>), dim3(cgrid), dim3(128), 0, stream, a, (int)head_dim);
-    else
-      hipLaunchKernelGGL((decode_attn_combine_kernel<_Float16>), dim3(cgrid), dim3(128), 0, stream, a, (int)head_dim);
+    const dim3 cgrid((unsigned)((batch * q_heads + kWaves - 1) / kWaves));
+    if (head_dim == 128) {
+      if (dtype == LL_BF16)
+        hipLaunchKernelGGL((decode_attn_combine_kernel<__bf16, 128>), cgrid, block, 0, stream, a);
+      else
+        hipLaunchKernelGGL((decode_attn_combine_kernel<_Float16, 128>), cgrid, block, 0, stream, a);
+    } else {
+      if (dtype == LL_BF16)
+        hipLaunchKernelGGL((decode_attn_combine_kernel<__bf16, 64>), cgrid, block, 0, stream, a);
+      else
+        hipLaunchKernelGGL((decode_attn_combine_kernel<_Float16, 64>), cgrid, block, 0, stream, a);
+    }
   }
   LL_RETURN_LAUNCH();
 }
