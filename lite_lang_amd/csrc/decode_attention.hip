@@ -133,9 +133,23 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
   const int n = lane & 15;  // MFMA column (query head within the group) / row
   const int j = lane >> 4;  // lane group
 
-  int64_t len = ll_load_idx(a.seq_len, b, a.len64);
-  if (len > a.max_len) len = a.max_len;
-  const int64_t rid = ll_load_idx(a.req_idx, b, a.req64);
+  // Q^T as the B operand: column n = head kvh*G + n, k-slots = d 32*s + 8*j + 0..7.
+  // Loaded first (it does not depend on the lengths); columns n >= G read a
+  // valid head and are zeroed once the loads have landed.
+  V8 qb[DS];
+  {
+    const int hq = kvh * a.G + min(n, a.G - 1);
+    const T* qp = (const T*)a.q + (int64_t)b * a.q_sb + (int64_t)hq * a.q_sh;
+#pragma unroll
+    for (int s = 0; s < DS; ++s) qb[s] = *(const V8*)(qp + 32 * s + 8 * j);
+  }
+  // sequence length and request row, both loads in flight together (the low
+  // word of an int64 entry is the value: lengths and rows are below 2^31)
+  const int32_t len32 = ((const int32_t*)a.seq_len)[a.len64 ? 2 * b : b];
+  const int32_t rid32 = ((const int32_t*)a.req_idx)[a.req64 ? 2 * b : b];
+  asm volatile("" ::"s"(len32), "s"(rid32));  // keeps both loads here, not sunk apart
+  int64_t len = len32 > a.max_len ? a.max_len : len32;
+  const int64_t rid = rid32;
   const int32_t* slot_row = a.r2t + rid * a.r2t_s;
   const int ntiles = (int)((len + kTT - 1) / kTT);
   const int per = (ntiles + a.nsplit - 1) / a.nsplit;
@@ -144,22 +158,28 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
   const int64_t tok0 = (int64_t)tb * kTT;
   const int ntok = (int)(min(len, (int64_t)te * kTT) - tok0);  // tokens of this split (may be 0)
 
-  // slot ids of the split -> LDS (tail entries point at slot 0, masked later)
-  for (int i = threadIdx.x; i < (te - tb) * kTT; i += kWaves * 64)
-    s_slots[i] = (i < ntok) ? slot_row[tok0 + i] : 0;
-
-  // Q^T as the B operand: column n = head kvh*G + n, k-slots = d 32*s + 8*j + 0..7
-  V8 qb[DS];
-  {
-    const T* qp = (const T*)a.q + (int64_t)b * a.q_sb + (int64_t)(kvh * a.G + n) * a.q_sh;
+  // slot ids of the split -> LDS (tail entries point at slot 0, masked later);
+  // four loads per thread in flight per round
+  const int nslots = (te - tb) * kTT;
+  for (int i0 = 0; i0 < nslots; i0 += 4 * kWaves * 64) {
+    int32_t v[4];
 #pragma unroll
-    for (int s = 0; s < DS; ++s) {
-      if (n < a.G) {
-        qb[s] = *(const V8*)(qp + 32 * s + 8 * j);
-      } else {
-        for (int e = 0; e < 8; ++e) qb[s][e] = (T)0.f;
-      }
+    for (int u = 0; u < 4; ++u) {
+      const int i = i0 + u * kWaves * 64 + threadIdx.x;
+      const int64_t t = min(tok0 + i, len > 0 ? len - 1 : (int64_t)0);  // always a valid entry
+      const int32_t sl = slot_row[t];
+      v[u] = (i < ntok) ? sl : 0;
     }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = i0 + u * kWaves * 64 + threadIdx.x;
+      if (i < nslots) s_slots[i] = v[u];
+    }
+  }
+  if (n >= a.G) {
+#pragma unroll
+    for (int s = 0; s < DS; ++s)
+      for (int e = 0; e < 8; ++e) qb[s][e] = (T)0.f;
   }
   __syncthreads();
 
@@ -320,15 +340,18 @@ __global__ __launch_bounds__(256) void decode_attn_combine_kernel(DecodeArgs a) 
   for (int s0 = 0; s0 < ns; s0 += SB) {
     // lane s < SB holds (m, l) of split s0 + s; rows past the last split are
     // clamped onto it and weighted 0
-    const int sl = min(s0 + (lane & (SB - 1)), ns - 1);
-    const float m = (lane < SB && s0 + lane < ns) ? a.part_ml[(p0 + sl) * 2] : -INFINITY;
-    const float l = a.part_ml[(p0 + sl) * 2 + 1];
     float av[SB][DPL];
 #pragma unroll
     for (int u = 0; u < SB; ++u)
 #pragma unroll
       for (int q = 0; q < DPL; ++q)
         av[u][q] = a.part_acc[(p0 + min(s0 + u, ns - 1)) * D + lane + 64 * q];
+    const int sl = min(s0 + (lane & (SB - 1)), ns - 1);
+    const float m0 = a.part_ml[(p0 + sl) * 2];
+    const float l = a.part_ml[(p0 + sl) * 2 + 1];
+    // every load of this chunk is issued before the first use of any of them
+    __builtin_amdgcn_sched_barrier(0);
+    const float m = (lane < SB && s0 + lane < ns) ? m0 : -INFINITY;
     float mc = m;
 #pragma unroll
     for (int off = SB / 2; off > 0; off >>= 1) mc = fmaxf(mc, __shfl_xor(mc, off, 64));
