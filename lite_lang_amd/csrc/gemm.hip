@@ -62,6 +62,11 @@ __device__ __forceinline__ void lds_barrier() {
 __device__ __forceinline__ void dma16(const void* g, void* lds) {
   __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0);
 }
+// Same, marked non-temporal: used for the weight stream, read once, so that it
+// does not evict the small, reused activation tensor from L2.
+__device__ __forceinline__ void dma16_stream(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 2 /* nt */);
+}
 
 // (1) Wide N: weight rows streamed through LDS. A workgroup (4 waves) owns 64
 // rows; every stage DMA's (global_load_lds_dwordx4, no VGPR staging) a
@@ -87,7 +92,15 @@ __device__ __forceinline__ void wait_stage(int later) {
   vm_wait<0>();
 }
 
-template <typename T, int MB, int NST>
+// PK: W is the pre-packed layout of ll_gemm_pack (every stage of every row
+// tile one contiguous, already swizzled 16 KB block, blocks ordered chunk-
+// major), so concurrent workgroups stream neighbouring blocks.
+// EPI 1 (with PK and the gate/up tile layout of ll_gemm_pack_gate_up, one
+// split): tile rows 0..31 are gate channels 32t.., rows 32..63 the matching up
+// channels; the epilogue writes Y[m, c] = T(T(up) * T(silu(T(gate)))) for the
+// 32 channels of the tile (N = 2 * channels), the rounding sequence of
+// ll_silu_and_mul_splitk applied to the same fp32 sums.
+template <typename T, int MB, int NST, bool PK, int EPI = 0>
 __global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, int64_t ldx,
                                                        const T* __restrict__ W, int64_t ldw,
                                                        const T* __restrict__ bias,
@@ -122,9 +135,15 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, 
 #pragma unroll
     for (int q = 0; q < W_PER_WAVE; ++q) {
       const int ii = wave * W_PER_WAVE + q;
-      const int r = ii * RPI + lr_in;
-      const T* g = W + (int64_t)min(row0 + r, N - 1) * ldw + k0 + (p ^ (r & 15)) * 8;
-      dma16(g, base + ii * 1024);
+      if constexpr (PK) {
+        const char* g = (const char*)W + ((int64_t)(k0 / KC) * gridDim.x + blockIdx.x) * (TR * ROWB) +
+                        ii * 1024 + lane * 16;
+        dma16_stream(g, base + ii * 1024);
+      } else {
+        const int r = ii * RPI + lr_in;
+        const T* g = W + (int64_t)min(row0 + r, N - 1) * ldw + k0 + (p ^ (r & 15)) * 8;
+        dma16_stream(g, base + ii * 1024);
+      }
     }
 #pragma unroll
     for (int q = 0; q < X_PER_WAVE; ++q) {
@@ -160,6 +179,36 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, 
     }
   }
   // acc[t][i] = Y[token 16t + n][channel row0 + 16*wave + 4j + i]
+  if constexpr (EPI == 1) {
+    // waves 2, 3 (up rows) hand their sums to waves 0, 1 (gate rows) through LDS
+    float* ub = (float*)smem;  // [32 channels][16 * MB tokens]
+    lds_barrier();             // every wave is done reading the last stage
+    if (wave >= 2) {
+#pragma unroll
+      for (int t = 0; t < MB; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ub[(16 * (wave - 2) + 4 * j + i) * (16 * MB) + 16 * t + n] = acc[t][i];
+    }
+    lds_barrier();
+    if (wave < 2) {
+      const int I = N / 2;
+      const int c0 = blockIdx.x * 32 + 16 * wave + 4 * j;
+#pragma unroll
+      for (int t = 0; t < MB; ++t) {
+        const int tok = 16 * t + n;
+        if (tok >= M) continue;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (c0 + i >= I) continue;
+          const float g = ll_to_f32(ll_from_f32<T>(acc[t][i]));
+          const float u = ll_to_f32(ll_from_f32<T>(ub[(16 * wave + 4 * j + i) * (16 * MB) + 16 * t + n]));
+          const T sv = ll_from_f32<T>(g / (1.0f + __expf(-g)));
+          Y[(int64_t)tok * ldy + c0 + i] = ll_from_f32<T>(u * ll_to_f32(sv));
+        }
+      }
+    }
+    return;
+  }
   const int ch = row0 + wave * 16 + 4 * j;
 #pragma unroll
   for (int t = 0; t < MB; ++t) {
@@ -178,6 +227,35 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, 
         yp[i] = ll_from_f32<T>(acc[t][i] + (bias != nullptr ? ll_to_f32(bias[ch + i]) : 0.f));
     }
   }
+}
+
+// Packed weight layout for the DMA kernel: block (kc, t) = rows 64t..64t+63,
+// columns 128kc..128kc+127, stored as the 16 KB LDS image of that stage
+// (unit u = 64 * ii + lane holds row 4 ii + lane / 16, 16 B chunk
+// (lane % 16) ^ (row & 15)); blocks ordered kc-major; rows >= N are zero.
+// gu_half > 0: W is [gate; up] with gu_half rows each, and tile t takes gate
+// rows 32t..32t+31 as its rows 0..31 and the same up rows as its rows 32..63.
+__global__ __launch_bounds__(256) void gemm_pack_kernel(const u32x4* __restrict__ W, int64_t ldw16,
+                                                        u32x4* __restrict__ out, int N, int tiles,
+                                                        int64_t units, int gu_half) {
+  const int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (u >= units) return;
+  const int64_t blk = u >> 10;
+  const int within = (int)(u & 1023);
+  const int ii = within >> 6, lane = within & 63;
+  const int kc = (int)(blk / tiles), t = (int)(blk - (int64_t)kc * tiles);
+  const int r = ii * 4 + (lane >> 4);
+  const int c = (lane & 15) ^ (r & 15);
+  int row = t * kDmaTR + r;
+  bool ok = row < N;
+  if (gu_half > 0) {
+    const int ch = t * 32 + (r & 31);
+    ok = ch < gu_half;
+    row = (r < 32) ? ch : gu_half + ch;
+  }
+  u32x4 v = {0u, 0u, 0u, 0u};
+  if (ok) v = W[(int64_t)row * ldw16 + (int64_t)kc * (kDmaKC / 8) + c];
+  out[u] = v;
 }
 
 // (2) Narrow N: direct operand loads. A workgroup owns 16*WR rows; its KW
@@ -445,6 +523,7 @@ struct SkinnyPlan {
   int tiles;   // row tiles
   int nst;     // LDS stage buffers of the DMA kernel
   int rotate;  // DMA kernel: rotate the k-chunk order per workgroup
+  bool packed; // DMA kernel: W in the ll_gemm_pack layout
 };
 
 constexpr int kDirWR = 2, kDirKW = 4, kDirU = 2;
@@ -453,6 +532,7 @@ SkinnyPlan plan_skinny(int64_t N, int64_t K) {
   SkinnyPlan p;
   p.nst = 2;
   p.rotate = 0;
+  p.packed = false;
   const int ksteps = (int)((K + 31) / 32);
   p.dma = (K % kDmaKC == 0);
   if (p.dma) {
@@ -490,15 +570,15 @@ void launch_skinny_mb(const SkinnyPlan& p, const T* X, int64_t ldx, const T* W, 
   const dim3 grid((unsigned)p.tiles, (unsigned)p.splits);
   if (p.dma) {
     const size_t lds = (size_t)p.nst * (kDmaTR + 16 * MB) * kDmaKC * 2;
-    if (p.nst == 4)
-      hipLaunchKernelGGL((gemm_dma_kernel<T, MB, 4>), grid, dim3(256), lds, stream, X, ldx, W, ldw,
-                         bias, Y, ldy, part, M, N, K, p.ksps, p.rotate);
-    else if (p.nst == 3)
-      hipLaunchKernelGGL((gemm_dma_kernel<T, MB, 3>), grid, dim3(256), lds, stream, X, ldx, W, ldw,
-                         bias, Y, ldy, part, M, N, K, p.ksps, p.rotate);
-    else
-      hipLaunchKernelGGL((gemm_dma_kernel<T, MB, 2>), grid, dim3(256), lds, stream, X, ldx, W, ldw,
-                         bias, Y, ldy, part, M, N, K, p.ksps, p.rotate);
+#define LL_DMA_LAUNCH(S, PKD)                                                                   \
+  hipLaunchKernelGGL((gemm_dma_kernel<T, MB, S, PKD>), grid, dim3(256), lds, stream, X, ldx, W, \
+                     ldw, bias, Y, ldy, part, M, N, K, p.ksps, p.rotate)
+    if (p.packed) {
+      if (p.nst == 3) LL_DMA_LAUNCH(3, true); else LL_DMA_LAUNCH(2, true);
+    } else {
+      if (p.nst == 3) LL_DMA_LAUNCH(3, false); else LL_DMA_LAUNCH(2, false);
+    }
+#undef LL_DMA_LAUNCH
   } else {
     hipLaunchKernelGGL((gemm_direct_kernel<T, MB, kDirWR, kDirKW, kDirU>), grid,
                        dim3(64 * kDirKW), 0, stream, X, ldx, W, ldw, bias, Y, ldy, part, M, N, K,
@@ -557,19 +637,26 @@ extern "C" int ll_gemm_splitk_count(int64_t M, int64_t N, int64_t K) {
   return plan_skinny(N, K).splits;
 }
 
-extern "C" int ll_gemm_splitk(const void* X, int64_t ldx, const void* W, int64_t ldw, int64_t M,
-                              int64_t N, int64_t K, int dtype, float* part, int64_t part_bytes,
-                              hipStream_t stream) {
-  LL_CHECK_ARG(X && W && part, "ll_gemm_splitk: null pointer");
-  LL_CHECK_ARG(M > 0 && M <= 64 && N > 0 && K > 0, "ll_gemm_splitk: needs 0 < M <= 64 (M=%lld)",
+namespace {
+
+int gemm_splitk_impl(const char* name, const void* X, int64_t ldx, const void* W, int64_t ldw,
+                     int64_t M, int64_t N, int64_t K, int dtype, float* part, int64_t part_bytes,
+                     bool packed, hipStream_t stream) {
+  LL_CHECK_ARG(X && W && part, "%s: null pointer", name);
+  LL_CHECK_ARG(M > 0 && M <= 64 && N > 0 && K > 0, "%s: needs 0 < M <= 64 (M=%lld)", name,
                (long long)M);
-  LL_CHECK_ARG(dtype == LL_BF16 || dtype == LL_F16, "ll_gemm_splitk: bf16/fp16 only");
+  LL_CHECK_ARG(dtype == LL_BF16 || dtype == LL_F16, "%s: bf16/fp16 only", name);
   LL_CHECK_ARG(K % 8 == 0 && ldx % 8 == 0 && ldw % 8 == 0,
-               "ll_gemm_splitk: K and leading dims must be multiples of 8");
-  LL_CHECK_ARG((((uintptr_t)X | (uintptr_t)W) % 16) == 0, "ll_gemm_splitk: X and W must be 16 B aligned");
-  const SkinnyPlan p = plan_skinny(N, K);
+               "%s: K and leading dims must be multiples of 8", name);
+  LL_CHECK_ARG((((uintptr_t)X | (uintptr_t)W) % 16) == 0, "%s: X and W must be 16 B aligned", name);
+  SkinnyPlan p = plan_skinny(N, K);
+  if (packed) {
+    LL_CHECK_ARG(p.dma, "%s: packed weights need K %% %d == 0", name, kDmaKC);
+    p.packed = true;
+    p.rotate = 0;  // neighbouring workgroups stream neighbouring blocks
+  }
   LL_CHECK_ARG(part_bytes >= (int64_t)p.splits * M * N * 4,
-               "ll_gemm_splitk: partial buffer too small (need %lld bytes)",
+               "%s: partial buffer too small (need %lld bytes)", name,
                (long long)((int64_t)p.splits * M * N * 4));
   if (dtype == LL_BF16)
     launch_skinny<__bf16>(p, (const __bf16*)X, ldx, (const __bf16*)W, ldw, nullptr, nullptr, 0,
@@ -577,6 +664,144 @@ extern "C" int ll_gemm_splitk(const void* X, int64_t ldx, const void* W, int64_t
   else
     launch_skinny<_Float16>(p, (const _Float16*)X, ldx, (const _Float16*)W, ldw, nullptr, nullptr,
                             0, part, (int)M, (int)N, (int)K, stream);
+  LL_RETURN_LAUNCH();
+}
+
+}  // namespace
+
+extern "C" int ll_gemm_splitk(const void* X, int64_t ldx, const void* W, int64_t ldw, int64_t M,
+                              int64_t N, int64_t K, int dtype, float* part, int64_t part_bytes,
+                              hipStream_t stream) {
+  return gemm_splitk_impl("ll_gemm_splitk", X, ldx, W, ldw, M, N, K, dtype, part, part_bytes,
+                          false, stream);
+}
+
+extern "C" int64_t ll_gemm_packed_bytes(int64_t N, int64_t K) {
+  if (N <= 0 || K <= 0 || K % kDmaKC != 0) return 0;
+  return ll_cdiv(N, kDmaTR) * kDmaTR * K * 2;
+}
+
+extern "C" int ll_gemm_pack(const void* W, int64_t ldw, int64_t N, int64_t K, int dtype, void* Wp,
+                            int64_t wp_bytes, hipStream_t stream) {
+  LL_CHECK_ARG(W && Wp, "ll_gemm_pack: null pointer");
+  LL_CHECK_ARG(dtype == LL_BF16 || dtype == LL_F16, "ll_gemm_pack: bf16/fp16 only");
+  LL_CHECK_ARG(N > 0 && K > 0 && K % kDmaKC == 0, "ll_gemm_pack: needs K %% %d == 0 (K=%lld)",
+               kDmaKC, (long long)K);
+  LL_CHECK_ARG(ldw >= K && ldw % 8 == 0 && ((uintptr_t)W | (uintptr_t)Wp) % 16 == 0,
+               "ll_gemm_pack: W rows must be 16 B aligned");
+  const int64_t bytes = ll_gemm_packed_bytes(N, K);
+  LL_CHECK_ARG(wp_bytes >= bytes, "ll_gemm_pack: output too small (need %lld bytes)",
+               (long long)bytes);
+  const int64_t units = bytes / 16;
+  const int tiles = (int)ll_cdiv(N, kDmaTR);
+  hipLaunchKernelGGL(gemm_pack_kernel, dim3((unsigned)ll_cdiv(units, 256)), dim3(256), 0, stream,
+                     (const u32x4*)W, ldw / 8, (u32x4*)Wp, (int)N, tiles, units, 0);
+  LL_RETURN_LAUNCH();
+}
+
+extern "C" int64_t ll_gemm_packed_gate_up_bytes(int64_t I, int64_t K) {
+  if (I <= 0 || K <= 0 || K % kDmaKC != 0) return 0;
+  return ll_cdiv(I, 32) * kDmaTR * K * 2;
+}
+
+extern "C" int ll_gemm_pack_gate_up(const void* W, int64_t ldw, int64_t I, int64_t K, int dtype,
+                                    void* Wp, int64_t wp_bytes, hipStream_t stream) {
+  LL_CHECK_ARG(W && Wp, "ll_gemm_pack_gate_up: null pointer");
+  LL_CHECK_ARG(dtype == LL_BF16 || dtype == LL_F16, "ll_gemm_pack_gate_up: bf16/fp16 only");
+  LL_CHECK_ARG(I > 0 && K > 0 && K % kDmaKC == 0,
+               "ll_gemm_pack_gate_up: needs K %% %d == 0 (K=%lld)", kDmaKC, (long long)K);
+  LL_CHECK_ARG(ldw >= K && ldw % 8 == 0 && ((uintptr_t)W | (uintptr_t)Wp) % 16 == 0,
+               "ll_gemm_pack_gate_up: W rows must be 16 B aligned");
+  const int64_t bytes = ll_gemm_packed_gate_up_bytes(I, K);
+  LL_CHECK_ARG(wp_bytes >= bytes, "ll_gemm_pack_gate_up: output too small (need %lld bytes)",
+               (long long)bytes);
+  const int64_t units = bytes / 16;
+  const int tiles = (int)ll_cdiv(I, 32);
+  hipLaunchKernelGGL(gemm_pack_kernel, dim3((unsigned)ll_cdiv(units, 256)), dim3(256), 0, stream,
+                     (const u32x4*)W, ldw / 8, (u32x4*)Wp, (int)(2 * I), tiles, units, (int)I);
+  LL_RETURN_LAUNCH();
+}
+
+extern "C" int ll_gemm_gate_up_silu_packed(const void* X, int64_t ldx, const void* Wp, int64_t M,
+                                           int64_t I, int64_t K, int dtype, void* act,
+                                           int64_t ld_act, hipStream_t stream) {
+  LL_CHECK_ARG(X && Wp && act, "ll_gemm_gate_up_silu_packed: null pointer");
+  LL_CHECK_ARG(M > 0 && M <= 64 && I > 0 && K > 0 && K % kDmaKC == 0,
+               "ll_gemm_gate_up_silu_packed: needs 0 < M <= 64 and K %% %d == 0", kDmaKC);
+  LL_CHECK_ARG(dtype == LL_BF16 || dtype == LL_F16, "ll_gemm_gate_up_silu_packed: bf16/fp16 only");
+  LL_CHECK_ARG(ldx % 8 == 0 && (((uintptr_t)X | (uintptr_t)Wp) % 16) == 0,
+               "ll_gemm_gate_up_silu_packed: X rows must be 16 B aligned");
+  const int tiles = (int)ll_cdiv(I, 32);
+  const int nst = tiles <= 256 ? 3 : 2;
+  const int ksps = (int)(K / 32);
+  auto run = [&](auto tag) {
+    typedef decltype(tag) T;
+    const T* x = (const T*)X;
+    const T* w = (const T*)Wp;
+    T* y = (T*)act;
+    const dim3 grid((unsigned)tiles, 1);
+#define LL_GU(MB_)                                                                              \
+  do {                                                                                          \
+    const size_t lds = (size_t)nst * (kDmaTR + 16 * MB_) * kDmaKC * 2;                          \
+    if (nst == 3)                                                                               \
+      hipLaunchKernelGGL((gemm_dma_kernel<T, MB_, 3, true, 1>), grid, dim3(256), lds, stream, x, \
+                         ldx, w, K, nullptr, y, ld_act, nullptr, (int)M, (int)(2 * I), (int)K,  \
+                         ksps, 0);                                                              \
+    else                                                                                        \
+      hipLaunchKernelGGL((gemm_dma_kernel<T, MB_, 2, true, 1>), grid, dim3(256), lds, stream, x, \
+                         ldx, w, K, nullptr, y, ld_act, nullptr, (int)M, (int)(2 * I), (int)K,  \
+                         ksps, 0);                                                              \
+  } while (0)
+    switch ((M + 15) / 16) {
+      case 1: LL_GU(1); break;
+      case 2: LL_GU(2); break;
+      case 3: LL_GU(3); break;
+      default: LL_GU(4); break;
+    }
+#undef LL_GU
+  };
+  if (dtype == LL_BF16) run(__bf16{}); else run(_Float16{});
+  LL_RETURN_LAUNCH();
+}
+
+extern "C" int ll_gemm_splitk_packed(const void* X, int64_t ldx, const void* Wp, int64_t M,
+                                     int64_t N, int64_t K, int dtype, float* part,
+                                     int64_t part_bytes, hipStream_t stream) {
+  return gemm_splitk_impl("ll_gemm_splitk_packed", X, ldx, Wp, K, M, N, K, dtype, part,
+                          part_bytes, true, stream);
+}
+
+extern "C" int ll_gemm_packed(const void* X, int64_t ldx, const void* Wp, const void* bias, void* Y,
+                              int64_t ldy, int64_t M, int64_t N, int64_t K, int dtype,
+                              void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  LL_CHECK_ARG(X && Wp && Y, "ll_gemm_packed: null pointer");
+  LL_CHECK_ARG(M > 0 && M <= 64 && N > 0 && K > 0 && K % kDmaKC == 0,
+               "ll_gemm_packed: needs 0 < M <= 64 and K %% %d == 0", kDmaKC);
+  LL_CHECK_ARG(dtype == LL_BF16 || dtype == LL_F16, "ll_gemm_packed: bf16/fp16 only");
+  LL_CHECK_ARG(ldx % 8 == 0 && (((uintptr_t)X | (uintptr_t)Wp) % 16) == 0,
+               "ll_gemm_packed: X rows must be 16 B aligned");
+  SkinnyPlan p = plan_skinny(N, K);
+  p.packed = true;
+  p.rotate = 0;
+  float* part = nullptr;
+  if (p.splits > 1) {
+    const int64_t need = (int64_t)p.splits * M * N * 4;
+    LL_CHECK_ARG(workspace != nullptr && workspace_bytes >= need,
+                 "ll_gemm_packed: workspace too small (need %lld bytes)", (long long)need);
+    part = (float*)workspace;
+  }
+  auto run = [&](auto tag) {
+    typedef decltype(tag) T;
+    launch_skinny<T>(p, (const T*)X, ldx, (const T*)Wp, K, (const T*)bias, (T*)Y, ldy, part, (int)M,
+                     (int)N, (int)K, stream);
+    if (p.splits > 1) {
+      const int64_t total = M * N;
+      hipLaunchKernelGGL((splitk_reduce_kernel<T>), dim3((unsigned)((total + 255) / 256)),
+                         dim3(256), 0, stream, part, p.splits, (const T*)bias, (T*)Y, ldy, (int)M,
+                         (int)N);
+    }
+  };
+  if (dtype == LL_BF16) run(__bf16{}); else run(_Float16{});
   LL_RETURN_LAUNCH();
 }
 

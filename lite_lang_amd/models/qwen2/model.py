@@ -101,10 +101,11 @@ class Qwen2Model:
         [B] int32 or int64, rids/slots [B] int32; max_len bounds seq_len.
         Writes the next tokens [B] int64 into `out` (may alias ids).
 
-        bf16/fp16 with B <= 64 runs the fused split-K layer: every projection
-        leaves fp32 partials that the next kernel finishes (RoPE + KV scatter,
-        residual + RMSNorm, SiLU_and_Mul), 9 launches per layer; other cases
-        run the generic layer."""
+        bf16/fp16 with B <= 64 runs the fused split-K layer: the projections
+        leave fp32 partials that the next kernel finishes (RoPE + KV scatter,
+        residual + RMSNorm) and the gate/up projection applies SiLU_and_Mul in
+        its own epilogue, 8 launches per layer; other cases run the generic
+        layer."""
         cfg = self.cfg
         H, KVH, D = cfg.num_heads, cfg.num_key_value_heads, cfg.head_dim
         B = ids.shape[0]
@@ -126,22 +127,34 @@ class Qwen2Model:
         act = torch.empty((B, cfg.intermediate_size), dtype=dt, device=dev)
         x = ops.rmsnorm(h, w.layers[0]["ln1"], cfg.rms_norm_eps)
         nl = len(w.layers)
-        for li, lw in enumerate(w.layers):
-            s = ops.gemm_splitk(x, lw["wqkv"], part)
+
+        def proj(xin, lw, pk, name):
+            if pk.get(name) is not None:
+                return ops.gemm_splitk_packed(xin, pk[name], part)
+            return ops.gemm_splitk(xin, lw[name], part)
+
+        for li, (lw, pk) in enumerate(zip(w.layers, w.packed)):
+            s = proj(x, lw, pk, "wqkv")
             ops.rope_kv_scatter_splitk(part, s, lw["bqkv"], q, H, KVH, D, positions, self.cos,
                                        self.sin, slots, pool[li])
             ops.decode_attention(q.view(B, H, D), r2t, rids, seq_len, max_len, pool[li, :, :KVH],
                                  pool[li, :, KVH:], attn)
-            s = ops.gemm_splitk(attn.view(B, H * D), lw["wo"], part)
+            s = proj(attn.view(B, H * D), lw, pk, "wo")
             x2 = ops.add_rmsnorm_splitk(h, part, s, lw["ln2"], cfg.rms_norm_eps)
-            s = ops.gemm_splitk(x2, lw["wgu"], part)
-            ops.silu_and_mul_splitk(part, s, act)
-            s = ops.gemm_splitk(act, lw["wdown"], part)
+            if pk.get("wgu_silu") is not None:
+                ops.gate_up_silu(x2, pk["wgu_silu"], out=act)
+            else:
+                s = proj(x2, lw, pk, "wgu")
+                ops.silu_and_mul_splitk(part, s, act)
+            s = proj(act, lw, pk, "wdown")
             if li + 1 < nl:
                 x = ops.add_rmsnorm_splitk(h, part, s, w.layers[li + 1]["ln1"], cfg.rms_norm_eps)
             else:
                 x = ops.add_rmsnorm_splitk(h, part, s, w.norm, cfg.final_norm_eps)
-        logits = ops.gemm(x, w.lm_head)
+        if w.lm_head_p is not None:
+            logits = ops.gemm_packed(x, w.lm_head_p)
+        else:
+            logits = ops.gemm(x, w.lm_head)
         self.last_logits = logits
         return ops.argmax(logits, out=out)
 

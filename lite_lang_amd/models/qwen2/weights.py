@@ -151,7 +151,7 @@ def load_state_dict(model_path: str):
 class DeviceWeights:
     """Packed device copy of a state dict (layout in the module docstring)."""
 
-    def __init__(self, cfg: Qwen2Config, sd: dict, dtype: torch.dtype, device):
+    def __init__(self, cfg: Qwen2Config, sd: dict, dtype: torch.dtype, device, pack: bool = True):
         def dev(t):
             return t.to(device=device, dtype=dtype).contiguous()
 
@@ -175,6 +175,18 @@ class DeviceWeights:
             lw["ln1"] = dev(sd[p + "input_layernorm.weight"])
             lw["ln2"] = dev(sd[p + "post_attention_layernorm.weight"])
             self.layers.append(lw)
+        # Decode-path projections also held in the weight-streaming kernel's
+        # packed layout (one more copy of those weights; prefill keeps using
+        # the [N, K] tensors). None where the layout does not apply.
+        self.packed = [{} for _ in self.layers]
+        self.lm_head_p = None
+        if pack and dtype in (torch.bfloat16, torch.float16) and torch.device(device).type == "cuda":
+            from lite_lang_amd import ops
+            for lw, pk in zip(self.layers, self.packed):
+                for name in ("wqkv", "wo", "wdown"):
+                    pk[name] = ops.pack_weight(lw[name])
+                pk["wgu_silu"] = ops.pack_gate_up(lw["wgu"])
+            self.lm_head_p = ops.pack_weight(self.lm_head)
 
     def nbytes_streamed_per_decode(self) -> int:
         """Weight bytes one decode forward reads (embedding rows excluded)."""

@@ -284,6 +284,105 @@ def gemm_splitk(x, w, part):
     return s
 
 
+class PackedWeight:
+    """A [N, K] nn.Linear weight in the weight-streaming kernel's packed layout
+    (ll_gemm_pack); keeps the logical shape next to the packed bytes."""
+
+    def __init__(self, w):
+        _dev(w)
+        N, K = w.shape
+        assert w.stride(1) == 1 and w.dtype in (torch.bfloat16, torch.float16)
+        nbytes = _L.ll_gemm_packed_bytes(N, K)
+        if nbytes <= 0:
+            raise _lib.LiteLangError(f"ll_gemm_pack: K={K} is not a multiple of 128")
+        self.shape, self.dtype, self.device = (N, K), w.dtype, w.device
+        self.data = torch.empty(nbytes, dtype=torch.uint8, device=w.device)
+        rc = _L.ll_gemm_pack(w.data_ptr(), w.stride(0), N, K, dtype_code(w), self.data.data_ptr(),
+                             nbytes, _stream(w))
+        _lib.check(rc, "ll_gemm_pack")
+
+
+class PackedGateUp:
+    """[gate; up] weight ([2I, K]) packed for the fused gate/up + SiLU_and_Mul GEMM."""
+
+    def __init__(self, w):
+        _dev(w)
+        N2, K = w.shape
+        assert N2 % 2 == 0 and w.stride(1) == 1 and w.dtype in (torch.bfloat16, torch.float16)
+        I = N2 // 2
+        nbytes = _L.ll_gemm_packed_gate_up_bytes(I, K)
+        if nbytes <= 0:
+            raise _lib.LiteLangError(f"ll_gemm_pack_gate_up: K={K} is not a multiple of 128")
+        self.shape, self.inter, self.dtype, self.device = (N2, K), I, w.dtype, w.device
+        self.data = torch.empty(nbytes, dtype=torch.uint8, device=w.device)
+        rc = _L.ll_gemm_pack_gate_up(w.data_ptr(), w.stride(0), I, K, dtype_code(w),
+                                     self.data.data_ptr(), nbytes, _stream(w))
+        _lib.check(rc, "ll_gemm_pack_gate_up")
+
+
+def pack_gate_up(w):
+    """Packed [gate; up] weight for gate_up_silu, or None when K % 128 != 0."""
+    if w.dtype not in (torch.bfloat16, torch.float16) or w.shape[1] % 128 != 0:
+        return None
+    return PackedGateUp(w)
+
+
+def gate_up_silu(x, wp: PackedGateUp, out=None):
+    """silu(x @ gate^T) * (x @ up^T) for M <= 64, rounded as silu_and_mul_splitk."""
+    _dev(x, out)
+    M, K = x.shape
+    assert wp.shape[1] == K and x.stride(1) == 1 and x.dtype == wp.dtype
+    if out is None:
+        out = torch.empty((M, wp.inter), dtype=x.dtype, device=x.device)
+    assert out.shape == (M, wp.inter) and out.stride(1) == 1
+    rc = _L.ll_gemm_gate_up_silu_packed(x.data_ptr(), x.stride(0), wp.data.data_ptr(), M, wp.inter,
+                                        K, dtype_code(x), out.data_ptr(), out.stride(0), _stream(x))
+    _lib.check(rc, "ll_gemm_gate_up_silu_packed")
+    return out
+
+
+def pack_weight(w):
+    """Packed copy of w for gemm_splitk / gemm with M <= 64, or None when K % 128 != 0."""
+    if w.dtype not in (torch.bfloat16, torch.float16) or w.shape[1] % 128 != 0:
+        return None
+    return PackedWeight(w)
+
+
+def gemm_splitk_packed(x, wp: PackedWeight, part):
+    """gemm_splitk with a packed weight; returns the split count."""
+    _dev(x, part)
+    M, K = x.shape
+    N = wp.shape[0]
+    assert wp.shape[1] == K and x.stride(1) == 1 and x.dtype == wp.dtype
+    assert part.dtype == torch.float32
+    s = _L.ll_gemm_splitk_count(M, N, K)
+    rc = _L.ll_gemm_splitk_packed(x.data_ptr(), x.stride(0), wp.data.data_ptr(), M, N, K,
+                                  dtype_code(x), part.data_ptr(), part.numel() * 4, _stream(x))
+    _lib.check(rc, "ll_gemm_splitk_packed")
+    return s
+
+
+def gemm_packed(x, wp: PackedWeight, bias=None, out=None):
+    """out[M, N] = x @ w^T (+ bias) for M <= 64 from a packed weight."""
+    _dev(x, bias, out)
+    M, K = x.shape
+    N = wp.shape[0]
+    assert wp.shape[1] == K and x.stride(1) == 1 and x.dtype == wp.dtype
+    if out is None:
+        out = torch.empty((M, N), dtype=x.dtype, device=x.device)
+    assert out.shape == (M, N) and out.stride(1) == 1
+    nbytes = _L.ll_gemm_workspace_size(M, N, K)
+    ws_ptr, ws_n = (None, 0)
+    if nbytes > 0:
+        ws = workspace(x.device, "gemm", nbytes)
+        ws_ptr, ws_n = ws.data_ptr(), ws.numel()
+    rc = _L.ll_gemm_packed(x.data_ptr(), x.stride(0), wp.data.data_ptr(),
+                           bias.data_ptr() if bias is not None else None, out.data_ptr(),
+                           out.stride(0), M, N, K, dtype_code(x), ws_ptr, ws_n, _stream(x))
+    _lib.check(rc, "ll_gemm_packed")
+    return out
+
+
 def add_rmsnorm_splitk(h, part, splits, gamma, eps, out=None):
     """h = dtype(h + dtype(sum part)); returns rmsnorm(h) * gamma."""
     _dev(h, part, gamma, out)

@@ -358,6 +358,104 @@ def test_gemm_wide_n_lds_path(cuda, M, N, K):
     assert _close_rel(y, O.linear(x, w, b))
 
 
+# ------------------------------------------------------------ packed weights
+def _pack_reference(w):
+    """Host restatement of the ll_gemm_pack layout: block (kc, t) of 16 KB holds
+    rows 64t + 4ii + lane//16, 16 B chunk (lane % 16) ^ (row % 16) of the
+    128-column chunk kc, at unit 64 ii + lane; blocks kc-major; rows >= N zero."""
+    N, K = w.shape
+    T = -(-N // 64)
+    wp = torch.zeros(T * 64, K, dtype=w.dtype)
+    wp[:N] = w
+    u = wp.view(torch.int16).numpy().reshape(T, 64, K // 128, 16, 8)  # [t, r, kc, chunk, 8]
+    ii, lane = np.meshgrid(np.arange(16), np.arange(64), indexing="ij")
+    r = 4 * ii + lane // 16
+    c = (lane % 16) ^ (r % 16)
+    blocks = u[:, r, :, c, :]  # advanced indices split by a slice lead: [16, 64, t, kc, 8]
+    return torch.from_numpy(np.ascontiguousarray(blocks.transpose(3, 2, 0, 1, 4))).reshape(-1)
+
+
+@pytest.mark.parametrize("N,K", [(200, 256), (128, 128), (2560, 2048)])
+def test_gemm_pack_layout(cuda, N, K):
+    g = torch.Generator().manual_seed(45)
+    w = torch.randn(N, K, generator=g).bfloat16()
+    print(f"case: gemm_pack N={N} K={K}", flush=True)
+    wp = _ops().pack_weight(w.to(cuda))
+    torch.cuda.synchronize()
+    got = wp.data.cpu().view(torch.int16)
+    assert torch.equal(got, _pack_reference(w))
+
+
+@pytest.mark.parametrize("M,N,K", [(40, 2560, 2048), (40, 2048, 11008), (1, 22016, 2048),
+                                   (64, 200, 384), (17, 4096, 1024)])
+def test_gemm_splitk_packed(cuda, M, N, K):
+    print(f"case: gemm_splitk_packed M={M} N={N} K={K}", flush=True)
+    x, w, part, s = _splitk(cuda, M, N, K, 46)
+    wp = _ops().pack_weight(w.to(cuda))
+    part2 = torch.full_like(part, float("nan"))
+    s2 = _ops().gemm_splitk_packed(x.to(cuda), wp, part2)
+    torch.cuda.synchronize()
+    assert s2 == s
+    total = part2[: s * M * N].view(s, M, N).sum(0).cpu().double()
+    ref = O.linear(x, w)
+    assert float((total - ref).abs().max()) <= 1e-4 * max(1.0, float(ref.abs().max()))
+    # same splits as the unpacked kernel: each split's partial agrees to fp32 rounding
+    a = part[: s * M * N].view(s, M, N).cpu().double()
+    b = part2[: s * M * N].view(s, M, N).cpu().double()
+    assert float((a - b).abs().max()) <= 1e-5 * max(1.0, float(a.abs().max()))
+
+
+@pytest.mark.parametrize("M,N,K", [(40, 151936, 2048), (3, 1000, 256)])
+def test_gemm_packed_with_bias(cuda, M, N, K):
+    g = torch.Generator().manual_seed(47)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    w = (torch.randn(N, K, generator=g) * 0.02).bfloat16()
+    b = (torch.randn(N, generator=g) * 0.1).bfloat16()
+    print(f"case: gemm_packed M={M} N={N} K={K}", flush=True)
+    y = _ops().gemm_packed(x.to(cuda), _ops().pack_weight(w.to(cuda)), b.to(cuda))
+    assert _close_rel(y, O.linear(x, w, b))
+
+
+@pytest.mark.parametrize("M,I,K", [(40, 11008, 2048), (1, 256, 128), (64, 200, 384), (17, 4864, 896 + 128)])
+def test_gate_up_silu_fused_equals_unfused(cuda, M, I, K):
+    """The fused epilogue rounds exactly as gemm_splitk + silu_and_mul_splitk do
+    with one split: bit-identical output; and within tolerance of the oracle."""
+    g = torch.Generator().manual_seed(48)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    w = (torch.randn(2 * I, K, generator=g) * 0.02).bfloat16()
+    print(f"case: gate_up_silu M={M} I={I} K={K}", flush=True)
+    ops = _ops()
+    xd, wd = x.to(cuda), w.to(cuda)
+    fused = ops.gate_up_silu(xd, ops.pack_gate_up(wd))
+    s = ops.gemm_splitk_count(M, 2 * I, K)
+    part = torch.zeros(s * M * 2 * I, dtype=torch.float32, device=cuda)
+    ops.gemm_splitk_packed(xd, ops.pack_weight(wd), part)
+    unfused = torch.empty(M, I, dtype=torch.bfloat16, device=cuda)
+    ops.silu_and_mul_splitk(part, s, unfused)
+    torch.cuda.synchronize()
+    if s == 1:  # the same fp32 sums reach the same rounding steps
+        assert torch.equal(fused, unfused)
+    ref = O.silu_and_mul(O.rnd(O.linear(x, w), torch.bfloat16), torch.bfloat16)
+    assert _close_rel(fused, ref)
+
+
+def test_gate_up_pack_layout(cuda):
+    g = torch.Generator().manual_seed(49)
+    I, K = 70, 256
+    w = torch.randn(2 * I, K, generator=g).bfloat16()
+    wp = _ops().pack_gate_up(w.to(cuda))
+    torch.cuda.synchronize()
+    T = -(-I // 32)
+    # interleaved row order: tile t = gate rows 32t..32t+31, then up rows 32t..32t+31
+    rows = torch.zeros(T * 64, K, dtype=torch.bfloat16)
+    for t in range(T):
+        for r in range(64):
+            ch = 32 * t + (r % 32)
+            if ch < I:
+                rows[64 * t + r] = w[ch] if r < 32 else w[I + ch]
+    assert torch.equal(wp.data.cpu().view(torch.int16), _pack_reference(rows))
+
+
 def test_add_rmsnorm_splitk(cuda):
     g = torch.Generator().manual_seed(42)
     M, N, S = 40, 2048, 3
