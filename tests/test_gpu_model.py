@@ -128,3 +128,54 @@ def test_qwen25_3b_geometry_two_layers_batch40(cuda):
             assert float(top2[0] - top2[1]) <= 2 * err_bf16, f"request {b} diverged without a near tie"
         alive &= ~mism & (tb[:, step] == tf[:, step])
     assert int(alive.sum()) >= 30
+
+
+@pytest.mark.parametrize("graph", [True, False])
+def test_radix_prefix_reuse_greedy_tokens(cuda, graph):
+    """Config-5 flow on the tiny fp32 model: request 0 (prompt P) finishes and
+    is inserted into the radix tree (runner_batch.py:184-204); request 1
+    (prompt P + 3 tokens) then matches the cached prefix at admission
+    (runner_batch.py:118-147), takes its slots without recomputing them, and
+    runs the prompt-cache prefill (flash_attn_v2.py:699-762) on the suffix.
+    Both requests' greedy tokens must equal the oracle's full recomputation."""
+    from lite_lang_amd.models.qwen2 import Qwen2ModelRunner
+    from lite_lang_amd.models.qwen2.weights import random_state_dict
+    from lite_lang_amd.models.runner_batch import RunnerBatch
+    cfg, ocfg = _cfgs()
+    sd = random_state_dict(cfg, seed=2)
+    g = torch.Generator().manual_seed(2)
+    P = torch.randint(0, 1024, (20,), generator=g).tolist()
+    Q = P + torch.randint(0, 1024, (3,), generator=g).tolist()
+    print(f"case: radix prefix reuse graph={graph}", flush=True)
+    orc = Qwen2Oracle(ocfg, sd, torch.float32, 8, 128, 1024)
+    ref0 = orc.generate([P], 4)[0].tolist()
+    ref1 = Qwen2Oracle(ocfg, sd, torch.float32, 8, 128, 1024).generate([Q], 6)[0].tolist()
+
+    runner = Qwen2ModelRunner(cfg.layer_nums, 8, cfg, max_length=128, dtype=torch.float32,
+                              state_dict=sd, kv_max_size=1024, device=cuda, use_radix_cache=True,
+                              use_cuda_graph=graph)
+    runner.init_model()
+    b0 = RunnerBatch.create_batch([{"id": 0, "input_tokens": P}], "b0", True, runner)
+    for _ in range(4):
+        b0.update_forward_message(runner.forward(b0))
+    assert b0.request_mapping[0].output_tokens == ref0
+    slots0 = runner.kv_cache.get_token_index([b0.request_mapping[0]]).tolist()
+    b0.filter([0])  # finish: P + 3 generated tokens go into the tree
+    assert runner.radix_cache.all_taken_tokens_ == len(P) + 3
+
+    b1 = RunnerBatch.create_batch([{"id": 1, "input_tokens": Q}], "b1", True, runner)
+    req = b1.request_mapping[1]
+    cached = P + ref0[:3]
+    expect_shared = 0
+    for a, b in zip(Q[:-1], cached):
+        if a != b:
+            break
+        expect_shared += 1
+    assert len(req.shared_tokens) == expect_shared >= len(P)
+    assert req.shared_tokens + req.input_tokens == Q
+    for _ in range(6):
+        b1.update_forward_message(runner.forward(b1))
+    assert b1.request_mapping[1].output_tokens == ref1
+    # the shared prefix is served from request 0's slots
+    slots1 = runner.kv_cache.get_token_index([req]).tolist()
+    assert slots1[:expect_shared] == slots0[:expect_shared]
