@@ -228,6 +228,35 @@ int ll_gemm_pack_gate_up(const void* W, int64_t ldw, int64_t I, int64_t K, int d
 int ll_gemm_gate_up_silu_packed(const void* X, int64_t ldx, const void* Wp, int64_t M, int64_t I,
                                 int64_t K, int dtype, void* act, int64_t ld_act,
                                 hipStream_t stream);
+/* ---------------------------------------------------------------- W8A8 */
+
+/* Symmetric int8 quantisation (replaces quantize_weight_per_channel_absmax,
+ * quantize/smooth_quant/layer.py:5-16, on its float path):
+ * scale[o] = dtype(max_i |W[o, i]| / 127), Q[o, i] = clamp(round_half_even(
+ * fp32(W[o, i]) / fp32(scale[o])), -128, 127); an all-zero row gives Q = 0. */
+int ll_quant_weight_per_channel(const void* W, int64_t ldw, int64_t N, int64_t K, int dtype,
+                                int8_t* Q, int64_t ldq, void* scale, hipStream_t stream);
+/* Dynamic per-token activation quantisation (no reference counterpart: the
+ * reference never quantises activations at run time): scale[t] =
+ * max_k |X[t, k]| / 127 in fp32 (1 for an all-zero row), Q = clamp(
+ * round_half_even(X / scale), -128, 127). */
+int ll_quant_per_token(const void* X, int64_t ldx, int64_t M, int64_t K, int dtype, int8_t* Q,
+                       int64_t ldq, float* scale, hipStream_t stream);
+/* int8 weight streaming for M <= 64 (no reference counterpart; the runtime of
+ * the reference's W8A8BFP32OFP32Linear, smooth_quant/layer.py:19-59, which has
+ * no forward). Wp is the packed image of an int8 [N, K] weight
+ * (ll_gemm_i8_pack; K % 256 == 0; size ll_gemm_i8_packed_bytes); part
+ * receives exact int32 partial sums [s][M][N], s < ll_gemm_i8_splitk_count. */
+int64_t ll_gemm_i8_packed_bytes(int64_t N, int64_t K);
+int ll_gemm_i8_pack(const int8_t* Wq, int64_t ldw, int64_t N, int64_t K, void* Wp,
+                    int64_t wp_bytes, hipStream_t stream);
+int ll_gemm_i8_splitk_count(int64_t M, int64_t N, int64_t K);
+int ll_gemm_i8_splitk_packed(const int8_t* Xq, int64_t ldx, const void* Wp, int64_t M, int64_t N,
+                             int64_t K, int32_t* part, int64_t part_bytes, hipStream_t stream);
+/* out[m][n] = fp32(sum_s part[s][m][n]) * s_tok[m] * fp32(s_ch[n]): the fp32
+ * single-split partial the fused consumers above read (N % 4 == 0). */
+int ll_dequant_splitk(const int32_t* part, int splits, const float* s_tok, const void* s_ch,
+                      int s_ch_dtype, float* out, int64_t M, int64_t N, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -19,15 +19,23 @@
 
 namespace {
 
+// 16-byte operand fragment of one lane and the MFMA accumulator, per element type
 template <typename T> struct Vec8;
 template <> struct Vec8<__bf16> { typedef bf16x8 type; };
 template <> struct Vec8<_Float16> { typedef f16x8 type; };
+template <> struct Vec8<int8_t> { typedef i32x4 type; };  // 16 int8
+template <typename T> struct AccOf { typedef f32x4 type; };
+template <> struct AccOf<int8_t> { typedef i32x4 type; };
 
 __device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 __device__ __forceinline__ f32x4 mfma16x16x32(f16x8 a, f16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+// int8: one 16-byte fragment per lane is a 64-deep k step (exact int32 sums)
+__device__ __forceinline__ i32x4 mfma16x16x32(i32x4 a, i32x4 b, i32x4 c) {
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 }
 
 template <typename V8> __device__ __forceinline__ V8 zero8() {
@@ -109,8 +117,13 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, 
                                                        int K, int ksps, int rotate) {
   static_assert(NST >= 2 && NST <= 4, "2 to 4 stage buffers");
   typedef typename Vec8<T>::type V8;
-  constexpr int TR = kDmaTR, XR = 16 * MB, KC = kDmaKC;
-  constexpr int ROWB = KC * 2, CH = ROWB / 16, RPI = 64 / CH;  // 16 chunks, 4 rows/instr
+  typedef typename AccOf<T>::type AccT;
+  constexpr int ES = (int)sizeof(T);
+  constexpr int TR = kDmaTR, XR = 16 * MB;
+  constexpr int KC = 256 / ES;            // elements per 256-byte row chunk (one stage)
+  constexpr int CE = 16 / ES;             // elements per 16-byte fragment
+  constexpr int KSTEP = 4 * CE;           // k per MFMA: 32 (16-bit types), 64 (int8)
+  constexpr int ROWB = 256, CH = ROWB / 16, RPI = 64 / CH;  // 16 chunks, 4 rows/instr
   constexpr int W_PER_WAVE = (TR / RPI) / 4;
   constexpr int X_PER_WAVE = (XR / RPI) / 4;
   constexpr int C = W_PER_WAVE + X_PER_WAVE;  // DMA instructions per wave per stage
@@ -120,8 +133,8 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, 
   const int n = lane & 15, j = lane >> 4;
   const int row0 = blockIdx.x * TR;
   const int split = blockIdx.y;
-  const int k_beg = split * ksps * 32;
-  const int k_end = min(K, k_beg + ksps * 32);
+  const int k_beg = split * ksps * KSTEP;
+  const int k_end = min(K, k_beg + ksps * KSTEP);
   const int nst = (k_end - k_beg) / KC;
   const int lr_in = lane / CH, p = lane % CH;
   // optional per-workgroup rotation of the k-chunk order, so that concurrent
@@ -141,7 +154,7 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, 
         dma16_stream(g, base + ii * 1024);
       } else {
         const int r = ii * RPI + lr_in;
-        const T* g = W + (int64_t)min(row0 + r, N - 1) * ldw + k0 + (p ^ (r & 15)) * 8;
+        const T* g = W + (int64_t)min(row0 + r, N - 1) * ldw + k0 + (p ^ (r & 15)) * CE;
         dma16_stream(g, base + ii * 1024);
       }
     }
@@ -149,13 +162,13 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, 
     for (int q = 0; q < X_PER_WAVE; ++q) {
       const int ii = wave + q * 4;
       const int r = ii * RPI + lr_in;
-      const T* g = X + (int64_t)min(r, M - 1) * ldx + k0 + (p ^ (r & 15)) * 8;
+      const T* g = X + (int64_t)min(r, M - 1) * ldx + k0 + (p ^ (r & 15)) * CE;
       dma16(g, base + TR * ROWB + ii * 1024);
     }
   };
-  f32x4 acc[MB];
+  AccT acc[MB];
 #pragma unroll
-  for (int t = 0; t < MB; ++t) acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t < MB; ++t) acc[t] = (AccT){0, 0, 0, 0};
 #pragma unroll
   for (int st = 0; st < NST - 1; ++st)
     if (st < nst) issue(st);
@@ -168,7 +181,7 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, 
     const char* wb = smem + (st % NST) * STAGE_B;
     const char* xb = wb + TR * ROWB;
 #pragma unroll
-    for (int s = 0; s < KC / 32; ++s) {
+    for (int s = 0; s < KC / KSTEP; ++s) {
       const V8 a = *(const V8*)(wb + lr * ROWB + (((4 * s + j) ^ (lr & 15)) * 16));
 #pragma unroll
       for (int t = 0; t < MB; ++t) {
@@ -179,7 +192,23 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, 
     }
   }
   // acc[t][i] = Y[token 16t + n][channel row0 + 16*wave + 4j + i]
-  if constexpr (EPI == 1) {
+  if constexpr (ES == 1) {
+    // int8: exact int32 partial sums, part[split][m][n] (part points at int32)
+    int32_t* ip = (int32_t*)part;
+    const int ch = row0 + wave * 16 + 4 * j;
+#pragma unroll
+    for (int t = 0; t < MB; ++t) {
+      const int tok = 16 * t + n;
+      if (tok >= M || ch >= N) continue;
+      int32_t* pp = ip + ((int64_t)split * M + tok) * N + ch;
+      if (ch + 3 < N && (N & 3) == 0) {
+        *(i32x4*)pp = acc[t];
+      } else {
+        for (int i = 0; i < 4 && ch + i < N; ++i) pp[i] = acc[t][i];
+      }
+    }
+    return;
+  } else if constexpr (EPI == 1) {
     // waves 2, 3 (up rows) hand their sums to waves 0, 1 (gate rows) through LDS
     float* ub = (float*)smem;  // [32 channels][16 * MB tokens]
     lds_barrier();             // every wave is done reading the last stage
@@ -208,23 +237,24 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, 
       }
     }
     return;
-  }
-  const int ch = row0 + wave * 16 + 4 * j;
+  } else {
+    const int ch = row0 + wave * 16 + 4 * j;
 #pragma unroll
-  for (int t = 0; t < MB; ++t) {
-    const int tok = 16 * t + n;
-    if (tok >= M || ch >= N) continue;
-    if (part != nullptr) {
-      float* pp = part + ((int64_t)split * M + tok) * N + ch;
-      if (ch + 3 < N && (N & 3) == 0) {
-        *(f32x4*)pp = acc[t];
+    for (int t = 0; t < MB; ++t) {
+      const int tok = 16 * t + n;
+      if (tok >= M || ch >= N) continue;
+      if (part != nullptr) {
+        float* pp = part + ((int64_t)split * M + tok) * N + ch;
+        if (ch + 3 < N && (N & 3) == 0) {
+          *(f32x4*)pp = acc[t];
+        } else {
+          for (int i = 0; i < 4 && ch + i < N; ++i) pp[i] = acc[t][i];
+        }
       } else {
-        for (int i = 0; i < 4 && ch + i < N; ++i) pp[i] = acc[t][i];
+        T* yp = Y + (int64_t)tok * ldy + ch;
+        for (int i = 0; i < 4 && ch + i < N; ++i)
+          yp[i] = ll_from_f32<T>(acc[t][i] + (bias != nullptr ? ll_to_f32(bias[ch + i]) : 0.f));
       }
-    } else {
-      T* yp = Y + (int64_t)tok * ldy + ch;
-      for (int i = 0; i < 4 && ch + i < N; ++i)
-        yp[i] = ll_from_f32<T>(acc[t][i] + (bias != nullptr ? ll_to_f32(bias[ch + i]) : 0.f));
     }
   }
 }
@@ -528,13 +558,15 @@ struct SkinnyPlan {
 
 constexpr int kDirWR = 2, kDirKW = 4, kDirU = 2;
 
-SkinnyPlan plan_skinny(int64_t N, int64_t K) {
+// es: element size in bytes (2 for bf16/fp16, 1 for int8). A stage is a
+// 256-byte row chunk: K * es / 256 chunks, four MFMA k-steps each.
+SkinnyPlan plan_skinny(int64_t N, int64_t K, int es = 2) {
   SkinnyPlan p;
   p.nst = 2;
   p.rotate = 0;
   p.packed = false;
   const int ksteps = (int)((K + 31) / 32);
-  p.dma = (K % kDmaKC == 0);
+  p.dma = ((K * es) % 256 == 0);
   if (p.dma) {
     // Measured at the Qwen2.5 decode shapes (M = 40): the weight stream is
     // fastest with about one workgroup per CU when the row tiles are few
@@ -542,14 +574,14 @@ SkinnyPlan plan_skinny(int64_t N, int64_t K) {
     // one split and two stage buffers (two workgroups per CU) when they are
     // many; rotating each workgroup's k-chunk order spreads the concurrent
     // reads over more HBM channels.
-    const int chunks = (int)(K / kDmaKC);
+    const int chunks = (int)(K * es / 256);
     p.tiles = (int)((N + kDmaTR - 1) / kDmaTR);
     int sp = 256 / p.tiles;
     if (sp > chunks / 2) sp = chunks / 2;
     if (sp < 1) sp = 1;
     const int per = (chunks + sp - 1) / sp;
     p.splits = (chunks + per - 1) / per;
-    p.ksps = per * (kDmaKC / 32);
+    p.ksps = per * 4;
     p.nst = (p.tiles * p.splits <= 256) ? 3 : 2;
     p.rotate = 1;
   } else {
@@ -569,7 +601,7 @@ void launch_skinny_mb(const SkinnyPlan& p, const T* X, int64_t ldx, const T* W, 
                       hipStream_t stream) {
   const dim3 grid((unsigned)p.tiles, (unsigned)p.splits);
   if (p.dma) {
-    const size_t lds = (size_t)p.nst * (kDmaTR + 16 * MB) * kDmaKC * 2;
+    const size_t lds = (size_t)p.nst * (kDmaTR + 16 * MB) * 256;
 #define LL_DMA_LAUNCH(S, PKD)                                                                   \
   hipLaunchKernelGGL((gemm_dma_kernel<T, MB, S, PKD>), grid, dim3(256), lds, stream, X, ldx, W, \
                      ldw, bias, Y, ldy, part, M, N, K, p.ksps, p.rotate)
@@ -579,7 +611,7 @@ void launch_skinny_mb(const SkinnyPlan& p, const T* X, int64_t ldx, const T* W, 
       if (p.nst == 3) LL_DMA_LAUNCH(3, false); else LL_DMA_LAUNCH(2, false);
     }
 #undef LL_DMA_LAUNCH
-  } else {
+  } else if constexpr (sizeof(T) == 2) {
     hipLaunchKernelGGL((gemm_direct_kernel<T, MB, kDirWR, kDirKW, kDirU>), grid,
                        dim3(64 * kDirKW), 0, stream, X, ldx, W, ldw, bias, Y, ldy, part, M, N, K,
                        p.ksps);
@@ -832,4 +864,55 @@ extern "C" int ll_gemm(const void* X, int64_t ldx, const void* W, int64_t ldw, c
                                  workspace_bytes, stream);
   ll_set_error("ll_gemm: unsupported dtype %d", dtype);
   return LL_ERR_UNSUPPORTED;
+}
+
+// ---------------------------------------------------------------- int8 (W8A8)
+// Weight streaming with int8 weights and per-token int8 activations, exact
+// int32 partial sums (no reference counterpart: the reference's W8A8 module
+// quantize/smooth_quant/layer.py:19-59 has no forward; this is its runtime).
+
+extern "C" int64_t ll_gemm_i8_packed_bytes(int64_t N, int64_t K) {
+  if (N <= 0 || K <= 0 || K % 256 != 0) return 0;
+  return ll_cdiv(N, kDmaTR) * kDmaTR * K;
+}
+
+extern "C" int ll_gemm_i8_pack(const int8_t* Wq, int64_t ldw, int64_t N, int64_t K, void* Wp,
+                               int64_t wp_bytes, hipStream_t stream) {
+  LL_CHECK_ARG(Wq && Wp, "ll_gemm_i8_pack: null pointer");
+  LL_CHECK_ARG(N > 0 && K > 0 && K % 256 == 0, "ll_gemm_i8_pack: needs K %% 256 == 0 (K=%lld)",
+               (long long)K);
+  LL_CHECK_ARG(ldw >= K && ldw % 16 == 0 && ((uintptr_t)Wq | (uintptr_t)Wp) % 16 == 0,
+               "ll_gemm_i8_pack: W rows must be 16 B aligned");
+  const int64_t bytes = ll_gemm_i8_packed_bytes(N, K);
+  LL_CHECK_ARG(wp_bytes >= bytes, "ll_gemm_i8_pack: output too small (need %lld bytes)",
+               (long long)bytes);
+  const int64_t units = bytes / 16;
+  hipLaunchKernelGGL(gemm_pack_kernel, dim3((unsigned)ll_cdiv(units, 256)), dim3(256), 0, stream,
+                     (const u32x4*)Wq, ldw / 16, (u32x4*)Wp, (int)N, (int)ll_cdiv(N, kDmaTR),
+                     units, 0);
+  LL_RETURN_LAUNCH();
+}
+
+extern "C" int ll_gemm_i8_splitk_count(int64_t M, int64_t N, int64_t K) {
+  if (M > 64 || M <= 0 || K % 256 != 0) return 0;
+  return plan_skinny(N, K, 1).splits;
+}
+
+extern "C" int ll_gemm_i8_splitk_packed(const int8_t* Xq, int64_t ldx, const void* Wp, int64_t M,
+                                        int64_t N, int64_t K, int32_t* part, int64_t part_bytes,
+                                        hipStream_t stream) {
+  LL_CHECK_ARG(Xq && Wp && part, "ll_gemm_i8_splitk_packed: null pointer");
+  LL_CHECK_ARG(M > 0 && M <= 64 && N > 0 && K > 0 && K % 256 == 0,
+               "ll_gemm_i8_splitk_packed: needs 0 < M <= 64 and K %% 256 == 0");
+  LL_CHECK_ARG(ldx % 16 == 0 && (((uintptr_t)Xq | (uintptr_t)Wp) % 16) == 0,
+               "ll_gemm_i8_splitk_packed: X rows must be 16 B aligned");
+  SkinnyPlan p = plan_skinny(N, K, 1);
+  p.packed = true;
+  p.rotate = 0;
+  LL_CHECK_ARG(part_bytes >= (int64_t)p.splits * M * N * 4,
+               "ll_gemm_i8_splitk_packed: partial buffer too small (need %lld bytes)",
+               (long long)((int64_t)p.splits * M * N * 4));
+  launch_skinny<int8_t>(p, Xq, ldx, (const int8_t*)Wp, K, nullptr, nullptr, 0, (float*)part,
+                        (int)M, (int)N, (int)K, stream);
+  LL_RETURN_LAUNCH();
 }

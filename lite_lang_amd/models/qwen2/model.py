@@ -37,11 +37,13 @@ def rope_tables(max_length: int, head_dim: int, theta: float, device):
 
 class Qwen2Model:
     def __init__(self, layer_nums, max_length, config: Qwen2Config, tp_rank=0, world_size=1,
-                 dtype=torch.bfloat16, device="cuda"):
+                 dtype=torch.bfloat16, device="cuda", quant=None):
         assert world_size == 1, "this build runs tp=1 (one GPU, no collectives)"
         assert layer_nums == config.layer_nums
+        assert quant in (None, "w8a8"), f"unknown quantisation {quant!r}"
         self.cfg = config
         self.dtype = dtype
+        self.quant = quant
         self.device = torch.device(device)
         self.max_length = max_length
         self.cos, self.sin = rope_tables(max_length, config.head_dim, config.rope_theta,
@@ -50,7 +52,13 @@ class Qwen2Model:
         self.last_logits = None  # logits of the latest forward (inspection only)
 
     def load_state_dict(self, sd):
-        self.w = DeviceWeights(self.cfg, sd, self.dtype, self.device)
+        self.w = DeviceWeights(self.cfg, sd, self.dtype, self.device, quant=self.quant)
+
+    def _proj(self, x, li, name, bias=None):
+        """One layer projection in the generic path (bf16 GEMM or W8A8)."""
+        if self.quant == "w8a8":
+            return ops.linear_w8a8(x, self.w.packed[li][name + "_i8"], bias)
+        return ops.gemm(x, self.w.layers[li][name], bias)
 
     # ------------------------------------------------------------ layer stack
     def _layers(self, h, T, slots, positions, pool, attention):
@@ -63,15 +71,15 @@ class Qwen2Model:
         f = None
         for li, lw in enumerate(w.layers):
             x = ops.rmsnorm(h, lw["ln1"], cfg.rms_norm_eps, residual=f)
-            qkv = ops.gemm(x, lw["wqkv"], lw["bqkv"])
+            qkv = self._proj(x, li, "wqkv", lw["bqkv"])
             ops.rope_kv_scatter(qkv, H, KVH, D, positions, self.cos, self.sin, slots, pool[li])
             q = qkv[:, : H * D].view(T, H, D)
             attention(li, q, attn)
-            o = ops.gemm(attn.view(T, H * D), lw["wo"])
+            o = self._proj(attn.view(T, H * D), li, "wo")
             x2 = ops.rmsnorm(h, lw["ln2"], cfg.rms_norm_eps, residual=o)
-            gu = ops.gemm(x2, lw["wgu"])
+            gu = self._proj(x2, li, "wgu")
             act = ops.silu_and_mul(gu)
-            f = ops.gemm(act, lw["wdown"])
+            f = self._proj(act, li, "wdown")
         return f
 
     def _post(self, hs, fs, out=None):
@@ -83,13 +91,23 @@ class Qwen2Model:
         return ops.argmax(logits, out=out)
 
     # ------------------------------------------------------------ decode
-    def splitk_part_numel(self, batch):
-        """fp32 elements of the partial-sum buffer the fused decode path needs."""
+    def _proj_shapes(self):
         cfg = self.cfg
         H, KVH, D, hd, I = (cfg.num_heads, cfg.num_key_value_heads, cfg.head_dim,
                             cfg.hidden_size, cfg.intermediate_size)
-        shapes = [((H + 2 * KVH) * D, hd), (hd, H * D), (2 * I, hd), (hd, I)]
-        return max(ops.gemm_splitk_count(batch, n, k) * batch * n for n, k in shapes)
+        return [((H + 2 * KVH) * D, hd), (hd, H * D), (2 * I, hd), (hd, I)]
+
+    def splitk_part_numel(self, batch):
+        """fp32 elements of the partial-sum buffer the fused decode path needs
+        (W8A8: one dequantised split)."""
+        if self.quant == "w8a8":
+            return max(batch * n for n, _ in self._proj_shapes())
+        return max(ops.gemm_splitk_count(batch, n, k) * batch * n for n, k in self._proj_shapes())
+
+    def w8a8_part_bytes(self, batch):
+        """int32 partial bytes of the W8A8 projections at this batch size."""
+        return max(ops.gemm_i8_splitk_count(batch, n, k) * batch * n * 4
+                   for n, k in self._proj_shapes())
 
     def fused_decode_ok(self, batch):
         return self.dtype in (torch.bfloat16, torch.float16) and 0 < batch <= 64
@@ -127,6 +145,9 @@ class Qwen2Model:
         act = torch.empty((B, cfg.intermediate_size), dtype=dt, device=dev)
         x = ops.rmsnorm(h, w.layers[0]["ln1"], cfg.rms_norm_eps)
         nl = len(w.layers)
+        if self.quant == "w8a8":
+            return self._decode_w8a8(h, B, part, q, attn, act, positions, seq_len, rids, slots,
+                                     pool, r2t, max_len, out)
 
         def proj(xin, lw, pk, name):
             if pk.get(name) is not None:
@@ -155,6 +176,39 @@ class Qwen2Model:
             logits = ops.gemm_packed(x, w.lm_head_p)
         else:
             logits = ops.gemm(x, w.lm_head)
+        self.last_logits = logits
+        return ops.argmax(logits, out=out)
+
+    def _decode_w8a8(self, h, B, part, q, attn, act, positions, seq_len, rids, slots, pool, r2t,
+                     max_len, out):
+        """The fused decode layer with int8 projections: each projection is
+        per-token quantisation + the int8 streaming GEMM + dequantisation into
+        one fp32 split, finished by the same consumer kernels."""
+        cfg, w = self.cfg, self.w
+        H, KVH, D = cfg.num_heads, cfg.num_key_value_heads, cfg.head_dim
+        nl = len(w.layers)
+
+        def proj(xin, pk, name):
+            qw = pk[name + "_i8"]
+            ops.linear_w8a8_fp32(xin, qw, out=part[: B * qw.shape[0]].view(B, qw.shape[0]))
+
+        x = ops.rmsnorm(h, w.layers[0]["ln1"], cfg.rms_norm_eps)
+        for li, (lw, pk) in enumerate(zip(w.layers, w.packed)):
+            proj(x, pk, "wqkv")
+            ops.rope_kv_scatter_splitk(part, 1, lw["bqkv"], q, H, KVH, D, positions, self.cos,
+                                       self.sin, slots, pool[li])
+            ops.decode_attention(q.view(B, H, D), r2t, rids, seq_len, max_len, pool[li, :, :KVH],
+                                 pool[li, :, KVH:], attn)
+            proj(attn.view(B, H * D), pk, "wo")
+            x2 = ops.add_rmsnorm_splitk(h, part, 1, lw["ln2"], cfg.rms_norm_eps)
+            proj(x2, pk, "wgu")
+            ops.silu_and_mul_splitk(part, 1, act)
+            proj(act, pk, "wdown")
+            if li + 1 < nl:
+                x = ops.add_rmsnorm_splitk(h, part, 1, w.layers[li + 1]["ln1"], cfg.rms_norm_eps)
+            else:
+                x = ops.add_rmsnorm_splitk(h, part, 1, w.norm, cfg.final_norm_eps)
+        logits = ops.gemm_packed(x, w.lm_head_p) if w.lm_head_p is not None else ops.gemm(x, w.lm_head)
         self.last_logits = logits
         return ops.argmax(logits, out=out)
 
@@ -208,7 +262,8 @@ class Qwen2ModelRunner:
         self.dtype_ = runner_kwargs.get("dtype", torch.bfloat16)
         self.device_ = torch.device(runner_kwargs.get("device", "cuda"))
         self.model_ins_ = Qwen2Model(layer_nums, runner_kwargs["max_length"], config,
-                                     self.tp_rank_, self.world_size_, self.dtype_, self.device_)
+                                     self.tp_rank_, self.world_size_, self.dtype_, self.device_,
+                                     quant=runner_kwargs.get("quant"))
         self.model_path_ = runner_kwargs.get("model_path")
         self.state_dict_ = runner_kwargs.get("state_dict")
         self.seed_ = runner_kwargs.get("seed", 0)

@@ -418,3 +418,114 @@ def rope_kv_scatter_splitk(part, splits, bias, q_out, q_heads, kv_heads, head_di
         cos_table.stride(0), dtype_code(cos_table), slots.data_ptr(), pool_layer.data_ptr(),
         pool_layer.stride(0), pool_layer.stride(1), dtype_code(q_out), _stream(q_out))
     _lib.check(rc, "ll_rope_kv_scatter_splitk")
+
+
+# ------------------------------------------------------------------ W8A8
+def quant_weight_per_channel(w):
+    """(int8 [N, K], scale [N] in w's dtype): smooth_quant/layer.py:5-16 on the float path."""
+    _dev(w)
+    N, K = w.shape
+    assert w.stride(1) == 1
+    q = torch.empty((N, K), dtype=torch.int8, device=w.device)
+    s = torch.empty((N,), dtype=w.dtype, device=w.device)
+    rc = _L.ll_quant_weight_per_channel(w.data_ptr(), w.stride(0), N, K, dtype_code(w),
+                                        q.data_ptr(), K, s.data_ptr(), _stream(w))
+    _lib.check(rc, "ll_quant_weight_per_channel")
+    return q, s
+
+
+def quant_per_token(x, q=None, s=None):
+    """(int8 [M, K], fp32 scale [M]): dynamic per-token absmax quantisation."""
+    _dev(x, q, s)
+    M, K = x.shape
+    assert x.stride(1) == 1
+    if q is None:
+        q = torch.empty((M, K), dtype=torch.int8, device=x.device)
+    if s is None:
+        s = torch.empty((M,), dtype=torch.float32, device=x.device)
+    rc = _L.ll_quant_per_token(x.data_ptr(), x.stride(0), M, K, dtype_code(x), q.data_ptr(),
+                               q.stride(0), s.data_ptr(), _stream(x))
+    _lib.check(rc, "ll_quant_per_token")
+    return q, s
+
+
+class PackedI8Weight:
+    """int8 weight [N, K] in the packed streaming layout, with its per-channel scale."""
+
+    def __init__(self, wq, scale):
+        _dev(wq, scale)
+        N, K = wq.shape
+        assert wq.dtype == torch.int8 and wq.stride(1) == 1 and scale.shape == (N,)
+        nbytes = _L.ll_gemm_i8_packed_bytes(N, K)
+        if nbytes <= 0:
+            raise _lib.LiteLangError(f"ll_gemm_i8_pack: K={K} is not a multiple of 256")
+        self.shape, self.scale, self.device = (N, K), scale, wq.device
+        self.data = torch.empty(nbytes, dtype=torch.uint8, device=wq.device)
+        rc = _L.ll_gemm_i8_pack(wq.data_ptr(), wq.stride(0), N, K, self.data.data_ptr(), nbytes,
+                                _stream(wq))
+        _lib.check(rc, "ll_gemm_i8_pack")
+
+
+def gemm_i8_splitk_count(M, N, K) -> int:
+    return _L.ll_gemm_i8_splitk_count(M, N, K)
+
+
+def gemm_i8_splitk_packed(xq, wp: PackedI8Weight, part):
+    """int32 partial sums of xq[M, K] @ wq[N, K]^T into part (flat int32); returns splits."""
+    _dev(xq, part)
+    M, K = xq.shape
+    N = wp.shape[0]
+    assert wp.shape[1] == K and xq.dtype == torch.int8 and part.dtype == torch.int32
+    s = _L.ll_gemm_i8_splitk_count(M, N, K)
+    rc = _L.ll_gemm_i8_splitk_packed(xq.data_ptr(), xq.stride(0), wp.data.data_ptr(), M, N, K,
+                                     part.data_ptr(), part.numel() * 4, _stream(xq))
+    _lib.check(rc, "ll_gemm_i8_splitk_packed")
+    return s
+
+
+def dequant_splitk(part, splits, s_tok, s_ch, out, M, N):
+    """out[M, N] fp32 = fp32(sum of int32 partials) * s_tok[m] * fp32(s_ch[n])."""
+    _dev(part, s_tok, s_ch, out)
+    assert part.dtype == torch.int32 and s_tok.dtype == torch.float32 and out.dtype == torch.float32
+    rc = _L.ll_dequant_splitk(part.data_ptr(), splits, s_tok.data_ptr(), s_ch.data_ptr(),
+                              dtype_code(s_ch), out.data_ptr(), M, N, _stream(part))
+    _lib.check(rc, "ll_dequant_splitk")
+    return out
+
+
+class QuantWeight:
+    """W8A8 projection weight: int8 [N, K] (per-channel scales in the model
+    dtype) plus its packed streaming image when K % 256 == 0."""
+
+    def __init__(self, w):
+        self.q, self.scale = quant_weight_per_channel(w)
+        self.shape = tuple(w.shape)
+        self.packed = PackedI8Weight(self.q, self.scale) if w.shape[1] % 256 == 0 else None
+
+
+def linear_w8a8_fp32(x, qw: QuantWeight, out=None):
+    """fp32 [M, N] = dequant(int8(x) @ int8(W)^T): the exact int32 product
+    (the streaming kernel for M <= 64, torch's int8 matmul above that),
+    scaled by the per-token and per-channel scales."""
+    _dev(x, out)
+    M, K = x.shape
+    N = qw.shape[0]
+    xq, st = quant_per_token(x)
+    if M <= 64 and qw.packed is not None:
+        s = gemm_i8_splitk_count(M, N, K)
+        part = workspace(x.device, "w8a8_part", s * M * N * 4).view(torch.int32)
+        gemm_i8_splitk_packed(xq, qw.packed, part)
+    else:
+        s = 1
+        part = torch._int_mm(xq, qw.q.t())
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float32, device=x.device)
+    return dequant_splitk(part, s, st, qw.scale, out, M, N)
+
+
+def linear_w8a8(x, qw: QuantWeight, bias=None):
+    """dtype(linear_w8a8_fp32(x) + bias), the rounding of the fused consumers."""
+    y = linear_w8a8_fp32(x, qw)
+    if bias is not None:
+        y = y + bias.float()
+    return y.to(x.dtype)

@@ -164,14 +164,18 @@ def argmax_first(x: torch.Tensor) -> torch.Tensor:
 
 # ---------------------------------------------------------------- W8A8
 def quantize_weight_per_channel_absmax(w: torch.Tensor):
-    """s_o = max_i |w[o, i]| / 127; w_q = clamp(round_half_even(w / s_o), -128, 127).
+    """s_o = max_i |w[o, i]| / 127 in w's dtype; w_q = clamp(round_half_even(
+    fp32(w) / fp32(s_o)), -128, 127).
 
-    Follows quantize/smooth_quant/layer.py:5-16 (float path: torch.round is
-    round-half-to-even). Returns (int8 weights [N, K], float scales [N]).
+    Follows quantize/smooth_quant/layer.py:5-16 on its CPU path: the scale is
+    computed in the weight's dtype (:8), then the weight is taken to fp32 (:11)
+    and divided by the promoted scale (:13); torch.round is round-half-to-even.
+    An all-zero row (0/0) is defined here as q = 0. Returns (int8 [N, K],
+    scales [N] in w's dtype).
     """
-    w = w.to(torch.float32)
     s = w.abs().max(dim=1)[0] / 127
-    q = (w / s.view(-1, 1)).round().clamp(-128, 127).to(torch.int8)
+    q = w.to(torch.float32) / s.to(torch.float32).view(-1, 1)
+    q = torch.nan_to_num(q, nan=0.0).round().clamp(-128, 127).to(torch.int8)
     return q, s
 
 
@@ -190,3 +194,9 @@ def quantize_per_token_absmax(x: torch.Tensor):
 def int8_gemm_i32(xq: torch.Tensor, wq: torch.Tensor) -> torch.Tensor:
     """Exact int32 accumulators acc[t, o] = sum_k xq[t, k] * wq[o, k] (int64 math)."""
     return (xq.to(torch.int64) @ wq.to(torch.int64).T).to(torch.int32)
+
+
+def dequant_int32(acc: torch.Tensor, s_tok: torch.Tensor, s_ch: torch.Tensor) -> torch.Tensor:
+    """fp32(acc) * s_tok[m] * fp32(s_ch[n]), evaluated in fp32 in that order
+    (build-defined dequantisation of the W8A8 runtime)."""
+    return (acc.to(torch.float32) * s_tok.to(torch.float32).view(-1, 1)) * s_ch.to(torch.float32).view(1, -1)

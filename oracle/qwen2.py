@@ -48,8 +48,13 @@ class Qwen2Cfg:
 
 class Qwen2Oracle:
     def __init__(self, cfg: Qwen2Cfg, sd: dict, dtype: torch.dtype, max_batch: int,
-                 max_length: int, kv_slots: int):
-        self.cfg, self.dtype = cfg, dtype
+                 max_length: int, kv_slots: int, quant: str = None):
+        """quant="w8a8": every layer projection is int8 x int8 -> int32 with
+        per-channel weight scales (quantize_weight_per_channel_absmax on the
+        dtype-rounded weight, smooth_quant/layer.py:5-16) and dynamic
+        per-token activation scales, dequantised in fp32 before the bias;
+        lm_head stays in the model dtype (smooth_quant/qwen2.py:249-250)."""
+        self.cfg, self.dtype, self.quant = cfg, dtype, quant
         r = lambda t: ops.rnd(t.detach().cpu(), dtype)  # noqa: E731
         self.embed = r(sd["model.embed_tokens.weight"])
         self.lm_head = self.embed if cfg.tie_word_embeddings else r(sd["lm_head.weight"])
@@ -67,11 +72,25 @@ class Qwen2Oracle:
                 ln1=r(sd[p + "input_layernorm.weight"]),
                 ln2=r(sd[p + "post_attention_layernorm.weight"]),
             ))
+        if quant == "w8a8":
+            for w in self.layers:
+                for name in ("wq", "wk", "wv", "wo", "wg", "wu", "wd"):
+                    w[name + "_i8"] = ops.quantize_weight_per_channel_absmax(w[name].to(dtype))
         D, KVH = cfg.head_dim, cfg.kv_heads
         self.pool = torch.zeros((cfg.num_layers, kv_slots, 2 * KVH, D), dtype=torch.float64)
         self.cache = PageCache(max_batch, max_length, kv_slots)
         cos, sin = ops.rope_table(max_length, D, cfg.theta)
         self.cos, self.sin = cos.to(torch.float64), sin.to(torch.float64)
+
+    def _linear(self, x, w, names, bias=None):
+        if self.quant != "w8a8":
+            wt = w[names[0]] if len(names) == 1 else torch.cat([w[n] for n in names], 0)
+            return ops.linear(x, wt, bias)
+        xq, st = ops.quantize_per_token_absmax(x.to(self.dtype))
+        wq = torch.cat([w[n + "_i8"][0] for n in names], 0)
+        so = torch.cat([w[n + "_i8"][1] for n in names], 0)
+        y = ops.dequant_int32(ops.int8_gemm_i32(xq, wq), st, so).to(torch.float64)
+        return y if bias is None else y + bias
 
     # ------------------------------------------------------------ one forward
     def forward(self, reqs, is_prefill: bool, ids):
@@ -90,9 +109,9 @@ class Qwen2Oracle:
         h = self.embed[torch.as_tensor(ids).long()]
         for li, w in enumerate(self.layers):
             x = ops.rnd(ops.rmsnorm(h, w["ln1"], cfg.eps), dt)
-            q = ops.rnd(ops.linear(x, w["wq"], w["bq"]), dt).view(T, H, D)
-            k = ops.rnd(ops.linear(x, w["wk"], w["bk"]), dt).view(T, KVH, D)
-            v = ops.rnd(ops.linear(x, w["wv"], w["bv"]), dt).view(T, KVH, D)
+            q = ops.rnd(self._linear(x, w, ["wq"], w["bq"]), dt).view(T, H, D)
+            k = ops.rnd(self._linear(x, w, ["wk"], w["bk"]), dt).view(T, KVH, D)
+            v = ops.rnd(self._linear(x, w, ["wv"], w["bv"]), dt).view(T, KVH, D)
             q = ops.rnd(ops.rotary(q, cos, sin), dt)
             k = ops.rnd(ops.rotary(k, cos, sin), dt)
             self.pool[li, mem, :KVH] = k
@@ -104,12 +123,12 @@ class Qwen2Oracle:
             else:
                 a = ops.decode_attention(q, r2t, rids, lens, kp, vp)
             a = ops.rnd(a, dt).view(T, H * D)
-            o = ops.rnd(ops.linear(a, w["wo"]), dt)
+            o = ops.rnd(self._linear(a, w, ["wo"]), dt)
             h = ops.rnd(h + o, dt)
             x2 = ops.rnd(ops.rmsnorm(h, w["ln2"], cfg.eps), dt)
-            gu = ops.rnd(ops.linear(x2, torch.cat([w["wg"], w["wu"]], 0)), dt)
+            gu = ops.rnd(self._linear(x2, w, ["wg", "wu"]), dt)
             act = ops.rnd(ops.silu_and_mul(gu, dt), dt)
-            f = ops.rnd(ops.linear(act, w["wd"]), dt)
+            f = ops.rnd(self._linear(act, w, ["wd"]), dt)
             h = ops.rnd(h + f, dt)
         if is_prefill:  # last row of each request (post_layer.py:56-71)
             rows = [st + (l - s) - 1 for st, l, s in zip(start, lens, shared)]

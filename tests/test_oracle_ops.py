@@ -188,3 +188,29 @@ def test_w8a8_quantisation_closed_forms():
     acc = ops.int8_gemm_i32(xq, wq)
     brute = [[sum(int(xq[t, k]) * int(wq[o, k]) for k in range(64)) for o in range(6)] for t in range(4)]
     assert acc.tolist() == brute
+
+
+def test_oracle_weight_quantiser_pinned():
+    """quantize_weight_per_channel_absmax against what the formula fixes
+    (smooth_quant/layer.py:5-16): the scale is dtype(absmax / 127); the
+    largest-magnitude entry maps to +-127; every code is within half a step of
+    w / s; exact halves round to even; an all-zero row gives zero codes."""
+    import torch
+    from oracle.ops import quantize_weight_per_channel_absmax
+    g = torch.Generator().manual_seed(70)
+    w = (torch.randn(8, 64, generator=g) * 0.03).bfloat16()
+    w[2] = 0
+    # row 3: scale exactly 1/127 * 127 -> s = 1 when absmax = 127 (bf16-exact);
+    # entries 2.5 and 3.5 are exact halves: round to 2 and 4
+    w[3] = 0
+    w[3, 0], w[3, 1], w[3, 2], w[3, 3] = 127.0, 2.5, 3.5, -0.5
+    q, s = quantize_weight_per_channel_absmax(w)
+    assert s.dtype == torch.bfloat16
+    assert torch.equal(s, (w.abs().max(dim=1)[0].float() / 127).bfloat16())
+    assert q[3, :4].tolist() == [127, 2, 4, 0]
+    assert torch.equal(q[2], torch.zeros(64, dtype=torch.int8))
+    wf, sf = w.float(), s.float().view(-1, 1)
+    for r in (0, 1, 4, 5, 6, 7):
+        assert int(q[r].abs().max()) == 127
+        err = (q[r].float() * sf[r] - wf[r]).abs()
+        assert float(err.max()) <= float(sf[r]) / 2 + 1e-7
