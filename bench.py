@@ -18,7 +18,9 @@ Also reported on the same JSON line:
   cpu_baseline  the CPU oracle (oracle/qwen2.py) timed on the host cores
                 on a bounded sample of the same decode workload.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3|5]
+  --config 3 and --config 5 print the line of that BASELINE config instead
+  (Qwen2-1.5B through the scheduler; 3B W8A8 with the radix cache).
 """
 from __future__ import annotations
 
@@ -165,6 +167,101 @@ def cpu_baseline(max_seconds=30.0):
                        f"= {step:.2f}s/step")}
 
 
+# ------------------------------------------------------------------ configs 3 and 5
+def bench_config3(dev, new_tokens=600):
+    """Qwen2-1.5B shape, 40 requests x 600 random prompt ids, 600 greedy new
+    tokens each, driven end to end by the continuous-batching scheduler
+    (admission, prefill, decode bursts of 10, filtering), one token readback
+    per step as the reference's scheduler loop does."""
+    from lite_lang_amd.models.qwen2 import Qwen2ModelRunner
+    from lite_lang_amd.models.qwen2.weights import qwen2_1p5b_config
+    from lite_lang_amd.scheduler import IdTokenizer, LocalModelClient, Scheduler
+    cfg = qwen2_1p5b_config()
+    max_length = PROMPT + new_tokens + 2
+    runner = Qwen2ModelRunner(cfg.layer_nums, B, cfg, max_length=max_length, dtype=torch.bfloat16,
+                              seed=0, kv_max_size=B * max_length + 64, device=dev)
+    sch = Scheduler(max_batch_size=B, tokenizer=IdTokenizer(eos_token_id=-1),
+                    max_total_length=PROMPT + new_tokens, max_output_length=new_tokens,
+                    max_reqs=4 * B, model_client=LocalModelClient(runner), busy_scale=0.9)
+    # warm-up: one short request through the same path (graph capture of B=1 and kernels)
+    w = sch.add_req_tokens(messages(8, seed=9)[0]["input_tokens"])
+    while not w.is_end:
+        sch.forward()
+    torch.cuda.synchronize(dev)
+    reqs = [sch.add_req_tokens(m["input_tokens"]) for m in messages(PROMPT, seed=3)]
+    t0 = time.perf_counter()
+    t_prefill = None
+    while not all(r.is_end for r in reqs):
+        sch.forward()
+        if t_prefill is None:
+            t_prefill = time.perf_counter() - t0  # first round: prefill + 10 decode steps
+    torch.cuda.synchronize(dev)
+    wall = time.perf_counter() - t0
+    gen = sum(r.output_length for r in reqs)
+    return {"metric": "config 3: generated tok/s Qwen2-1.5B bs40 ctx600 +600 (scheduler, end to end)",
+            "value": round(gen / wall, 2), "unit": "tok/s", "n_gpus": 1, "higher_is_better": True,
+            "dtype": "bf16", "data": "synthetic (random-init weights, uniform random prompt ids)",
+            "config": {"workload": "Qwen2-1.5B shape, 40 x 600-token prompts, 600 greedy tokens each, "
+                                   "continuous batching through lite_lang_amd.scheduler",
+                       "global_batch": B, "seq_len": PROMPT, "new_tokens": new_tokens},
+            "wall_s": round(wall, 3), "generated_tokens": gen,
+            "first_round_s": round(t_prefill, 4)}
+
+
+def bench_config5(dev, steps=300, warmup=2):
+    """Qwen2.5-3B shape with W8A8 projections (int8 per-channel weights,
+    per-token int8 activations, bf16 lm_head) and the radix cache: a warm
+    request leaves a 400-token prefix in the tree; then 40 requests, 32 of
+    them starting with that prefix (200 new prompt tokens each) and 8 with
+    600 unique tokens, are prefilled and decoded; decode tok/s at batch 40."""
+    from lite_lang_amd.models.qwen2 import Qwen2ModelRunner
+    from lite_lang_amd.models.qwen2.weights import qwen25_3b_config
+    from lite_lang_amd.models.runner_batch import RunnerBatch
+    cfg = qwen25_3b_config()
+    max_length = PROMPT + steps + warmup + 8
+    runner = Qwen2ModelRunner(cfg.layer_nums, B + 1, cfg, max_length=max_length,
+                              dtype=torch.bfloat16, seed=0, kv_max_size=(B + 2) * max_length * 2,
+                              device=dev, quant="w8a8", use_radix_cache=True)
+    runner.init_model()
+    rs = np.random.RandomState(5)
+    prefix = rs.randint(0, 151936, size=400).tolist()
+    warm = RunnerBatch.create_batch([{"id": 999, "input_tokens": prefix + rs.randint(0, 151936, size=8).tolist()}],
+                                    "warm", True, runner)
+    for _ in range(3):
+        warm.update_forward_message(runner.forward(warm))
+    warm.filter([999])
+    msgs = []
+    for i in range(B):
+        toks = (prefix + rs.randint(0, 151936, size=200).tolist()) if i < 32 else \
+            rs.randint(0, 151936, size=PROMPT).tolist()
+        msgs.append({"id": i, "input_tokens": toks})
+    batch = RunnerBatch.create_batch(msgs, "c5", True, runner)
+    shared = sum(len(r.shared_tokens) for r in batch.request_mapping.values())
+    torch.cuda.synchronize(dev)
+    t0 = time.perf_counter()
+    batch.update_forward_message(runner.forward(batch))
+    torch.cuda.synchronize(dev)
+    t_prefill = time.perf_counter() - t0
+    for _ in range(warmup):
+        batch.update_forward_message(runner.forward(batch))
+    torch.cuda.synchronize(dev)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        batch.update_forward_message(runner.forward(batch))
+    torch.cuda.synchronize(dev)
+    dt = time.perf_counter() - t0
+    wbytes = runner.model_ins_.w.nbytes_streamed_per_decode()
+    return {"metric": "config 5: decode tok/s Qwen2.5-3B W8A8 + radix bs40 ctx600",
+            "value": round(steps * B / dt, 2), "unit": "tok/s", "n_gpus": 1, "steps": steps,
+            "warmup": warmup, "ms_per_step": round(dt / steps * 1e3, 4), "higher_is_better": True,
+            "dtype": "int8 x int8 -> int32 (projections), bf16 elsewhere",
+            "data": "synthetic (random-init weights quantised per channel, random prompt ids)",
+            "config": {"workload": "Qwen2.5-3B shape W8A8, radix on: 32 of 40 prompts share a "
+                                   "400-token cached prefix", "global_batch": B, "seq_len": PROMPT},
+            "prefill_s": round(t_prefill, 4), "prefix_tokens_reused": shared,
+            "weight_bytes_per_step": int(wbytes)}
+
+
 # ------------------------------------------------------------------ main
 def main():
     ap = argparse.ArgumentParser()
@@ -172,6 +269,9 @@ def main():
     ap.add_argument("--steps", type=int, default=600)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--config", type=int, default=4, choices=(3, 4, 5),
+                    help="4: the headline line (default); 3: Qwen2-1.5B through the scheduler; "
+                         "5: 3B W8A8 + radix cache")
     ap.add_argument("--attention-only", action="store_true",
                     help="run only the config-2 decode attention launches plus a 256 MiB "
                          "device copy of known size (for rocprofv3 --pmc traffic runs)")
@@ -187,6 +287,13 @@ def main():
     from lite_lang_amd.models.qwen2.weights import qwen25_3b_config
     cfg = qwen25_3b_config()
     K, W = args.steps, args.warmup
+
+    if args.config == 3:
+        print(json.dumps(bench_config3(dev)), flush=True)
+        return
+    if args.config == 5:
+        print(json.dumps(bench_config5(dev)), flush=True)
+        return
 
     if args.attention_only:
         src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
