@@ -39,7 +39,7 @@ B, PROMPT = 40, 600
 # rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of `bench.py --attention-only`,
 # scaled by what the counters read for a 256 MiB copy (fetch x2.0, write x1.0).
 # Measured on the current kernels; re-measure when they change.
-ATTN_TRAFFIC_BYTES = 27120 * 1024
+ATTN_TRAFFIC_BYTES = 28253244
 
 
 def log(msg):
@@ -355,7 +355,7 @@ def main():
         "decode_tok_s": round(decode_tok_s, 1) if decode_tok_s else None,
         "decode_step": {"ms": round(step_sec * 1e3, 4), "bytes": int(step_bytes),
                         "hbm_frac": round(step_bytes / step_sec / 1e9 / HBM_PEAK_GBS, 4)},
-        "roofline": {"kernel": "decode_attn_mfma_kernel (config 2)", "bound": "hbm",
+        "roofline": {"kernel": "decode_attn_dma_kernel + decode_attn_combine_kernel (config 2)", "bound": "hbm",
                      "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "traffic": ATTN_TRAFFIC_BYTES,
                      "avg_us": round(attn_sec * 1e6, 3), "bytes_per_launch": attn_bytes},
