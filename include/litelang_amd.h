@@ -193,6 +193,29 @@ int ll_rope_kv_scatter_splitk(const float* part, int splits, const void* bias, v
                               int64_t table_row_stride, int cs_dtype, const int32_t* slots,
                               void* pool_layer, int64_t pool_slot_stride,
                               int64_t pool_head_stride, int dtype, hipStream_t stream);
+/* ll_rope_kv_scatter_splitk followed by ll_decode_attention in one launch
+ * (plus the split merge): replaces, for one decode step,
+ *   rotary_emb_fwd + the KV-cache write (transformer_layer.py:112-115,142-160)
+ *   and token_decode_attention_flash_decoding (flash_decoding.py:262-312).
+ * qkv_part [qkv_splits][batch][(q_heads + 2*kv_heads)*head_dim] fp32 partials
+ * of the QKV projection; every workgroup rebuilds its query heads from them,
+ * and the one holding a sequence's last tile writes the new token's rotated K
+ * and V to k_cache/v_cache[new_slots[b]]. Results (out and the pool) are bit
+ * identical to the two-call sequence. Precondition: new_slots[b] is the entry
+ * req_to_tokens[b_req_idx[b], b_seq_len[b] - 1] and appears in no other
+ * sequence's first b_seq_len entries (what a decode step guarantees).
+ * bf16/fp16, head_dim 64 or 128, q_heads/kv_heads <= 16, fp32 cos/sin tables;
+ * other shapes use the two calls. workspace: ll_decode_attention_workspace_size. */
+int ll_decode_attention_rope_splitk(
+    const float* qkv_part, int qkv_splits, const void* qkv_bias, const void* positions,
+    int positions_i64, const void* cos_table, const void* sin_table, int64_t table_row_stride,
+    int cs_dtype, const int32_t* new_slots, void* k_cache, int64_t k_stride_tok,
+    int64_t k_stride_head, void* v_cache, int64_t v_stride_tok, int64_t v_stride_head,
+    const int32_t* req_to_tokens, int64_t req_to_tokens_stride, const void* b_req_idx,
+    int req_idx_i64, const void* b_seq_len, int seq_len_i64, void* out, int64_t out_stride_b,
+    int64_t out_stride_h, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+    int64_t max_len_in_batch, float sm_scale, int dtype, void* workspace,
+    int64_t workspace_bytes, hipStream_t stream);
 
 /* Pre-packed weights for the decode projections (no reference counterpart:
  * a layout of the same nn.Linear weight [N, K], chosen for MI355X). The

@@ -88,7 +88,54 @@ struct DecodeArgs {
   float scale_log2;   // sm_scale * log2(e)
   float* part_acc;    // [B*H*nsplit, D] unnormalised partial outputs
   float* part_ml;     // [B*H*nsplit, 2] running max (log2 domain) and sum
+  // fused RoPE + new-token K/V write (ROPE kernels only)
+  const float* qkv_part;   // [qkv_splits][B][(H + 2 KVH) * D] fp32 split-K partials
+  int qkv_splits;
+  const void* qkv_bias;    // [(H + 2 KVH) * D] of the model dtype, or null
+  const void* pos; int pos64;
+  const float* cos_tab; const float* sin_tab; int64_t tab_stride;
+  const int32_t* new_slots;  // [B] pool slot of each sequence's new token
 };
+
+// One job of the fused RoPE: 4 rotation pairs (i..i+3 with i+D/2..i+D/2+3) of
+// the head whose columns start at hcol, with the arithmetic of the split-K
+// RoPE/scatter kernel: sum of the partials in split order, + bias in fp32,
+// rounded to T, rotated in fp32 with explicit FMAs, rounded to T. V heads are
+// only rounded. Results go to LDS and, when glb is set, to global memory.
+template <typename T, int D>
+__device__ __forceinline__ void rope_job(const DecodeArgs& a, int64_t sstride, int64_t row,
+                                         int hcol, int i, const float* cs, const float* sn,
+                                         bool rotate, T* lds, T* glb) {
+  constexpr int HALF = D / 2;
+  const int c0 = hcol + i, c1 = c0 + HALF;
+  f32x4 x0 = ll_sum_splits4(a.qkv_part, a.qkv_splits, sstride, row + c0);
+  f32x4 x1 = ll_sum_splits4(a.qkv_part, a.qkv_splits, sstride, row + c1);
+  const T* bias = (const T*)a.qkv_bias;
+  if (bias != nullptr) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x0[e] += ll_to_f32(bias[c0 + e]);
+      x1[e] += ll_to_f32(bias[c1 + e]);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    T y0, y1;
+    if (rotate) {
+      const float u = ll_to_f32(ll_from_f32<T>(x0[e])), w = ll_to_f32(ll_from_f32<T>(x1[e]));
+      ll_rope_pair(u, w, cs[i + e], sn[i + e], y0, y1);
+    } else {
+      y0 = ll_from_f32<T>(x0[e]);
+      y1 = ll_from_f32<T>(x1[e]);
+    }
+    lds[i + e] = y0;
+    lds[i + HALF + e] = y1;
+    if (glb != nullptr) {
+      glb[i + e] = y0;
+      glb[i + HALF + e] = y1;
+    }
+  }
+}
 
 // XCD-aware unit mapping: workgroups are dispatched round-robin over the 8
 // XCDs, so all splits of one (sequence, KV head) land on the same XCD.
@@ -113,7 +160,14 @@ template <int D> struct TileGeom {
   static __device__ __forceinline__ int swz(int c, int r) { return c ^ ((r / ROWS_PER_BANKS) & (CH - 1)); }
 };
 
-template <typename T, int D>
+// ROPE: q comes from the QKV projection's split-K partials (bias, RoPE) instead
+// of a q tensor, and the workgroup whose split holds the sequence's last tile
+// also builds the new token's K/V, writes them to new_slots[b] in the pool and
+// patches the tile rows carrying that slot in its own LDS copy (the DMA may
+// have read the slot before the write landed). Precondition: a sequence's new
+// slot appears in no other sequence's first seq_len entries and in its own
+// only within the last split (the decode step puts it at seq_len - 1).
+template <typename T, int D, bool ROPE>
 __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs a) {
   typedef typename Vec8<T>::type V8;
   typedef typename Vec4<T>::type V4;
@@ -137,7 +191,27 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
   // Loaded first (it does not depend on the lengths); columns n >= G read a
   // valid head and are zeroed once the loads have landed.
   V8 qb[DS];
-  {
+  T* s_q = (T*)(smem + TG::MAIN_B + (size_t)a.slots_cap * 4);  // ROPE: [G][D] rotated q
+  T* s_kv = s_q + a.G * D;                                     // ROPE: new token's K, V
+  constexpr int QD = D / 8;  // RoPE jobs per head
+  int32_t new_slot = 0;
+  int64_t qkv_sstride = 0, qkv_row = 0;
+  const float* cs = nullptr;
+  const float* sn = nullptr;
+  if constexpr (ROPE) {
+    const int width = (a.H + 2 * a.KVH) * D;
+    qkv_sstride = (int64_t)a.B * width;
+    qkv_row = (int64_t)b * width;
+    const int64_t p = ll_load_idx(a.pos, b, a.pos64);
+    cs = a.cos_tab + p * a.tab_stride;
+    sn = a.sin_tab + p * a.tab_stride;
+    new_slot = a.new_slots[b];
+    if ((int)threadIdx.x < a.G * QD) {  // G * QD <= 16 * D / 8 <= 256
+      const int g = threadIdx.x / QD, i = (threadIdx.x % QD) * 4;
+      rope_job<T, D>(a, qkv_sstride, qkv_row, (kvh * a.G + g) * D, i, cs, sn, true, s_q + g * D,
+                     nullptr);
+    }
+  } else {
     const int hq = kvh * a.G + min(n, a.G - 1);
     const T* qp = (const T*)a.q + (int64_t)b * a.q_sb + (int64_t)hq * a.q_sh;
 #pragma unroll
@@ -158,6 +232,22 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
   const int64_t tok0 = (int64_t)tb * kTT;
   const int ntok = (int)(min(len, (int64_t)te * kTT) - tok0);  // tokens of this split (may be 0)
 
+  // ROPE: the split holding the last tile (split 0 for an empty sequence)
+  // writes the new token's K and V (the last 2 * QD threads, one job each)
+  bool writer = false;
+  if constexpr (ROPE) {
+    writer = split == (ntiles > 0 ? (ntiles - 1) / per : 0);
+    const int jb = (int)threadIdx.x - (kWaves * 64 - 2 * QD);
+    if (writer && jb >= 0) {
+      const bool isv = jb >= QD;
+      const int i = (isv ? jb - QD : jb) * 4;
+      T* glb = isv ? (T*)a.v + (int64_t)new_slot * a.v_st + (int64_t)kvh * a.v_sh
+                   : (T*)a.k + (int64_t)new_slot * a.k_st + (int64_t)kvh * a.k_sh;
+      rope_job<T, D>(a, qkv_sstride, qkv_row, (a.H + (isv ? a.KVH : 0) + kvh) * D, i, cs, sn,
+                     !isv, s_kv + (isv ? D : 0), glb);
+    }
+  }
+
   // slot ids of the split -> LDS (tail entries point at slot 0, masked later);
   // four loads per thread in flight per round
   const int nslots = (te - tb) * kTT;
@@ -176,12 +266,18 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
       if (i < nslots) s_slots[i] = v[u];
     }
   }
+  if constexpr (ROPE) {
+    __syncthreads();  // s_q, s_kv and the slot table are complete
+    const T* qs = s_q + min(n, a.G - 1) * D;
+#pragma unroll
+    for (int s = 0; s < DS; ++s) qb[s] = *(const V8*)(qs + 32 * s + 8 * j);
+  }
   if (n >= a.G) {
 #pragma unroll
     for (int s = 0; s < DS; ++s)
       for (int e = 0; e < 8; ++e) qb[s][e] = (T)0.f;
   }
-  __syncthreads();
+  if constexpr (!ROPE) __syncthreads();
 
   const char* kbase = (const char*)((const T*)a.k + (int64_t)kvh * a.k_sh);
   const char* vbase = (const char*)((const T*)a.v + (int64_t)kvh * a.v_sh);
@@ -219,9 +315,27 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
     } else {
       vm_wait<0>();
     }
-    const char* kb = ring + (k % kRing) * TG::TILE_B;
+    char* kb = ring + (k % kRing) * TG::TILE_B;
     const char* vb = kb + kTT * TG::ROWB;
     const int t0 = (wave + k * kWaves) * kTT;
+    if constexpr (ROPE) {
+      if (writer) {
+        // rows of this tile that carry the new slot get the fresh K/V (in-wave
+        // LDS order puts these writes before the reads below)
+        const bool hit = (t0 + n) < ntok && s_slots[t0 + n] == new_slot;
+        uint64_t hits = __ballot(hit) & 0xffffull;
+        while (hits) {
+          const int r = __builtin_ctzll(hits);
+          hits &= hits - 1;
+          if (lane < 2 * TG::CH) {
+            const int isv = lane >= TG::CH ? 1 : 0;
+            const int cc = lane - isv * TG::CH;
+            const u32x4 v = *(const u32x4*)((const char*)s_kv + isv * TG::ROWB + cc * 16);
+            *(u32x4*)(kb + isv * kTT * TG::ROWB + r * TG::ROWB + TG::swz(cc, r) * 16) = v;
+          }
+        }
+      }
+    }
 
     // S^T block: rows = tokens 4j+i, column = head n
     f32x4 s4 = {0.f, 0.f, 0.f, 0.f};
@@ -458,16 +572,81 @@ int choose_nsplit(int B, int KVH, int64_t max_len) {
 int64_t align256(int64_t x) { return ((x + 255) / 256) * 256; }
 
 
+
+template <int D, bool ROPE>
+void launch_split_stage(const DecodeArgs& a, int dtype, unsigned grid, size_t lds,
+                        hipStream_t stream) {
+  if (dtype == LL_BF16)
+    hipLaunchKernelGGL((decode_attn_dma_kernel<__bf16, D, ROPE>), dim3(grid), dim3(kWaves * 64),
+                       lds, stream, a);
+  else
+    hipLaunchKernelGGL((decode_attn_dma_kernel<_Float16, D, ROPE>), dim3(grid), dim3(kWaves * 64),
+                       lds, stream, a);
+}
+
+template <int D>
+void launch_combine(const DecodeArgs& a, int dtype, hipStream_t stream) {
+  const dim3 cgrid((unsigned)((a.B * a.H + kWaves - 1) / kWaves));
+  if (dtype == LL_BF16)
+    hipLaunchKernelGGL((decode_attn_combine_kernel<__bf16, D>), cgrid, dim3(kWaves * 64), 0,
+                       stream, a);
+  else
+    hipLaunchKernelGGL((decode_attn_combine_kernel<_Float16, D>), cgrid, dim3(kWaves * 64), 0,
+                       stream, a);
+}
+
+int64_t workspace_bytes_for(int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                            int64_t max_len) {
+  const int ns = choose_nsplit((int)batch, (int)kv_heads, max_len);
+  if (ns <= 1) return 0;
+  const int64_t parts = batch * q_heads * ns;
+  return align256(parts * head_dim * 4)  // partial acc
+         + align256(parts * 2 * 4);        // partial (m, l)
+}
+
+// Split stage (+ combine when the sequence is split) of the MFMA path; a has
+// every field but the split geometry and the workspace pointers set.
+int launch_mfma(DecodeArgs& a, int64_t head_dim, int dtype, bool rope, int64_t max_len,
+                void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  a.nsplit = choose_nsplit(a.B, a.KVH, max_len);
+  if (a.nsplit > 1) {
+    const int64_t need = workspace_bytes_for(a.B, a.H, a.KVH, head_dim, max_len);
+    LL_CHECK_ARG(workspace != nullptr && workspace_bytes >= need,
+                 "decode attention: workspace too small (need %lld bytes, got %lld)",
+                 (long long)need, (long long)workspace_bytes);
+    char* w = (char*)workspace;
+    const int64_t parts = (int64_t)a.B * a.H * a.nsplit;
+    a.part_acc = (float*)w;
+    w += align256(parts * head_dim * 4);
+    a.part_ml = (float*)w;
+  }
+  const int64_t tiles = (max_len + kTT - 1) / kTT;
+  a.slots_cap = (int)((tiles + a.nsplit - 1) / a.nsplit) * kTT;
+  const int groups = (a.units + 7) / 8;
+  const unsigned grid = (unsigned)(groups * 8 * a.nsplit);
+  const size_t extra = (size_t)a.slots_cap * 4 + (rope ? (size_t)(a.G + 2) * head_dim * 2 : 0);
+  if (head_dim == 128) {
+    const size_t lds = TileGeom<128>::MAIN_B + extra;
+    if (rope) launch_split_stage<128, true>(a, dtype, grid, lds, stream);
+    else launch_split_stage<128, false>(a, dtype, grid, lds, stream);
+  } else {
+    const size_t lds = TileGeom<64>::MAIN_B + extra;
+    if (rope) launch_split_stage<64, true>(a, dtype, grid, lds, stream);
+    else launch_split_stage<64, false>(a, dtype, grid, lds, stream);
+  }
+  if (a.nsplit > 1) {
+    if (head_dim == 128) launch_combine<128>(a, dtype, stream);
+    else launch_combine<64>(a, dtype, stream);
+  }
+  LL_RETURN_LAUNCH();
+}
+
 }  // namespace
 
 extern "C" int64_t ll_decode_attention_workspace_size(int64_t batch, int64_t q_heads,
                                                       int64_t kv_heads, int64_t head_dim,
                                                       int64_t max_len_in_batch) {
-  const int ns = choose_nsplit((int)batch, (int)kv_heads, max_len_in_batch);
-  if (ns <= 1) return 0;
-  const int64_t parts = batch * q_heads * ns;
-  return align256(parts * head_dim * 4)  // partial acc
-         + align256(parts * 2 * 4);        // partial (m, l)
+  return workspace_bytes_for(batch, q_heads, kv_heads, head_dim, max_len_in_batch);
 }
 
 extern "C" int ll_decode_attention(const void* q, int64_t q_stride_b, int64_t q_stride_h,
@@ -491,7 +670,7 @@ extern "C" int ll_decode_attention(const void* q, int64_t q_stride_b, int64_t q_
                "ll_decode_attention: max_len_in_batch %lld out of range",
                (long long)max_len_in_batch);
   if (batch == 0) return LL_OK;
-  DecodeArgs a;
+  DecodeArgs a = {};
   a.q = q; a.q_sb = q_stride_b; a.q_sh = q_stride_h;
   a.k = k_cache; a.k_st = k_stride_tok; a.k_sh = k_stride_head;
   a.v = v_cache; a.v_st = v_stride_tok; a.v_sh = v_stride_head;
@@ -521,50 +700,55 @@ extern "C" int ll_decode_attention(const void* q, int64_t q_stride_b, int64_t q_
     });
   }
 
-  a.nsplit = choose_nsplit(a.B, a.KVH, max_len_in_batch);
-  if (a.nsplit > 1) {
-    const int64_t need = ll_decode_attention_workspace_size(batch, q_heads, kv_heads, head_dim,
-                                                            max_len_in_batch);
-    LL_CHECK_ARG(workspace != nullptr && workspace_bytes >= need,
-                 "ll_decode_attention: workspace too small (need %lld bytes, got %lld)",
-                 (long long)need, (long long)workspace_bytes);
-    char* w = (char*)workspace;
-    const int64_t parts = batch * q_heads * a.nsplit;
-    a.part_acc = (float*)w;
-    w += align256(parts * head_dim * 4);
-    a.part_ml = (float*)w;
-  }
-  const int64_t tiles = (max_len_in_batch + kTT - 1) / kTT;
-  a.slots_cap = (int)((tiles + a.nsplit - 1) / a.nsplit) * kTT;
-  const int groups = (a.units + 7) / 8;
-  const unsigned grid = (unsigned)(groups * 8 * a.nsplit);
-  const dim3 block(kWaves * 64);
-  if (head_dim == 128) {
-    const size_t lds = TileGeom<128>::MAIN_B + (size_t)a.slots_cap * 4;
-    if (dtype == LL_BF16)
-      hipLaunchKernelGGL((decode_attn_dma_kernel<__bf16, 128>), dim3(grid), block, lds, stream, a);
-    else
-      hipLaunchKernelGGL((decode_attn_dma_kernel<_Float16, 128>), dim3(grid), block, lds, stream, a);
-  } else {
-    const size_t lds = TileGeom<64>::MAIN_B + (size_t)a.slots_cap * 4;
-    if (dtype == LL_BF16)
-      hipLaunchKernelGGL((decode_attn_dma_kernel<__bf16, 64>), dim3(grid), block, lds, stream, a);
-    else
-      hipLaunchKernelGGL((decode_attn_dma_kernel<_Float16, 64>), dim3(grid), block, lds, stream, a);
-  }
-  if (a.nsplit > 1) {
-    const dim3 cgrid((unsigned)((batch * q_heads + kWaves - 1) / kWaves));
-    if (head_dim == 128) {
-      if (dtype == LL_BF16)
-        hipLaunchKernelGGL((decode_attn_combine_kernel<__bf16, 128>), cgrid, block, 0, stream, a);
-      else
-        hipLaunchKernelGGL((decode_attn_combine_kernel<_Float16, 128>), cgrid, block, 0, stream, a);
-    } else {
-      if (dtype == LL_BF16)
-        hipLaunchKernelGGL((decode_attn_combine_kernel<__bf16, 64>), cgrid, block, 0, stream, a);
-      else
-        hipLaunchKernelGGL((decode_attn_combine_kernel<_Float16, 64>), cgrid, block, 0, stream, a);
-    }
-  }
-  LL_RETURN_LAUNCH();
+  return launch_mfma(a, head_dim, dtype, false, max_len_in_batch, workspace, workspace_bytes,
+                     stream);
+}
+
+extern "C" int ll_decode_attention_rope_splitk(
+    const float* qkv_part, int qkv_splits, const void* qkv_bias, const void* positions,
+    int positions_i64, const void* cos_table, const void* sin_table, int64_t table_row_stride,
+    int cs_dtype, const int32_t* new_slots, void* k_cache, int64_t k_stride_tok,
+    int64_t k_stride_head, void* v_cache, int64_t v_stride_tok, int64_t v_stride_head,
+    const int32_t* req_to_tokens, int64_t req_to_tokens_stride, const void* b_req_idx,
+    int req_idx_i64, const void* b_seq_len, int seq_len_i64, void* out, int64_t out_stride_b,
+    int64_t out_stride_h, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+    int64_t max_len_in_batch, float sm_scale, int dtype, void* workspace,
+    int64_t workspace_bytes, hipStream_t stream) {
+  LL_CHECK_ARG(qkv_part && positions && cos_table && sin_table && new_slots && k_cache &&
+                   v_cache && req_to_tokens && b_req_idx && b_seq_len && out,
+               "ll_decode_attention_rope_splitk: null pointer");
+  LL_CHECK_ARG(qkv_splits >= 1, "ll_decode_attention_rope_splitk: qkv_splits must be >= 1");
+  LL_CHECK_ARG(cs_dtype == LL_F32, "ll_decode_attention_rope_splitk: cos/sin tables must be fp32");
+  LL_CHECK_ARG(kv_heads > 0 && q_heads % kv_heads == 0 && q_heads / kv_heads <= 16,
+               "ll_decode_attention_rope_splitk: needs q_heads = G * kv_heads with G <= 16");
+  LL_CHECK_ARG((dtype == LL_BF16 || dtype == LL_F16) && (head_dim == 128 || head_dim == 64),
+               "ll_decode_attention_rope_splitk: bf16/fp16 with head_dim 64 or 128 only "
+               "(other shapes: ll_rope_kv_scatter_splitk + ll_decode_attention)");
+  LL_CHECK_ARG(k_stride_tok % 8 == 0 && k_stride_head % 8 == 0 && v_stride_tok % 8 == 0 &&
+                   v_stride_head % 8 == 0 &&
+                   (((uintptr_t)qkv_part | (uintptr_t)k_cache | (uintptr_t)v_cache) % 16 == 0),
+               "ll_decode_attention_rope_splitk: K/V strides must be multiples of 8 elements, "
+               "partials and caches 16 B aligned");
+  LL_CHECK_ARG(max_len_in_batch >= 0 && max_len_in_batch <= INT32_MAX,
+               "ll_decode_attention_rope_splitk: max_len_in_batch %lld out of range",
+               (long long)max_len_in_batch);
+  if (batch == 0) return LL_OK;
+  DecodeArgs a = {};
+  a.k = k_cache; a.k_st = k_stride_tok; a.k_sh = k_stride_head;
+  a.v = v_cache; a.v_st = v_stride_tok; a.v_sh = v_stride_head;
+  a.r2t = req_to_tokens; a.r2t_s = req_to_tokens_stride;
+  a.req_idx = b_req_idx; a.req64 = req_idx_i64;
+  a.seq_len = b_seq_len; a.len64 = seq_len_i64;
+  a.out = out; a.o_sb = out_stride_b; a.o_sh = out_stride_h;
+  a.B = (int)batch; a.H = (int)q_heads; a.KVH = (int)kv_heads; a.G = (int)(q_heads / kv_heads);
+  a.units = a.B * a.KVH;
+  a.max_len = (int)max_len_in_batch;
+  a.scale_log2 = sm_scale * 1.4426950408889634f;
+  a.qkv_part = qkv_part; a.qkv_splits = qkv_splits; a.qkv_bias = qkv_bias;
+  a.pos = positions; a.pos64 = positions_i64;
+  a.cos_tab = (const float*)cos_table; a.sin_tab = (const float*)sin_table;
+  a.tab_stride = table_row_stride;
+  a.new_slots = new_slots;
+  return launch_mfma(a, head_dim, dtype, true, max_len_in_batch, workspace, workspace_bytes,
+                     stream);
 }

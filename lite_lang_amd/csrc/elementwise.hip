@@ -105,8 +105,7 @@ __global__ void rope_kernel(T* __restrict__ q, int64_t q_st, int64_t q_sh, int H
   const float s = ll_to_f32(sn[t * s_st + i]);
   const float x0 = ll_to_f32(base[i]);
   const float x1 = ll_to_f32(base[i + half]);
-  base[i] = ll_from_f32<T>(x0 * c - x1 * s);
-  base[i + half] = ll_from_f32<T>(x0 * s + x1 * c);
+  ll_rope_pair(x0, x1, c, s, base[i], base[i + half]);
 }
 
 extern "C" int ll_rotary_emb(void* q, int64_t q_tok_stride, int64_t q_head_stride, int64_t q_heads,
@@ -164,8 +163,8 @@ __global__ void rope_kv_scatter_kernel(T* __restrict__ qkv, int64_t ld, int H, i
     const float s = ll_to_f32(sin_tab[p * tab_stride + i]);
     const float x0 = ll_to_f32(src[i]);
     const float x1 = ll_to_f32(src[i + half]);
-    const T y0 = ll_from_f32<T>(x0 * c - x1 * s);
-    const T y1 = ll_from_f32<T>(x0 * s + x1 * c);
+    T y0, y1;
+    ll_rope_pair(x0, x1, c, s, y0, y1);
     if (h < H) {
       src[i] = y0;
       src[i + half] = y1;
@@ -255,11 +254,46 @@ __global__ void silu_and_mul_kernel(const T* x, int64_t x_rs, T* out, int64_t o_
   out[m * o_rs + n] = ll_from_f32<T>(u * ll_to_f32(s));
 }
 
+// Same, 8 elements (16 B) per thread for 16-bit types: one thread reads its
+// gate and up chunks before writing, so in-place use stays safe.
+template <typename T>
+__global__ __launch_bounds__(256) void silu_and_mul_vec8_kernel(const T* x, int64_t x_rs, T* out,
+                                                                int64_t o_rs, int64_t M, int N8) {
+  typedef T V8 __attribute__((ext_vector_type(8)));
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t m = gid / N8;
+  if (m >= M) return;
+  const int n = (int)(gid - m * N8) * 8;
+  const V8 g8 = *(const V8*)(x + m * x_rs + n);
+  const V8 u8 = *(const V8*)(x + m * x_rs + n + (int64_t)N8 * 8);
+  V8 o8;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float g = ll_to_f32(g8[e]);
+    const T s = ll_from_f32<T>(g / (1.0f + __expf(-g)));
+    o8[e] = ll_from_f32<T>(ll_to_f32(u8[e]) * ll_to_f32(s));
+  }
+  *(V8*)(out + m * o_rs + n) = o8;
+}
+
 extern "C" int ll_silu_and_mul(const void* x, int64_t x_row_stride, void* out,
                                int64_t out_row_stride, int64_t M, int64_t N, int dtype,
                                hipStream_t stream) {
   LL_CHECK_ARG(x && out, "ll_silu_and_mul: null pointer");
   if (M == 0 || N == 0) return LL_OK;
+  const bool vec = (dtype == LL_BF16 || dtype == LL_F16) && N % 8 == 0 && x_row_stride % 8 == 0 &&
+                   out_row_stride % 8 == 0 && (((uintptr_t)x | (uintptr_t)out) % 16) == 0;
+  if (vec) {
+    const unsigned grid = (unsigned)ll_cdiv(M * (N / 8), 256);
+    if (dtype == LL_BF16)
+      hipLaunchKernelGGL((silu_and_mul_vec8_kernel<__bf16>), dim3(grid), dim3(256), 0, stream,
+                         (const __bf16*)x, x_row_stride, (__bf16*)out, out_row_stride, M, (int)(N / 8));
+    else
+      hipLaunchKernelGGL((silu_and_mul_vec8_kernel<_Float16>), dim3(grid), dim3(256), 0, stream,
+                         (const _Float16*)x, x_row_stride, (_Float16*)out, out_row_stride, M,
+                         (int)(N / 8));
+    LL_RETURN_LAUNCH();
+  }
   const int64_t total = M * N;
   const unsigned grid = (unsigned)((total + 255) / 256);
   return LL_DISPATCH_DTYPE(dtype, T, [&]() -> int {
@@ -425,26 +459,6 @@ __device__ __forceinline__ float ll_sum_splits(const float* __restrict__ part, i
   return s;
 }
 
-// Sum of 4 consecutive partial columns over all splits, loads batched 4 at a
-// time (the additions still run in split order 0, 1, 2, ...).
-__device__ __forceinline__ f32x4 ll_sum_splits4(const float* __restrict__ part, int splits,
-                                                int64_t split_stride, int64_t idx) {
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  int sp = 0;
-  for (; sp + 4 <= splits; sp += 4) {
-    const f32x4 a = *(const f32x4*)(part + (sp + 0) * split_stride + idx);
-    const f32x4 b = *(const f32x4*)(part + (sp + 1) * split_stride + idx);
-    const f32x4 c = *(const f32x4*)(part + (sp + 2) * split_stride + idx);
-    const f32x4 d = *(const f32x4*)(part + (sp + 3) * split_stride + idx);
-    acc += a;
-    acc += b;
-    acc += c;
-    acc += d;
-  }
-  for (; sp < splits; ++sp) acc += *(const f32x4*)(part + sp * split_stride + idx);
-  return acc;
-}
-
 // h[m] = T(h[m] + T(sum_s part[s][m])); out[m] = rmsnorm(h[m]) * gamma.
 // One workgroup per row, 4 consecutive columns per thread (N % 4 == 0).
 template <typename T, int BLOCK>
@@ -593,8 +607,7 @@ __global__ void rope_kv_scatter_splitk_kernel(const float* __restrict__ part, in
       const float c = ll_to_f32(cos_tab[p * tab_stride + i + e]);
       const float s = ll_to_f32(sin_tab[p * tab_stride + i + e]);
       const float a = ll_to_f32(ll_from_f32<T>(x0[e])), b = ll_to_f32(ll_from_f32<T>(x1[e]));
-      dst[i + e] = ll_from_f32<T>(a * c - b * s);
-      dst[i + half + e] = ll_from_f32<T>(a * s + b * c);
+      ll_rope_pair(a, b, c, s, dst[i + e], dst[i + half + e]);
     }
   } else {
 #pragma unroll

@@ -62,6 +62,35 @@ __device__ __forceinline__ int64_t ll_load_idx(const void* p, int64_t i, int is6
   return is64 ? ((const int64_t*)p)[i] : (int64_t)((const int32_t*)p)[i];
 }
 
+// Sum of 4 consecutive partial columns over all splits, loads batched 4 at a
+// time (the additions still run in split order 0, 1, 2, ...).
+__device__ __forceinline__ f32x4 ll_sum_splits4(const float* __restrict__ part, int splits,
+                                                int64_t split_stride, int64_t idx) {
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  int sp = 0;
+  for (; sp + 4 <= splits; sp += 4) {
+    const f32x4 a = *(const f32x4*)(part + (sp + 0) * split_stride + idx);
+    const f32x4 b = *(const f32x4*)(part + (sp + 1) * split_stride + idx);
+    const f32x4 c = *(const f32x4*)(part + (sp + 2) * split_stride + idx);
+    const f32x4 d = *(const f32x4*)(part + (sp + 3) * split_stride + idx);
+    acc += a;
+    acc += b;
+    acc += c;
+    acc += d;
+  }
+  for (; sp < splits; ++sp) acc += *(const f32x4*)(part + sp * split_stride + idx);
+  return acc;
+}
+
+// Rotate-half RoPE of one (x_i, x_{i+D/2}) pair, rounded to T. The fused
+// multiply-adds are written out so every kernel rotating a pair rounds it the
+// same way: y0 = fma(a, c, -(b*s)), y1 = fma(a, s, b*c).
+template <typename T>
+__device__ __forceinline__ void ll_rope_pair(float a, float b, float c, float s, T& y0, T& y1) {
+  y0 = ll_from_f32<T>(__builtin_fmaf(a, c, -(b * s)));
+  y1 = ll_from_f32<T>(__builtin_fmaf(a, s, b * c));
+}
+
 // ---------------------------------------------------------------- wave helpers
 __device__ __forceinline__ float ll_wave_max(float v) {
 #pragma unroll

@@ -121,6 +121,24 @@ class Qwen2Model:
         return max(ops.gemm_i8_splitk_count(batch, n, k) * batch * n * 4
                    for n, k in self._proj_shapes())
 
+    def _rope_attention(self, part, splits, bias, q, attn, positions, slots, pool_layer, r2t,
+                        rids, seq_len, max_len):
+        """RoPE + new-token K/V write + decode attention from the QKV split-K
+        partials: one fused launch (plus the split merge) where the kernel
+        covers the shape, else the scatter kernel followed by attention."""
+        cfg = self.cfg
+        H, KVH, D = cfg.num_heads, cfg.num_key_value_heads, cfg.head_dim
+        if D in (64, 128) and H // KVH <= 16:
+            ops.decode_attention_rope_splitk(part, splits, bias, positions, self.cos, self.sin,
+                                             slots, r2t, rids, seq_len, max_len,
+                                             pool_layer[:, :KVH], pool_layer[:, KVH:], attn)
+            return
+        B = attn.shape[0]
+        ops.rope_kv_scatter_splitk(part, splits, bias, q, H, KVH, D, positions, self.cos, self.sin,
+                                   slots, pool_layer)
+        ops.decode_attention(q.view(B, H, D), r2t, rids, seq_len, max_len, pool_layer[:, :KVH],
+                             pool_layer[:, KVH:], attn)
+
     def fused_decode_ok(self, batch):
         return self.dtype in (torch.bfloat16, torch.float16) and 0 < batch <= 64
 
@@ -168,10 +186,8 @@ class Qwen2Model:
 
         for li, (lw, pk) in enumerate(zip(w.layers, w.packed)):
             s = proj(x, lw, pk, "wqkv")
-            ops.rope_kv_scatter_splitk(part, s, lw["bqkv"], q, H, KVH, D, positions, self.cos,
-                                       self.sin, slots, pool[li])
-            ops.decode_attention(q.view(B, H, D), r2t, rids, seq_len, max_len, pool[li, :, :KVH],
-                                 pool[li, :, KVH:], attn)
+            self._rope_attention(part, s, lw["bqkv"], q, attn, positions, slots, pool[li], r2t,
+                                 rids, seq_len, max_len)
             s = proj(attn.view(B, H * D), lw, pk, "wo")
             x2 = ops.add_rmsnorm_splitk(h, part, s, lw["ln2"], cfg.rms_norm_eps)
             if pk.get("wgu_silu") is not None:
@@ -207,10 +223,8 @@ class Qwen2Model:
         x = ops.rmsnorm(h, w.layers[0]["ln1"], cfg.rms_norm_eps)
         for li, (lw, pk) in enumerate(zip(w.layers, w.packed)):
             proj(x, pk, "wqkv")
-            ops.rope_kv_scatter_splitk(part, 1, lw["bqkv"], q, H, KVH, D, positions, self.cos,
-                                       self.sin, slots, pool[li])
-            ops.decode_attention(q.view(B, H, D), r2t, rids, seq_len, max_len, pool[li, :, :KVH],
-                                 pool[li, :, KVH:], attn)
+            self._rope_attention(part, 1, lw["bqkv"], q, attn, positions, slots, pool[li], r2t,
+                                 rids, seq_len, max_len)
             proj(attn.view(B, H * D), pk, "wo")
             x2 = ops.add_rmsnorm_splitk(h, part, 1, lw["ln2"], cfg.rms_norm_eps)
             proj(x2, pk, "wgu")

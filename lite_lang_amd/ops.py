@@ -420,6 +420,41 @@ def rope_kv_scatter_splitk(part, splits, bias, q_out, q_heads, kv_heads, head_di
     _lib.check(rc, "ll_rope_kv_scatter_splitk")
 
 
+def decode_attention_rope_splitk(part, splits, bias, positions, cos_table, sin_table, slots,
+                                 req_to_tokens, b_req_idx, b_seq_len, max_len_in_batch, cache_k,
+                                 cache_v, out, sm_scale=None):
+    """rope_kv_scatter_splitk + decode_attention in one launch: q is rebuilt
+    from the QKV split-K partials inside the attention kernel and the new
+    token's K/V are written to cache_k/cache_v[slots[b]] by the workgroup that
+    attends over that token."""
+    _dev(part, positions, cos_table, sin_table, slots, req_to_tokens, b_req_idx, b_seq_len,
+         cache_k, cache_v, out)
+    B, H, D = out.shape
+    KVH = cache_k.shape[1]
+    assert slots.dtype == torch.int32 and req_to_tokens.dtype == torch.int32
+    assert cache_k.stride(-1) == 1 and cache_v.stride(-1) == 1 and out.stride(-1) == 1
+    assert req_to_tokens.stride(-1) == 1 and cos_table.dtype == torch.float32
+    if sm_scale is None:
+        sm_scale = 1.0 / (D ** 0.5)
+    max_len = int(max_len_in_batch)
+    nbytes = _L.ll_decode_attention_workspace_size(B, H, KVH, D, max_len)
+    ws = workspace(out.device, "decode_attention", nbytes)
+    rc = _L.ll_decode_attention_rope_splitk(
+        part.data_ptr(), splits, bias.data_ptr() if bias is not None else None,
+        positions.data_ptr(), _idx(positions, "positions"), cos_table.data_ptr(),
+        sin_table.data_ptr(), cos_table.stride(0), dtype_code(cos_table), slots.data_ptr(),
+        cache_k.data_ptr(), cache_k.stride(0), cache_k.stride(1),
+        cache_v.data_ptr(), cache_v.stride(0), cache_v.stride(1),
+        req_to_tokens.data_ptr(), req_to_tokens.stride(0),
+        b_req_idx.data_ptr(), _idx(b_req_idx, "b_req_idx"),
+        b_seq_len.data_ptr(), _idx(b_seq_len, "b_seq_len"),
+        out.data_ptr(), out.stride(0), out.stride(1),
+        B, H, KVH, D, max_len, float(sm_scale), dtype_code(out), ws.data_ptr(), ws.numel(),
+        _stream(out))
+    _lib.check(rc, "ll_decode_attention_rope_splitk")
+    return out
+
+
 # ------------------------------------------------------------------ W8A8
 def quant_weight_per_channel(w):
     """(int8 [N, K], scale [N] in w's dtype): smooth_quant/layer.py:5-16 on the float path."""
