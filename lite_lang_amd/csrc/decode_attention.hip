@@ -108,14 +108,25 @@ __device__ __forceinline__ void rope_job(const DecodeArgs& a, int64_t sstride, i
                                          bool rotate, T* lds, T* glb) {
   constexpr int HALF = D / 2;
   const int c0 = hcol + i, c1 = c0 + HALF;
+  // bias and the cos/sin entries first: their loads share the partials' round trip
+  const T* bias = (const T*)a.qkv_bias;
+  float b0[4] = {0.f, 0.f, 0.f, 0.f}, b1[4] = {0.f, 0.f, 0.f, 0.f}, cv[4], sv[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    if (bias != nullptr) {
+      b0[e] = ll_to_f32(bias[c0 + e]);
+      b1[e] = ll_to_f32(bias[c1 + e]);
+    }
+    cv[e] = cs[i + e];
+    sv[e] = sn[i + e];
+  }
   f32x4 x0 = ll_sum_splits4(a.qkv_part, a.qkv_splits, sstride, row + c0);
   f32x4 x1 = ll_sum_splits4(a.qkv_part, a.qkv_splits, sstride, row + c1);
-  const T* bias = (const T*)a.qkv_bias;
   if (bias != nullptr) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      x0[e] += ll_to_f32(bias[c0 + e]);
-      x1[e] += ll_to_f32(bias[c1 + e]);
+      x0[e] += b0[e];
+      x1[e] += b1[e];
     }
   }
 #pragma unroll
@@ -123,7 +134,7 @@ __device__ __forceinline__ void rope_job(const DecodeArgs& a, int64_t sstride, i
     T y0, y1;
     if (rotate) {
       const float u = ll_to_f32(ll_from_f32<T>(x0[e])), w = ll_to_f32(ll_from_f32<T>(x1[e]));
-      ll_rope_pair(u, w, cs[i + e], sn[i + e], y0, y1);
+      ll_rope_pair(u, w, cv[e], sv[e], y0, y1);
     } else {
       y0 = ll_from_f32<T>(x0[e]);
       y1 = ll_from_f32<T>(x1[e]);

@@ -460,16 +460,27 @@ __device__ __forceinline__ float ll_sum_splits(const float* __restrict__ part, i
 }
 
 // h[m] = T(h[m] + T(sum_s part[s][m])); out[m] = rmsnorm(h[m]) * gamma.
-// One workgroup per row, 4 consecutive columns per thread (N % 4 == 0).
-template <typename T, int BLOCK>
+// One workgroup per row, 4 consecutive columns per thread and pass (N % 4 == 0,
+// N <= 4 * BLOCK * MAXP). The residual and gamma loads are unconditional (a
+// clamped column) so they join the partials' memory round trip.
+template <typename T, int BLOCK, int MAXP>
 __global__ __launch_bounds__(BLOCK) void add_rmsnorm_splitk_kernel(
     T* __restrict__ h, int64_t h_rs, const float* __restrict__ part, int splits,
     const T* __restrict__ gamma, T* __restrict__ out, int64_t o_rs, int M, int N, float eps) {
+  constexpr int PER = 4;
   const int row = blockIdx.x;
   T* hr = h + (int64_t)row * h_rs;
   const int64_t sstride = (int64_t)M * N;
-  constexpr int PER = 4;  // columns per thread per pass
-  constexpr int MAXP = 4; // passes kept in registers (N <= 4 * BLOCK * MAXP)
+  T hraw[MAXP][PER], graw[MAXP][PER];
+#pragma unroll
+  for (int ps = 0; ps < MAXP; ++ps) {
+    const int c = min((ps * BLOCK + (int)threadIdx.x) * PER, N - PER);
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+      hraw[ps][e] = hr[c + e];
+      graw[ps][e] = gamma[c + e];
+    }
+  }
   float hv[MAXP][PER];
   float ss = 0.f;
 #pragma unroll
@@ -479,7 +490,7 @@ __global__ __launch_bounds__(BLOCK) void add_rmsnorm_splitk_kernel(
       const f32x4 o = ll_sum_splits4(part, splits, sstride, (int64_t)row * N + c);
 #pragma unroll
       for (int e = 0; e < PER; ++e) {
-        const T nh = ll_from_f32<T>(ll_to_f32(hr[c + e]) + ll_to_f32(ll_from_f32<T>(o[e])));
+        const T nh = ll_from_f32<T>(ll_to_f32(hraw[ps][e]) + ll_to_f32(ll_from_f32<T>(o[e])));
         hr[c + e] = nh;
         hv[ps][e] = ll_to_f32(nh);
         ss += hv[ps][e] * hv[ps][e];
@@ -501,7 +512,7 @@ __global__ __launch_bounds__(BLOCK) void add_rmsnorm_splitk_kernel(
     if (c < N) {
 #pragma unroll
       for (int e = 0; e < PER; ++e)
-        orow[c + e] = ll_from_f32<T>(hv[ps][e] / denom * ll_to_f32(gamma[c + e]));
+        orow[c + e] = ll_from_f32<T>(hv[ps][e] / denom * ll_to_f32(graw[ps][e]));
     }
   }
 }
@@ -517,9 +528,18 @@ extern "C" int ll_add_rmsnorm_splitk(void* h, int64_t h_row_stride, const float*
   LL_CHECK_ARG(((uintptr_t)part) % 16 == 0, "ll_add_rmsnorm_splitk: partials must be 16 B aligned");
   if (M == 0) return LL_OK;
   return LL_DISPATCH_DTYPE(dtype, T, [&]() -> int {
-    hipLaunchKernelGGL((add_rmsnorm_splitk_kernel<T, 512>), dim3((unsigned)M), dim3(512), 0, stream,
-                       (T*)h, h_row_stride, part, splits, (const T*)gamma, (T*)out, out_row_stride,
-                       (int)M, (int)N, eps);
+    if (N <= 4 * 512)
+      hipLaunchKernelGGL((add_rmsnorm_splitk_kernel<T, 512, 1>), dim3((unsigned)M), dim3(512), 0,
+                         stream, (T*)h, h_row_stride, part, splits, (const T*)gamma, (T*)out,
+                         out_row_stride, (int)M, (int)N, eps);
+    else if (N <= 4 * 512 * 2)
+      hipLaunchKernelGGL((add_rmsnorm_splitk_kernel<T, 512, 2>), dim3((unsigned)M), dim3(512), 0,
+                         stream, (T*)h, h_row_stride, part, splits, (const T*)gamma, (T*)out,
+                         out_row_stride, (int)M, (int)N, eps);
+    else
+      hipLaunchKernelGGL((add_rmsnorm_splitk_kernel<T, 512, 4>), dim3((unsigned)M), dim3(512), 0,
+                         stream, (T*)h, h_row_stride, part, splits, (const T*)gamma, (T*)out,
+                         out_row_stride, (int)M, (int)N, eps);
     LL_RETURN_LAUNCH();
   });
 }

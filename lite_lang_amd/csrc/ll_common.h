@@ -62,10 +62,30 @@ __device__ __forceinline__ int64_t ll_load_idx(const void* p, int64_t i, int is6
   return is64 ? ((const int64_t*)p)[i] : (int64_t)((const int32_t*)p)[i];
 }
 
-// Sum of 4 consecutive partial columns over all splits, loads batched 4 at a
-// time (the additions still run in split order 0, 1, 2, ...).
+// Up to U splits at once: every load is issued before the first addition (the
+// split index is clamped so the loads need no branch; the surplus ones re-read
+// the last split and are not added).
+template <int U>
+__device__ __forceinline__ f32x4 ll_sum_splits4_upto(const float* __restrict__ part, int splits,
+                                                     int64_t split_stride, int64_t idx) {
+  f32x4 v[U];
+#pragma unroll
+  for (int sp = 0; sp < U; ++sp)
+    v[sp] = *(const f32x4*)(part + (int64_t)min(sp, splits - 1) * split_stride + idx);
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int sp = 0; sp < U; ++sp)
+    if (sp < splits) acc += v[sp];
+  return acc;
+}
+
+// Sum of 4 consecutive partial columns over all splits, added in split order
+// 0, 1, 2, ... starting from +0. Up to 8 splits take one memory round trip;
+// more splits go 4 loads at a time.
 __device__ __forceinline__ f32x4 ll_sum_splits4(const float* __restrict__ part, int splits,
                                                 int64_t split_stride, int64_t idx) {
+  if (splits <= 4) return ll_sum_splits4_upto<4>(part, splits, split_stride, idx);
+  if (splits <= 8) return ll_sum_splits4_upto<8>(part, splits, split_stride, idx);
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   int sp = 0;
   for (; sp + 4 <= splits; sp += 4) {
