@@ -219,15 +219,18 @@ int ll_decode_attention_rope_splitk(
 
 /* Pre-packed weights for the decode projections (no reference counterpart:
  * a layout of the same nn.Linear weight [N, K], chosen for MI355X). The
- * packed image stores every (64-row tile, 128-column chunk) stage of the
- * weight-streaming kernel as one contiguous, already swizzled 16 KB block,
- * blocks ordered chunk-major, so the workgroups of a launch stream
- * neighbouring blocks instead of rows 2K bytes apart. K % 128 == 0; rows are
- * padded to a multiple of 64 with zeros. ll_gemm_packed_bytes returns the size
- * (0 if K % 128 != 0). The packed GEMMs compute what ll_gemm_splitk / ll_gemm
- * compute for M <= 64 from the unpacked weight, with Wp in place of W: same
- * split count and split boundaries (the 128-column chunks inside a split may
- * be summed in another order). */
+ * packed image stores every (row tile, 128-column chunk) stage of the
+ * weight-streaming kernel as one contiguous, already swizzled block of
+ * tile_rows * 256 bytes, blocks ordered chunk-major, so the workgroups of a
+ * launch stream neighbouring blocks instead of rows 2K bytes apart. The tile
+ * height (ll_gemm_packed_tile_rows: 64, or 128 when one split covers K and
+ * there are more than 256 64-row tiles) is a function of (N, K) only. K % 128
+ * == 0; rows are padded to a multiple of the tile height with zeros.
+ * ll_gemm_packed_bytes returns the size (0 if K % 128 != 0). The packed GEMMs
+ * compute what ll_gemm_splitk / ll_gemm compute for M <= 64 from the unpacked
+ * weight, with Wp in place of W: same split count and split boundaries (the
+ * 128-column chunks inside a split may be summed in another order). */
+int ll_gemm_packed_tile_rows(int64_t N, int64_t K);
 int64_t ll_gemm_packed_bytes(int64_t N, int64_t K);
 int ll_gemm_pack(const void* W, int64_t ldw, int64_t N, int64_t K, int dtype, void* Wp,
                  int64_t wp_bytes, hipStream_t stream);
@@ -240,11 +243,13 @@ int ll_gemm_packed(const void* X, int64_t ldx, const void* Wp, const void* bias,
 /* Gate/up projection fused with SiLU_and_Mul (replaces the gate_up projection
  * plus silu_and_mul_fwd of transformer_layer.py:80-81 for M <= 64). The weight
  * is [gate; up] ([2I, K], the reference's two nn.Linear weights stacked);
- * ll_gemm_pack_gate_up packs it so that every 64-row tile holds 32 gate rows
- * and the 32 up rows of the same channels (size from
+ * ll_gemm_pack_gate_up packs it so that every tile of R rows
+ * (ll_gemm_packed_gate_up_tile_rows: 64, or 128 when I > 8192) holds R/2 gate
+ * rows and the R/2 up rows of the same channels (size from
  * ll_gemm_packed_gate_up_bytes, 0 if K % 128 != 0). act[m, c] =
  * dtype(dtype(up) * dtype(silu(dtype(gate)))), the rounding sequence of
  * ll_silu_and_mul_splitk, from one split (full fp32 sums). */
+int ll_gemm_packed_gate_up_tile_rows(int64_t I);
 int64_t ll_gemm_packed_gate_up_bytes(int64_t I, int64_t K);
 int ll_gemm_pack_gate_up(const void* W, int64_t ldw, int64_t I, int64_t K, int dtype, void* Wp,
                          int64_t wp_bytes, hipStream_t stream);

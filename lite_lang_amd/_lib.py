@@ -49,6 +49,8 @@ SIGNATURES = {
     "ll_gemm_packed": (I32, [P, I64, P, P, P, I64, I64, I64, I64, I32, P, I64, P]),
     "ll_gemm_packed_gate_up_bytes": (I64, [I64, I64]),
     "ll_gemm_pack_gate_up": (I32, [P, I64, I64, I64, I32, P, I64, P]),
+    "ll_gemm_packed_tile_rows": (I32, [I64, I64]),
+    "ll_gemm_packed_gate_up_tile_rows": (I32, [I64]),
     "ll_gemm_gate_up_silu_packed": (I32, [P, I64, P, I64, I64, I64, I32, P, I64, P]),
     "ll_quant_weight_per_channel": (I32, [P, I64, I64, I64, I32, P, I64, P, P]),
     "ll_quant_per_token": (I32, [P, I64, I64, I64, I32, P, I64, P, P]),

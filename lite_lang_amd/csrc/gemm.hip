@@ -108,7 +108,7 @@ __device__ __forceinline__ void wait_stage(int later) {
 // channels; the epilogue writes Y[m, c] = T(T(up) * T(silu(T(gate)))) for the
 // 32 channels of the tile (N = 2 * channels), the rounding sequence of
 // ll_silu_and_mul_splitk applied to the same fp32 sums.
-template <typename T, int MB, int NST, bool PK, int EPI = 0>
+template <typename T, int MB, int NST, bool PK, int EPI = 0, int TR = 64>
 __global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, int64_t ldx,
                                                        const T* __restrict__ W, int64_t ldw,
                                                        const T* __restrict__ bias,
@@ -119,7 +119,9 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, 
   typedef typename Vec8<T>::type V8;
   typedef typename AccOf<T>::type AccT;
   constexpr int ES = (int)sizeof(T);
-  constexpr int TR = kDmaTR, XR = 16 * MB;
+  static_assert(TR == 64 || (TR == 128 && sizeof(T) == 2), "64-row tiles, or 128 for 16-bit types");
+  constexpr int XR = 16 * MB;
+  constexpr int RB = TR / 64;             // 16-row MFMA blocks per wave
   constexpr int KC = 256 / ES;            // elements per 256-byte row chunk (one stage)
   constexpr int CE = 16 / ES;             // elements per 16-byte fragment
   constexpr int KSTEP = 4 * CE;           // k per MFMA: 32 (16-bit types), 64 (int8)
@@ -166,13 +168,14 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, 
       dma16(g, base + TR * ROWB + ii * 1024);
     }
   };
-  AccT acc[MB];
+  AccT acc[RB][MB];
 #pragma unroll
-  for (int t = 0; t < MB; ++t) acc[t] = (AccT){0, 0, 0, 0};
+  for (int b = 0; b < RB; ++b)
+#pragma unroll
+    for (int t = 0; t < MB; ++t) acc[b][t] = (AccT){0, 0, 0, 0};
 #pragma unroll
   for (int st = 0; st < NST - 1; ++st)
     if (st < nst) issue(st);
-  const int lr = wave * 16 + n;
   for (int st = 0; st < nst; ++st) {
     // issued so far: stages 0 .. min(nst, st + NST - 1) - 1
     wait_stage<C, NST>(min(NST - 2, nst - 1 - st));
@@ -182,16 +185,22 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, 
     const char* xb = wb + TR * ROWB;
 #pragma unroll
     for (int s = 0; s < KC / KSTEP; ++s) {
-      const V8 a = *(const V8*)(wb + lr * ROWB + (((4 * s + j) ^ (lr & 15)) * 16));
+      V8 a[RB];
+#pragma unroll
+      for (int b = 0; b < RB; ++b) {
+        const int lr = wave * 16 * RB + 16 * b + n;
+        a[b] = *(const V8*)(wb + lr * ROWB + (((4 * s + j) ^ (lr & 15)) * 16));
+      }
 #pragma unroll
       for (int t = 0; t < MB; ++t) {
         const int xr = 16 * t + n;
-        const V8 b = *(const V8*)(xb + xr * ROWB + (((4 * s + j) ^ (xr & 15)) * 16));
-        acc[t] = mfma16x16x32(a, b, acc[t]);
+        const V8 xv = *(const V8*)(xb + xr * ROWB + (((4 * s + j) ^ (xr & 15)) * 16));
+#pragma unroll
+        for (int b = 0; b < RB; ++b) acc[b][t] = mfma16x16x32(a[b], xv, acc[b][t]);
       }
     }
   }
-  // acc[t][i] = Y[token 16t + n][channel row0 + 16*wave + 4j + i]
+  // acc[b][t][i] = Y[token 16t + n][channel row0 + 16*RB*wave + 16b + 4j + i]
   if constexpr (ES == 1) {
     // int8: exact int32 partial sums, part[split][m][n] (part points at int32)
     int32_t* ip = (int32_t*)part;
@@ -202,86 +211,100 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, 
       if (tok >= M || ch >= N) continue;
       int32_t* pp = ip + ((int64_t)split * M + tok) * N + ch;
       if (ch + 3 < N && (N & 3) == 0) {
-        *(i32x4*)pp = acc[t];
+        *(i32x4*)pp = acc[0][t];
       } else {
-        for (int i = 0; i < 4 && ch + i < N; ++i) pp[i] = acc[t][i];
+        for (int i = 0; i < 4 && ch + i < N; ++i) pp[i] = acc[0][t][i];
       }
     }
     return;
   } else if constexpr (EPI == 1) {
     // waves 2, 3 (up rows) hand their sums to waves 0, 1 (gate rows) through LDS
-    float* ub = (float*)smem;  // [32 channels][16 * MB tokens]
-    lds_barrier();             // every wave is done reading the last stage
+    constexpr int HALF = TR / 2;  // gate channels of the tile
+    float* ub = (float*)smem;     // [HALF channels][16 * MB tokens]
+    lds_barrier();                // every wave is done reading the last stage
     if (wave >= 2) {
 #pragma unroll
-      for (int t = 0; t < MB; ++t)
+      for (int b = 0; b < RB; ++b)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) ub[(16 * (wave - 2) + 4 * j + i) * (16 * MB) + 16 * t + n] = acc[t][i];
+        for (int t = 0; t < MB; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            ub[(16 * RB * (wave - 2) + 16 * b + 4 * j + i) * (16 * MB) + 16 * t + n] = acc[b][t][i];
     }
     lds_barrier();
     if (wave < 2) {
       const int I = N / 2;
-      const int c0 = blockIdx.x * 32 + 16 * wave + 4 * j;
 #pragma unroll
-      for (int t = 0; t < MB; ++t) {
-        const int tok = 16 * t + n;
-        if (tok >= M) continue;
+      for (int b = 0; b < RB; ++b) {
+        const int cl = 16 * RB * wave + 16 * b + 4 * j;  // channel within the tile
+        const int c0 = blockIdx.x * HALF + cl;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          if (c0 + i >= I) continue;
-          const float g = ll_to_f32(ll_from_f32<T>(acc[t][i]));
-          const float u = ll_to_f32(ll_from_f32<T>(ub[(16 * wave + 4 * j + i) * (16 * MB) + 16 * t + n]));
-          const T sv = ll_from_f32<T>(g / (1.0f + __expf(-g)));
-          Y[(int64_t)tok * ldy + c0 + i] = ll_from_f32<T>(u * ll_to_f32(sv));
+        for (int t = 0; t < MB; ++t) {
+          const int tok = 16 * t + n;
+          if (tok >= M) continue;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            if (c0 + i >= I) continue;
+            const float g = ll_to_f32(ll_from_f32<T>(acc[b][t][i]));
+            const float u = ll_to_f32(ll_from_f32<T>(ub[(cl + i) * (16 * MB) + 16 * t + n]));
+            const T sv = ll_from_f32<T>(g / (1.0f + __expf(-g)));
+            Y[(int64_t)tok * ldy + c0 + i] = ll_from_f32<T>(u * ll_to_f32(sv));
+          }
         }
       }
     }
     return;
   } else {
-    const int ch = row0 + wave * 16 + 4 * j;
 #pragma unroll
-    for (int t = 0; t < MB; ++t) {
-      const int tok = 16 * t + n;
-      if (tok >= M || ch >= N) continue;
-      if (part != nullptr) {
-        float* pp = part + ((int64_t)split * M + tok) * N + ch;
-        if (ch + 3 < N && (N & 3) == 0) {
-          *(f32x4*)pp = acc[t];
+    for (int b = 0; b < RB; ++b) {
+      const int ch = row0 + wave * 16 * RB + 16 * b + 4 * j;
+#pragma unroll
+      for (int t = 0; t < MB; ++t) {
+        const int tok = 16 * t + n;
+        if (tok >= M || ch >= N) continue;
+        if (part != nullptr) {
+          float* pp = part + ((int64_t)split * M + tok) * N + ch;
+          if (ch + 3 < N && (N & 3) == 0) {
+            *(f32x4*)pp = acc[b][t];
+          } else {
+            for (int i = 0; i < 4 && ch + i < N; ++i) pp[i] = acc[b][t][i];
+          }
         } else {
-          for (int i = 0; i < 4 && ch + i < N; ++i) pp[i] = acc[t][i];
+          T* yp = Y + (int64_t)tok * ldy + ch;
+          for (int i = 0; i < 4 && ch + i < N; ++i)
+            yp[i] = ll_from_f32<T>(acc[b][t][i] + (bias != nullptr ? ll_to_f32(bias[ch + i]) : 0.f));
         }
-      } else {
-        T* yp = Y + (int64_t)tok * ldy + ch;
-        for (int i = 0; i < 4 && ch + i < N; ++i)
-          yp[i] = ll_from_f32<T>(acc[t][i] + (bias != nullptr ? ll_to_f32(bias[ch + i]) : 0.f));
       }
     }
   }
 }
 
-// Packed weight layout for the DMA kernel: block (kc, t) = rows 64t..64t+63,
-// columns 128kc..128kc+127, stored as the 16 KB LDS image of that stage
-// (unit u = 64 * ii + lane holds row 4 ii + lane / 16, 16 B chunk
+// Packed weight layout for the DMA kernel with tr-row tiles (64 or 128):
+// block (kc, t) = rows tr*t..tr*t+tr-1, row chunk kc (256 bytes: 128 bf16/fp16
+// or 256 int8 columns), stored as the LDS image of that stage (unit
+// u = 64 * ii + lane holds row 4 ii + lane / 16, 16 B chunk
 // (lane % 16) ^ (row & 15)); blocks ordered kc-major; rows >= N are zero.
 // gu_half > 0: W is [gate; up] with gu_half rows each, and tile t takes gate
-// rows 32t..32t+31 as its rows 0..31 and the same up rows as its rows 32..63.
+// rows (tr/2)t.. as its rows 0..tr/2-1 and the same up rows as the rest.
 __global__ __launch_bounds__(256) void gemm_pack_kernel(const u32x4* __restrict__ W, int64_t ldw16,
                                                         u32x4* __restrict__ out, int N, int tiles,
-                                                        int64_t units, int gu_half) {
+                                                        int64_t units, int gu_half, int tr) {
   const int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (u >= units) return;
-  const int64_t blk = u >> 10;
-  const int within = (int)(u & 1023);
+  const int per_blk = tr * 16;  // 16 B units of one block
+  const int64_t blk = u / per_blk;
+  const int within = (int)(u - blk * per_blk);
   const int ii = within >> 6, lane = within & 63;
   const int kc = (int)(blk / tiles), t = (int)(blk - (int64_t)kc * tiles);
   const int r = ii * 4 + (lane >> 4);
   const int c = (lane & 15) ^ (r & 15);
-  int row = t * kDmaTR + r;
+  int row = t * tr + r;
   bool ok = row < N;
   if (gu_half > 0) {
-    const int ch = t * 32 + (r & 31);
+    const int half = tr / 2;
+    const int ch = t * half + (r % half);
     ok = ch < gu_half;
-    row = (r < 32) ? ch : gu_half + ch;
+    row = (r < half) ? ch : gu_half + ch;
   }
   u32x4 v = {0u, 0u, 0u, 0u};
   if (ok) v = W[(int64_t)row * ldw16 + (int64_t)kc * (kDmaKC / 8) + c];
@@ -550,6 +573,7 @@ struct SkinnyPlan {
   bool dma;
   int splits;  // K splits across workgroups (all non-empty)
   int ksps;    // 32-wide k-steps per split
+  int tr;      // DMA kernel: rows per tile (64, or 128 for wide one-split 16-bit weights)
   int tiles;   // row tiles
   int nst;     // LDS stage buffers of the DMA kernel
   int rotate;  // DMA kernel: rotate the k-chunk order per workgroup
@@ -565,6 +589,7 @@ SkinnyPlan plan_skinny(int64_t N, int64_t K, int es = 2) {
   p.nst = 2;
   p.rotate = 0;
   p.packed = false;
+  p.tr = kDmaTR;
   const int ksteps = (int)((K + 31) / 32);
   p.dma = ((K * es) % 256 == 0);
   if (p.dma) {
@@ -574,6 +599,9 @@ SkinnyPlan plan_skinny(int64_t N, int64_t K, int es = 2) {
     // one split and two stage buffers (two workgroups per CU) when they are
     // many; rotating each workgroup's k-chunk order spreads the concurrent
     // reads over more HBM channels.
+    // With one split and more 64-row tiles than CUs (lm_head), 128-row tiles
+    // with three stage buffers (one workgroup per CU) are faster: each
+    // activation stage then serves twice the weight rows.
     const int chunks = (int)(K * es / 256);
     p.tiles = (int)((N + kDmaTR - 1) / kDmaTR);
     int sp = 256 / p.tiles;
@@ -584,6 +612,11 @@ SkinnyPlan plan_skinny(int64_t N, int64_t K, int es = 2) {
     p.ksps = per * 4;
     p.nst = (p.tiles * p.splits <= 256) ? 3 : 2;
     p.rotate = 1;
+    if (es == 2 && p.splits == 1 && p.tiles > 256) {
+      p.tr = 128;
+      p.tiles = (int)((N + 127) / 128);
+      p.nst = 3;
+    }
   } else {
     p.tiles = (int)((N + 16 * kDirWR - 1) / (16 * kDirWR));
     int sp = 1;
@@ -595,20 +628,30 @@ SkinnyPlan plan_skinny(int64_t N, int64_t K, int es = 2) {
   return p;
 }
 
+// Tile height of the fused gate/up kernel (one split): 128 rows (64 gate + 64
+// up channels) once 64-row tiles would outnumber the CUs, as for plan_skinny.
+int gate_up_tr(int64_t I) { return ll_cdiv(I, 32) > 256 ? 128 : 64; }
+
 template <typename T, int MB>
 void launch_skinny_mb(const SkinnyPlan& p, const T* X, int64_t ldx, const T* W, int64_t ldw,
                       const T* bias, T* Y, int64_t ldy, float* part, int M, int N, int K,
                       hipStream_t stream) {
   const dim3 grid((unsigned)p.tiles, (unsigned)p.splits);
   if (p.dma) {
-    const size_t lds = (size_t)p.nst * (kDmaTR + 16 * MB) * 256;
-#define LL_DMA_LAUNCH(S, PKD)                                                                   \
-  hipLaunchKernelGGL((gemm_dma_kernel<T, MB, S, PKD>), grid, dim3(256), lds, stream, X, ldx, W, \
-                     ldw, bias, Y, ldy, part, M, N, K, p.ksps, p.rotate)
+    const size_t lds = (size_t)p.nst * (p.tr + 16 * MB) * 256;
+#define LL_DMA_LAUNCH(S, PKD, TR_)                                                              \
+  hipLaunchKernelGGL((gemm_dma_kernel<T, MB, S, PKD, 0, TR_>), grid, dim3(256), lds, stream, X, \
+                     ldx, W, ldw, bias, Y, ldy, part, M, N, K, p.ksps, p.rotate)
+    if constexpr (sizeof(T) == 2) {
+      if (p.tr == 128) {
+        if (p.packed) LL_DMA_LAUNCH(3, true, 128); else LL_DMA_LAUNCH(3, false, 128);
+        return;
+      }
+    }
     if (p.packed) {
-      if (p.nst == 3) LL_DMA_LAUNCH(3, true); else LL_DMA_LAUNCH(2, true);
+      if (p.nst == 3) LL_DMA_LAUNCH(3, true, 64); else LL_DMA_LAUNCH(2, true, 64);
     } else {
-      if (p.nst == 3) LL_DMA_LAUNCH(3, false); else LL_DMA_LAUNCH(2, false);
+      if (p.nst == 3) LL_DMA_LAUNCH(3, false, 64); else LL_DMA_LAUNCH(2, false, 64);
     }
 #undef LL_DMA_LAUNCH
   } else if constexpr (sizeof(T) == 2) {
@@ -708,9 +751,19 @@ extern "C" int ll_gemm_splitk(const void* X, int64_t ldx, const void* W, int64_t
                           false, stream);
 }
 
+extern "C" int ll_gemm_packed_tile_rows(int64_t N, int64_t K) {
+  if (N <= 0 || K <= 0 || K % kDmaKC != 0) return 0;
+  return plan_skinny(N, K).tr;
+}
+
+extern "C" int ll_gemm_packed_gate_up_tile_rows(int64_t I) {
+  return I > 0 ? gate_up_tr(I) : 0;
+}
+
 extern "C" int64_t ll_gemm_packed_bytes(int64_t N, int64_t K) {
   if (N <= 0 || K <= 0 || K % kDmaKC != 0) return 0;
-  return ll_cdiv(N, kDmaTR) * kDmaTR * K * 2;
+  const int tr = plan_skinny(N, K).tr;
+  return ll_cdiv(N, tr) * tr * K * 2;
 }
 
 extern "C" int ll_gemm_pack(const void* W, int64_t ldw, int64_t N, int64_t K, int dtype, void* Wp,
@@ -725,15 +778,17 @@ extern "C" int ll_gemm_pack(const void* W, int64_t ldw, int64_t N, int64_t K, in
   LL_CHECK_ARG(wp_bytes >= bytes, "ll_gemm_pack: output too small (need %lld bytes)",
                (long long)bytes);
   const int64_t units = bytes / 16;
-  const int tiles = (int)ll_cdiv(N, kDmaTR);
+  const int tr = plan_skinny(N, K).tr;
+  const int tiles = (int)ll_cdiv(N, tr);
   hipLaunchKernelGGL(gemm_pack_kernel, dim3((unsigned)ll_cdiv(units, 256)), dim3(256), 0, stream,
-                     (const u32x4*)W, ldw / 8, (u32x4*)Wp, (int)N, tiles, units, 0);
+                     (const u32x4*)W, ldw / 8, (u32x4*)Wp, (int)N, tiles, units, 0, tr);
   LL_RETURN_LAUNCH();
 }
 
 extern "C" int64_t ll_gemm_packed_gate_up_bytes(int64_t I, int64_t K) {
   if (I <= 0 || K <= 0 || K % kDmaKC != 0) return 0;
-  return ll_cdiv(I, 32) * kDmaTR * K * 2;
+  const int tr = gate_up_tr(I);
+  return ll_cdiv(I, tr / 2) * tr * K * 2;
 }
 
 extern "C" int ll_gemm_pack_gate_up(const void* W, int64_t ldw, int64_t I, int64_t K, int dtype,
@@ -748,9 +803,10 @@ extern "C" int ll_gemm_pack_gate_up(const void* W, int64_t ldw, int64_t I, int64
   LL_CHECK_ARG(wp_bytes >= bytes, "ll_gemm_pack_gate_up: output too small (need %lld bytes)",
                (long long)bytes);
   const int64_t units = bytes / 16;
-  const int tiles = (int)ll_cdiv(I, 32);
+  const int tr = gate_up_tr(I);
+  const int tiles = (int)ll_cdiv(I, tr / 2);
   hipLaunchKernelGGL(gemm_pack_kernel, dim3((unsigned)ll_cdiv(units, 256)), dim3(256), 0, stream,
-                     (const u32x4*)W, ldw / 8, (u32x4*)Wp, (int)(2 * I), tiles, units, (int)I);
+                     (const u32x4*)W, ldw / 8, (u32x4*)Wp, (int)(2 * I), tiles, units, (int)I, tr);
   LL_RETURN_LAUNCH();
 }
 
@@ -763,8 +819,9 @@ extern "C" int ll_gemm_gate_up_silu_packed(const void* X, int64_t ldx, const voi
   LL_CHECK_ARG(dtype == LL_BF16 || dtype == LL_F16, "ll_gemm_gate_up_silu_packed: bf16/fp16 only");
   LL_CHECK_ARG(ldx % 8 == 0 && (((uintptr_t)X | (uintptr_t)Wp) % 16) == 0,
                "ll_gemm_gate_up_silu_packed: X rows must be 16 B aligned");
-  const int tiles = (int)ll_cdiv(I, 32);
-  const int nst = tiles <= 256 ? 3 : 2;
+  const int tr = gate_up_tr(I);
+  const int tiles = (int)ll_cdiv(I, tr / 2);
+  const int nst = (tr == 128 || tiles <= 256) ? 3 : 2;
   const int ksps = (int)(K / 32);
   auto run = [&](auto tag) {
     typedef decltype(tag) T;
@@ -774,8 +831,12 @@ extern "C" int ll_gemm_gate_up_silu_packed(const void* X, int64_t ldx, const voi
     const dim3 grid((unsigned)tiles, 1);
 #define LL_GU(MB_)                                                                              \
   do {                                                                                          \
-    const size_t lds = (size_t)nst * (kDmaTR + 16 * MB_) * kDmaKC * 2;                          \
-    if (nst == 3)                                                                               \
+    const size_t lds = (size_t)nst * (tr + 16 * MB_) * kDmaKC * 2;                              \
+    if (tr == 128)                                                                              \
+      hipLaunchKernelGGL((gemm_dma_kernel<T, MB_, 3, true, 1, 128>), grid, dim3(256), lds,       \
+                         stream, x, ldx, w, K, nullptr, y, ld_act, nullptr, (int)M, (int)(2 * I), \
+                         (int)K, ksps, 0);                                                      \
+    else if (nst == 3)                                                                          \
       hipLaunchKernelGGL((gemm_dma_kernel<T, MB_, 3, true, 1>), grid, dim3(256), lds, stream, x, \
                          ldx, w, K, nullptr, y, ld_act, nullptr, (int)M, (int)(2 * I), (int)K,  \
                          ksps, 0);                                                              \
@@ -889,7 +950,7 @@ extern "C" int ll_gemm_i8_pack(const int8_t* Wq, int64_t ldw, int64_t N, int64_t
   const int64_t units = bytes / 16;
   hipLaunchKernelGGL(gemm_pack_kernel, dim3((unsigned)ll_cdiv(units, 256)), dim3(256), 0, stream,
                      (const u32x4*)Wq, ldw / 16, (u32x4*)Wp, (int)N, (int)ll_cdiv(N, kDmaTR),
-                     units, 0);
+                     units, 0, kDmaTR);
   LL_RETURN_LAUNCH();
 }
 

@@ -359,31 +359,39 @@ def test_gemm_wide_n_lds_path(cuda, M, N, K):
 
 
 # ------------------------------------------------------------ packed weights
-def _pack_reference(w):
-    """Host restatement of the ll_gemm_pack layout: block (kc, t) of 16 KB holds
-    rows 64t + 4ii + lane//16, 16 B chunk (lane % 16) ^ (row % 16) of the
-    128-column chunk kc, at unit 64 ii + lane; blocks kc-major; rows >= N zero."""
+def _pack_reference(w, tr=64):
+    """Host restatement of the ll_gemm_pack layout with tr-row tiles: block
+    (kc, t) of tr * 256 bytes holds rows tr*t + 4ii + lane//16, 16 B chunk
+    (lane % 16) ^ (row % 16) of the 128-column chunk kc, at unit 64 ii + lane;
+    blocks kc-major; rows >= N zero."""
     N, K = w.shape
-    T = -(-N // 64)
-    wp = torch.zeros(T * 64, K, dtype=w.dtype)
+    T = -(-N // tr)
+    wp = torch.zeros(T * tr, K, dtype=w.dtype)
     wp[:N] = w
-    u = wp.view(torch.int16).numpy().reshape(T, 64, K // 128, 16, 8)  # [t, r, kc, chunk, 8]
-    ii, lane = np.meshgrid(np.arange(16), np.arange(64), indexing="ij")
+    u = wp.view(torch.int16).numpy().reshape(T, tr, K // 128, 16, 8)  # [t, r, kc, chunk, 8]
+    ii, lane = np.meshgrid(np.arange(tr // 4), np.arange(64), indexing="ij")
     r = 4 * ii + lane // 16
     c = (lane % 16) ^ (r % 16)
-    blocks = u[:, r, :, c, :]  # advanced indices split by a slice lead: [16, 64, t, kc, 8]
+    blocks = u[:, r, :, c, :]  # advanced indices split by a slice lead: [tr/4, 64, t, kc, 8]
     return torch.from_numpy(np.ascontiguousarray(blocks.transpose(3, 2, 0, 1, 4))).reshape(-1)
 
 
-@pytest.mark.parametrize("N,K", [(200, 256), (128, 128), (2560, 2048)])
-def test_gemm_pack_layout(cuda, N, K):
+def _tile_rows(N, K):
+    from lite_lang_amd import _lib
+    return _lib.load().ll_gemm_packed_tile_rows(N, K)
+
+
+@pytest.mark.parametrize("N,K,tr", [(200, 256, 64), (128, 128, 64), (2560, 2048, 64),
+                                    (16500, 256, 128), (17000, 384, 128)])
+def test_gemm_pack_layout(cuda, N, K, tr):
     g = torch.Generator().manual_seed(45)
     w = torch.randn(N, K, generator=g).bfloat16()
     print(f"case: gemm_pack N={N} K={K}", flush=True)
+    assert _tile_rows(N, K) == tr  # one split over > 256 64-row tiles -> 128-row tiles
     wp = _ops().pack_weight(w.to(cuda))
     torch.cuda.synchronize()
     got = wp.data.cpu().view(torch.int16)
-    assert torch.equal(got, _pack_reference(w))
+    assert torch.equal(got, _pack_reference(w, tr))
 
 
 @pytest.mark.parametrize("M,N,K", [(40, 2560, 2048), (40, 2048, 11008), (1, 22016, 2048),
@@ -439,21 +447,25 @@ def test_gate_up_silu_fused_equals_unfused(cuda, M, I, K):
     assert _close_rel(fused, ref)
 
 
-def test_gate_up_pack_layout(cuda):
+@pytest.mark.parametrize("I,K,tr", [(70, 256, 64), (8200, 128, 128)])
+def test_gate_up_pack_layout(cuda, I, K, tr):
+    from lite_lang_amd import _lib
     g = torch.Generator().manual_seed(49)
-    I, K = 70, 256
     w = torch.randn(2 * I, K, generator=g).bfloat16()
+    print(f"case: gate_up pack I={I} K={K}", flush=True)
+    assert _lib.load().ll_gemm_packed_gate_up_tile_rows(I) == tr
     wp = _ops().pack_gate_up(w.to(cuda))
     torch.cuda.synchronize()
-    T = -(-I // 32)
-    # interleaved row order: tile t = gate rows 32t..32t+31, then up rows 32t..32t+31
-    rows = torch.zeros(T * 64, K, dtype=torch.bfloat16)
-    for t in range(T):
-        for r in range(64):
-            ch = 32 * t + (r % 32)
-            if ch < I:
-                rows[64 * t + r] = w[ch] if r < 32 else w[I + ch]
-    assert torch.equal(wp.data.cpu().view(torch.int16), _pack_reference(rows))
+    half = tr // 2
+    T = -(-I // half)
+    # interleaved row order: tile t = gate rows half*t.., then the same up rows
+    r = np.arange(T * tr)
+    ch = (r // tr) * half + (r % half)
+    src = np.where((r % tr) < half, ch, I + ch)
+    rows = torch.zeros(T * tr, K, dtype=torch.bfloat16)
+    ok = torch.from_numpy(ch < I)
+    rows[ok] = w[torch.from_numpy(src[ch < I])]
+    assert torch.equal(wp.data.cpu().view(torch.int16), _pack_reference(rows, tr))
 
 
 def test_add_rmsnorm_splitk(cuda):
