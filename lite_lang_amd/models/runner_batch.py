@@ -127,7 +127,8 @@ class RunnerBatch:
         self.host = None
         self._dev = None
         self._ring = None
-        self._pending = []  # (ring row, requests, event)
+        self._pending = []  # (ring row, requests, event), oldest first
+        self._next_row = 0  # ring rows are used cyclically
         self._refresh_host()
 
     # ------------------------------------------------------------ metadata
@@ -199,6 +200,19 @@ class RunnerBatch:
                 req._output_tokens.append(int(ring[row, j]))
                 req._batch = None
         self._pending = []
+        self._next_row = 0
+
+    def _retire_oldest(self):
+        """Hand the oldest in-flight step's tokens to its requests and free its
+        ring row. That step finished long before the newest one, so this waits
+        for nothing in steady state (flush() would drain the whole stream)."""
+        row, reqs, ev = self._pending.pop(0)
+        ev.synchronize()
+        vals = self._ring[row].numpy()
+        for j, req in enumerate(reqs):
+            if req._output_tokens is None:
+                req._output_tokens = []
+            req._output_tokens.append(int(vals[j]))
 
     def update_forward_message(self, output_token_ids):
         """Record one generated token per request and move to decode metadata
@@ -213,8 +227,9 @@ class RunnerBatch:
             self._ring = torch.empty((self.TOKEN_RING, max(B, 1)), dtype=torch.int64,
                                      pin_memory=True)
         if len(self._pending) == self.TOKEN_RING:
-            self.flush()
-        row = len(self._pending)
+            self._retire_oldest()
+        row = self._next_row
+        self._next_row = (row + 1) % self.TOKEN_RING
         self._ring[row, :B].copy_(out, non_blocking=True)
         ev = torch.cuda.Event()
         ev.record()

@@ -58,6 +58,36 @@ def test_config1_fp32_greedy_tokens_identical(cuda, graph):
     assert got.tolist() == ref.tolist()
 
 
+def test_token_ring_wraps(cuda):
+    """150 decode steps: the host token ring (64 rows) wraps twice, retiring its
+    oldest row each step; every request's output_tokens must equal the tokens
+    the device produced, in order."""
+    from lite_lang_amd.models.qwen2 import Qwen2ModelRunner
+    from lite_lang_amd.models.qwen2.weights import random_state_dict
+    from lite_lang_amd.models.runner_batch import RunnerBatch
+    cfg, _ = _cfgs()
+    sd = random_state_dict(cfg, seed=3)
+    print("case: token ring 150 steps batch 3", flush=True)
+    runner = Qwen2ModelRunner(cfg.layer_nums, 8, cfg, tp_rank=0, world_size=1, model_path=None,
+                              max_length=256, mem_usage=0.5, use_radix_cache=False,
+                              dtype=torch.bfloat16, state_dict=sd, kv_max_size=2048, device=cuda,
+                              use_cuda_graph=True)
+    runner.init_model()
+    g = torch.Generator().manual_seed(9)
+    prompts = [torch.randint(0, 1024, (n,), generator=g).tolist() for n in (5, 12, 9)]
+    msgs = [{"id": i, "input_tokens": p, "temperature": 0.0, "top_p": 1.0, "top_k": 1,
+             "do_sample": False} for i, p in enumerate(prompts)]
+    batch = RunnerBatch.create_batch(msgs, "ring", is_prefill=True, model_runner=runner)
+    seen = []
+    for _ in range(150):
+        out = runner.forward(batch)
+        seen.append(out.view(-1).cpu().clone())
+        batch.update_forward_message(out)
+    want = torch.stack(seen, 1).tolist()
+    got = [r.output_tokens for r in batch.request_mapping.values()]
+    assert got == want
+
+
 @pytest.mark.parametrize("graph", [True, False])
 def test_tiny_bf16_ragged_batch_logits(cuda, graph):
     from lite_lang_amd.models.qwen2.weights import random_state_dict
