@@ -11,6 +11,8 @@ from .pause_strategy import STRATEGY_REGISTRY, select_swapped_reqs
 from .req_queue import ReadyQue, Req, ReqStatus, SchedulerRunnerQue
 from .scheduler import Scheduler
 from .model_client import LocalModelClient, IdTokenizer
+from .tokenizer import Tokenizer
 
 __all__ = ["Scheduler", "Req", "ReqStatus", "ReadyQue", "SchedulerRunnerQue",
-           "STRATEGY_REGISTRY", "select_swapped_reqs", "LocalModelClient", "IdTokenizer"]
+           "STRATEGY_REGISTRY", "select_swapped_reqs", "LocalModelClient", "IdTokenizer",
+           "Tokenizer"]

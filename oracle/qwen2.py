@@ -40,6 +40,7 @@ class Qwen2Cfg:
     eps: float = 1e-6
     final_eps: float = 1e-5
     theta: float = 1e6
+    table_dtype: torch.dtype = torch.float16  # storage of the cos/sin table (pre_layer.py:30)
 
     @property
     def head_dim(self) -> int:
@@ -79,7 +80,7 @@ class Qwen2Oracle:
         D, KVH = cfg.head_dim, cfg.kv_heads
         self.pool = torch.zeros((cfg.num_layers, kv_slots, 2 * KVH, D), dtype=torch.float64)
         self.cache = PageCache(max_batch, max_length, kv_slots)
-        cos, sin = ops.rope_table(max_length, D, cfg.theta)
+        cos, sin = ops.rope_table(max_length, D, cfg.theta, cfg.table_dtype)
         self.cos, self.sin = cos.to(torch.float64), sin.to(torch.float64)
 
     def _linear(self, x, w, names, bias=None):

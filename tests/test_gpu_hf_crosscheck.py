@@ -1,0 +1,105 @@
+"""The GPU path loading a checkpoint written by Hugging Face transformers
+(tests/hf_tiny.py) through model_path, against transformers' own greedy
+generation on the CPU.
+
+The product keeps the reference's fp16-stored cos/sin table (pre_layer.py:30),
+so its logits differ from HF's by that rounding: fp32 runs are held to
+max-abs 2e-2 on the logits, and a generated token is compared wherever HF's
+top-1 margin exceeds four times the logits difference observed at that step
+(with this checkpoint every step qualifies; the test asserts so). The final
+norm uses HF's eps (HF has one eps; the reference's final norm has its own).
+The scheduler test goes text -> Tokenizer -> Scheduler -> runner -> text and
+compares token ids and decoded text with HF's, up to the first eos, on prompts
+whose HF top-1 margins all exceed 0.05 (asserted). Where HF has a near tie the
+fp16 table may pick the other token: with prompt seed 21 the fourth request
+meets a 0.002 margin at step 4, and there the GPU path picks what the CPU
+oracle with the reference's fp16 table picks.
+"""
+import os
+
+import pytest
+import torch
+
+from tests.hf_tiny import EOS, corpus, hf_greedy, make_checkpoint, min_margin
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ckpt(tmp_path_factory):
+    d = str(tmp_path_factory.mktemp("qwen2_tiny_hf_gpu"))
+    return d, make_checkpoint(d, seed=0)
+
+
+def _runner(path, cuda, dtype, graph=True, max_batch=8):
+    from lite_lang_amd.models.qwen2 import Qwen2ModelRunner
+    from lite_lang_amd.models.qwen2.weights import Qwen2Config
+    cfg = Qwen2Config.from_json(os.path.join(path, "config.json"))
+    cfg.final_norm_eps = cfg.rms_norm_eps  # HF applies one eps to every norm
+    runner = Qwen2ModelRunner(cfg.layer_nums, max_batch, cfg, model_path=path, max_length=128,
+                              dtype=dtype, kv_max_size=1024, device=cuda, use_cuda_graph=graph)
+    runner.init_model()
+    return runner
+
+
+@pytest.mark.parametrize("graph", [True, False])
+def test_product_greedy_matches_hf(cuda, ckpt, graph):
+    from transformers import AutoTokenizer
+    from lite_lang_amd.models.runner_batch import RunnerBatch
+    d, hf = ckpt
+    tok = AutoTokenizer.from_pretrained(d, local_files_only=True)
+    prompts = [tok(t)["input_ids"] for t in corpus(3, seed=7)]
+    n_new = 12
+    print(f"case: HF checkpoint fp32 via model_path, graph={graph}", flush=True)
+    runner = _runner(d, cuda, torch.float32, graph)
+    msgs = [{"id": i, "input_tokens": list(p), "temperature": 0.0, "top_p": 1.0, "top_k": 1,
+             "do_sample": False} for i, p in enumerate(prompts)]
+    batch = RunnerBatch.create_batch(msgs, "hf", is_prefill=True, model_runner=runner)
+    logits = []
+    for _ in range(n_new):
+        out = runner.forward(batch)
+        logits.append(runner.model_ins_.last_logits.float().cpu())
+        batch.update_forward_message(out)
+    got = [r.output_tokens for r in batch.request_mapping.values()]
+    logits = torch.stack(logits, 1)
+    for b, p in enumerate(prompts):
+        ref_ids, ref_logits = hf_greedy(hf, p, n_new)
+        for s in range(n_new):
+            err = float((logits[b, s] - ref_logits[s]).abs().max())
+            assert err <= 2e-2, f"prompt {b} step {s}: logits differ by {err}"
+            top2 = ref_logits[s].topk(2).values
+            margin = float(top2[0] - top2[1])
+            assert margin > 4 * err, f"prompt {b} step {s}: near tie in HF ({margin} vs {err})"
+            assert got[b][s] == int(ref_ids[s]), f"prompt {b} step {s}"
+
+
+def test_scheduler_text_matches_hf(cuda, ckpt):
+    from transformers import AutoTokenizer
+    from lite_lang_amd.scheduler import LocalModelClient, Scheduler, Tokenizer
+    d, hf = ckpt
+    ref_tok = AutoTokenizer.from_pretrained(d, local_files_only=True)
+    texts = corpus(4, seed=7)
+    max_out = 10
+    print("case: HF checkpoint text through the scheduler", flush=True)
+    runner = _runner(d, cuda, torch.float32)
+    sch = Scheduler(max_batch_size=4, tokenizer=Tokenizer(d), max_total_length=max_out + 1,
+                    max_output_length=max_out, max_reqs=16, model_client=LocalModelClient(runner),
+                    busy_scale=0.9)
+    reqs = [sch.add_req(t, 1.0, 1, 0.0, False) for t in texts]
+    rounds = 0
+    while rounds < 100 and not all(r.is_end for r in reqs):
+        sch.forward()
+        rounds += 1
+    assert all(r.is_end for r in reqs)
+    for r, t in zip(reqs, texts):
+        ids = ref_tok(t)["input_ids"]
+        assert r.input_tokens == ids
+        ref, ref_logits = hf_greedy(hf, ids, max_out)
+        # precondition: no near tie in HF, so the fp16 cos/sin table cannot flip a choice
+        assert min_margin(ref_logits) > 0.05, "prompt set has a near tie; pick another seed"
+        ref_ids = ref.tolist()
+        if EOS in ref_ids:
+            ref_ids = ref_ids[: ref_ids.index(EOS) + 1]
+        assert r.output_tokens == ref_ids, f"request {r.id}"
+        want = ref_tok.decode(ref_ids, skip_special_tokens=True, clean_up_tokenization_spaces=False)
+        assert sch.tokenizer_.decode([r.output_tokens]) == [want]
