@@ -16,7 +16,9 @@
 //     token loop -- the kernel is bound by how many bytes are in flight;
 //   * per tile S^T = K . Q^T on v_mfma_f32_16x16x32 (the G heads padded to 16
 //     columns) and O^T += V^T . P^T on v_mfma_f32_16x16x16, whose B operand
-//     is exactly the S^T accumulator layout, so P never leaves registers;
+//     is exactly the S^T accumulator layout, so P never leaves registers; P
+//     enters as a high and a low part in the KV dtype (two MFMAs), keeping
+//     the reference's fp32 probabilities to ~2^-17 instead of rounding them;
 //   * the split count is fixed per launch and each sequence divides its own
 //     length into that many tile-aligned chunks, so the grid does not depend
 //     on the lengths (graph safe);
@@ -367,13 +369,18 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
     const float m_new = fmaxf(m_run, tmax);  // finite: the tile's first token is valid
     const float alpha = exp2f(m_run - m_new);
-    V4 pb;
+    // P stays (nearly) fp32 as in the reference's fp32 p * v accumulation
+    // (flash_decoding.py:94-98): p = hi + lo with both parts in T, two MFMAs,
+    // relative error of hi + lo about 2^-17 (bf16) / 2^-22 (fp16)
+    V4 pb, pl;
     float psum = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float p = exp2f(x[i] - m_new);
       psum += p;
-      pb[i] = bits16((T)p);
+      const T ph = (T)p;
+      pb[i] = bits16(ph);
+      pl[i] = bits16((T)(p - ll_to_f32(ph)));
     }
     l_run = l_run * alpha + psum;
     m_run = m_new;
@@ -389,7 +396,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
         const T v = *(const T*)(vb + r * TG::ROWB + TG::swz(d >> 3, r) * 16 + (d & 7) * 2);
         va[i] = bits16(ok[i] ? v : (T)0.f);
       }
-      acc[c] = mfma16x16x16(va, pb, acc[c] * alpha);
+      acc[c] = mfma16x16x16(va, pl, mfma16x16x16(va, pb, acc[c] * alpha));
     }
     // this buffer is refilled by the next issue: its LDS reads must be done
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
