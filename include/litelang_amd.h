@@ -281,6 +281,14 @@ int ll_gemm_i8_pack(const int8_t* Wq, int64_t ldw, int64_t N, int64_t K, void* W
 int ll_gemm_i8_splitk_count(int64_t M, int64_t N, int64_t K);
 int ll_gemm_i8_splitk_packed(const int8_t* Xq, int64_t ldx, const void* Wp, int64_t M, int64_t N,
                              int64_t K, int32_t* part, int64_t part_bytes, hipStream_t stream);
+/* Static per-tensor activation quantisation with a calibrated input scale
+ * (the quant_scale buffer of W8A8BFP32OFP32LinearWithQuantScale,
+ * quantize/smooth_quant/layer.py:63-94, whose runtime the reference never
+ * wrote): Q[m, k] = clamp(round_half_even(fp32(X[m, k]) / s), -128, 127) with
+ * s = *scale (device fp32, > 0); s_tok[m] = s for ll_dequant_splitk. */
+int ll_quant_static(const void* X, int64_t ldx, int64_t M, int64_t K, int dtype,
+                    const float* scale, int8_t* Q, int64_t ldq, float* s_tok,
+                    hipStream_t stream);
 /* out[m][n] = fp32(sum_s part[s][m][n]) * s_tok[m] * fp32(s_ch[n]): the fp32
  * single-split partial the fused consumers above read (N % 4 == 0). */
 int ll_dequant_splitk(const int32_t* part, int splits, const float* s_tok, const void* s_ch,

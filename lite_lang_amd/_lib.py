@@ -58,6 +58,7 @@ SIGNATURES = {
     "ll_gemm_i8_pack": (I32, [P, I64, I64, I64, P, I64, P]),
     "ll_gemm_i8_splitk_count": (I32, [I64, I64, I64]),
     "ll_gemm_i8_splitk_packed": (I32, [P, I64, P, I64, I64, I64, P, I64, P]),
+    "ll_quant_static": (I32, [P, I64, I64, I64, I32, P, P, I64, P, P]),
     "ll_dequant_splitk": (I32, [P, I32, P, P, I32, P, I64, I64, P]),
     "ll_add_rmsnorm_splitk": (I32, [P, I64, P, I32, P, P, I64, I64, I64, F32, I32, P]),
     "ll_silu_and_mul_splitk": (I32, [P, I32, P, I64, I64, I64, I32, P]),

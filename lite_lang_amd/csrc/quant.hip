@@ -9,6 +9,8 @@
 // activation quantisation; the north star fixes per-token absmax):
 //   s_t = max_k |x[t, k]| / 127 in fp32 (1 when the row is all zeros)
 //   q   = clamp(round_half_even(x / s_t), -128, 127)
+// or static per tensor where a converted checkpoint carries a calibrated
+// input scale (quant_scale of smooth_quant/layer.py:63-94): s_t = fp32(s_a).
 // Dequantisation: y = fp32(sum of int32 partials) * s_t * fp32(s_o).
 #include "ll_common.h"
 
@@ -62,6 +64,21 @@ __global__ __launch_bounds__(256) void quant_token_kernel(const T* __restrict__ 
   for (int k = threadIdx.x; k < K; k += 256) q[k] = quant1(ll_to_f32(row[k]), s);
 }
 
+// Static per-tensor activation quantisation with a calibrated scale held in
+// device memory (*scale > 0): q = clamp(rne(x / s)); s_tok[m] = s so that the
+// dequantisation below applies unchanged.
+template <typename T>
+__global__ __launch_bounds__(256) void quant_static_kernel(const T* __restrict__ X, int64_t ldx,
+                                                           int K, const float* __restrict__ scale,
+                                                           int8_t* __restrict__ Q, int64_t ldq,
+                                                           float* __restrict__ s_tok) {
+  const float s = *scale;
+  if (threadIdx.x == 0) s_tok[blockIdx.x] = s;
+  const T* row = X + (int64_t)blockIdx.x * ldx;
+  int8_t* q = Q + (int64_t)blockIdx.x * ldq;
+  for (int k = threadIdx.x; k < K; k += 256) q[k] = quant1(ll_to_f32(row[k]), s);
+}
+
 // out[m][n] = fp32(sum_s part[s][m][n]) * s_tok[m] * fp32(s_ch[n]); 4 columns per thread
 template <typename S>
 __global__ __launch_bounds__(256) void dequant_splitk_kernel(const int32_t* __restrict__ part,
@@ -106,6 +123,19 @@ extern "C" int ll_quant_per_token(const void* X, int64_t ldx, int64_t M, int64_t
   return LL_DISPATCH_DTYPE(dtype, T, [&]() -> int {
     hipLaunchKernelGGL((quant_token_kernel<T>), dim3((unsigned)M), dim3(256), 0, stream,
                        (const T*)X, ldx, (int)K, Q, ldq, scale);
+    LL_RETURN_LAUNCH();
+  });
+}
+
+extern "C" int ll_quant_static(const void* X, int64_t ldx, int64_t M, int64_t K, int dtype,
+                               const float* scale, int8_t* Q, int64_t ldq, float* s_tok,
+                               hipStream_t stream) {
+  LL_CHECK_ARG(X && scale && Q && s_tok, "ll_quant_static: null pointer");
+  LL_CHECK_ARG(M >= 0 && K > 0 && ldx >= K && ldq >= K, "ll_quant_static: bad shape");
+  if (M == 0) return LL_OK;
+  return LL_DISPATCH_DTYPE(dtype, T, [&]() -> int {
+    hipLaunchKernelGGL((quant_static_kernel<T>), dim3((unsigned)M), dim3(256), 0, stream,
+                       (const T*)X, ldx, (int)K, scale, Q, ldq, s_tok);
     LL_RETURN_LAUNCH();
   });
 }

@@ -21,7 +21,8 @@ from lite_lang_amd import ops
 from lite_lang_amd.models.cache import PageCache
 from lite_lang_amd.models.radix_cache import RadixTree
 from .decode_graph import DecodeGraph
-from .weights import DeviceWeights, Qwen2Config, load_state_dict, random_state_dict
+from .weights import (DeviceWeights, Qwen2Config, check_smoothquant_config, is_int8_checkpoint,
+                      load_state_dict, random_state_dict)
 
 
 def rope_tables(max_length: int, head_dim: int, theta: float, device):
@@ -310,6 +311,11 @@ class Qwen2ModelRunner:
             sd = self.state_dict_
         elif self.model_path_:
             sd = load_state_dict(self.model_path_)
+            if is_int8_checkpoint(sd):
+                # the SmoothQuant converter's output runs on the W8A8 runtime
+                check_smoothquant_config(self.model_path_)
+                if self.model_ins_.quant is None:
+                    self.model_ins_.quant = "w8a8"
         else:
             sd = random_state_dict(self.config_, seed=self.seed_, device=self.device_,
                                    dtype=self.dtype_)

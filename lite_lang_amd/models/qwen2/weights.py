@@ -126,26 +126,65 @@ def random_state_dict(cfg: Qwen2Config, seed: int = 0, std: float = 0.02, device
 
 
 def load_state_dict(model_path: str):
-    """Read every tensor of a (possibly sharded) safetensors checkpoint on the
-    CPU (model.py:61-97)."""
-    from safetensors import safe_open
+    """Read every tensor of a (possibly sharded) checkpoint on the CPU
+    (model.py:61-97): safetensors files, or the pytorch_model*.bin files the
+    SmoothQuant converter writes (save_pretrained(..., safe_serialization=
+    False), quantize/smooth_quant.py:245), read with torch.load(weights_only=
+    True) so nothing in them is executed."""
+    def shards(index_name):
+        with open(os.path.join(model_path, index_name)) as f:
+            return sorted(set(json.load(f)["weight_map"].values()))
 
-    index = None
-    for name in ("model.safetensors.index.json", "pytorch_model.safetensors.index.json"):
-        if os.path.exists(os.path.join(model_path, name)):
-            index = os.path.join(model_path, name)
-    files = []
-    if index is not None:
-        with open(index) as f:
-            files = sorted(set(json.load(f)["weight_map"].values()))
-    else:
+    def exists(name):
+        return os.path.exists(os.path.join(model_path, name))
+
+    if exists("model.safetensors.index.json"):
+        files = shards("model.safetensors.index.json")
+    elif exists("model.safetensors"):
         files = ["model.safetensors"]
+    elif exists("pytorch_model.bin.index.json"):
+        files = shards("pytorch_model.bin.index.json")
+    elif exists("pytorch_model.bin"):
+        files = ["pytorch_model.bin"]
+    else:
+        raise FileNotFoundError(f"no model.safetensors or pytorch_model.bin in {model_path}")
     sd = {}
     for fn in files:
-        with safe_open(os.path.join(model_path, fn), framework="pt") as f:
-            for k in f.keys():
-                sd[k] = f.get_tensor(k)
+        path = os.path.join(model_path, fn)
+        if fn.endswith(".safetensors"):
+            from safetensors import safe_open
+            with safe_open(path, framework="pt") as f:
+                for k in f.keys():
+                    sd[k] = f.get_tensor(k)
+        else:
+            sd.update(torch.load(path, map_location="cpu", weights_only=True))
     return sd
+
+
+def is_int8_checkpoint(sd: dict) -> bool:
+    """True for the SmoothQuant converter's output: int8 projection weights
+    with per-channel weight_scale (quantize/smooth_quant/layer.py:19-94)."""
+    w = sd.get("model.layers.0.self_attn.q_proj.weight")
+    return w is not None and w.dtype == torch.int8
+
+
+def check_smoothquant_config(model_path: str) -> None:
+    """Reject converter settings this runtime cannot serve. With "qkv" or
+    "fc1" set to "per-channel" the converter divides input_layernorm /
+    post_attention_layernorm by the calibrated input scale
+    (smooth_quant/qwen2.py:183-192) but stores that scale nowhere, so the
+    int8 products of q/k/v (gate/up) could not be scaled back."""
+    path = os.path.join(model_path, "quant_config.json")
+    if not os.path.exists(path):
+        return
+    with open(path, encoding="utf-8") as f:
+        qc = json.load(f)
+    for key, norm in (("qkv", "input_layernorm"), ("fc1", "post_attention_layernorm")):
+        if qc.get(key) == "per-channel":
+            raise ValueError(
+                f"quant_config {key!r} = 'per-channel': the converter folded the calibrated "
+                f"input scale into {norm} without saving it, so these int8 outputs cannot be "
+                "dequantised; convert with per-token activations for this projection")
 
 
 class DeviceWeights:
@@ -159,20 +198,26 @@ class DeviceWeights:
         self.embed = dev(sd["model.embed_tokens.weight"])
         self.norm = dev(sd["model.norm.weight"])
         self.lm_head = self.embed if cfg.tie_word_embeddings else dev(sd["lm_head.weight"])
+        int8 = is_int8_checkpoint(sd)
+        if int8 and quant != "w8a8":
+            raise ValueError("an int8 (SmoothQuant converter) checkpoint runs with quant='w8a8'")
         self.layers = []
         for i in range(cfg.layer_nums):
             p = f"model.layers.{i}."
             lw = {}
-            lw["wqkv"] = dev(torch.cat([sd[p + "self_attn.q_proj.weight"],
-                                        sd[p + "self_attn.k_proj.weight"],
-                                        sd[p + "self_attn.v_proj.weight"]], 0))
+            if int8:  # the projections exist only as int8 (below)
+                lw["wqkv"] = lw["wo"] = lw["wgu"] = lw["wdown"] = None
+            else:
+                lw["wqkv"] = dev(torch.cat([sd[p + "self_attn.q_proj.weight"],
+                                            sd[p + "self_attn.k_proj.weight"],
+                                            sd[p + "self_attn.v_proj.weight"]], 0))
+                lw["wo"] = dev(sd[p + "self_attn.o_proj.weight"])
+                lw["wgu"] = dev(torch.cat([sd[p + "mlp.gate_proj.weight"],
+                                           sd[p + "mlp.up_proj.weight"]], 0))
+                lw["wdown"] = dev(sd[p + "mlp.down_proj.weight"])
             bq = sd.get(p + "self_attn.q_proj.bias")
             lw["bqkv"] = None if bq is None else dev(torch.cat([
                 bq, sd[p + "self_attn.k_proj.bias"], sd[p + "self_attn.v_proj.bias"]], 0))
-            lw["wo"] = dev(sd[p + "self_attn.o_proj.weight"])
-            lw["wgu"] = dev(torch.cat([sd[p + "mlp.gate_proj.weight"],
-                                       sd[p + "mlp.up_proj.weight"]], 0))
-            lw["wdown"] = dev(sd[p + "mlp.down_proj.weight"])
             lw["ln1"] = dev(sd[p + "input_layernorm.weight"])
             lw["ln2"] = dev(sd[p + "post_attention_layernorm.weight"])
             self.layers.append(lw)
@@ -186,7 +231,11 @@ class DeviceWeights:
             # int8 projections (per-channel scales), the lm_head stays in the
             # model dtype as in the reference (smooth_quant/qwen2.py:249-250)
             from lite_lang_amd import ops
-            for lw, pk in zip(self.layers, self.packed):
+            for i, (lw, pk) in enumerate(zip(self.layers, self.packed)):
+                if int8:
+                    for name, parts in _I8_GROUPS:
+                        pk[name + "_i8"] = _int8_group(sd, f"model.layers.{i}.", parts, device)
+                    continue
                 for name in ("wqkv", "wo", "wgu", "wdown"):
                     pk[name + "_i8"] = ops.QuantWeight(lw[name])
             if pack and dtype in (torch.bfloat16, torch.float16):
@@ -205,8 +254,34 @@ class DeviceWeights:
         n = (self.norm.numel() + self.lm_head.numel()) * es
         for lw, pk in zip(self.layers, self.packed):
             for name, v in lw.items():
-                if v is None:
-                    continue
                 qw = pk.get(name + "_i8")
-                n += (v.numel() + qw.scale.numel() * es) if qw is not None else v.numel() * es
+                if qw is not None:
+                    n += qw.q.numel() + qw.scale.numel() * qw.scale.element_size()
+                elif v is not None:
+                    n += v.numel() * es
         return n
+
+
+# int8 projection groups of a converted checkpoint: (runtime name, checkpoint
+# modules concatenated along the output rows)
+_I8_GROUPS = (("wqkv", ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj")),
+              ("wo", ("self_attn.o_proj",)),
+              ("wgu", ("mlp.gate_proj", "mlp.up_proj")),
+              ("wdown", ("mlp.down_proj",)))
+
+
+def _int8_group(sd, prefix, parts, device):
+    """QuantWeight of the converter's modules (W8A8BFP32OFP32Linear[WithQuantScale],
+    smooth_quant/layer.py:19-94): int8 `weight` [out, in], `weight_scale` [out, 1]
+    kept in its stored dtype, `quant_scale` (static input scale) when present."""
+    from lite_lang_amd import ops
+    q = torch.cat([sd[prefix + m + ".weight"] for m in parts], 0)
+    s = torch.cat([sd[prefix + m + ".weight_scale"].reshape(-1) for m in parts], 0)
+    a = [sd.get(prefix + m + ".quant_scale") for m in parts]
+    if any(x is not None for x in a):
+        if any(x is None for x in a) or len({float(x) for x in a}) != 1:
+            raise ValueError(f"{prefix}{parts}: fused projections need one static input scale")
+        a = float(a[0])
+    else:
+        a = None
+    return ops.QuantWeight.from_int8(q.to(device), s.to(device), a)

@@ -484,6 +484,22 @@ def quant_per_token(x, q=None, s=None):
     return q, s
 
 
+def quant_static(x, scale, q=None, s=None):
+    """(int8 [M, K], fp32 scale [M] all equal to *scale): static per-tensor
+    quantisation with a calibrated input scale (device fp32 tensor, one element)."""
+    _dev(x, scale, q, s)
+    M, K = x.shape
+    assert x.stride(1) == 1 and scale.dtype == torch.float32 and scale.numel() == 1
+    if q is None:
+        q = torch.empty((M, K), dtype=torch.int8, device=x.device)
+    if s is None:
+        s = torch.empty((M,), dtype=torch.float32, device=x.device)
+    rc = _L.ll_quant_static(x.data_ptr(), x.stride(0), M, K, dtype_code(x), scale.data_ptr(),
+                            q.data_ptr(), q.stride(0), s.data_ptr(), _stream(x))
+    _lib.check(rc, "ll_quant_static")
+    return q, s
+
+
 class PackedI8Weight:
     """int8 weight [N, K] in the packed streaming layout, with its per-channel scale."""
 
@@ -529,30 +545,59 @@ def dequant_splitk(part, splits, s_tok, s_ch, out, M, N):
 
 
 class QuantWeight:
-    """W8A8 projection weight: int8 [N, K] (per-channel scales in the model
-    dtype) plus its packed streaming image when K % 256 == 0."""
+    """W8A8 projection weight: int8 [N, K] with per-channel scales (the model
+    dtype when quantised here, the checkpoint's dtype when loaded), its packed
+    streaming image when K % 256 == 0, and optionally a calibrated static
+    input scale (fp32 device tensor, one element; None = dynamic per token)."""
 
-    def __init__(self, w):
+    def __init__(self, w=None):
+        self.input_scale = None
+        if w is None:
+            return
         self.q, self.scale = quant_weight_per_channel(w)
         self.shape = tuple(w.shape)
         self.packed = PackedI8Weight(self.q, self.scale) if w.shape[1] % 256 == 0 else None
+
+    @classmethod
+    def from_int8(cls, q, scale, input_scale=None):
+        """Wrap an already quantised weight (a converted checkpoint's int8
+        `weight` and `weight_scale`, and its `quant_scale` when present)."""
+        _dev(q, scale)
+        self = cls()
+        N, K = q.shape
+        assert q.dtype == torch.int8 and scale.numel() == N
+        self.q, self.scale = q.contiguous(), scale.reshape(N).contiguous()
+        self.shape = (N, K)
+        self.packed = PackedI8Weight(self.q, self.scale) if K % 256 == 0 else None
+        if input_scale is not None:
+            s = float(input_scale)
+            if not s > 0.0:
+                raise _lib.LiteLangError(f"static input scale must be > 0 (got {s})")
+            self.input_scale = torch.tensor([s], dtype=torch.float32, device=q.device)
+        return self
 
 
 def linear_w8a8_fp32(x, qw: QuantWeight, out=None):
     """fp32 [M, N] = dequant(int8(x) @ int8(W)^T): the exact int32 product
     (the streaming kernel for M <= 64, torch's int8 matmul above that),
-    scaled by the per-token and per-channel scales."""
+    scaled by the activation (per-token, or the static input scale) and
+    per-channel weight scales."""
     _dev(x, out)
     M, K = x.shape
     N = qw.shape[0]
-    xq, st = quant_per_token(x)
+    xq, st = quant_per_token(x) if qw.input_scale is None else quant_static(x, qw.input_scale)
     if M <= 64 and qw.packed is not None:
         s = gemm_i8_splitk_count(M, N, K)
         part = workspace(x.device, "w8a8_part", s * M * N * 4).view(torch.int32)
         gemm_i8_splitk_packed(xq, qw.packed, part)
     else:
         s = 1
-        part = torch._int_mm(xq, qw.q.t())
+        if M <= 16:  # the library int8 GEMM takes more than 16 rows: zero rows, exact
+            xp = torch.zeros((17, K), dtype=torch.int8, device=x.device)
+            xp[:M] = xq
+            part = torch._int_mm(xp, qw.q.t())[:M]
+        else:
+            part = torch._int_mm(xq, qw.q.t())
     if out is None:
         out = torch.empty((M, N), dtype=torch.float32, device=x.device)
     return dequant_splitk(part, s, st, qw.scale, out, M, N)

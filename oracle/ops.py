@@ -196,6 +196,18 @@ def int8_gemm_i32(xq: torch.Tensor, wq: torch.Tensor) -> torch.Tensor:
     return (xq.to(torch.int64) @ wq.to(torch.int64).T).to(torch.int32)
 
 
+def quantize_static(x: torch.Tensor, s_a):
+    """Static per-tensor activation quantisation with a calibrated input scale
+    (the quant_scale buffer of smooth_quant/layer.py:63-94; the reference has
+    no runtime that applies it, so the rule is build-defined and the same as
+    the per-token one with a fixed scale): s = fp32(s_a);
+    q = clamp(round_half_even(fp32(x) / s), -128, 127). Returns (q, s_tok [M]
+    all equal to s)."""
+    s = float(s_a)
+    q = (x.to(torch.float32) / torch.tensor(s, dtype=torch.float32)).round().clamp(-128, 127)
+    return q.to(torch.int8), torch.full((x.shape[0],), s, dtype=torch.float32)
+
+
 def dequant_int32(acc: torch.Tensor, s_tok: torch.Tensor, s_ch: torch.Tensor) -> torch.Tensor:
     """fp32(acc) * s_tok[m] * fp32(s_ch[n]), evaluated in fp32 in that order
     (build-defined dequantisation of the W8A8 runtime)."""

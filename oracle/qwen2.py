@@ -54,15 +54,38 @@ class Qwen2Oracle:
         per-channel weight scales (quantize_weight_per_channel_absmax on the
         dtype-rounded weight, smooth_quant/layer.py:5-16) and dynamic
         per-token activation scales, dequantised in fp32 before the bias;
-        lm_head stays in the model dtype (smooth_quant/qwen2.py:249-250)."""
+        lm_head stays in the model dtype (smooth_quant/qwen2.py:249-250).
+        An int8 state dict (the SmoothQuant converter's output) supplies the
+        int8 weights and scales itself, and a projection with a quant_scale
+        quantises its input statically with that scale."""
         self.cfg, self.dtype, self.quant = cfg, dtype, quant
         r = lambda t: ops.rnd(t.detach().cpu(), dtype)  # noqa: E731
         self.embed = r(sd["model.embed_tokens.weight"])
         self.lm_head = self.embed if cfg.tie_word_embeddings else r(sd["lm_head.weight"])
         self.norm = r(sd["model.norm.weight"])
         self.layers = []
+        int8 = sd["model.layers.0.self_attn.q_proj.weight"].dtype == torch.int8
+        assert not int8 or quant == "w8a8", "an int8 checkpoint runs with quant='w8a8'"
         for i in range(cfg.num_layers):
             p = f"model.layers.{i}."
+            if int8:
+                # converter output (smooth_quant/layer.py:19-94): int8 weight,
+                # weight_scale [out, 1] in its stored dtype, quant_scale = static
+                # input scale where present; biases and norms stay float
+                w = dict(bq=r(sd[p + "self_attn.q_proj.bias"]), bk=r(sd[p + "self_attn.k_proj.bias"]),
+                         bv=r(sd[p + "self_attn.v_proj.bias"]),
+                         ln1=r(sd[p + "input_layernorm.weight"]),
+                         ln2=r(sd[p + "post_attention_layernorm.weight"]))
+                for nm, mod in (("wq", "self_attn.q_proj"), ("wk", "self_attn.k_proj"),
+                                ("wv", "self_attn.v_proj"), ("wo", "self_attn.o_proj"),
+                                ("wg", "mlp.gate_proj"), ("wu", "mlp.up_proj"),
+                                ("wd", "mlp.down_proj")):
+                    w[nm + "_i8"] = (sd[p + mod + ".weight"],
+                                     sd[p + mod + ".weight_scale"].reshape(-1))
+                    if sd.get(p + mod + ".quant_scale") is not None:
+                        w[nm + "_as"] = sd[p + mod + ".quant_scale"]
+                self.layers.append(w)
+                continue
             self.layers.append(dict(
                 wq=r(sd[p + "self_attn.q_proj.weight"]), bq=r(sd[p + "self_attn.q_proj.bias"]),
                 wk=r(sd[p + "self_attn.k_proj.weight"]), bk=r(sd[p + "self_attn.k_proj.bias"]),
@@ -73,7 +96,7 @@ class Qwen2Oracle:
                 ln1=r(sd[p + "input_layernorm.weight"]),
                 ln2=r(sd[p + "post_attention_layernorm.weight"]),
             ))
-        if quant == "w8a8":
+        if quant == "w8a8" and not int8:
             for w in self.layers:
                 for name in ("wq", "wk", "wv", "wo", "wg", "wu", "wd"):
                     w[name + "_i8"] = ops.quantize_weight_per_channel_absmax(w[name].to(dtype))
@@ -87,7 +110,11 @@ class Qwen2Oracle:
         if self.quant != "w8a8":
             wt = w[names[0]] if len(names) == 1 else torch.cat([w[n] for n in names], 0)
             return ops.linear(x, wt, bias)
-        xq, st = ops.quantize_per_token_absmax(x.to(self.dtype))
+        sa = w.get(names[0] + "_as")  # static input scale (o_proj, down_proj of a converted model)
+        if sa is not None:
+            xq, st = ops.quantize_static(x.to(self.dtype), sa)
+        else:
+            xq, st = ops.quantize_per_token_absmax(x.to(self.dtype))
         wq = torch.cat([w[n + "_i8"][0] for n in names], 0)
         so = torch.cat([w[n + "_i8"][1] for n in names], 0)
         y = ops.dequant_int32(ops.int8_gemm_i32(xq, wq), st, so).to(torch.float64)

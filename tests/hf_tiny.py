@@ -96,3 +96,61 @@ def min_margin(logits):
     """Smallest top-1 minus top-2 logit gap over the steps."""
     top2 = logits.topk(2, dim=-1).values
     return float((top2[:, 0] - top2[:, 1]).min())
+
+
+PROJ = ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj",
+        "mlp.gate_proj", "mlp.up_proj", "mlp.down_proj")
+
+
+def make_smoothquant_checkpoint(path: str, model, calib_ids, dtype=torch.float16,
+                                quant_config=None):
+    """Write what the reference's SmoothQuant converter saves
+    (quantize/smooth_quant.py:225-245 via QuantizedQwen2ForCausalLM,
+    smooth_quant/qwen2.py) for the float HF model, with smoothing factors of 1
+    (smoothing re-balances float weights before quantisation and does not
+    change the format):
+      * every projection: int8 `weight` and `weight_scale` [out, 1] from
+        quantize_weight_per_channel_absmax on the weight in `dtype`
+        (smooth_quant/layer.py:5-16, restated in oracle/ops.py);
+      * o_proj and down_proj: `quant_scale` = max |input| / 127 in `dtype`
+        over the calibration prompts (collect_llama_layer_scales,
+        quantize/smooth_quant.py:123-140);
+      * q/k/v biases, norms and embeddings in `dtype`; lm_head tied (not
+        stored); pytorch_model.bin (save_pretrained(safe_serialization=False)),
+        config.json and quant_config.json."""
+    import os
+    from oracle.ops import quantize_weight_per_channel_absmax
+    act = {}
+
+    def hook(mod, inp, out, name):
+        act[name] = max(act.get(name, 0.0), float(inp[0].abs().max()))
+
+    hooks = [m.register_forward_hook(lambda mod, i, o, name=name: hook(mod, i, o, name))
+             for name, m in model.named_modules()
+             if name.endswith("self_attn.o_proj") or name.endswith("mlp.down_proj")]
+    with torch.no_grad():
+        for ids in calib_ids:
+            model(torch.tensor([list(ids)]), use_cache=False)
+    for h in hooks:
+        h.remove()
+    sd = {}
+    for k, v in model.state_dict().items():
+        if k == "lm_head.weight":
+            continue
+        mod = k.rsplit(".", 1)[0]
+        if k.endswith(".weight") and mod.split("layers.")[-1].split(".", 1)[-1] in PROJ:
+            q, s = quantize_weight_per_channel_absmax(v.to(dtype))
+            sd[k] = q
+            sd[mod + ".weight_scale"] = s.view(-1, 1)
+            if mod in act:
+                sd[mod + ".quant_scale"] = torch.tensor(act[mod] / 127, dtype=dtype)
+        else:
+            sd[k] = v.to(dtype)
+    os.makedirs(path, exist_ok=True)
+    torch.save(sd, os.path.join(path, "pytorch_model.bin"))
+    model.config.save_pretrained(path)
+    qc = quant_config or {"qkv": "per-token", "out": "per-tensor", "fc1": "per-token",
+                          "fc2": "per-tensor"}
+    with open(os.path.join(path, "quant_config.json"), "w", encoding="utf-8") as f:
+        json.dump(qc, f)
+    return sd

@@ -42,7 +42,8 @@ def test_quant_per_token(cuda, M, K):
 
 
 @pytest.mark.parametrize("M,N,K", [(40, 2560, 2048), (40, 2048, 2048), (40, 22016, 2048),
-                                   (40, 2048, 11008), (1, 300, 512), (64, 200, 768), (17, 4096, 1536)])
+                                   (40, 2048, 11008), (1, 300, 512), (64, 200, 768), (17, 4096, 1536),
+                                   (3, 512, 256), (3, 256, 256), (3, 1376, 256), (40, 22016, 256)])
 def test_gemm_i8_splitk_exact(cuda, M, N, K):
     g = torch.Generator().manual_seed(62)
     xq = torch.randint(-128, 128, (M, K), generator=g, dtype=torch.int8)
