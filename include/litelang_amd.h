@@ -184,6 +184,23 @@ int ll_add_rmsnorm_splitk(void* h, int64_t h_row_stride, const float* part, int 
 /* part covers [M, 2N] (gate then up); out[m, n] = up * dtype(silu(gate)) */
 int ll_silu_and_mul_splitk(const float* part, int splits, void* out, int64_t out_row_stride,
                            int64_t M, int64_t N, int dtype, hipStream_t stream);
+/* W8A8 forms of the two consumers above (no reference counterpart: they fold
+ * ll_dequant_splitk into add+RMSNorm and SiLU_and_Mul for the int8 decode
+ * layer): int32 partials [splits][M][N] ([M][2N] for SiLU) with per-row
+ * activation scales s_tok [M] and per-column weight scales s_ch of
+ * s_ch_dtype, dequantised as ll_dequant_splitk does. With q_out (and
+ * q_scale), the RMSNorm output is also quantised per token for the next
+ * projection, with ll_quant_per_token's rule, into int8 q_out [M, ldq] and
+ * fp32 q_scale [M]; both null skips it. */
+int ll_add_rmsnorm_splitk_i32(void* h, int64_t h_row_stride, const int32_t* part, int splits,
+                              const float* s_tok, const void* s_ch, int s_ch_dtype,
+                              const void* gamma, void* out, int64_t out_row_stride, int64_t M,
+                              int64_t N, float eps, int dtype, int8_t* q_out, int64_t ldq,
+                              float* q_scale, hipStream_t stream);
+int ll_silu_and_mul_splitk_i32(const int32_t* part, int splits, const float* s_tok,
+                               const void* s_ch, int s_ch_dtype, void* out,
+                               int64_t out_row_stride, int64_t M, int64_t N, int dtype,
+                               hipStream_t stream);
 /* part covers [T, (q_heads + 2*kv_heads)*D]; adds bias, rotates q into q_out
  * [T, q_heads*D] and writes rotated K and V to pool_layer[slots[t]] */
 int ll_rope_kv_scatter_splitk(const float* part, int splits, const void* bias, void* q_out,
@@ -216,6 +233,21 @@ int ll_decode_attention_rope_splitk(
     int64_t out_stride_h, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
     int64_t max_len_in_batch, float sm_scale, int dtype, void* workspace,
     int64_t workspace_bytes, hipStream_t stream);
+/* The same with the W8A8 projection's int32 partials
+ * [qkv_splits][batch][(q_heads + 2*kv_heads)*head_dim] and their scales in
+ * place of fp32 partials: each column is dequantised as in ll_dequant_splitk
+ * (fp32(sum) * s_tok[b] * fp32(s_ch[col]), s_ch of s_ch_dtype) and then
+ * treated exactly as the fp32 entry point treats its partial sums. */
+int ll_decode_attention_rope_splitk_i32(
+    const int32_t* qkv_part, int qkv_splits, const float* s_tok, const void* s_ch, int s_ch_dtype,
+    const void* qkv_bias, const void* positions, int positions_i64, const void* cos_table,
+    const void* sin_table, int64_t table_row_stride, int cs_dtype, const int32_t* new_slots,
+    void* k_cache, int64_t k_stride_tok, int64_t k_stride_head, void* v_cache,
+    int64_t v_stride_tok, int64_t v_stride_head, const int32_t* req_to_tokens,
+    int64_t req_to_tokens_stride, const void* b_req_idx, int req_idx_i64, const void* b_seq_len,
+    int seq_len_i64, void* out, int64_t out_stride_b, int64_t out_stride_h, int64_t batch,
+    int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t max_len_in_batch,
+    float sm_scale, int dtype, void* workspace, int64_t workspace_bytes, hipStream_t stream);
 
 /* Pre-packed weights for the decode projections (no reference counterpart:
  * a layout of the same nn.Linear weight [N, K], chosen for MI355X). The

@@ -91,8 +91,7 @@ struct DecodeArgs {
   float* part_acc;    // [B*H*nsplit, D] unnormalised partial outputs
   float* part_ml;     // [B*H*nsplit, 2] running max (log2 domain) and sum
   // fused RoPE + new-token K/V write (ROPE kernels only)
-  const float* qkv_part;   // [qkv_splits][B][(H + 2 KVH) * D] fp32 split-K partials
-  int qkv_splits;
+  LLPartials qkv;          // [splits][B][(H + 2 KVH) * D] split-K partials (fp32, or int32 + scales)
   const void* qkv_bias;    // [(H + 2 KVH) * D] of the model dtype, or null
   const void* pos; int pos64;
   const float* cos_tab; const float* sin_tab; int64_t tab_stride;
@@ -105,9 +104,9 @@ struct DecodeArgs {
 // rounded to T, rotated in fp32 with explicit FMAs, rounded to T. V heads are
 // only rounded. Results go to LDS and, when glb is set, to global memory.
 template <typename T, int D>
-__device__ __forceinline__ void rope_job(const DecodeArgs& a, int64_t sstride, int64_t row,
-                                         int hcol, int i, const float* cs, const float* sn,
-                                         bool rotate, T* lds, T* glb) {
+__device__ __forceinline__ void rope_job(const DecodeArgs& a, int64_t m, int64_t row, int hcol,
+                                         int i, const float* cs, const float* sn, bool rotate,
+                                         T* lds, T* glb) {
   constexpr int HALF = D / 2;
   const int c0 = hcol + i, c1 = c0 + HALF;
   // bias and the cos/sin entries first: their loads share the partials' round trip
@@ -122,8 +121,8 @@ __device__ __forceinline__ void rope_job(const DecodeArgs& a, int64_t sstride, i
     cv[e] = cs[i + e];
     sv[e] = sn[i + e];
   }
-  f32x4 x0 = ll_sum_splits4(a.qkv_part, a.qkv_splits, sstride, row + c0);
-  f32x4 x1 = ll_sum_splits4(a.qkv_part, a.qkv_splits, sstride, row + c1);
+  f32x4 x0 = ll_partials_sum4(a.qkv, row + c0, m, c0);
+  f32x4 x1 = ll_partials_sum4(a.qkv, row + c1, m, c1);
   if (bias != nullptr) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -208,12 +207,11 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
   T* s_kv = s_q + a.G * D;                                     // ROPE: new token's K, V
   constexpr int QD = D / 8;  // RoPE jobs per head
   int32_t new_slot = 0;
-  int64_t qkv_sstride = 0, qkv_row = 0;
+  int64_t qkv_row = 0;
   const float* cs = nullptr;
   const float* sn = nullptr;
   if constexpr (ROPE) {
     const int width = (a.H + 2 * a.KVH) * D;
-    qkv_sstride = (int64_t)a.B * width;
     qkv_row = (int64_t)b * width;
     const int64_t p = ll_load_idx(a.pos, b, a.pos64);
     cs = a.cos_tab + p * a.tab_stride;
@@ -221,7 +219,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
     new_slot = a.new_slots[b];
     if ((int)threadIdx.x < a.G * QD) {  // G * QD <= 16 * D / 8 <= 256
       const int g = threadIdx.x / QD, i = (threadIdx.x % QD) * 4;
-      rope_job<T, D>(a, qkv_sstride, qkv_row, (kvh * a.G + g) * D, i, cs, sn, true, s_q + g * D,
+      rope_job<T, D>(a, b, qkv_row, (kvh * a.G + g) * D, i, cs, sn, true, s_q + g * D,
                      nullptr);
     }
   } else {
@@ -256,7 +254,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
       const int i = (isv ? jb - QD : jb) * 4;
       T* glb = isv ? (T*)a.v + (int64_t)new_slot * a.v_st + (int64_t)kvh * a.v_sh
                    : (T*)a.k + (int64_t)new_slot * a.k_st + (int64_t)kvh * a.k_sh;
-      rope_job<T, D>(a, qkv_sstride, qkv_row, (a.H + (isv ? a.KVH : 0) + kvh) * D, i, cs, sn,
+      rope_job<T, D>(a, b, qkv_row, (a.H + (isv ? a.KVH : 0) + kvh) * D, i, cs, sn,
                      !isv, s_kv + (isv ? D : 0), glb);
     }
   }
@@ -722,20 +720,22 @@ extern "C" int ll_decode_attention(const void* q, int64_t q_stride_b, int64_t q_
                      stream);
 }
 
-extern "C" int ll_decode_attention_rope_splitk(
-    const float* qkv_part, int qkv_splits, const void* qkv_bias, const void* positions,
-    int positions_i64, const void* cos_table, const void* sin_table, int64_t table_row_stride,
-    int cs_dtype, const int32_t* new_slots, void* k_cache, int64_t k_stride_tok,
-    int64_t k_stride_head, void* v_cache, int64_t v_stride_tok, int64_t v_stride_head,
-    const int32_t* req_to_tokens, int64_t req_to_tokens_stride, const void* b_req_idx,
-    int req_idx_i64, const void* b_seq_len, int seq_len_i64, void* out, int64_t out_stride_b,
-    int64_t out_stride_h, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
-    int64_t max_len_in_batch, float sm_scale, int dtype, void* workspace,
-    int64_t workspace_bytes, hipStream_t stream) {
-  LL_CHECK_ARG(qkv_part && positions && cos_table && sin_table && new_slots && k_cache &&
-                   v_cache && req_to_tokens && b_req_idx && b_seq_len && out,
+namespace {
+
+int rope_attention_impl(const LLPartials& qkv, const void* qkv_bias, const void* positions,
+                        int positions_i64, const void* cos_table, const void* sin_table,
+                        int64_t table_row_stride, int cs_dtype, const int32_t* new_slots,
+                        void* k_cache, int64_t k_stride_tok, int64_t k_stride_head, void* v_cache,
+                        int64_t v_stride_tok, int64_t v_stride_head, const int32_t* req_to_tokens,
+                        int64_t req_to_tokens_stride, const void* b_req_idx, int req_idx_i64,
+                        const void* b_seq_len, int seq_len_i64, void* out, int64_t out_stride_b,
+                        int64_t out_stride_h, int64_t batch, int64_t q_heads, int64_t kv_heads,
+                        int64_t head_dim, int64_t max_len_in_batch, float sm_scale, int dtype,
+                        void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  LL_CHECK_ARG(qkv.p && positions && cos_table && sin_table && new_slots && k_cache && v_cache &&
+                   req_to_tokens && b_req_idx && b_seq_len && out,
                "ll_decode_attention_rope_splitk: null pointer");
-  LL_CHECK_ARG(qkv_splits >= 1, "ll_decode_attention_rope_splitk: qkv_splits must be >= 1");
+  LL_CHECK_ARG(qkv.splits >= 1, "ll_decode_attention_rope_splitk: qkv_splits must be >= 1");
   LL_CHECK_ARG(cs_dtype == LL_F32, "ll_decode_attention_rope_splitk: cos/sin tables must be fp32");
   LL_CHECK_ARG(kv_heads > 0 && q_heads % kv_heads == 0 && q_heads / kv_heads <= 16,
                "ll_decode_attention_rope_splitk: needs q_heads = G * kv_heads with G <= 16");
@@ -744,7 +744,7 @@ extern "C" int ll_decode_attention_rope_splitk(
                "(other shapes: ll_rope_kv_scatter_splitk + ll_decode_attention)");
   LL_CHECK_ARG(k_stride_tok % 8 == 0 && k_stride_head % 8 == 0 && v_stride_tok % 8 == 0 &&
                    v_stride_head % 8 == 0 &&
-                   (((uintptr_t)qkv_part | (uintptr_t)k_cache | (uintptr_t)v_cache) % 16 == 0),
+                   (((uintptr_t)qkv.p | (uintptr_t)k_cache | (uintptr_t)v_cache) % 16 == 0),
                "ll_decode_attention_rope_splitk: K/V strides must be multiples of 8 elements, "
                "partials and caches 16 B aligned");
   LL_CHECK_ARG(max_len_in_batch >= 0 && max_len_in_batch <= INT32_MAX,
@@ -762,11 +762,56 @@ extern "C" int ll_decode_attention_rope_splitk(
   a.units = a.B * a.KVH;
   a.max_len = (int)max_len_in_batch;
   a.scale_log2 = sm_scale * 1.4426950408889634f;
-  a.qkv_part = qkv_part; a.qkv_splits = qkv_splits; a.qkv_bias = qkv_bias;
+  a.qkv = qkv;
+  a.qkv.sstride = batch * (q_heads + 2 * kv_heads) * head_dim;
+  a.qkv_bias = qkv_bias;
   a.pos = positions; a.pos64 = positions_i64;
   a.cos_tab = (const float*)cos_table; a.sin_tab = (const float*)sin_table;
   a.tab_stride = table_row_stride;
   a.new_slots = new_slots;
   return launch_mfma(a, head_dim, dtype, true, max_len_in_batch, workspace, workspace_bytes,
                      stream);
+}
+
+}  // namespace
+
+extern "C" int ll_decode_attention_rope_splitk(
+    const float* qkv_part, int qkv_splits, const void* qkv_bias, const void* positions,
+    int positions_i64, const void* cos_table, const void* sin_table, int64_t table_row_stride,
+    int cs_dtype, const int32_t* new_slots, void* k_cache, int64_t k_stride_tok,
+    int64_t k_stride_head, void* v_cache, int64_t v_stride_tok, int64_t v_stride_head,
+    const int32_t* req_to_tokens, int64_t req_to_tokens_stride, const void* b_req_idx,
+    int req_idx_i64, const void* b_seq_len, int seq_len_i64, void* out, int64_t out_stride_b,
+    int64_t out_stride_h, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+    int64_t max_len_in_batch, float sm_scale, int dtype, void* workspace,
+    int64_t workspace_bytes, hipStream_t stream) {
+  return rope_attention_impl(ll_partials_f32(qkv_part, qkv_splits, 0), qkv_bias, positions,
+                             positions_i64, cos_table, sin_table, table_row_stride, cs_dtype,
+                             new_slots, k_cache, k_stride_tok, k_stride_head, v_cache, v_stride_tok,
+                             v_stride_head, req_to_tokens, req_to_tokens_stride, b_req_idx,
+                             req_idx_i64, b_seq_len, seq_len_i64, out, out_stride_b, out_stride_h,
+                             batch, q_heads, kv_heads, head_dim, max_len_in_batch, sm_scale, dtype,
+                             workspace, workspace_bytes, stream);
+}
+
+extern "C" int ll_decode_attention_rope_splitk_i32(
+    const int32_t* qkv_part, int qkv_splits, const float* s_tok, const void* s_ch, int s_ch_dtype,
+    const void* qkv_bias, const void* positions, int positions_i64, const void* cos_table,
+    const void* sin_table, int64_t table_row_stride, int cs_dtype, const int32_t* new_slots,
+    void* k_cache, int64_t k_stride_tok, int64_t k_stride_head, void* v_cache,
+    int64_t v_stride_tok, int64_t v_stride_head, const int32_t* req_to_tokens,
+    int64_t req_to_tokens_stride, const void* b_req_idx, int req_idx_i64, const void* b_seq_len,
+    int seq_len_i64, void* out, int64_t out_stride_b, int64_t out_stride_h, int64_t batch,
+    int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t max_len_in_batch,
+    float sm_scale, int dtype, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  LL_CHECK_ARG(s_tok && s_ch, "ll_decode_attention_rope_splitk_i32: null scale pointer");
+  LL_CHECK_ARG(s_ch_dtype == LL_F32 || s_ch_dtype == LL_F16 || s_ch_dtype == LL_BF16,
+               "ll_decode_attention_rope_splitk_i32: bad scale dtype %d", s_ch_dtype);
+  LLPartials P = {qkv_part, qkv_splits, 0, s_tok, s_ch, s_ch_dtype, 1};
+  return rope_attention_impl(P, qkv_bias, positions, positions_i64, cos_table, sin_table,
+                             table_row_stride, cs_dtype, new_slots, k_cache, k_stride_tok,
+                             k_stride_head, v_cache, v_stride_tok, v_stride_head, req_to_tokens,
+                             req_to_tokens_stride, b_req_idx, req_idx_i64, b_seq_len, seq_len_i64,
+                             out, out_stride_b, out_stride_h, batch, q_heads, kv_heads, head_dim,
+                             max_len_in_batch, sm_scale, dtype, workspace, workspace_bytes, stream);
 }

@@ -462,15 +462,17 @@ __device__ __forceinline__ float ll_sum_splits(const float* __restrict__ part, i
 // h[m] = T(h[m] + T(sum_s part[s][m])); out[m] = rmsnorm(h[m]) * gamma.
 // One workgroup per row, 4 consecutive columns per thread and pass (N % 4 == 0,
 // N <= 4 * BLOCK * MAXP). The residual and gamma loads are unconditional (a
-// clamped column) so they join the partials' memory round trip.
+// clamped column) so they join the partials' memory round trip. With qout,
+// the stored output row is also quantised per token (ll_quant_per_token's
+// rule: s = max |out| / 127, 1 for a zero row) into qout / qscale.
 template <typename T, int BLOCK, int MAXP>
 __global__ __launch_bounds__(BLOCK) void add_rmsnorm_splitk_kernel(
-    T* __restrict__ h, int64_t h_rs, const float* __restrict__ part, int splits,
-    const T* __restrict__ gamma, T* __restrict__ out, int64_t o_rs, int M, int N, float eps) {
+    T* __restrict__ h, int64_t h_rs, LLPartials P, const T* __restrict__ gamma,
+    T* __restrict__ out, int64_t o_rs, int M, int N, float eps, int8_t* __restrict__ qout,
+    int64_t ldq, float* __restrict__ qscale) {
   constexpr int PER = 4;
   const int row = blockIdx.x;
   T* hr = h + (int64_t)row * h_rs;
-  const int64_t sstride = (int64_t)M * N;
   T hraw[MAXP][PER], graw[MAXP][PER];
 #pragma unroll
   for (int ps = 0; ps < MAXP; ++ps) {
@@ -487,7 +489,7 @@ __global__ __launch_bounds__(BLOCK) void add_rmsnorm_splitk_kernel(
   for (int ps = 0; ps < MAXP; ++ps) {
     const int c = (ps * BLOCK + threadIdx.x) * PER;
     if (c < N) {
-      const f32x4 o = ll_sum_splits4(part, splits, sstride, (int64_t)row * N + c);
+      const f32x4 o = ll_partials_sum4(P, (int64_t)row * N + c, row, c);
 #pragma unroll
       for (int e = 0; e < PER; ++e) {
         const T nh = ll_from_f32<T>(ll_to_f32(hraw[ps][e]) + ll_to_f32(ll_from_f32<T>(o[e])));
@@ -506,15 +508,66 @@ __global__ __launch_bounds__(BLOCK) void add_rmsnorm_splitk_kernel(
   for (int w = 0; w < BLOCK / 64; ++w) tot += red[w];
   const float denom = sqrtf(tot / (float)N + eps);
   T* orow = out + (int64_t)row * o_rs;
+  float amax = 0.f;
 #pragma unroll
   for (int ps = 0; ps < MAXP; ++ps) {
     const int c = (ps * BLOCK + threadIdx.x) * PER;
     if (c < N) {
 #pragma unroll
-      for (int e = 0; e < PER; ++e)
-        orow[c + e] = ll_from_f32<T>(hv[ps][e] / denom * ll_to_f32(graw[ps][e]));
+      for (int e = 0; e < PER; ++e) {
+        const T y = ll_from_f32<T>(hv[ps][e] / denom * ll_to_f32(graw[ps][e]));
+        orow[c + e] = y;
+        hv[ps][e] = ll_to_f32(y);
+        amax = fmaxf(amax, fabsf(hv[ps][e]));
+      }
     }
   }
+  if (qout == nullptr) return;
+  __shared__ float redm[BLOCK / 64];
+  amax = ll_wave_max(amax);
+  if ((threadIdx.x & 63) == 0) redm[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  float m = 0.f;
+#pragma unroll
+  for (int w = 0; w < BLOCK / 64; ++w) m = fmaxf(m, redm[w]);
+  float s = m / 127.f;
+  if (!(s > 0.f)) s = 1.f;
+  if (threadIdx.x == 0) qscale[row] = s;
+  int8_t* qrow = qout + (int64_t)row * ldq;
+#pragma unroll
+  for (int ps = 0; ps < MAXP; ++ps) {
+    const int c = (ps * BLOCK + threadIdx.x) * PER;
+    if (c < N) {
+#pragma unroll
+      for (int e = 0; e < PER; ++e) qrow[c + e] = ll_quant1(hv[ps][e], s);
+    }
+  }
+}
+
+template <typename T, int MAXP>
+void launch_add_rmsnorm_t(void* h, int64_t h_rs, const LLPartials& P, const void* gamma, void* out,
+                          int64_t o_rs, int64_t M, int64_t N, float eps, int8_t* qout, int64_t ldq,
+                          float* qscale, hipStream_t stream) {
+  hipLaunchKernelGGL((add_rmsnorm_splitk_kernel<T, 512, MAXP>), dim3((unsigned)M), dim3(512), 0,
+                     stream, (T*)h, h_rs, P, (const T*)gamma, (T*)out, o_rs, (int)M, (int)N, eps,
+                     qout, ldq, qscale);
+}
+
+int launch_add_rmsnorm(void* h, int64_t h_row_stride, const LLPartials& P, const void* gamma,
+                       void* out, int64_t out_row_stride, int64_t M, int64_t N, float eps,
+                       int dtype, int8_t* qout, int64_t ldq, float* qscale, hipStream_t stream) {
+  return LL_DISPATCH_DTYPE(dtype, T, [&]() -> int {
+    if (N <= 4 * 512)
+      launch_add_rmsnorm_t<T, 1>(h, h_row_stride, P, gamma, out, out_row_stride, M, N, eps, qout,
+                                 ldq, qscale, stream);
+    else if (N <= 4 * 512 * 2)
+      launch_add_rmsnorm_t<T, 2>(h, h_row_stride, P, gamma, out, out_row_stride, M, N, eps, qout,
+                                 ldq, qscale, stream);
+    else
+      launch_add_rmsnorm_t<T, 4>(h, h_row_stride, P, gamma, out, out_row_stride, M, N, eps, qout,
+                                 ldq, qscale, stream);
+    LL_RETURN_LAUNCH();
+  });
 }
 
 extern "C" int ll_add_rmsnorm_splitk(void* h, int64_t h_row_stride, const float* part, int splits,
@@ -527,37 +580,44 @@ extern "C" int ll_add_rmsnorm_splitk(void* h, int64_t h_row_stride, const float*
                (long long)N);
   LL_CHECK_ARG(((uintptr_t)part) % 16 == 0, "ll_add_rmsnorm_splitk: partials must be 16 B aligned");
   if (M == 0) return LL_OK;
-  return LL_DISPATCH_DTYPE(dtype, T, [&]() -> int {
-    if (N <= 4 * 512)
-      hipLaunchKernelGGL((add_rmsnorm_splitk_kernel<T, 512, 1>), dim3((unsigned)M), dim3(512), 0,
-                         stream, (T*)h, h_row_stride, part, splits, (const T*)gamma, (T*)out,
-                         out_row_stride, (int)M, (int)N, eps);
-    else if (N <= 4 * 512 * 2)
-      hipLaunchKernelGGL((add_rmsnorm_splitk_kernel<T, 512, 2>), dim3((unsigned)M), dim3(512), 0,
-                         stream, (T*)h, h_row_stride, part, splits, (const T*)gamma, (T*)out,
-                         out_row_stride, (int)M, (int)N, eps);
-    else
-      hipLaunchKernelGGL((add_rmsnorm_splitk_kernel<T, 512, 4>), dim3((unsigned)M), dim3(512), 0,
-                         stream, (T*)h, h_row_stride, part, splits, (const T*)gamma, (T*)out,
-                         out_row_stride, (int)M, (int)N, eps);
-    LL_RETURN_LAUNCH();
-  });
+  return launch_add_rmsnorm(h, h_row_stride, ll_partials_f32(part, splits, M * N), gamma, out,
+                            out_row_stride, M, N, eps, dtype, nullptr, 0, nullptr, stream);
+}
+
+extern "C" int ll_add_rmsnorm_splitk_i32(void* h, int64_t h_row_stride, const int32_t* part,
+                                         int splits, const float* s_tok, const void* s_ch,
+                                         int s_ch_dtype, const void* gamma, void* out,
+                                         int64_t out_row_stride, int64_t M, int64_t N, float eps,
+                                         int dtype, int8_t* q_out, int64_t ldq, float* q_scale,
+                                         hipStream_t stream) {
+  LL_CHECK_ARG(h && part && s_tok && s_ch && gamma && out, "ll_add_rmsnorm_splitk_i32: null pointer");
+  LL_CHECK_ARG(splits >= 1 && N > 0 && N % 4 == 0 && N <= 4 * 512 * 4,
+               "ll_add_rmsnorm_splitk_i32: N must be a multiple of 4 and <= 8192 (N=%lld)",
+               (long long)N);
+  LL_CHECK_ARG(((uintptr_t)part) % 16 == 0, "ll_add_rmsnorm_splitk_i32: partials must be 16 B aligned");
+  LL_CHECK_ARG((q_out == nullptr) == (q_scale == nullptr) && (q_out == nullptr || ldq >= N),
+               "ll_add_rmsnorm_splitk_i32: q_out and q_scale go together (ldq >= N)");
+  LL_CHECK_ARG(s_ch_dtype == LL_F32 || s_ch_dtype == LL_F16 || s_ch_dtype == LL_BF16,
+               "ll_add_rmsnorm_splitk_i32: bad scale dtype %d", s_ch_dtype);
+  if (M == 0) return LL_OK;
+  LLPartials P = {part, splits, M * N, s_tok, s_ch, s_ch_dtype, 1};
+  return launch_add_rmsnorm(h, h_row_stride, P, gamma, out, out_row_stride, M, N, eps, dtype,
+                            q_out, ldq, q_scale, stream);
 }
 
 // out[m][n] = T(u * T(silu(g))), g = T(sum part[.][m][n]), u = T(sum part[.][m][N + n]);
 // 4 consecutive columns per thread (N % 4 == 0).
 template <typename T>
-__global__ void silu_and_mul_splitk_kernel(const float* __restrict__ part, int splits,
-                                           T* __restrict__ out, int64_t o_rs, int M, int N) {
+__global__ void silu_and_mul_splitk_kernel(LLPartials P, T* __restrict__ out, int64_t o_rs, int M,
+                                           int N) {
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int q = N / 4;
   const int m = (int)(gid / q);
   if (m >= M) return;
   const int n = (int)(gid - (int64_t)m * q) * 4;
-  const int64_t sstride = (int64_t)M * 2 * N;
   const int64_t base = (int64_t)m * 2 * N;
-  const f32x4 g4 = ll_sum_splits4(part, splits, sstride, base + n);
-  const f32x4 u4 = ll_sum_splits4(part, splits, sstride, base + N + n);
+  const f32x4 g4 = ll_partials_sum4(P, base + n, m, n);
+  const f32x4 u4 = ll_partials_sum4(P, base + N + n, m, N + n);
   T* op = out + (int64_t)m * o_rs + n;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
@@ -568,6 +628,16 @@ __global__ void silu_and_mul_splitk_kernel(const float* __restrict__ part, int s
   }
 }
 
+int launch_silu_and_mul_splitk(const LLPartials& P, void* out, int64_t out_row_stride, int64_t M,
+                               int64_t N, int dtype, hipStream_t stream) {
+  const int64_t total = M * N / 4;
+  return LL_DISPATCH_DTYPE(dtype, T, [&]() -> int {
+    hipLaunchKernelGGL((silu_and_mul_splitk_kernel<T>), dim3((unsigned)((total + 255) / 256)),
+                       dim3(256), 0, stream, P, (T*)out, out_row_stride, (int)M, (int)N);
+    LL_RETURN_LAUNCH();
+  });
+}
+
 extern "C" int ll_silu_and_mul_splitk(const float* part, int splits, void* out,
                                       int64_t out_row_stride, int64_t M, int64_t N, int dtype,
                                       hipStream_t stream) {
@@ -575,12 +645,22 @@ extern "C" int ll_silu_and_mul_splitk(const float* part, int splits, void* out,
   LL_CHECK_ARG(N % 4 == 0 && ((uintptr_t)part) % 16 == 0,
                "ll_silu_and_mul_splitk: N must be a multiple of 4, partials 16 B aligned");
   if (M == 0 || N == 0) return LL_OK;
-  const int64_t total = M * N / 4;
-  return LL_DISPATCH_DTYPE(dtype, T, [&]() -> int {
-    hipLaunchKernelGGL((silu_and_mul_splitk_kernel<T>), dim3((unsigned)((total + 255) / 256)),
-                       dim3(256), 0, stream, part, splits, (T*)out, out_row_stride, (int)M, (int)N);
-    LL_RETURN_LAUNCH();
-  });
+  return launch_silu_and_mul_splitk(ll_partials_f32(part, splits, M * 2 * N), out, out_row_stride,
+                                    M, N, dtype, stream);
+}
+
+extern "C" int ll_silu_and_mul_splitk_i32(const int32_t* part, int splits, const float* s_tok,
+                                          const void* s_ch, int s_ch_dtype, void* out,
+                                          int64_t out_row_stride, int64_t M, int64_t N, int dtype,
+                                          hipStream_t stream) {
+  LL_CHECK_ARG(part && s_tok && s_ch && out, "ll_silu_and_mul_splitk_i32: null pointer");
+  LL_CHECK_ARG(N % 4 == 0 && ((uintptr_t)part) % 16 == 0 && splits >= 1,
+               "ll_silu_and_mul_splitk_i32: N must be a multiple of 4, partials 16 B aligned");
+  LL_CHECK_ARG(s_ch_dtype == LL_F32 || s_ch_dtype == LL_F16 || s_ch_dtype == LL_BF16,
+               "ll_silu_and_mul_splitk_i32: bad scale dtype %d", s_ch_dtype);
+  if (M == 0 || N == 0) return LL_OK;
+  LLPartials P = {part, splits, M * 2 * N, s_tok, s_ch, s_ch_dtype, 1};
+  return launch_silu_and_mul_splitk(P, out, out_row_stride, M, N, dtype, stream);
 }
 
 // qkv = T(sum part + bias); q heads rotated -> q_out [T, H*D]; k rotated and

@@ -102,6 +102,70 @@ __device__ __forceinline__ f32x4 ll_sum_splits4(const float* __restrict__ part, 
   return acc;
 }
 
+// One int8 code: clamp(round_half_even(x / s), -128, 127) with IEEE division.
+__device__ __forceinline__ int8_t ll_quant1(float x, float s) {
+  float q = __builtin_rintf(x / s);
+  q = fminf(fmaxf(q, -128.f), 127.f);
+  return (int8_t)(int)q;
+}
+
+// int32 counterpart of ll_sum_splits4 (exact in any order).
+__device__ __forceinline__ i32x4 ll_sum_splits4_i32(const int32_t* __restrict__ part, int splits,
+                                                    int64_t split_stride, int64_t idx) {
+  i32x4 acc = {0, 0, 0, 0};
+  int sp = 0;
+  if (splits <= 8) {
+    i32x4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      v[u] = *(const i32x4*)(part + (int64_t)min(u, splits - 1) * split_stride + idx);
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (u < splits) acc += v[u];
+    return acc;
+  }
+  for (; sp < splits; ++sp) acc += *(const i32x4*)(part + sp * split_stride + idx);
+  return acc;
+}
+
+// Split-K partial sums as the consumer kernels read them: fp32 partials (the
+// bf16/fp16 GEMMs) or the W8A8 GEMM's int32 partials with their activation
+// and channel scales, dequantised as fp32(sum) * s_tok[m] * fp32(s_ch[n]) --
+// the arithmetic of ll_dequant_splitk, so a fused consumer equals dequant +
+// the fp32 consumer bit for bit.
+struct LLPartials {
+  const void* p;        // const float* or const int32_t*
+  int splits;
+  int64_t sstride;      // elements between consecutive splits
+  const float* s_tok;   // int32 partials: per-row activation scale [M]
+  const void* s_ch;     // int32 partials: per-column weight scale [N]
+  int s_ch_dtype;       // LL_F32 / LL_F16 / LL_BF16
+  int i32;              // 1: int32 partials
+};
+
+__device__ __forceinline__ float ll_load_scale(const void* s, int dtype, int64_t i) {
+  if (dtype == LL_F16) return (float)((const _Float16*)s)[i];
+  if (dtype == LL_BF16) return (float)((const __bf16*)s)[i];
+  return ((const float*)s)[i];
+}
+
+// Columns col..col+3 of row m (idx = m * row_stride + col), summed over the splits.
+__device__ __forceinline__ f32x4 ll_partials_sum4(const LLPartials& P, int64_t idx, int64_t m,
+                                                  int64_t col) {
+  if (!P.i32) return ll_sum_splits4((const float*)P.p, P.splits, P.sstride, idx);
+  const i32x4 acc = ll_sum_splits4_i32((const int32_t*)P.p, P.splits, P.sstride, idx);
+  const float st = P.s_tok[m];
+  f32x4 o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = (float)acc[e] * st * ll_load_scale(P.s_ch, P.s_ch_dtype, col + e);
+  return o;
+}
+
+__host__ __device__ inline LLPartials ll_partials_f32(const float* p, int splits, int64_t sstride) {
+  LLPartials P = {p, splits, sstride, nullptr, nullptr, 0, 0};
+  return P;
+}
+
 // Rotate-half RoPE of one (x_i, x_{i+D/2}) pair, rounded to T. The fused
 // multiply-adds are written out so every kernel rotating a pair rounds it the
 // same way: y0 = fma(a, c, -(b*s)), y1 = fma(a, s, b*c).

@@ -30,11 +30,7 @@ __device__ float row_absmax(const T* __restrict__ row, int K, float* red) {
   return m;
 }
 
-__device__ __forceinline__ int8_t quant1(float x, float s) {
-  float q = __builtin_rintf(x / s);  // IEEE division, round half to even
-  q = fminf(fmaxf(q, -128.f), 127.f);
-  return (int8_t)(int)q;
-}
+__device__ __forceinline__ int8_t quant1(float x, float s) { return ll_quant1(x, s); }
 
 template <typename T>
 __global__ __launch_bounds__(256) void quant_weight_kernel(const T* __restrict__ W, int64_t ldw,

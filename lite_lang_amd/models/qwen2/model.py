@@ -122,6 +122,10 @@ class Qwen2Model:
         return max(ops.gemm_i8_splitk_count(batch, n, k) * batch * n * 4
                    for n, k in self._proj_shapes())
 
+    def _fused_rope_ok(self):
+        cfg = self.cfg
+        return cfg.head_dim in (64, 128) and cfg.num_heads // cfg.num_key_value_heads <= 16
+
     def _rope_attention(self, part, splits, bias, q, attn, positions, slots, pool_layer, r2t,
                         rids, seq_len, max_len):
         """RoPE + new-token K/V write + decode attention from the QKV split-K
@@ -129,7 +133,7 @@ class Qwen2Model:
         covers the shape, else the scatter kernel followed by attention."""
         cfg = self.cfg
         H, KVH, D = cfg.num_heads, cfg.num_key_value_heads, cfg.head_dim
-        if D in (64, 128) and H // KVH <= 16:
+        if self._fused_rope_ok():
             ops.decode_attention_rope_splitk(part, splits, bias, positions, self.cos, self.sin,
                                              slots, r2t, rids, seq_len, max_len,
                                              pool_layer[:, :KVH], pool_layer[:, KVH:], attn)
@@ -210,31 +214,56 @@ class Qwen2Model:
 
     def _decode_w8a8(self, h, B, part, q, attn, act, positions, seq_len, rids, slots, pool, r2t,
                      max_len, out):
-        """The fused decode layer with int8 projections: each projection is
-        per-token quantisation + the int8 streaming GEMM + dequantisation into
-        one fp32 split, finished by the same consumer kernels."""
+        """The fused decode layer with int8 projections (11 launches per layer):
+        each int8 GEMM leaves int32 partials that the next kernel dequantises
+        inline (fused RoPE attention, add+RMSNorm, SiLU_and_Mul), and add+RMSNorm
+        also emits the per-token int8 input of the following projection. Inputs
+        with a static scale (o_proj, down_proj of converted checkpoints) and the
+        attention output / SiLU product are quantised by their own kernel."""
         cfg, w = self.cfg, self.w
         H, KVH, D = cfg.num_heads, cfg.num_key_value_heads, cfg.head_dim
         nl = len(w.layers)
 
-        def proj(xin, pk, name):
-            qw = pk[name + "_i8"]
-            ops.linear_w8a8_fp32(xin, qw, out=part[: B * qw.shape[0]].view(B, qw.shape[0]))
+        def fused_quant(pk, name):
+            return pk[name + "_i8"].input_scale is None
 
         x = ops.rmsnorm(h, w.layers[0]["ln1"], cfg.rms_norm_eps)
+        xq, xs = ops.quant_input(x, w.packed[0]["wqkv_i8"])
         for li, (lw, pk) in enumerate(zip(w.layers, w.packed)):
-            proj(x, pk, "wqkv")
-            self._rope_attention(part, 1, lw["bqkv"], q, attn, positions, slots, pool[li], r2t,
-                                 rids, seq_len, max_len)
-            proj(attn.view(B, H * D), pk, "wo")
-            x2 = ops.add_rmsnorm_splitk(h, part, 1, lw["ln2"], cfg.rms_norm_eps)
-            proj(x2, pk, "wgu")
-            ops.silu_and_mul_splitk(part, 1, act)
-            proj(act, pk, "wdown")
-            if li + 1 < nl:
-                x = ops.add_rmsnorm_splitk(h, part, 1, w.layers[li + 1]["ln1"], cfg.rms_norm_eps)
+            p = ops.gemm_w8a8_i32(xq, xs, pk["wqkv_i8"])
+            if self._fused_rope_ok():
+                ops.decode_attention_rope_splitk_i32(
+                    p, lw["bqkv"], positions, self.cos, self.sin, slots, r2t, rids, seq_len,
+                    max_len, pool[li, :, :KVH], pool[li, :, KVH:], attn)
             else:
-                x = ops.add_rmsnorm_splitk(h, part, 1, w.norm, cfg.final_norm_eps)
+                n = p.s_ch.numel()
+                ops.dequant_splitk(p.part, p.splits, p.s_tok, p.s_ch, part[: B * n].view(B, n),
+                                   B, n)
+                self._rope_attention(part, 1, lw["bqkv"], q, attn, positions, slots, pool[li],
+                                     r2t, rids, seq_len, max_len)
+            aq, as_ = ops.quant_input(attn.view(B, H * D), pk["wo_i8"])
+            p = ops.gemm_w8a8_i32(aq, as_, pk["wo_i8"])
+            if fused_quant(pk, "wgu"):
+                _, x2q, x2s = ops.add_rmsnorm_splitk_i32(h, p, lw["ln2"], cfg.rms_norm_eps,
+                                                         quant=True)
+            else:
+                x2 = ops.add_rmsnorm_splitk_i32(h, p, lw["ln2"], cfg.rms_norm_eps)
+                x2q, x2s = ops.quant_input(x2, pk["wgu_i8"])
+            p = ops.gemm_w8a8_i32(x2q, x2s, pk["wgu_i8"])
+            ops.silu_and_mul_splitk_i32(p, act)
+            dq, ds = ops.quant_input(act, pk["wdown_i8"])
+            p = ops.gemm_w8a8_i32(dq, ds, pk["wdown_i8"])
+            if li + 1 < nl:
+                nxt = w.packed[li + 1]
+                if fused_quant(nxt, "wqkv"):
+                    x, xq, xs = ops.add_rmsnorm_splitk_i32(
+                        h, p, w.layers[li + 1]["ln1"], cfg.rms_norm_eps, quant=True)
+                else:
+                    x = ops.add_rmsnorm_splitk_i32(h, p, w.layers[li + 1]["ln1"],
+                                                   cfg.rms_norm_eps)
+                    xq, xs = ops.quant_input(x, nxt["wqkv_i8"])
+            else:
+                x = ops.add_rmsnorm_splitk_i32(h, p, w.norm, cfg.final_norm_eps)
         logits = ops.gemm_packed(x, w.lm_head_p) if w.lm_head_p is not None else ops.gemm(x, w.lm_head)
         self.last_logits = logits
         return ops.argmax(logits, out=out)

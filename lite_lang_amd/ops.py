@@ -455,6 +455,40 @@ def decode_attention_rope_splitk(part, splits, bias, positions, cos_table, sin_t
     return out
 
 
+def decode_attention_rope_splitk_i32(p, bias, positions, cos_table, sin_table, slots,
+                                     req_to_tokens, b_req_idx, b_seq_len, max_len_in_batch,
+                                     cache_k, cache_v, out, sm_scale=None):
+    """decode_attention_rope_splitk from the int8 QKV projection's int32
+    partials (an I8Partials), dequantised inline."""
+    _dev(p.part, positions, cos_table, sin_table, slots, req_to_tokens, b_req_idx, b_seq_len,
+         cache_k, cache_v, out)
+    B, H, D = out.shape
+    KVH = cache_k.shape[1]
+    assert slots.dtype == torch.int32 and req_to_tokens.dtype == torch.int32
+    assert cache_k.stride(-1) == 1 and cache_v.stride(-1) == 1 and out.stride(-1) == 1
+    assert req_to_tokens.stride(-1) == 1 and cos_table.dtype == torch.float32
+    if sm_scale is None:
+        sm_scale = 1.0 / (D ** 0.5)
+    max_len = int(max_len_in_batch)
+    nbytes = _L.ll_decode_attention_workspace_size(B, H, KVH, D, max_len)
+    ws = workspace(out.device, "decode_attention", nbytes)
+    rc = _L.ll_decode_attention_rope_splitk_i32(
+        p.part.data_ptr(), p.splits, p.s_tok.data_ptr(), p.s_ch.data_ptr(), dtype_code(p.s_ch),
+        bias.data_ptr() if bias is not None else None,
+        positions.data_ptr(), _idx(positions, "positions"), cos_table.data_ptr(),
+        sin_table.data_ptr(), cos_table.stride(0), dtype_code(cos_table), slots.data_ptr(),
+        cache_k.data_ptr(), cache_k.stride(0), cache_k.stride(1),
+        cache_v.data_ptr(), cache_v.stride(0), cache_v.stride(1),
+        req_to_tokens.data_ptr(), req_to_tokens.stride(0),
+        b_req_idx.data_ptr(), _idx(b_req_idx, "b_req_idx"),
+        b_seq_len.data_ptr(), _idx(b_seq_len, "b_seq_len"),
+        out.data_ptr(), out.stride(0), out.stride(1),
+        B, H, KVH, D, max_len, float(sm_scale), dtype_code(out), ws.data_ptr(), ws.numel(),
+        _stream(out))
+    _lib.check(rc, "ll_decode_attention_rope_splitk_i32")
+    return out
+
+
 # ------------------------------------------------------------------ W8A8
 def quant_weight_per_channel(w):
     """(int8 [N, K], scale [N] in w's dtype): smooth_quant/layer.py:5-16 on the float path."""
@@ -577,30 +611,81 @@ class QuantWeight:
         return self
 
 
-def linear_w8a8_fp32(x, qw: QuantWeight, out=None):
-    """fp32 [M, N] = dequant(int8(x) @ int8(W)^T): the exact int32 product
-    (the streaming kernel for M <= 64, torch's int8 matmul above that),
-    scaled by the activation (per-token, or the static input scale) and
-    per-channel weight scales."""
-    _dev(x, out)
-    M, K = x.shape
+class I8Partials:
+    """int32 split-K partials [splits, M, N] of an int8 projection with the
+    scales that dequantise them (s_tok [M] fp32, s_ch [N])."""
+
+    def __init__(self, part, splits, s_tok, s_ch):
+        self.part, self.splits, self.s_tok, self.s_ch = part, splits, s_tok, s_ch
+
+
+def quant_input(x, qw: QuantWeight):
+    """int8 codes and scales of a projection's input: static when the weight
+    carries a calibrated input scale, per token otherwise."""
+    return quant_per_token(x) if qw.input_scale is None else quant_static(x, qw.input_scale)
+
+
+def gemm_w8a8_i32(xq, st, qw: QuantWeight) -> I8Partials:
+    """The exact int32 product int8(x) @ int8(W)^T (the streaming kernel for
+    M <= 64, torch's int8 matmul above that) as partials with their scales."""
+    M, K = xq.shape
     N = qw.shape[0]
-    xq, st = quant_per_token(x) if qw.input_scale is None else quant_static(x, qw.input_scale)
     if M <= 64 and qw.packed is not None:
         s = gemm_i8_splitk_count(M, N, K)
-        part = workspace(x.device, "w8a8_part", s * M * N * 4).view(torch.int32)
+        part = workspace(xq.device, "w8a8_part", s * M * N * 4).view(torch.int32)
         gemm_i8_splitk_packed(xq, qw.packed, part)
     else:
         s = 1
         if M <= 16:  # the library int8 GEMM takes more than 16 rows: zero rows, exact
-            xp = torch.zeros((17, K), dtype=torch.int8, device=x.device)
+            xp = torch.zeros((17, K), dtype=torch.int8, device=xq.device)
             xp[:M] = xq
             part = torch._int_mm(xp, qw.q.t())[:M]
         else:
             part = torch._int_mm(xq, qw.q.t())
+    return I8Partials(part, s, st, qw.scale)
+
+
+def linear_w8a8_fp32(x, qw: QuantWeight, out=None):
+    """fp32 [M, N] = dequant(int8(x) @ int8(W)^T): the exact int32 product
+    scaled by the activation (per-token, or the static input scale) and
+    per-channel weight scales."""
+    _dev(x, out)
+    M = x.shape[0]
+    N = qw.shape[0]
+    xq, st = quant_input(x, qw)
+    p = gemm_w8a8_i32(xq, st, qw)
     if out is None:
         out = torch.empty((M, N), dtype=torch.float32, device=x.device)
-    return dequant_splitk(part, s, st, qw.scale, out, M, N)
+    return dequant_splitk(p.part, p.splits, p.s_tok, p.s_ch, out, M, N)
+
+
+def add_rmsnorm_splitk_i32(h, p: I8Partials, gamma, eps, out=None, quant=False):
+    """add_rmsnorm_splitk from int32 partials (dequantised inline); with quant,
+    also returns the output's per-token int8 codes and scales."""
+    _dev(h, p.part, gamma, out)
+    M, N = h.shape
+    if out is None:
+        out = torch.empty_like(h)
+    q = torch.empty((M, N), dtype=torch.int8, device=h.device) if quant else None
+    s = torch.empty((M,), dtype=torch.float32, device=h.device) if quant else None
+    rc = _L.ll_add_rmsnorm_splitk_i32(
+        h.data_ptr(), h.stride(0), p.part.data_ptr(), p.splits, p.s_tok.data_ptr(),
+        p.s_ch.data_ptr(), dtype_code(p.s_ch), gamma.data_ptr(), out.data_ptr(), out.stride(0), M,
+        N, float(eps), dtype_code(h), q.data_ptr() if quant else None, N,
+        s.data_ptr() if quant else None, _stream(h))
+    _lib.check(rc, "ll_add_rmsnorm_splitk_i32")
+    return (out, q, s) if quant else out
+
+
+def silu_and_mul_splitk_i32(p: I8Partials, out):
+    """silu_and_mul_splitk from int32 partials of the [M, 2N] product."""
+    _dev(p.part, out)
+    M, N = out.shape
+    rc = _L.ll_silu_and_mul_splitk_i32(p.part.data_ptr(), p.splits, p.s_tok.data_ptr(),
+                                       p.s_ch.data_ptr(), dtype_code(p.s_ch), out.data_ptr(),
+                                       out.stride(0), M, N, dtype_code(out), _stream(out))
+    _lib.check(rc, "ll_silu_and_mul_splitk_i32")
+    return out
 
 
 def linear_w8a8(x, qw: QuantWeight, bias=None):

@@ -1,0 +1,109 @@
+"""W8A8 consumers that dequantise int32 partials inline, against
+ll_dequant_splitk followed by the fp32 consumer on the same partials: every
+output bit-identical (the inline dequantisation is the same fp32 arithmetic
+in the same order), including add+RMSNorm's per-token int8 output against
+ll_quant_per_token on its stored row, and the fused RoPE attention's output
+and pool. Scale dtypes fp32 / fp16 / bf16, several split counts."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import ops as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _ops():
+    from lite_lang_amd import ops
+    return ops
+
+
+def _parts(g, S, M, N, sdt, cuda):
+    part = torch.randint(-30000, 30000, (S, M, N), generator=g, dtype=torch.int32)
+    st = torch.rand(M, generator=g) * 1e-3 + 1e-5
+    sc = (torch.rand(N, generator=g) * 1e-2 + 1e-4).to(sdt)
+    ops = _ops()
+    return ops.I8Partials(part.to(cuda).reshape(-1), S, st.to(cuda), sc.to(cuda))
+
+
+def _dequant(p, M, N, cuda):
+    out = torch.empty(M, N, device=cuda)
+    _ops().dequant_splitk(p.part, p.splits, p.s_tok, p.s_ch, out, M, N)
+    return out
+
+
+@pytest.mark.parametrize("S,N,sdt", [(3, 2048, torch.bfloat16), (1, 1536, torch.float16),
+                                     (8, 2048, torch.float32), (5, 3584, torch.bfloat16)])
+def test_add_rmsnorm_i32_with_quant(cuda, S, N, sdt):
+    g = torch.Generator().manual_seed(70 + S)
+    M = 40
+    print(f"case: add_rmsnorm_i32 S={S} N={N} {sdt}", flush=True)
+    ops = _ops()
+    p = _parts(g, S, M, N, sdt, cuda)
+    h0 = torch.randn(M, N, generator=g).bfloat16().to(cuda)
+    gamma = (torch.rand(N, generator=g) + 0.5).bfloat16().to(cuda)
+    ha, hb = h0.clone(), h0.clone()
+    outa, qa, sa = ops.add_rmsnorm_splitk_i32(ha, p, gamma, 1e-6, quant=True)
+    f = _dequant(p, M, N, cuda)
+    outb = ops.add_rmsnorm_splitk(hb, f.reshape(-1), 1, gamma, 1e-6)
+    qb, sb = ops.quant_per_token(outb)
+    torch.cuda.synchronize()
+    assert torch.equal(ha, hb) and torch.equal(outa, outb)
+    assert torch.equal(qa, qb) and torch.equal(sa, sb)
+    # the no-quant form writes the same h and output
+    hc = h0.clone()
+    outc = ops.add_rmsnorm_splitk_i32(hc, p, gamma, 1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(hc, hb) and torch.equal(outc, outb)
+
+
+@pytest.mark.parametrize("S,N,sdt", [(1, 1376, torch.float16), (4, 11008, torch.bfloat16)])
+def test_silu_and_mul_i32(cuda, S, N, sdt):
+    g = torch.Generator().manual_seed(80 + S)
+    M = 40
+    print(f"case: silu_and_mul_i32 S={S} N={N}", flush=True)
+    ops = _ops()
+    p = _parts(g, S, M, 2 * N, sdt, cuda)
+    a = torch.empty(M, N, dtype=torch.bfloat16, device=cuda)
+    b = torch.empty_like(a)
+    ops.silu_and_mul_splitk_i32(p, a)
+    f = _dequant(p, M, 2 * N, cuda)
+    ops.silu_and_mul_splitk(f.reshape(-1), 1, b)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("S,H,KVH,D,sdt", [(4, 16, 2, 128, torch.bfloat16),
+                                           (1, 14, 2, 64, torch.float16)])
+def test_rope_attention_i32(cuda, S, H, KVH, D, sdt):
+    g = torch.Generator().manual_seed(90 + S)
+    B = 6
+    lens = [1, 17, 300, 64, 5, 129]
+    cap = max(lens)
+    W = (H + 2 * KVH) * D
+    dt = torch.bfloat16 if sdt == torch.bfloat16 else torch.float16
+    print(f"case: rope attention i32 S={S} H={H} KVH={KVH} D={D}", flush=True)
+    ops = _ops()
+    p = _parts(g, S, B, W, sdt, cuda)
+    bias = (torch.randn(W, generator=g) * 0.1).to(dt).to(cuda)
+    P = B * cap + 3
+    pool = torch.randn(P, 2 * KVH, D, generator=g).to(dt).to(cuda)
+    perm = torch.from_numpy(np.random.RandomState(S).permutation(P)[: B * cap].astype(np.int32))
+    r2t = perm.view(B, cap).to(cuda)
+    slots = torch.tensor([int(r2t[b, l - 1]) for b, l in enumerate(lens)], dtype=torch.int32,
+                         device=cuda)
+    pos = torch.tensor([l - 1 for l in lens], dtype=torch.int32, device=cuda)
+    lens_t = torch.tensor(lens, dtype=torch.int32, device=cuda)
+    rids = torch.arange(B, dtype=torch.int32, device=cuda)
+    cos, sin = O.rope_table(cap + 8, D)
+    cos, sin = cos.float().to(cuda), sin.float().to(cuda)
+    pa, pb = pool.clone(), pool.clone()
+    oa = torch.empty(B, H, D, dtype=dt, device=cuda)
+    ob = torch.empty_like(oa)
+    ops.decode_attention_rope_splitk_i32(p, bias, pos, cos, sin, slots, r2t, rids, lens_t, cap,
+                                         pa[:, :KVH], pa[:, KVH:], oa)
+    f = _dequant(p, B, W, cuda)
+    ops.decode_attention_rope_splitk(f.reshape(-1), 1, bias, pos, cos, sin, slots, r2t, rids,
+                                     lens_t, cap, pb[:, :KVH], pb[:, KVH:], ob)
+    torch.cuda.synchronize()
+    assert torch.equal(pa, pb) and torch.equal(oa, ob)
