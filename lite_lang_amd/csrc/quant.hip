@@ -46,6 +46,82 @@ __global__ __launch_bounds__(256) void quant_weight_kernel(const T* __restrict__
   for (int k = threadIdx.x; k < K; k += 256) q[k] = (s > 0.f) ? quant1(ll_to_f32(row[k]), s) : 0;
 }
 
+template <typename T> struct QVec8;
+template <> struct QVec8<__bf16> { typedef bf16x8 type; };
+template <> struct QVec8<_Float16> { typedef f16x8 type; };
+typedef int8_t i8x8 __attribute__((ext_vector_type(8)));
+
+// Vectorised row quantiser for bf16/fp16 rows with K % 8 == 0 (16 B aligned
+// rows, 8 B aligned codes): each thread keeps VPT vectors of 8 elements in
+// registers, so the row is read once. STATIC: scale = *s_static instead of
+// the row absmax. Same arithmetic as the scalar kernels.
+template <typename T, int VPT, bool STATIC>
+__global__ __launch_bounds__(256) void quant_row_vec_kernel(const T* __restrict__ X, int64_t ldx,
+                                                            int K, int8_t* __restrict__ Q,
+                                                            int64_t ldq, float* __restrict__ scale,
+                                                            const float* __restrict__ s_static) {
+  typedef typename QVec8<T>::type V8;
+  const T* row = X + (int64_t)blockIdx.x * ldx;
+  V8 v[VPT];
+  float m = 0.f;
+#pragma unroll
+  for (int u = 0; u < VPT; ++u) {
+    const int k = (u * 256 + (int)threadIdx.x) * 8;
+    if (k < K) {
+      v[u] = *(const V8*)(row + k);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(ll_to_f32(v[u][e])));
+    }
+  }
+  float s;
+  if constexpr (STATIC) {
+    s = *s_static;
+  } else {
+    __shared__ float red[4];
+    m = ll_wave_max(m);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    s = m / 127.f;
+    if (!(s > 0.f)) s = 1.f;
+  }
+  if (threadIdx.x == 0) scale[blockIdx.x] = s;
+  int8_t* q = Q + (int64_t)blockIdx.x * ldq;
+#pragma unroll
+  for (int u = 0; u < VPT; ++u) {
+    const int k = (u * 256 + (int)threadIdx.x) * 8;
+    if (k < K) {
+      i8x8 o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = quant1(ll_to_f32(v[u][e]), s);
+      *(i8x8*)(q + k) = o;
+    }
+  }
+}
+
+template <typename T, bool STATIC>
+bool launch_quant_vec(const void* X, int64_t ldx, int64_t M, int64_t K, int8_t* Q, int64_t ldq,
+                      float* scale, const float* s_static, hipStream_t stream) {
+  if (K % 8 != 0 || ldx % 8 != 0 || ldq % 8 != 0 || ((uintptr_t)X % 16) != 0 ||
+      ((uintptr_t)Q % 8) != 0 || K > 8 * 256 * 8)
+    return false;
+  const int vpt = (int)((K + 2047) / 2048);
+  const dim3 grid((unsigned)M), block(256);
+  if (vpt <= 1)
+    hipLaunchKernelGGL((quant_row_vec_kernel<T, 1, STATIC>), grid, block, 0, stream, (const T*)X,
+                       ldx, (int)K, Q, ldq, scale, s_static);
+  else if (vpt <= 2)
+    hipLaunchKernelGGL((quant_row_vec_kernel<T, 2, STATIC>), grid, block, 0, stream, (const T*)X,
+                       ldx, (int)K, Q, ldq, scale, s_static);
+  else if (vpt <= 4)
+    hipLaunchKernelGGL((quant_row_vec_kernel<T, 4, STATIC>), grid, block, 0, stream, (const T*)X,
+                       ldx, (int)K, Q, ldq, scale, s_static);
+  else
+    hipLaunchKernelGGL((quant_row_vec_kernel<T, 8, STATIC>), grid, block, 0, stream, (const T*)X,
+                       ldx, (int)K, Q, ldq, scale, s_static);
+  return true;
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void quant_token_kernel(const T* __restrict__ X, int64_t ldx,
                                                           int K, int8_t* __restrict__ Q,
@@ -116,6 +192,12 @@ extern "C" int ll_quant_per_token(const void* X, int64_t ldx, int64_t M, int64_t
   LL_CHECK_ARG(X && Q && scale, "ll_quant_per_token: null pointer");
   LL_CHECK_ARG(M >= 0 && K > 0 && ldx >= K && ldq >= K, "ll_quant_per_token: bad shape");
   if (M == 0) return LL_OK;
+  if (dtype == LL_BF16 && launch_quant_vec<__bf16, false>(X, ldx, M, K, Q, ldq, scale, nullptr,
+                                                          stream))
+    LL_RETURN_LAUNCH();
+  if (dtype == LL_F16 && launch_quant_vec<_Float16, false>(X, ldx, M, K, Q, ldq, scale, nullptr,
+                                                           stream))
+    LL_RETURN_LAUNCH();
   return LL_DISPATCH_DTYPE(dtype, T, [&]() -> int {
     hipLaunchKernelGGL((quant_token_kernel<T>), dim3((unsigned)M), dim3(256), 0, stream,
                        (const T*)X, ldx, (int)K, Q, ldq, scale);
@@ -129,6 +211,12 @@ extern "C" int ll_quant_static(const void* X, int64_t ldx, int64_t M, int64_t K,
   LL_CHECK_ARG(X && scale && Q && s_tok, "ll_quant_static: null pointer");
   LL_CHECK_ARG(M >= 0 && K > 0 && ldx >= K && ldq >= K, "ll_quant_static: bad shape");
   if (M == 0) return LL_OK;
+  if (dtype == LL_BF16 && launch_quant_vec<__bf16, true>(X, ldx, M, K, Q, ldq, s_tok, scale,
+                                                         stream))
+    LL_RETURN_LAUNCH();
+  if (dtype == LL_F16 && launch_quant_vec<_Float16, true>(X, ldx, M, K, Q, ldq, s_tok, scale,
+                                                          stream))
+    LL_RETURN_LAUNCH();
   return LL_DISPATCH_DTYPE(dtype, T, [&]() -> int {
     hipLaunchKernelGGL((quant_static_kernel<T>), dim3((unsigned)M), dim3(256), 0, stream,
                        (const T*)X, ldx, (int)K, scale, Q, ldq, s_tok);
