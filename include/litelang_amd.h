@@ -237,7 +237,11 @@ int ll_decode_attention_rope_splitk(
  * [qkv_splits][batch][(q_heads + 2*kv_heads)*head_dim] and their scales in
  * place of fp32 partials: each column is dequantised as in ll_dequant_splitk
  * (fp32(sum) * s_tok[b] * fp32(s_ch[col]), s_ch of s_ch_dtype) and then
- * treated exactly as the fp32 entry point treats its partial sums. */
+ * treated exactly as the fp32 entry point treats its partial sums. With q_out
+ * (and q_scale; out rows contiguous, ldq >= q_heads*head_dim) the stored
+ * output rows are also quantised for the o_proj, by ll_quant_per_token's rule
+ * or with the calibrated scale *q_static (as ll_quant_static), in the split
+ * merge when there is one. */
 int ll_decode_attention_rope_splitk_i32(
     const int32_t* qkv_part, int qkv_splits, const float* s_tok, const void* s_ch, int s_ch_dtype,
     const void* qkv_bias, const void* positions, int positions_i64, const void* cos_table,
@@ -247,7 +251,8 @@ int ll_decode_attention_rope_splitk_i32(
     int64_t req_to_tokens_stride, const void* b_req_idx, int req_idx_i64, const void* b_seq_len,
     int seq_len_i64, void* out, int64_t out_stride_b, int64_t out_stride_h, int64_t batch,
     int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t max_len_in_batch,
-    float sm_scale, int dtype, void* workspace, int64_t workspace_bytes, hipStream_t stream);
+    float sm_scale, int dtype, void* workspace, int64_t workspace_bytes, const float* q_static,
+    int8_t* q_out, int64_t ldq, float* q_scale, hipStream_t stream);
 
 /* Pre-packed weights for the decode projections (no reference counterpart:
  * a layout of the same nn.Linear weight [N, K], chosen for MI355X). The

@@ -96,6 +96,8 @@ struct DecodeArgs {
   const void* pos; int pos64;
   const float* cos_tab; const float* sin_tab; int64_t tab_stride;
   const int32_t* new_slots;  // [B] pool slot of each sequence's new token
+  // optional quantisation of the output rows for the next int8 projection
+  int8_t* qout; int64_t ldq; float* qscale; const float* qstatic;
 };
 
 // One job of the fused RoPE: 4 rotation pairs (i..i+3 with i+D/2..i+D/2+3) of
@@ -454,14 +456,12 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
 // Log-sum-exp merge of the split partials: one wave per (sequence, head),
 // lane l owns d = l + 64 q. Splits are taken 16 at a time with all their
 // loads issued before any is used (one memory round trip per 16 splits).
-template <typename T, int D>
-__global__ __launch_bounds__(256) void decode_attn_combine_kernel(DecodeArgs a) {
+// Merge of the partials of one (sequence, head) by one wave: lane l returns
+// out[d = l + 64 q] (unrounded).
+template <int D>
+__device__ __forceinline__ void combine_bh(const DecodeArgs& a, int bh, int lane, float (&o)[D / 64]) {
   constexpr int DPL = D / 64;
   constexpr int SB = 16;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int bh = blockIdx.x * kWaves + wave;
-  if (bh >= a.B * a.H) return;
-  const int b = bh / a.H, h = bh - b * a.H;
   const int ns = a.nsplit;
   const int64_t p0 = (int64_t)bh * ns;  // partial rows of (b, h): p0 .. p0 + ns - 1
   float M = -INFINITY, L = 0.f, A[DPL];
@@ -502,9 +502,74 @@ __global__ __launch_bounds__(256) void decode_attn_combine_kernel(DecodeArgs a) 
     }
     M = Mn;
   }
+#pragma unroll
+  for (int q = 0; q < DPL; ++q) o[q] = L > 0.f ? A[q] / L : 0.f;
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void decode_attn_combine_kernel(DecodeArgs a) {
+  constexpr int DPL = D / 64;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int bh = blockIdx.x * kWaves + wave;
+  if (bh >= a.B * a.H) return;
+  const int b = bh / a.H, h = bh - b * a.H;
+  float o[DPL];
+  combine_bh<D>(a, bh, lane, o);
   T* op = (T*)a.out + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh;
 #pragma unroll
-  for (int q = 0; q < DPL; ++q) op[lane + 64 * q] = ll_from_f32<T>(L > 0.f ? A[q] / L : 0.f);
+  for (int q = 0; q < DPL; ++q) op[lane + 64 * q] = ll_from_f32<T>(o[q]);
+}
+
+// Combine of one sequence per workgroup (HPW heads per wave, H <= 16 * HPW),
+// then the o_proj input quantisation of the stored row out[b] (H * D values):
+// codes by ll_quant_per_token's rule, or by *a.qstatic when set.
+template <typename T, int D, int HPW>
+__global__ __launch_bounds__(1024) void decode_attn_combine_quant_kernel(DecodeArgs a) {
+  constexpr int DPL = D / 64;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int nw = blockDim.x >> 6;
+  const int b = blockIdx.x;
+  float y[HPW][DPL];
+  float amax = 0.f;
+#pragma unroll
+  for (int k = 0; k < HPW; ++k) {
+    const int h = wave + k * nw;
+    if (h < a.H) {
+      float o[DPL];
+      combine_bh<D>(a, b * a.H + h, lane, o);
+      T* op = (T*)a.out + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh;
+#pragma unroll
+      for (int q = 0; q < DPL; ++q) {
+        const T v = ll_from_f32<T>(o[q]);
+        op[lane + 64 * q] = v;
+        y[k][q] = ll_to_f32(v);
+        amax = fmaxf(amax, fabsf(y[k][q]));
+      }
+    }
+  }
+  float s;
+  if (a.qstatic != nullptr) {
+    s = *a.qstatic;
+  } else {
+    __shared__ float red[16];
+    amax = ll_wave_max(amax);
+    if (lane == 0) red[wave] = amax;
+    __syncthreads();
+    float mx = 0.f;
+    for (int w = 0; w < nw; ++w) mx = fmaxf(mx, red[w]);
+    s = mx / 127.f;
+    if (!(s > 0.f)) s = 1.f;
+  }
+  if (threadIdx.x == 0) a.qscale[b] = s;
+  int8_t* qrow = a.qout + (int64_t)b * a.ldq;
+#pragma unroll
+  for (int k = 0; k < HPW; ++k) {
+    const int h = wave + k * nw;
+    if (h < a.H) {
+#pragma unroll
+      for (int q = 0; q < DPL; ++q) qrow[h * D + lane + 64 * q] = ll_quant1(y[k][q], s);
+    }
+  }
 }
 
 // ---------------------------------------------------------------- generic path
@@ -602,6 +667,19 @@ void launch_split_stage(const DecodeArgs& a, int dtype, unsigned grid, size_t ld
 
 template <int D>
 void launch_combine(const DecodeArgs& a, int dtype, hipStream_t stream) {
+  if (a.qout != nullptr) {
+    const int nw = a.H < 16 ? a.H : 16;
+    const dim3 qgrid((unsigned)a.B), qblock((unsigned)(64 * nw));
+    const bool two = a.H > 16;
+    if (dtype == LL_BF16) {
+      if (two) hipLaunchKernelGGL((decode_attn_combine_quant_kernel<__bf16, D, 2>), qgrid, qblock, 0, stream, a);
+      else hipLaunchKernelGGL((decode_attn_combine_quant_kernel<__bf16, D, 1>), qgrid, qblock, 0, stream, a);
+    } else {
+      if (two) hipLaunchKernelGGL((decode_attn_combine_quant_kernel<_Float16, D, 2>), qgrid, qblock, 0, stream, a);
+      else hipLaunchKernelGGL((decode_attn_combine_quant_kernel<_Float16, D, 1>), qgrid, qblock, 0, stream, a);
+    }
+    return;
+  }
   const dim3 cgrid((unsigned)((a.B * a.H + kWaves - 1) / kWaves));
   if (dtype == LL_BF16)
     hipLaunchKernelGGL((decode_attn_combine_kernel<__bf16, D>), cgrid, dim3(kWaves * 64), 0,
@@ -653,6 +731,15 @@ int launch_mfma(DecodeArgs& a, int64_t head_dim, int dtype, bool rope, int64_t m
   if (a.nsplit > 1) {
     if (head_dim == 128) launch_combine<128>(a, dtype, stream);
     else launch_combine<64>(a, dtype, stream);
+  } else if (a.qout != nullptr) {
+    // one split: the split stage stored the rows; quantise them here
+    const int64_t W = (int64_t)a.H * head_dim;
+    const int rc = a.qstatic != nullptr
+                       ? ll_quant_static(a.out, a.o_sb, a.B, W, dtype, a.qstatic, a.qout, a.ldq,
+                                         a.qscale, stream)
+                       : ll_quant_per_token(a.out, a.o_sb, a.B, W, dtype, a.qout, a.ldq, a.qscale,
+                                            stream);
+    if (rc != LL_OK) return rc;
   }
   LL_RETURN_LAUNCH();
 }
@@ -731,7 +818,12 @@ int rope_attention_impl(const LLPartials& qkv, const void* qkv_bias, const void*
                         const void* b_seq_len, int seq_len_i64, void* out, int64_t out_stride_b,
                         int64_t out_stride_h, int64_t batch, int64_t q_heads, int64_t kv_heads,
                         int64_t head_dim, int64_t max_len_in_batch, float sm_scale, int dtype,
-                        void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+                        void* workspace, int64_t workspace_bytes, const float* q_static,
+                        int8_t* q_out, int64_t ldq, float* q_scale, hipStream_t stream) {
+  LL_CHECK_ARG((q_out == nullptr) == (q_scale == nullptr) &&
+                   (q_out == nullptr || (out_stride_h == head_dim && ldq >= q_heads * head_dim)),
+               "ll_decode_attention_rope_splitk: q_out needs q_scale, contiguous output rows "
+               "and ldq >= q_heads * head_dim");
   LL_CHECK_ARG(qkv.p && positions && cos_table && sin_table && new_slots && k_cache && v_cache &&
                    req_to_tokens && b_req_idx && b_seq_len && out,
                "ll_decode_attention_rope_splitk: null pointer");
@@ -769,6 +861,7 @@ int rope_attention_impl(const LLPartials& qkv, const void* qkv_bias, const void*
   a.cos_tab = (const float*)cos_table; a.sin_tab = (const float*)sin_table;
   a.tab_stride = table_row_stride;
   a.new_slots = new_slots;
+  a.qout = q_out; a.ldq = ldq; a.qscale = q_scale; a.qstatic = q_static;
   return launch_mfma(a, head_dim, dtype, true, max_len_in_batch, workspace, workspace_bytes,
                      stream);
 }
@@ -791,7 +884,7 @@ extern "C" int ll_decode_attention_rope_splitk(
                              v_stride_head, req_to_tokens, req_to_tokens_stride, b_req_idx,
                              req_idx_i64, b_seq_len, seq_len_i64, out, out_stride_b, out_stride_h,
                              batch, q_heads, kv_heads, head_dim, max_len_in_batch, sm_scale, dtype,
-                             workspace, workspace_bytes, stream);
+                             workspace, workspace_bytes, nullptr, nullptr, 0, nullptr, stream);
 }
 
 extern "C" int ll_decode_attention_rope_splitk_i32(
@@ -803,7 +896,8 @@ extern "C" int ll_decode_attention_rope_splitk_i32(
     int64_t req_to_tokens_stride, const void* b_req_idx, int req_idx_i64, const void* b_seq_len,
     int seq_len_i64, void* out, int64_t out_stride_b, int64_t out_stride_h, int64_t batch,
     int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t max_len_in_batch,
-    float sm_scale, int dtype, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+    float sm_scale, int dtype, void* workspace, int64_t workspace_bytes, const float* q_static,
+    int8_t* q_out, int64_t ldq, float* q_scale, hipStream_t stream) {
   LL_CHECK_ARG(s_tok && s_ch, "ll_decode_attention_rope_splitk_i32: null scale pointer");
   LL_CHECK_ARG(s_ch_dtype == LL_F32 || s_ch_dtype == LL_F16 || s_ch_dtype == LL_BF16,
                "ll_decode_attention_rope_splitk_i32: bad scale dtype %d", s_ch_dtype);
@@ -813,5 +907,6 @@ extern "C" int ll_decode_attention_rope_splitk_i32(
                              k_stride_head, v_cache, v_stride_tok, v_stride_head, req_to_tokens,
                              req_to_tokens_stride, b_req_idx, req_idx_i64, b_seq_len, seq_len_i64,
                              out, out_stride_b, out_stride_h, batch, q_heads, kv_heads, head_dim,
-                             max_len_in_batch, sm_scale, dtype, workspace, workspace_bytes, stream);
+                             max_len_in_batch, sm_scale, dtype, workspace, workspace_bytes,
+                             q_static, q_out, ldq, q_scale, stream);
 }

@@ -214,12 +214,15 @@ class Qwen2Model:
 
     def _decode_w8a8(self, h, B, part, q, attn, act, positions, seq_len, rids, slots, pool, r2t,
                      max_len, out):
-        """The fused decode layer with int8 projections (11 launches per layer):
+        """The fused decode layer with int8 projections (10 launches per layer):
         each int8 GEMM leaves int32 partials that the next kernel dequantises
-        inline (fused RoPE attention, add+RMSNorm, SiLU_and_Mul), and add+RMSNorm
-        also emits the per-token int8 input of the following projection. Inputs
-        with a static scale (o_proj, down_proj of converted checkpoints) and the
-        attention output / SiLU product are quantised by their own kernel."""
+        inline (fused RoPE attention, add+RMSNorm, SiLU_and_Mul); the attention's
+        split merge and add+RMSNorm also emit the int8 input of the following
+        projection (per token, or with the static scale of a converted
+        checkpoint's o_proj). The SiLU product is quantised by its own
+        vectorised kernel: a row-per-workgroup fusion measured slower (40 CUs
+        cannot pull the row's int32 partials as fast as the elementwise kernel
+        spread over all of them)."""
         cfg, w = self.cfg, self.w
         H, KVH, D = cfg.num_heads, cfg.num_key_value_heads, cfg.head_dim
         nl = len(w.layers)
@@ -232,16 +235,17 @@ class Qwen2Model:
         for li, (lw, pk) in enumerate(zip(w.layers, w.packed)):
             p = ops.gemm_w8a8_i32(xq, xs, pk["wqkv_i8"])
             if self._fused_rope_ok():
-                ops.decode_attention_rope_splitk_i32(
+                _, aq, as_ = ops.decode_attention_rope_splitk_i32(
                     p, lw["bqkv"], positions, self.cos, self.sin, slots, r2t, rids, seq_len,
-                    max_len, pool[li, :, :KVH], pool[li, :, KVH:], attn)
+                    max_len, pool[li, :, :KVH], pool[li, :, KVH:], attn, quant=True,
+                    input_scale=pk["wo_i8"].input_scale)
             else:
                 n = p.s_ch.numel()
                 ops.dequant_splitk(p.part, p.splits, p.s_tok, p.s_ch, part[: B * n].view(B, n),
                                    B, n)
                 self._rope_attention(part, 1, lw["bqkv"], q, attn, positions, slots, pool[li],
                                      r2t, rids, seq_len, max_len)
-            aq, as_ = ops.quant_input(attn.view(B, H * D), pk["wo_i8"])
+                aq, as_ = ops.quant_input(attn.view(B, H * D), pk["wo_i8"])
             p = ops.gemm_w8a8_i32(aq, as_, pk["wo_i8"])
             if fused_quant(pk, "wgu"):
                 _, x2q, x2s = ops.add_rmsnorm_splitk_i32(h, p, lw["ln2"], cfg.rms_norm_eps,

@@ -457,9 +457,12 @@ def decode_attention_rope_splitk(part, splits, bias, positions, cos_table, sin_t
 
 def decode_attention_rope_splitk_i32(p, bias, positions, cos_table, sin_table, slots,
                                      req_to_tokens, b_req_idx, b_seq_len, max_len_in_batch,
-                                     cache_k, cache_v, out, sm_scale=None):
+                                     cache_k, cache_v, out, sm_scale=None, quant=False,
+                                     input_scale=None):
     """decode_attention_rope_splitk from the int8 QKV projection's int32
-    partials (an I8Partials), dequantised inline."""
+    partials (an I8Partials), dequantised inline. With quant, also returns
+    the output rows' int8 codes and scales for the o_proj (per token, or
+    static with input_scale)."""
     _dev(p.part, positions, cos_table, sin_table, slots, req_to_tokens, b_req_idx, b_seq_len,
          cache_k, cache_v, out)
     B, H, D = out.shape
@@ -472,6 +475,8 @@ def decode_attention_rope_splitk_i32(p, bias, positions, cos_table, sin_table, s
     max_len = int(max_len_in_batch)
     nbytes = _L.ll_decode_attention_workspace_size(B, H, KVH, D, max_len)
     ws = workspace(out.device, "decode_attention", nbytes)
+    q = torch.empty((B, H * D), dtype=torch.int8, device=out.device) if quant else None
+    s = torch.empty((B,), dtype=torch.float32, device=out.device) if quant else None
     rc = _L.ll_decode_attention_rope_splitk_i32(
         p.part.data_ptr(), p.splits, p.s_tok.data_ptr(), p.s_ch.data_ptr(), dtype_code(p.s_ch),
         bias.data_ptr() if bias is not None else None,
@@ -484,9 +489,10 @@ def decode_attention_rope_splitk_i32(p, bias, positions, cos_table, sin_table, s
         b_seq_len.data_ptr(), _idx(b_seq_len, "b_seq_len"),
         out.data_ptr(), out.stride(0), out.stride(1),
         B, H, KVH, D, max_len, float(sm_scale), dtype_code(out), ws.data_ptr(), ws.numel(),
-        _stream(out))
+        input_scale.data_ptr() if input_scale is not None else None,
+        q.data_ptr() if quant else None, H * D, s.data_ptr() if quant else None, _stream(out))
     _lib.check(rc, "ll_decode_attention_rope_splitk_i32")
-    return out
+    return (out, q, s) if quant else out
 
 
 # ------------------------------------------------------------------ W8A8

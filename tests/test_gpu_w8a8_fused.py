@@ -3,7 +3,9 @@ ll_dequant_splitk followed by the fp32 consumer on the same partials: every
 output bit-identical (the inline dequantisation is the same fp32 arithmetic
 in the same order), including add+RMSNorm's per-token int8 output against
 ll_quant_per_token on its stored row, and the fused RoPE attention's output
-and pool. Scale dtypes fp32 / fp16 / bf16, several split counts."""
+and pool. The fused quantisation of the attention output for the o_proj
+(per token and static) equals the separate quantiser on the stored rows. Scale dtypes fp32 / fp16 / bf16, several split counts, the
+attention with several splits (quantised in the merge) and with one."""
 import numpy as np
 import pytest
 import torch
@@ -107,3 +109,45 @@ def test_rope_attention_i32(cuda, S, H, KVH, D, sdt):
                                      lens_t, cap, pb[:, :KVH], pb[:, KVH:], ob)
     torch.cuda.synchronize()
     assert torch.equal(pa, pb) and torch.equal(oa, ob)
+
+
+@pytest.mark.parametrize("lens,static", [([1, 17, 300, 64, 5, 129], False),
+                                         ([1, 17, 300, 64, 5, 129], True),
+                                         ([3, 9, 12, 1, 20, 7], False)])
+def test_rope_attention_i32_quant(cuda, lens, static):
+    g = torch.Generator().manual_seed(95)
+    S, H, KVH, D, B = 4, 16, 2, 128, 6
+    cap = max(lens)
+    W = (H + 2 * KVH) * D
+    ops = _ops()
+    from lite_lang_amd import _lib
+    nsplit_gt1 = _lib.load().ll_decode_attention_workspace_size(B, H, KVH, D, cap) > 0
+    print(f"case: rope attention i32 quant static={static} several splits={nsplit_gt1}",
+          flush=True)
+    p = _parts(g, S, B, W, torch.bfloat16, cuda)
+    bias = (torch.randn(W, generator=g) * 0.1).bfloat16().to(cuda)
+    P = B * cap + 3
+    pool = torch.randn(P, 2 * KVH, D, generator=g).bfloat16().to(cuda)
+    perm = torch.from_numpy(np.random.RandomState(4).permutation(P)[: B * cap].astype(np.int32))
+    r2t = perm.view(B, cap).to(cuda)
+    slots = torch.tensor([int(r2t[b, l - 1]) for b, l in enumerate(lens)], dtype=torch.int32,
+                         device=cuda)
+    pos = torch.tensor([l - 1 for l in lens], dtype=torch.int32, device=cuda)
+    lens_t = torch.tensor(lens, dtype=torch.int32, device=cuda)
+    rids = torch.arange(B, dtype=torch.int32, device=cuda)
+    cos, sin = O.rope_table(cap + 8, D)
+    cos, sin = cos.float().to(cuda), sin.float().to(cuda)
+    sa = torch.tensor([0.021], device=cuda) if static else None
+    pa, pb = pool.clone(), pool.clone()
+    oa = torch.empty(B, H, D, dtype=torch.bfloat16, device=cuda)
+    ob = torch.empty_like(oa)
+    _, qa, sqa = ops.decode_attention_rope_splitk_i32(
+        p, bias, pos, cos, sin, slots, r2t, rids, lens_t, cap, pa[:, :KVH], pa[:, KVH:], oa,
+        quant=True, input_scale=sa)
+    ops.decode_attention_rope_splitk_i32(p, bias, pos, cos, sin, slots, r2t, rids, lens_t, cap,
+                                         pb[:, :KVH], pb[:, KVH:], ob)
+    flat = ob.view(B, H * D)
+    qb, sqb = ops.quant_static(flat, sa) if static else ops.quant_per_token(flat)
+    torch.cuda.synchronize()
+    assert torch.equal(oa, ob) and torch.equal(pa, pb)
+    assert torch.equal(qa, qb) and torch.equal(sqa, sqb)
