@@ -310,7 +310,9 @@ int ll_quant_per_token(const void* X, int64_t ldx, int64_t M, int64_t K, int dty
 /* int8 weight streaming for M <= 64 (no reference counterpart; the runtime of
  * the reference's W8A8BFP32OFP32Linear, smooth_quant/layer.py:19-59, which has
  * no forward). Wp is the packed image of an int8 [N, K] weight
- * (ll_gemm_i8_pack; K % 256 == 0; size ll_gemm_i8_packed_bytes); part
+ * (ll_gemm_i8_pack; K % 256 == 0; size ll_gemm_i8_packed_bytes; stages of
+ * 256 int8 columns, tile height chosen as for the 16-bit layout: 128 rows
+ * when one split covers K and 64-row tiles would outnumber the CUs); part
  * receives exact int32 partial sums [s][M][N], s < ll_gemm_i8_splitk_count. */
 int64_t ll_gemm_i8_packed_bytes(int64_t N, int64_t K);
 int ll_gemm_i8_pack(const int8_t* Wq, int64_t ldw, int64_t N, int64_t K, void* Wp,

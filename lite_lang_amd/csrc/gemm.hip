@@ -119,7 +119,7 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, 
   typedef typename Vec8<T>::type V8;
   typedef typename AccOf<T>::type AccT;
   constexpr int ES = (int)sizeof(T);
-  static_assert(TR == 64 || (TR == 128 && sizeof(T) == 2), "64-row tiles, or 128 for 16-bit types");
+  static_assert(TR == 64 || TR == 128, "64- or 128-row tiles");
   constexpr int XR = 16 * MB;
   constexpr int RB = TR / 64;             // 16-row MFMA blocks per wave
   constexpr int KC = 256 / ES;            // elements per 256-byte row chunk (one stage)
@@ -204,16 +204,19 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, 
   if constexpr (ES == 1) {
     // int8: exact int32 partial sums, part[split][m][n] (part points at int32)
     int32_t* ip = (int32_t*)part;
-    const int ch = row0 + wave * 16 + 4 * j;
 #pragma unroll
-    for (int t = 0; t < MB; ++t) {
-      const int tok = 16 * t + n;
-      if (tok >= M || ch >= N) continue;
-      int32_t* pp = ip + ((int64_t)split * M + tok) * N + ch;
-      if (ch + 3 < N && (N & 3) == 0) {
-        *(i32x4*)pp = acc[0][t];
-      } else {
-        for (int i = 0; i < 4 && ch + i < N; ++i) pp[i] = acc[0][t][i];
+    for (int b = 0; b < RB; ++b) {
+      const int ch = row0 + wave * 16 * RB + 16 * b + 4 * j;
+#pragma unroll
+      for (int t = 0; t < MB; ++t) {
+        const int tok = 16 * t + n;
+        if (tok >= M || ch >= N) continue;
+        int32_t* pp = ip + ((int64_t)split * M + tok) * N + ch;
+        if (ch + 3 < N && (N & 3) == 0) {
+          *(i32x4*)pp = acc[b][t];
+        } else {
+          for (int i = 0; i < 4 && ch + i < N; ++i) pp[i] = acc[b][t][i];
+        }
       }
     }
     return;
@@ -612,7 +615,7 @@ SkinnyPlan plan_skinny(int64_t N, int64_t K, int es = 2) {
     p.ksps = per * 4;
     p.nst = (p.tiles * p.splits <= 256) ? 3 : 2;
     p.rotate = 1;
-    if (es == 2 && p.splits == 1 && p.tiles > 256) {
+    if (p.splits == 1 && p.tiles > 256) {
       p.tr = 128;
       p.tiles = (int)((N + 127) / 128);
       p.nst = 3;
@@ -642,11 +645,9 @@ void launch_skinny_mb(const SkinnyPlan& p, const T* X, int64_t ldx, const T* W, 
 #define LL_DMA_LAUNCH(S, PKD, TR_)                                                              \
   hipLaunchKernelGGL((gemm_dma_kernel<T, MB, S, PKD, 0, TR_>), grid, dim3(256), lds, stream, X, \
                      ldx, W, ldw, bias, Y, ldy, part, M, N, K, p.ksps, p.rotate)
-    if constexpr (sizeof(T) == 2) {
-      if (p.tr == 128) {
-        if (p.packed) LL_DMA_LAUNCH(3, true, 128); else LL_DMA_LAUNCH(3, false, 128);
-        return;
-      }
+    if (p.tr == 128) {
+      if (p.packed) LL_DMA_LAUNCH(3, true, 128); else LL_DMA_LAUNCH(3, false, 128);
+      return;
     }
     if (p.packed) {
       if (p.nst == 3) LL_DMA_LAUNCH(3, true, 64); else LL_DMA_LAUNCH(2, true, 64);
@@ -934,7 +935,8 @@ extern "C" int ll_gemm(const void* X, int64_t ldx, const void* W, int64_t ldw, c
 
 extern "C" int64_t ll_gemm_i8_packed_bytes(int64_t N, int64_t K) {
   if (N <= 0 || K <= 0 || K % 256 != 0) return 0;
-  return ll_cdiv(N, kDmaTR) * kDmaTR * K;
+  const int tr = plan_skinny(N, K, 1).tr;
+  return ll_cdiv(N, tr) * tr * K;
 }
 
 extern "C" int ll_gemm_i8_pack(const int8_t* Wq, int64_t ldw, int64_t N, int64_t K, void* Wp,
@@ -949,8 +951,8 @@ extern "C" int ll_gemm_i8_pack(const int8_t* Wq, int64_t ldw, int64_t N, int64_t
                (long long)bytes);
   const int64_t units = bytes / 16;
   hipLaunchKernelGGL(gemm_pack_kernel, dim3((unsigned)ll_cdiv(units, 256)), dim3(256), 0, stream,
-                     (const u32x4*)Wq, ldw / 16, (u32x4*)Wp, (int)N, (int)ll_cdiv(N, kDmaTR),
-                     units, 0, kDmaTR);
+                     (const u32x4*)Wq, ldw / 16, (u32x4*)Wp, (int)N,
+                     (int)ll_cdiv(N, plan_skinny(N, K, 1).tr), units, 0, plan_skinny(N, K, 1).tr);
   LL_RETURN_LAUNCH();
 }
 
