@@ -320,6 +320,21 @@ int ll_gemm_i8_pack(const int8_t* Wq, int64_t ldw, int64_t N, int64_t K, void* W
 int ll_gemm_i8_splitk_count(int64_t M, int64_t N, int64_t K);
 int ll_gemm_i8_splitk_packed(const int8_t* Xq, int64_t ldx, const void* Wp, int64_t M, int64_t N,
                              int64_t K, int32_t* part, int64_t part_bytes, hipStream_t stream);
+/* int8 gate/up projection fused with dequantisation and SiLU_and_Mul (the
+ * int8 counterpart of ll_gemm_gate_up_silu_packed, for M <= 64): Wp is the
+ * int8 [gate; up] weight [2I, K] packed by ll_gemm_i8_pack_gate_up (tiles of
+ * R/2 gate and the same R/2 up rows, R as ll_gemm_packed_gate_up_tile_rows),
+ * s_tok [M] the activation scales of Xq, s_ch [2I] the channel scales (gate
+ * then up). act[m, c] = dtype(dtype(u) * dtype(silu(dtype(g)))) with
+ * g = fp32(acc) * s_tok[m] * fp32(s_ch[c]) and u likewise with s_ch[I + c]:
+ * ll_silu_and_mul_splitk_i32 on the one-split int32 product, bit for bit. */
+int64_t ll_gemm_i8_packed_gate_up_bytes(int64_t I, int64_t K);
+int ll_gemm_i8_pack_gate_up(const int8_t* Wq, int64_t ldw, int64_t I, int64_t K, void* Wp,
+                            int64_t wp_bytes, hipStream_t stream);
+int ll_gemm_i8_gate_up_silu_packed(const int8_t* Xq, int64_t ldx, const void* Wp, int64_t M,
+                                   int64_t I, int64_t K, const float* s_tok, const void* s_ch,
+                                   int s_ch_dtype, void* act, int64_t ld_act, int dtype,
+                                   hipStream_t stream);
 /* Static per-tensor activation quantisation with a calibrated input scale
  * (the quant_scale buffer of W8A8BFP32OFP32LinearWithQuantScale,
  * quantize/smooth_quant/layer.py:63-94, whose runtime the reference never

@@ -56,6 +56,9 @@ SIGNATURES = {
     "ll_quant_per_token": (I32, [P, I64, I64, I64, I32, P, I64, P, P]),
     "ll_gemm_i8_packed_bytes": (I64, [I64, I64]),
     "ll_gemm_i8_pack": (I32, [P, I64, I64, I64, P, I64, P]),
+    "ll_gemm_i8_packed_gate_up_bytes": (I64, [I64, I64]),
+    "ll_gemm_i8_pack_gate_up": (I32, [P, I64, I64, I64, P, I64, P]),
+    "ll_gemm_i8_gate_up_silu_packed": (I32, [P, I64, P, I64, I64, I64, P, P, I32, P, I64, I32, P]),
     "ll_gemm_i8_splitk_count": (I32, [I64, I64, I64]),
     "ll_gemm_i8_splitk_packed": (I32, [P, I64, P, I64, I64, I64, P, I64, P]),
     "ll_quant_static": (I32, [P, I64, I64, I64, I32, P, P, I64, P, P]),

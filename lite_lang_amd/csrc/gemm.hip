@@ -108,13 +108,24 @@ __device__ __forceinline__ void wait_stage(int later) {
 // channels; the epilogue writes Y[m, c] = T(T(up) * T(silu(T(gate)))) for the
 // 32 channels of the tile (N = 2 * channels), the rounding sequence of
 // ll_silu_and_mul_splitk applied to the same fp32 sums.
-template <typename T, int MB, int NST, bool PK, int EPI = 0, int TR = 64>
+// int8 gate/up epilogue (EPI 1 with int8 operands): the int32 sums are
+// dequantised as fp32(acc) * s_tok[m] * fp32(s_ch[col]) (col = channel for
+// gate, I + channel for up) and SiLU_and_Mul is written to y (type TO).
+struct I8Epi {
+  const float* s_tok;
+  const void* s_ch;
+  int s_ch_dtype;
+  void* y;
+  int64_t ldy;
+};
+
+template <typename T, int MB, int NST, bool PK, int EPI = 0, int TR = 64, typename TO = T>
 __global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, int64_t ldx,
                                                        const T* __restrict__ W, int64_t ldw,
                                                        const T* __restrict__ bias,
                                                        T* __restrict__ Y, int64_t ldy,
                                                        float* __restrict__ part, int M, int N,
-                                                       int K, int ksps, int rotate) {
+                                                       int K, int ksps, int rotate, I8Epi e8) {
   static_assert(NST >= 2 && NST <= 4, "2 to 4 stage buffers");
   typedef typename Vec8<T>::type V8;
   typedef typename AccOf<T>::type AccT;
@@ -173,6 +184,30 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, 
   for (int b = 0; b < RB; ++b)
 #pragma unroll
     for (int t = 0; t < MB; ++t) acc[b][t] = (AccT){0, 0, 0, 0};
+  // int8 gate/up epilogue scales, loaded (clamped, unconditionally) before the
+  // weight stream so that their latency hides behind it: the token scales of
+  // this lane's tokens and the raw bits of the channel scales of its gate
+  // (waves 0, 1) or up (waves 2, 3) channels, converted only in the epilogue
+  // (a conversion here would wait for the loads before the stream starts)
+  float e_st[MB];
+  uint32_t e_sc[RB][4];
+  if constexpr (ES == 1 && EPI == 1) {
+    const int I = N / 2;
+#pragma unroll
+    for (int t = 0; t < MB; ++t) e_st[t] = e8.s_tok[min(16 * t + n, M - 1)];
+    const int cbase = blockIdx.x * (TR / 2) + 16 * RB * (wave & 1) + 4 * j;
+    const int coff = wave >= 2 ? I : 0;
+    auto load_sc = [&](auto tag) {
+      typedef decltype(tag) S;
+      const S* s = (const S*)e8.s_ch;
+#pragma unroll
+      for (int b = 0; b < RB; ++b)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) e_sc[b][i] = s[coff + min(cbase + 16 * b + i, I - 1)];
+    };
+    if (e8.s_ch_dtype == LL_F32) load_sc(uint32_t{});
+    else load_sc((unsigned short){});
+  }
 #pragma unroll
   for (int st = 0; st < NST - 1; ++st)
     if (st < nst) issue(st);
@@ -201,7 +236,74 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, 
     }
   }
   // acc[b][t][i] = Y[token 16t + n][channel row0 + 16*RB*wave + 16b + 4j + i]
-  if constexpr (ES == 1) {
+  if constexpr (ES == 1 && EPI == 1) {
+    // int8 gate/up, one split: dequantise, then SiLU_and_Mul with the rounding
+    // sequence of silu_and_mul_splitk (waves 2, 3 hand the up values to 0, 1)
+    constexpr int HALF = TR / 2;
+    const int I = N / 2;
+    float* ub = (float*)smem;  // [HALF channels][16 * MB tokens]
+    float sc[RB][4];
+    auto cvt = [&](auto dt) {
+#pragma unroll
+      for (int b = 0; b < RB; ++b)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sc[b][i] = ll_scale_bits_to_f32(e_sc[b][i], decltype(dt)::value);
+    };
+    if (e8.s_ch_dtype == LL_F16) cvt(std::integral_constant<int, LL_F16>{});
+    else if (e8.s_ch_dtype == LL_BF16) cvt(std::integral_constant<int, LL_BF16>{});
+    else cvt(std::integral_constant<int, LL_F32>{});
+    lds_barrier();
+    if (wave >= 2) {
+#pragma unroll
+      for (int b = 0; b < RB; ++b)
+#pragma unroll
+        for (int t = 0; t < MB; ++t) {
+          const int cl = 16 * RB * (wave - 2) + 16 * b + 4 * j;
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            ub[(cl + i) * (16 * MB) + 16 * t + n] = (float)acc[b][t][i] * e_st[t] * sc[b][i];
+        }
+    }
+    lds_barrier();
+    if (wave < 2) {
+      // every output of the lane first (one wait for the scales and the LDS
+      // exchange), then the guarded stores, 4 channels per 8-byte store
+      TO y[RB][MB][4];
+#pragma unroll
+      for (int b = 0; b < RB; ++b) {
+        const int cl = 16 * RB * wave + 16 * b + 4 * j;
+#pragma unroll
+        for (int t = 0; t < MB; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float gf = (float)acc[b][t][i] * e_st[t] * sc[b][i];
+            const float g = ll_to_f32(ll_from_f32<TO>(gf));
+            const float u = ll_to_f32(ll_from_f32<TO>(ub[(cl + i) * (16 * MB) + 16 * t + n]));
+            const TO sv = ll_from_f32<TO>(g / (1.0f + __expf(-g)));
+            y[b][t][i] = ll_from_f32<TO>(u * ll_to_f32(sv));
+          }
+      }
+      TO* Yo = (TO*)e8.y;
+      const bool vec = ((I | e8.ldy) & 3) == 0;
+#pragma unroll
+      for (int b = 0; b < RB; ++b) {
+        const int c0 = blockIdx.x * HALF + 16 * RB * wave + 16 * b + 4 * j;
+#pragma unroll
+        for (int t = 0; t < MB; ++t) {
+          const int tok = 16 * t + n;
+          if (tok >= M || c0 >= I) continue;
+          TO* yp = Yo + (int64_t)tok * e8.ldy + c0;
+          if (vec) {
+            typedef TO V4 __attribute__((ext_vector_type(4)));
+            *(V4*)yp = (V4){y[b][t][0], y[b][t][1], y[b][t][2], y[b][t][3]};
+          } else {
+            for (int i = 0; i < 4 && c0 + i < I; ++i) yp[i] = y[b][t][i];
+          }
+        }
+      }
+    }
+    return;
+  } else if constexpr (ES == 1) {
     // int8: exact int32 partial sums, part[split][m][n] (part points at int32)
     int32_t* ip = (int32_t*)part;
 #pragma unroll
@@ -644,7 +746,7 @@ void launch_skinny_mb(const SkinnyPlan& p, const T* X, int64_t ldx, const T* W, 
     const size_t lds = (size_t)p.nst * (p.tr + 16 * MB) * 256;
 #define LL_DMA_LAUNCH(S, PKD, TR_)                                                              \
   hipLaunchKernelGGL((gemm_dma_kernel<T, MB, S, PKD, 0, TR_>), grid, dim3(256), lds, stream, X, \
-                     ldx, W, ldw, bias, Y, ldy, part, M, N, K, p.ksps, p.rotate)
+                     ldx, W, ldw, bias, Y, ldy, part, M, N, K, p.ksps, p.rotate, I8Epi{})
     if (p.tr == 128) {
       if (p.packed) LL_DMA_LAUNCH(3, true, 128); else LL_DMA_LAUNCH(3, false, 128);
       return;
@@ -836,15 +938,15 @@ extern "C" int ll_gemm_gate_up_silu_packed(const void* X, int64_t ldx, const voi
     if (tr == 128)                                                                              \
       hipLaunchKernelGGL((gemm_dma_kernel<T, MB_, 3, true, 1, 128>), grid, dim3(256), lds,       \
                          stream, x, ldx, w, K, nullptr, y, ld_act, nullptr, (int)M, (int)(2 * I), \
-                         (int)K, ksps, 0);                                                      \
+                         (int)K, ksps, 0, I8Epi{});                                             \
     else if (nst == 3)                                                                          \
       hipLaunchKernelGGL((gemm_dma_kernel<T, MB_, 3, true, 1>), grid, dim3(256), lds, stream, x, \
                          ldx, w, K, nullptr, y, ld_act, nullptr, (int)M, (int)(2 * I), (int)K,  \
-                         ksps, 0);                                                              \
+                         ksps, 0, I8Epi{});                                                     \
     else                                                                                        \
       hipLaunchKernelGGL((gemm_dma_kernel<T, MB_, 2, true, 1>), grid, dim3(256), lds, stream, x, \
                          ldx, w, K, nullptr, y, ld_act, nullptr, (int)M, (int)(2 * I), (int)K,  \
-                         ksps, 0);                                                              \
+                         ksps, 0, I8Epi{});                                                     \
   } while (0)
     switch ((M + 15) / 16) {
       case 1: LL_GU(1); break;
@@ -953,6 +1055,80 @@ extern "C" int ll_gemm_i8_pack(const int8_t* Wq, int64_t ldw, int64_t N, int64_t
   hipLaunchKernelGGL(gemm_pack_kernel, dim3((unsigned)ll_cdiv(units, 256)), dim3(256), 0, stream,
                      (const u32x4*)Wq, ldw / 16, (u32x4*)Wp, (int)N,
                      (int)ll_cdiv(N, plan_skinny(N, K, 1).tr), units, 0, plan_skinny(N, K, 1).tr);
+  LL_RETURN_LAUNCH();
+}
+
+extern "C" int64_t ll_gemm_i8_packed_gate_up_bytes(int64_t I, int64_t K) {
+  if (I <= 0 || K <= 0 || K % 256 != 0) return 0;
+  const int tr = gate_up_tr(I);
+  return ll_cdiv(I, tr / 2) * tr * K;
+}
+
+extern "C" int ll_gemm_i8_pack_gate_up(const int8_t* Wq, int64_t ldw, int64_t I, int64_t K,
+                                       void* Wp, int64_t wp_bytes, hipStream_t stream) {
+  LL_CHECK_ARG(Wq && Wp, "ll_gemm_i8_pack_gate_up: null pointer");
+  LL_CHECK_ARG(I > 0 && K > 0 && K % 256 == 0,
+               "ll_gemm_i8_pack_gate_up: needs K %% 256 == 0 (K=%lld)", (long long)K);
+  LL_CHECK_ARG(ldw >= K && ldw % 16 == 0 && ((uintptr_t)Wq | (uintptr_t)Wp) % 16 == 0,
+               "ll_gemm_i8_pack_gate_up: W rows must be 16 B aligned");
+  const int64_t bytes = ll_gemm_i8_packed_gate_up_bytes(I, K);
+  LL_CHECK_ARG(wp_bytes >= bytes, "ll_gemm_i8_pack_gate_up: output too small (need %lld bytes)",
+               (long long)bytes);
+  const int64_t units = bytes / 16;
+  const int tr = gate_up_tr(I);
+  hipLaunchKernelGGL(gemm_pack_kernel, dim3((unsigned)ll_cdiv(units, 256)), dim3(256), 0, stream,
+                     (const u32x4*)Wq, ldw / 16, (u32x4*)Wp, (int)(2 * I),
+                     (int)ll_cdiv(I, tr / 2), units, (int)I, tr);
+  LL_RETURN_LAUNCH();
+}
+
+namespace {
+
+template <int MB, int NST, int TR, typename TO>
+void launch_i8_gate_up(const int8_t* x, int64_t ldx, const int8_t* w, int64_t M, int64_t I,
+                       int64_t K, unsigned tiles, const I8Epi& e, hipStream_t stream) {
+  const size_t lds = (size_t)NST * (TR + 16 * MB) * 256;
+  hipLaunchKernelGGL((gemm_dma_kernel<int8_t, MB, NST, true, 1, TR, TO>), dim3(tiles, 1),
+                     dim3(256), lds, stream, x, ldx, w, K, nullptr, nullptr, 0, nullptr, (int)M,
+                     (int)(2 * I), (int)K, (int)(K / 64), 0, e);
+}
+
+template <int MB, typename TO>
+void launch_i8_gate_up_mb(const int8_t* x, int64_t ldx, const int8_t* w, int64_t M, int64_t I,
+                          int64_t K, const I8Epi& e, hipStream_t stream) {
+  const int tr = gate_up_tr(I);
+  const unsigned tiles = (unsigned)ll_cdiv(I, tr / 2);
+  if (tr == 128) launch_i8_gate_up<MB, 3, 128, TO>(x, ldx, w, M, I, K, tiles, e, stream);
+  else if (tiles <= 256) launch_i8_gate_up<MB, 3, 64, TO>(x, ldx, w, M, I, K, tiles, e, stream);
+  else launch_i8_gate_up<MB, 2, 64, TO>(x, ldx, w, M, I, K, tiles, e, stream);
+}
+
+}  // namespace
+
+extern "C" int ll_gemm_i8_gate_up_silu_packed(const int8_t* Xq, int64_t ldx, const void* Wp,
+                                              int64_t M, int64_t I, int64_t K, const float* s_tok,
+                                              const void* s_ch, int s_ch_dtype, void* act,
+                                              int64_t ld_act, int dtype, hipStream_t stream) {
+  LL_CHECK_ARG(Xq && Wp && s_tok && s_ch && act, "ll_gemm_i8_gate_up_silu_packed: null pointer");
+  LL_CHECK_ARG(M > 0 && M <= 64 && I > 0 && K > 0 && K % 256 == 0,
+               "ll_gemm_i8_gate_up_silu_packed: needs 0 < M <= 64 and K %% 256 == 0");
+  LL_CHECK_ARG(dtype == LL_BF16 || dtype == LL_F16, "ll_gemm_i8_gate_up_silu_packed: bf16/fp16 output");
+  LL_CHECK_ARG(s_ch_dtype == LL_F32 || s_ch_dtype == LL_F16 || s_ch_dtype == LL_BF16,
+               "ll_gemm_i8_gate_up_silu_packed: bad scale dtype %d", s_ch_dtype);
+  LL_CHECK_ARG(ldx % 16 == 0 && (((uintptr_t)Xq | (uintptr_t)Wp) % 16) == 0,
+               "ll_gemm_i8_gate_up_silu_packed: X rows must be 16 B aligned");
+  const I8Epi e = {s_tok, s_ch, s_ch_dtype, act, ld_act};
+  const int8_t* w = (const int8_t*)Wp;
+  auto run = [&](auto tag) {
+    typedef decltype(tag) TO;
+    switch ((M + 15) / 16) {
+      case 1: launch_i8_gate_up_mb<1, TO>(Xq, ldx, w, M, I, K, e, stream); break;
+      case 2: launch_i8_gate_up_mb<2, TO>(Xq, ldx, w, M, I, K, e, stream); break;
+      case 3: launch_i8_gate_up_mb<3, TO>(Xq, ldx, w, M, I, K, e, stream); break;
+      default: launch_i8_gate_up_mb<4, TO>(Xq, ldx, w, M, I, K, e, stream); break;
+    }
+  };
+  if (dtype == LL_BF16) run(__bf16{}); else run(_Float16{});
   LL_RETURN_LAUNCH();
 }
 

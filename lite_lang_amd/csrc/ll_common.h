@@ -149,6 +149,13 @@ __device__ __forceinline__ float ll_load_scale(const void* s, int dtype, int64_t
   return ((const float*)s)[i];
 }
 
+// A scale loaded as raw bits (fp32, or a zero-extended fp16 / bf16 code).
+__device__ __forceinline__ float ll_scale_bits_to_f32(uint32_t bits, int dtype) {
+  if (dtype == LL_F16) return (float)__builtin_bit_cast(_Float16, (unsigned short)bits);
+  if (dtype == LL_BF16) return __builtin_bit_cast(float, bits << 16);
+  return __builtin_bit_cast(float, bits);
+}
+
 // Columns col..col+3 of row m (idx = m * row_stride + col), summed over the splits.
 __device__ __forceinline__ f32x4 ll_partials_sum4(const LLPartials& P, int64_t idx, int64_t m,
                                                   int64_t col) {

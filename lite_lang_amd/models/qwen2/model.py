@@ -214,15 +214,16 @@ class Qwen2Model:
 
     def _decode_w8a8(self, h, B, part, q, attn, act, positions, seq_len, rids, slots, pool, r2t,
                      max_len, out):
-        """The fused decode layer with int8 projections (10 launches per layer):
+        """The fused decode layer with int8 projections (9 launches per layer):
         each int8 GEMM leaves int32 partials that the next kernel dequantises
-        inline (fused RoPE attention, add+RMSNorm, SiLU_and_Mul); the attention's
-        split merge and add+RMSNorm also emit the int8 input of the following
-        projection (per token, or with the static scale of a converted
-        checkpoint's o_proj). The SiLU product is quantised by its own
-        vectorised kernel: a row-per-workgroup fusion measured slower (40 CUs
-        cannot pull the row's int32 partials as fast as the elementwise kernel
-        spread over all of them)."""
+        inline (fused RoPE attention, add+RMSNorm), the gate/up GEMM applies
+        dequantisation and SiLU_and_Mul in its own epilogue, and the
+        attention's split merge and add+RMSNorm also emit the int8 input of
+        the following projection (per token, or with the static scale of a
+        converted checkpoint's o_proj). The SiLU product is quantised by its
+        own vectorised kernel: a row-per-workgroup fusion measured slower (40
+        CUs cannot pull the row's int32 partials as fast as the elementwise
+        kernel spread over all of them)."""
         cfg, w = self.cfg, self.w
         H, KVH, D = cfg.num_heads, cfg.num_key_value_heads, cfg.head_dim
         nl = len(w.layers)
@@ -253,8 +254,10 @@ class Qwen2Model:
             else:
                 x2 = ops.add_rmsnorm_splitk_i32(h, p, lw["ln2"], cfg.rms_norm_eps)
                 x2q, x2s = ops.quant_input(x2, pk["wgu_i8"])
-            p = ops.gemm_w8a8_i32(x2q, x2s, pk["wgu_i8"])
-            ops.silu_and_mul_splitk_i32(p, act)
+            if pk["wgu_i8"].packed_gu is not None:
+                ops.gemm_i8_gate_up_silu(x2q, x2s, pk["wgu_i8"].packed_gu, act)
+            else:
+                ops.silu_and_mul_splitk_i32(ops.gemm_w8a8_i32(x2q, x2s, pk["wgu_i8"]), act)
             dq, ds = ops.quant_input(act, pk["wdown_i8"])
             p = ops.gemm_w8a8_i32(dq, ds, pk["wdown_i8"])
             if li + 1 < nl:

@@ -237,7 +237,7 @@ class DeviceWeights:
                         pk[name + "_i8"] = _int8_group(sd, f"model.layers.{i}.", parts, device)
                     continue
                 for name in ("wqkv", "wo", "wgu", "wdown"):
-                    pk[name + "_i8"] = ops.QuantWeight(lw[name])
+                    pk[name + "_i8"] = ops.QuantWeight(lw[name], gate_up=(name == "wgu"))
             if pack and dtype in (torch.bfloat16, torch.float16):
                 self.lm_head_p = ops.pack_weight(self.lm_head)
         elif pack and dtype in (torch.bfloat16, torch.float16) and torch.device(device).type == "cuda":
@@ -284,4 +284,5 @@ def _int8_group(sd, prefix, parts, device):
         a = float(a[0])
     else:
         a = None
-    return ops.QuantWeight.from_int8(q.to(device), s.to(device), a)
+    return ops.QuantWeight.from_int8(q.to(device), s.to(device), a,
+                                     gate_up=(parts[0] == "mlp.gate_proj"))

@@ -557,6 +557,37 @@ class PackedI8Weight:
         _lib.check(rc, "ll_gemm_i8_pack")
 
 
+class PackedI8GateUp:
+    """int8 [gate; up] weight [2I, K] packed for the fused gate/up + SiLU GEMM."""
+
+    def __init__(self, wq, scale):
+        _dev(wq, scale)
+        N2, K = wq.shape
+        assert wq.dtype == torch.int8 and wq.stride(1) == 1 and N2 % 2 == 0 and scale.shape == (N2,)
+        I = N2 // 2
+        nbytes = _L.ll_gemm_i8_packed_gate_up_bytes(I, K)
+        if nbytes <= 0:
+            raise _lib.LiteLangError(f"ll_gemm_i8_pack_gate_up: K={K} is not a multiple of 256")
+        self.shape, self.inter, self.scale, self.device = (N2, K), I, scale, wq.device
+        self.data = torch.empty(nbytes, dtype=torch.uint8, device=wq.device)
+        rc = _L.ll_gemm_i8_pack_gate_up(wq.data_ptr(), wq.stride(0), I, K, self.data.data_ptr(),
+                                        nbytes, _stream(wq))
+        _lib.check(rc, "ll_gemm_i8_pack_gate_up")
+
+
+def gemm_i8_gate_up_silu(xq, st, pg: PackedI8GateUp, out):
+    """out[M, I] = dtype(u * dtype(silu(g))) of the dequantised int8 gate/up
+    product (one launch)."""
+    _dev(xq, st, out)
+    M, K = xq.shape
+    rc = _L.ll_gemm_i8_gate_up_silu_packed(
+        xq.data_ptr(), xq.stride(0), pg.data.data_ptr(), M, pg.inter, K, st.data_ptr(),
+        pg.scale.data_ptr(), dtype_code(pg.scale), out.data_ptr(), out.stride(0),
+        dtype_code(out), _stream(out))
+    _lib.check(rc, "ll_gemm_i8_gate_up_silu_packed")
+    return out
+
+
 def gemm_i8_splitk_count(M, N, K) -> int:
     return _L.ll_gemm_i8_splitk_count(M, N, K)
 
@@ -590,16 +621,27 @@ class QuantWeight:
     streaming image when K % 256 == 0, and optionally a calibrated static
     input scale (fp32 device tensor, one element; None = dynamic per token)."""
 
-    def __init__(self, w=None):
+    def __init__(self, w=None, gate_up=False):
         self.input_scale = None
+        self.packed = self.packed_gu = None
         if w is None:
             return
         self.q, self.scale = quant_weight_per_channel(w)
         self.shape = tuple(w.shape)
-        self.packed = PackedI8Weight(self.q, self.scale) if w.shape[1] % 256 == 0 else None
+        self._pack(gate_up)
+
+    def _pack(self, gate_up):
+        """Streaming image for M <= 64: the plain layout, or for a [gate; up]
+        weight the fused gate/up + SiLU layout (decode uses only that one)."""
+        if self.shape[1] % 256 != 0:
+            return
+        if gate_up:
+            self.packed_gu = PackedI8GateUp(self.q, self.scale)
+        else:
+            self.packed = PackedI8Weight(self.q, self.scale)
 
     @classmethod
-    def from_int8(cls, q, scale, input_scale=None):
+    def from_int8(cls, q, scale, input_scale=None, gate_up=False):
         """Wrap an already quantised weight (a converted checkpoint's int8
         `weight` and `weight_scale`, and its `quant_scale` when present)."""
         _dev(q, scale)
@@ -608,7 +650,7 @@ class QuantWeight:
         assert q.dtype == torch.int8 and scale.numel() == N
         self.q, self.scale = q.contiguous(), scale.reshape(N).contiguous()
         self.shape = (N, K)
-        self.packed = PackedI8Weight(self.q, self.scale) if K % 256 == 0 else None
+        self._pack(gate_up)
         if input_scale is not None:
             s = float(input_scale)
             if not s > 0.0:

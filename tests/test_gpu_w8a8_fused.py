@@ -151,3 +151,35 @@ def test_rope_attention_i32_quant(cuda, lens, static):
     torch.cuda.synchronize()
     assert torch.equal(oa, ob) and torch.equal(pa, pb)
     assert torch.equal(qa, qb) and torch.equal(sqa, sqb)
+
+
+@pytest.mark.parametrize("M,I,K,sdt,odt", [(40, 11008, 2048, torch.bfloat16, torch.bfloat16),
+                                           (1, 1376, 512, torch.float16, torch.float16),
+                                           (17, 8960, 1536, torch.float32, torch.bfloat16),
+                                           (64, 1000, 256, torch.bfloat16, torch.bfloat16)])
+def test_i8_gate_up_silu_fused(cuda, M, I, K, sdt, odt):
+    """The int8 gate/up GEMM with dequantisation and SiLU_and_Mul in its
+    epilogue against the int32 partials of the plain int8 GEMM followed by
+    silu_and_mul_splitk_i32: bit-identical (the int32 sums are exact whatever
+    the split, and both sides dequantise and round in the same order). I=11008
+    takes 128-row tiles, the others 64-row ones; I=1000 ends in a partial tile."""
+    g = torch.Generator().manual_seed(100 + M)
+    print(f"case: i8 gate/up silu M={M} I={I} K={K} {sdt} -> {odt}", flush=True)
+    ops = _ops()
+    wq = torch.randint(-127, 128, (2 * I, K), generator=g, dtype=torch.int8).to(cuda)
+    sc = (torch.rand(2 * I, generator=g) * 2e-3 + 1e-4).to(sdt).to(cuda)
+    xq = torch.randint(-128, 128, (M, K), generator=g, dtype=torch.int8).to(cuda)
+    st = (torch.rand(M, generator=g) * 1e-2 + 1e-4).to(cuda)
+    pg = ops.PackedI8GateUp(wq, sc)
+    a = torch.empty(M, I, dtype=odt, device=cuda)
+    ops.gemm_i8_gate_up_silu(xq, st, pg, a)
+    pw = ops.PackedI8Weight(wq, sc)
+    s = ops.gemm_i8_splitk_count(M, 2 * I, K)
+    part = torch.empty(s * M * 2 * I, dtype=torch.int32, device=cuda)
+    ops.gemm_i8_splitk_packed(xq, pw, part)
+    b = torch.empty_like(a)
+    ops.silu_and_mul_splitk_i32(ops.I8Partials(part, s, st, sc), b)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    # the products are not degenerate: some outputs are far from zero
+    assert float(a.float().abs().max()) > 1.0
