@@ -188,7 +188,7 @@ int ll_silu_and_mul_splitk(const float* part, int splits, void* out, int64_t out
  * ll_dequant_splitk into add+RMSNorm and SiLU_and_Mul for the int8 decode
  * layer): int32 partials [splits][M][N] ([M][2N] for SiLU) with per-row
  * activation scales s_tok [M] and per-column weight scales s_ch of
- * s_ch_dtype, dequantised as ll_dequant_splitk does. With q_out (and
+ * s_ch_dtype (4-byte aligned), dequantised as ll_dequant_splitk does. With q_out (and
  * q_scale), the RMSNorm output is also quantised per token for the next
  * projection, with ll_quant_per_token's rule, into int8 q_out [M, ldq] and
  * fp32 q_scale [M]; both null skips it. */
@@ -236,7 +236,7 @@ int ll_decode_attention_rope_splitk(
 /* The same with the W8A8 projection's int32 partials
  * [qkv_splits][batch][(q_heads + 2*kv_heads)*head_dim] and their scales in
  * place of fp32 partials: each column is dequantised as in ll_dequant_splitk
- * (fp32(sum) * s_tok[b] * fp32(s_ch[col]), s_ch of s_ch_dtype) and then
+ * (fp32(sum) * s_tok[b] * fp32(s_ch[col]), s_ch of s_ch_dtype, 4-byte aligned) and then
  * treated exactly as the fp32 entry point treats its partial sums. With q_out
  * (and q_scale; out rows contiguous, ldq >= q_heads*head_dim) the stored
  * output rows are also quantised for the o_proj, by ll_quant_per_token's rule

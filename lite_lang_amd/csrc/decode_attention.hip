@@ -111,26 +111,29 @@ __device__ __forceinline__ void rope_job(const DecodeArgs& a, int64_t m, int64_t
                                          T* lds, T* glb) {
   constexpr int HALF = D / 2;
   const int c0 = hcol + i, c1 = c0 + HALF;
-  // bias and the cos/sin entries first: their loads share the partials' round trip
-  const T* bias = (const T*)a.qkv_bias;
-  float b0[4] = {0.f, 0.f, 0.f, 0.f}, b1[4] = {0.f, 0.f, 0.f, 0.f}, cv[4], sv[4];
+  // bias and the cos/sin entries first: their loads share the partials' round
+  // trip. The bias is loaded unconditionally (from the partials, a valid
+  // buffer wider than a row, when there is none) and selected after the sums:
+  // a load used only under a branch is waited for inside it, one round trip
+  // per element.
+  const bool has_bias = a.qkv_bias != nullptr;
+  const T* bsrc = has_bias ? (const T*)a.qkv_bias : (const T*)a.qkv.p;
+  T rb0[4], rb1[4];
+  float cv[4], sv[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    if (bias != nullptr) {
-      b0[e] = ll_to_f32(bias[c0 + e]);
-      b1[e] = ll_to_f32(bias[c1 + e]);
-    }
+    rb0[e] = bsrc[c0 + e];
+    rb1[e] = bsrc[c1 + e];
     cv[e] = cs[i + e];
     sv[e] = sn[i + e];
   }
-  f32x4 x0 = ll_partials_sum4(a.qkv, row + c0, m, c0);
-  f32x4 x1 = ll_partials_sum4(a.qkv, row + c1, m, c1);
-  if (bias != nullptr) {
+  f32x4 x0, x1;
+  ll_partials_sum4_pair(a.qkv, row + c0, row + c1, m, c0, c1, x0, x1);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      x0[e] += b0[e];
-      x1[e] += b1[e];
-    }
+  for (int e = 0; e < 4; ++e) {
+    const float s0 = x0[e] + ll_to_f32(rb0[e]), s1 = x1[e] + ll_to_f32(rb1[e]);
+    x0[e] = has_bias ? s0 : x0[e];
+    x1[e] = has_bias ? s1 : x1[e];
   }
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
@@ -208,33 +211,31 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
   T* s_q = (T*)(smem + TG::MAIN_B + (size_t)a.slots_cap * 4);  // ROPE: [G][D] rotated q
   T* s_kv = s_q + a.G * D;                                     // ROPE: new token's K, V
   constexpr int QD = D / 8;  // RoPE jobs per head
-  int32_t new_slot = 0;
-  int64_t qkv_row = 0;
-  const float* cs = nullptr;
-  const float* sn = nullptr;
-  if constexpr (ROPE) {
-    const int width = (a.H + 2 * a.KVH) * D;
-    qkv_row = (int64_t)b * width;
-    const int64_t p = ll_load_idx(a.pos, b, a.pos64);
-    cs = a.cos_tab + p * a.tab_stride;
-    sn = a.sin_tab + p * a.tab_stride;
-    new_slot = a.new_slots[b];
-    if ((int)threadIdx.x < a.G * QD) {  // G * QD <= 16 * D / 8 <= 256
-      const int g = threadIdx.x / QD, i = (threadIdx.x % QD) * 4;
-      rope_job<T, D>(a, b, qkv_row, (kvh * a.G + g) * D, i, cs, sn, true, s_q + g * D,
-                     nullptr);
-    }
-  } else {
+  if constexpr (!ROPE) {
     const int hq = kvh * a.G + min(n, a.G - 1);
     const T* qp = (const T*)a.q + (int64_t)b * a.q_sb + (int64_t)hq * a.q_sh;
 #pragma unroll
     for (int s = 0; s < DS; ++s) qb[s] = *(const V8*)(qp + 32 * s + 8 * j);
   }
-  // sequence length and request row, both loads in flight together (the low
-  // word of an int64 entry is the value: lengths and rows are below 2^31)
+  // sequence length and request row (and with ROPE the position and the new
+  // slot), all loads in flight together (the low word of an int64 entry is the
+  // value: lengths, rows and positions are below 2^31). The RoPE jobs come
+  // after the first slot loads are issued, so that the two dependent chains
+  // (length/row -> slots, position -> cos/sin) overlap.
+  // (the pointers and flags first, so that the four data loads go out together)
+  if constexpr (ROPE)
+    asm volatile("" ::"s"(a.seq_len), "s"(a.req_idx), "s"(a.len64), "s"(a.req64), "s"(a.pos),
+                 "s"(a.pos64), "s"(a.new_slots));
+  else
+    asm volatile("" ::"s"(a.seq_len), "s"(a.req_idx), "s"(a.len64), "s"(a.req64));
   const int32_t len32 = ((const int32_t*)a.seq_len)[a.len64 ? 2 * b : b];
   const int32_t rid32 = ((const int32_t*)a.req_idx)[a.req64 ? 2 * b : b];
-  asm volatile("" ::"s"(len32), "s"(rid32));  // keeps both loads here, not sunk apart
+  int32_t pos32 = 0, new_slot = 0;
+  if constexpr (ROPE) {
+    pos32 = ((const int32_t*)a.pos)[a.pos64 ? 2 * b : b];
+    new_slot = a.new_slots[b];
+  }
+  asm volatile("" ::"s"(len32), "s"(rid32), "s"(pos32), "s"(new_slot));  // keeps the loads here
   int64_t len = len32 > a.max_len ? a.max_len : len32;
   const int64_t rid = rid32;
   const int32_t* slot_row = a.r2t + rid * a.r2t_s;
@@ -245,10 +246,42 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
   const int64_t tok0 = (int64_t)tb * kTT;
   const int ntok = (int)(min(len, (int64_t)te * kTT) - tok0);  // tokens of this split (may be 0)
 
-  // ROPE: the split holding the last tile (split 0 for an empty sequence)
-  // writes the new token's K and V (the last 2 * QD threads, one job each)
+  // slot ids of the split -> LDS (tail entries point at slot 0, masked later);
+  // four loads per thread in flight per round, the first round's issued
+  // before the RoPE jobs
+  const int nslots = (te - tb) * kTT;
+  auto load_slots = [&](int i0, int32_t (&v)[4]) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = i0 + u * kWaves * 64 + threadIdx.x;
+      const int64_t t = min(tok0 + i, len > 0 ? len - 1 : (int64_t)0);  // always a valid entry
+      const int32_t sl = slot_row[t];
+      v[u] = (i < ntok) ? sl : 0;
+    }
+  };
+  auto store_slots = [&](int i0, const int32_t (&v)[4]) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = i0 + u * kWaves * 64 + threadIdx.x;
+      if (i < nslots) s_slots[i] = v[u];
+    }
+  };
+  int32_t v0[4];
+  load_slots(0, v0);
+
+  // ROPE: q of the group's heads into LDS; the split holding the last tile
+  // (split 0 for an empty sequence) also writes the new token's K and V (the
+  // last 2 * QD threads, one job each)
   bool writer = false;
   if constexpr (ROPE) {
+    const int64_t qkv_row = (int64_t)b * ((a.H + 2 * a.KVH) * D);
+    const float* cs = a.cos_tab + (int64_t)pos32 * a.tab_stride;
+    const float* sn = a.sin_tab + (int64_t)pos32 * a.tab_stride;
+    if ((int)threadIdx.x < a.G * QD) {  // G * QD <= 16 * D / 8 <= 256
+      const int g = threadIdx.x / QD, i = (threadIdx.x % QD) * 4;
+      rope_job<T, D>(a, b, qkv_row, (kvh * a.G + g) * D, i, cs, sn, true, s_q + g * D,
+                     nullptr);
+    }
     writer = split == (ntiles > 0 ? (ntiles - 1) / per : 0);
     const int jb = (int)threadIdx.x - (kWaves * 64 - 2 * QD);
     if (writer && jb >= 0) {
@@ -260,24 +293,11 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
                      !isv, s_kv + (isv ? D : 0), glb);
     }
   }
-
-  // slot ids of the split -> LDS (tail entries point at slot 0, masked later);
-  // four loads per thread in flight per round
-  const int nslots = (te - tb) * kTT;
-  for (int i0 = 0; i0 < nslots; i0 += 4 * kWaves * 64) {
+  store_slots(0, v0);
+  for (int i0 = 4 * kWaves * 64; i0 < nslots; i0 += 4 * kWaves * 64) {
     int32_t v[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int i = i0 + u * kWaves * 64 + threadIdx.x;
-      const int64_t t = min(tok0 + i, len > 0 ? len - 1 : (int64_t)0);  // always a valid entry
-      const int32_t sl = slot_row[t];
-      v[u] = (i < ntok) ? sl : 0;
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int i = i0 + u * kWaves * 64 + threadIdx.x;
-      if (i < nslots) s_slots[i] = v[u];
-    }
+    load_slots(i0, v);
+    store_slots(i0, v);
   }
   if constexpr (ROPE) {
     __syncthreads();  // s_q, s_kv and the slot table are complete
@@ -901,6 +921,8 @@ extern "C" int ll_decode_attention_rope_splitk_i32(
   LL_CHECK_ARG(s_tok && s_ch, "ll_decode_attention_rope_splitk_i32: null scale pointer");
   LL_CHECK_ARG(s_ch_dtype == LL_F32 || s_ch_dtype == LL_F16 || s_ch_dtype == LL_BF16,
                "ll_decode_attention_rope_splitk_i32: bad scale dtype %d", s_ch_dtype);
+  LL_CHECK_ARG(((uintptr_t)s_ch) % 4 == 0,
+               "ll_decode_attention_rope_splitk_i32: s_ch must be 4 B aligned");
   LLPartials P = {qkv_part, qkv_splits, 0, s_tok, s_ch, s_ch_dtype, 1};
   return rope_attention_impl(P, qkv_bias, positions, positions_i64, cos_table, sin_table,
                              table_row_stride, cs_dtype, new_slots, k_cache, k_stride_tok,

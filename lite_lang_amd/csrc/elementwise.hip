@@ -599,6 +599,7 @@ extern "C" int ll_add_rmsnorm_splitk_i32(void* h, int64_t h_row_stride, const in
                "ll_add_rmsnorm_splitk_i32: q_out and q_scale go together (ldq >= N)");
   LL_CHECK_ARG(s_ch_dtype == LL_F32 || s_ch_dtype == LL_F16 || s_ch_dtype == LL_BF16,
                "ll_add_rmsnorm_splitk_i32: bad scale dtype %d", s_ch_dtype);
+  LL_CHECK_ARG(((uintptr_t)s_ch) % 4 == 0, "ll_add_rmsnorm_splitk_i32: s_ch must be 4 B aligned");
   if (M == 0) return LL_OK;
   LLPartials P = {part, splits, M * N, s_tok, s_ch, s_ch_dtype, 1};
   return launch_add_rmsnorm(h, h_row_stride, P, gamma, out, out_row_stride, M, N, eps, dtype,
@@ -616,8 +617,8 @@ __global__ void silu_and_mul_splitk_kernel(LLPartials P, T* __restrict__ out, in
   if (m >= M) return;
   const int n = (int)(gid - (int64_t)m * q) * 4;
   const int64_t base = (int64_t)m * 2 * N;
-  const f32x4 g4 = ll_partials_sum4(P, base + n, m, n);
-  const f32x4 u4 = ll_partials_sum4(P, base + N + n, m, N + n);
+  f32x4 g4, u4;
+  ll_partials_sum4_pair(P, base + n, base + N + n, m, n, N + n, g4, u4);
   T* op = out + (int64_t)m * o_rs + n;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
@@ -658,6 +659,7 @@ extern "C" int ll_silu_and_mul_splitk_i32(const int32_t* part, int splits, const
                "ll_silu_and_mul_splitk_i32: N must be a multiple of 4, partials 16 B aligned");
   LL_CHECK_ARG(s_ch_dtype == LL_F32 || s_ch_dtype == LL_F16 || s_ch_dtype == LL_BF16,
                "ll_silu_and_mul_splitk_i32: bad scale dtype %d", s_ch_dtype);
+  LL_CHECK_ARG(((uintptr_t)s_ch) % 4 == 0, "ll_silu_and_mul_splitk_i32: s_ch must be 4 B aligned");
   if (M == 0 || N == 0) return LL_OK;
   LLPartials P = {part, splits, M * 2 * N, s_tok, s_ch, s_ch_dtype, 1};
   return launch_silu_and_mul_splitk(P, out, out_row_stride, M, N, dtype, stream);

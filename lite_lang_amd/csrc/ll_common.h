@@ -160,12 +160,110 @@ __device__ __forceinline__ float ll_scale_bits_to_f32(uint32_t bits, int dtype) 
 __device__ __forceinline__ f32x4 ll_partials_sum4(const LLPartials& P, int64_t idx, int64_t m,
                                                   int64_t col) {
   if (!P.i32) return ll_sum_splits4((const float*)P.p, P.splits, P.sstride, idx);
-  const i32x4 acc = ll_sum_splits4_i32((const int32_t*)P.p, P.splits, P.sstride, idx);
+  // the scales' raw bits are loaded ahead of the partials and converted after
+  // the sum, so that all loads share one round trip (a conversion next to a
+  // load under the dtype branch would wait for it there)
+  // (16-bit scales as the two whole dwords holding them: col is a multiple of
+  // 4 and s_ch 4-byte aligned; the halves are taken apart only at the end)
   const float st = P.s_tok[m];
+  const uint32_t* sw = (const uint32_t*)P.s_ch;
+  const bool f32 = P.s_ch_dtype == LL_F32;
+  uint32_t sb[4];
+  if (f32) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sb[e] = sw[col + e];
+  } else {
+    sb[0] = sw[col / 2];
+    sb[1] = sw[col / 2 + 1];
+    sb[2] = sb[3] = 0u;
+  }
+  const i32x4 acc = ll_sum_splits4_i32((const int32_t*)P.p, P.splits, P.sstride, idx);
   f32x4 o;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) o[e] = (float)acc[e] * st * ll_load_scale(P.s_ch, P.s_ch_dtype, col + e);
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t bits = f32 ? sb[e] : (sb[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+    o[e] = (float)acc[e] * st * ll_scale_bits_to_f32(bits, P.s_ch_dtype);
+  }
   return o;
+}
+
+// Two column groups (idx0/col0 and idx1/col1) of ll_partials_sum4 with every
+// load of both issued before either sum (one memory round trip for up to 8
+// splits); each group is summed exactly as ll_partials_sum4 sums it.
+template <int U>
+__device__ __forceinline__ void ll_sum_splits4_pair_upto(const float* __restrict__ part, int splits,
+                                                         int64_t ss, int64_t i0, int64_t i1,
+                                                         f32x4& a0, f32x4& a1) {
+  f32x4 v[U], w[U];
+#pragma unroll
+  for (int sp = 0; sp < U; ++sp) {
+    const int64_t o = (int64_t)min(sp, splits - 1) * ss;
+    v[sp] = *(const f32x4*)(part + o + i0);
+    w[sp] = *(const f32x4*)(part + o + i1);
+  }
+  a0 = (f32x4){0.f, 0.f, 0.f, 0.f};
+  a1 = a0;
+#pragma unroll
+  for (int sp = 0; sp < U; ++sp)
+    if (sp < splits) {
+      a0 += v[sp];
+      a1 += w[sp];
+    }
+}
+
+__device__ __forceinline__ void ll_partials_sum4_pair(const LLPartials& P, int64_t idx0,
+                                                      int64_t idx1, int64_t m, int64_t col0,
+                                                      int64_t col1, f32x4& o0, f32x4& o1) {
+  if (P.splits > 8) {
+    o0 = ll_partials_sum4(P, idx0, m, col0);
+    o1 = ll_partials_sum4(P, idx1, m, col1);
+    return;
+  }
+  if (!P.i32) {
+    const float* part = (const float*)P.p;
+    if (P.splits <= 4) ll_sum_splits4_pair_upto<4>(part, P.splits, P.sstride, idx0, idx1, o0, o1);
+    else ll_sum_splits4_pair_upto<8>(part, P.splits, P.sstride, idx0, idx1, o0, o1);
+    return;
+  }
+  const float st = P.s_tok[m];
+  const uint32_t* sw = (const uint32_t*)P.s_ch;
+  const bool f32 = P.s_ch_dtype == LL_F32;
+  uint32_t sb0[4], sb1[4];
+  if (f32) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      sb0[e] = sw[col0 + e];
+      sb1[e] = sw[col1 + e];
+    }
+  } else {
+    sb0[0] = sw[col0 / 2];
+    sb0[1] = sw[col0 / 2 + 1];
+    sb1[0] = sw[col1 / 2];
+    sb1[1] = sw[col1 / 2 + 1];
+    sb0[2] = sb0[3] = sb1[2] = sb1[3] = 0u;
+  }
+  const int32_t* part = (const int32_t*)P.p;
+  i32x4 v[8], w[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const int64_t o = (int64_t)min(u, P.splits - 1) * P.sstride;
+    v[u] = *(const i32x4*)(part + o + idx0);
+    w[u] = *(const i32x4*)(part + o + idx1);
+  }
+  i32x4 a0 = {0, 0, 0, 0}, a1 = {0, 0, 0, 0};
+#pragma unroll
+  for (int u = 0; u < 8; ++u)
+    if (u < P.splits) {
+      a0 += v[u];
+      a1 += w[u];
+    }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t b0 = f32 ? sb0[e] : (sb0[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+    const uint32_t b1 = f32 ? sb1[e] : (sb1[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+    o0[e] = (float)a0[e] * st * ll_scale_bits_to_f32(b0, P.s_ch_dtype);
+    o1[e] = (float)a1[e] * st * ll_scale_bits_to_f32(b1, P.s_ch_dtype);
+  }
 }
 
 __host__ __device__ inline LLPartials ll_partials_f32(const float* p, int splits, int64_t sstride) {
