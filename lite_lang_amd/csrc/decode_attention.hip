@@ -22,7 +22,7 @@
 //   * the split count is fixed per launch and each sequence divides its own
 //     length into that many tile-aligned chunks, so the grid does not depend
 //     on the lengths (graph safe);
-//   * the 4 waves merge in LDS; the splits of a (sequence, KV head) are merged
+//   * the 8 waves merge in LDS; the splits of a (sequence, KV head) are merged
 //     by a second kernel, one wave per (sequence, head) with the partials of
 //     all splits in flight at once. Merging in the same launch (the last
 //     split to finish merges, signalled through a device-scope counter) was
@@ -34,7 +34,8 @@
 namespace {
 
 constexpr int kTT = 16;     // tokens per tile
-constexpr int kWaves = 4;   // waves per workgroup
+constexpr int kWaves = 8;   // waves per split-stage workgroup
+constexpr int kCombWaves = 4;  // waves (one (sequence, head) each) per combine workgroup
 constexpr int kRing = 2;    // tile buffers per wave
 
 template <typename T> struct Vec8;
@@ -527,10 +528,10 @@ __device__ __forceinline__ void combine_bh(const DecodeArgs& a, int bh, int lane
 }
 
 template <typename T, int D>
-__global__ __launch_bounds__(256) void decode_attn_combine_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(kCombWaves * 64) void decode_attn_combine_kernel(DecodeArgs a) {
   constexpr int DPL = D / 64;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int bh = blockIdx.x * kWaves + wave;
+  const int bh = blockIdx.x * kCombWaves + wave;
   if (bh >= a.B * a.H) return;
   const int b = bh / a.H, h = bh - b * a.H;
   float o[DPL];
@@ -656,12 +657,18 @@ __global__ __launch_bounds__(64) void decode_attn_generic_kernel(DecodeArgs a, i
 
 constexpr int kMaxSplitTokens = 4096;  // LDS slot table bound per split (16 KB)
 
-int choose_nsplit(int B, int KVH, int64_t max_len) {
+int choose_nsplit(int B, int KVH, int64_t max_len, int64_t head_dim) {
   const int units = B * KVH;
   const int64_t tiles = (max_len + kTT - 1) / kTT;
-  // Two workgroups fit a CU (256 CUs): fill one dispatch round, never more,
+  // Fill one dispatch round of the 256 CUs, never more (as many split-stage
+  // workgroups per CU as their LDS allows: one at head_dim 128, two at 64),
   // while giving every wave at least one tile and bounding the slot table.
-  int ns = 512 / units;
+  // Measured at 40 sequences x 2 KV heads: one workgroup of 8 waves per CU
+  // beats two of 4 waves from 600 tokens up (fewer splits to merge, the same
+  // bytes in flight per CU).
+  const int64_t main_b = head_dim == 64 ? TileGeom<64>::MAIN_B : TileGeom<128>::MAIN_B;
+  const int per_cu = (int)(160 * 1024 / (main_b + 8192)) > 1 ? (int)(160 * 1024 / (main_b + 8192)) : 1;
+  int ns = 256 * per_cu / units;
   const int64_t max_ns = tiles / kWaves;
   if (ns > max_ns) ns = (int)max_ns;
   const int64_t min_ns = (tiles * kTT + kMaxSplitTokens - 1) / kMaxSplitTokens;
@@ -700,18 +707,18 @@ void launch_combine(const DecodeArgs& a, int dtype, hipStream_t stream) {
     }
     return;
   }
-  const dim3 cgrid((unsigned)((a.B * a.H + kWaves - 1) / kWaves));
+  const dim3 cgrid((unsigned)((a.B * a.H + kCombWaves - 1) / kCombWaves));
   if (dtype == LL_BF16)
-    hipLaunchKernelGGL((decode_attn_combine_kernel<__bf16, D>), cgrid, dim3(kWaves * 64), 0,
+    hipLaunchKernelGGL((decode_attn_combine_kernel<__bf16, D>), cgrid, dim3(kCombWaves * 64), 0,
                        stream, a);
   else
-    hipLaunchKernelGGL((decode_attn_combine_kernel<_Float16, D>), cgrid, dim3(kWaves * 64), 0,
+    hipLaunchKernelGGL((decode_attn_combine_kernel<_Float16, D>), cgrid, dim3(kCombWaves * 64), 0,
                        stream, a);
 }
 
 int64_t workspace_bytes_for(int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
                             int64_t max_len) {
-  const int ns = choose_nsplit((int)batch, (int)kv_heads, max_len);
+  const int ns = choose_nsplit((int)batch, (int)kv_heads, max_len, head_dim);
   if (ns <= 1) return 0;
   const int64_t parts = batch * q_heads * ns;
   return align256(parts * head_dim * 4)  // partial acc
@@ -722,7 +729,7 @@ int64_t workspace_bytes_for(int64_t batch, int64_t q_heads, int64_t kv_heads, in
 // every field but the split geometry and the workspace pointers set.
 int launch_mfma(DecodeArgs& a, int64_t head_dim, int dtype, bool rope, int64_t max_len,
                 void* workspace, int64_t workspace_bytes, hipStream_t stream) {
-  a.nsplit = choose_nsplit(a.B, a.KVH, max_len);
+  a.nsplit = choose_nsplit(a.B, a.KVH, max_len, head_dim);
   if (a.nsplit > 1) {
     const int64_t need = workspace_bytes_for(a.B, a.H, a.KVH, head_dim, max_len);
     LL_CHECK_ARG(workspace != nullptr && workspace_bytes >= need,
