@@ -104,10 +104,11 @@ __device__ __forceinline__ void wait_stage(int later) {
 // tile one contiguous, already swizzled 16 KB block, blocks ordered chunk-
 // major), so concurrent workgroups stream neighbouring blocks.
 // EPI 1 (with PK and the gate/up tile layout of ll_gemm_pack_gate_up, one
-// split): tile rows 0..31 are gate channels 32t.., rows 32..63 the matching up
-// channels; the epilogue writes Y[m, c] = T(T(up) * T(silu(T(gate)))) for the
-// 32 channels of the tile (N = 2 * channels), the rounding sequence of
-// ll_silu_and_mul_splitk applied to the same fp32 sums.
+// split): tile rows 0..TR/2-1 are gate channels (TR/2)t.., the other TR/2 rows
+// the matching up channels; the epilogue writes Y[m, c] =
+// T(T(up) * T(silu(T(gate)))) for the TR/2 channels of the tile (N = 2 *
+// channels), the rounding sequence of ll_silu_and_mul_splitk applied to the
+// same fp32 sums.
 // int8 gate/up epilogue (EPI 1 with int8 operands): the int32 sums are
 // dequantised as fp32(acc) * s_tok[m] * fp32(s_ch[col]) (col = channel for
 // gate, I + channel for up) and SiLU_and_Mul is written to y (type TO).
@@ -236,69 +237,84 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, 
     }
   }
   // acc[b][t][i] = Y[token 16t + n][channel row0 + 16*RB*wave + 16b + 4j + i]
-  if constexpr (ES == 1 && EPI == 1) {
-    // int8 gate/up, one split: dequantise, then SiLU_and_Mul with the rounding
-    // sequence of silu_and_mul_splitk (waves 2, 3 hand the up values to 0, 1)
-    constexpr int HALF = TR / 2;
+  if constexpr (EPI == 1) {
+    // gate/up, one split: every wave puts its sums (int8: dequantised as
+    // fp32(acc) * s_tok[m] * fp32(s_ch[col])) into LDS rows [token][channel],
+    // gate from waves 0, 1 and up from waves 2, 3; then each thread takes 4
+    // consecutive channels of one token through SiLU_and_Mul with the rounding
+    // sequence of silu_and_mul_splitk, computed before its one guarded 8-byte
+    // store. All four waves share the arithmetic.
+    constexpr int HALF = TR / 2;      // gate (and up) channels of the tile
+    constexpr int PITCH = HALF + 4;   // floats per LDS row: rows shift by 16 B across the banks
+    constexpr int XT = 16 * MB;       // token rows
     const int I = N / 2;
-    float* ub = (float*)smem;  // [HALF channels][16 * MB tokens]
-    float sc[RB][4];
-    auto cvt = [&](auto dt) {
+    float* gbuf = (float*)smem;
+    float* ubuf = gbuf + XT * PITCH;
+    float vs[RB][MB][4];
+    if constexpr (ES == 1) {
+      float sc[RB][4];
+      auto cvt = [&](auto dt) {
+#pragma unroll
+        for (int b = 0; b < RB; ++b)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) sc[b][i] = ll_scale_bits_to_f32(e_sc[b][i], decltype(dt)::value);
+      };
+      if (e8.s_ch_dtype == LL_F16) cvt(std::integral_constant<int, LL_F16>{});
+      else if (e8.s_ch_dtype == LL_BF16) cvt(std::integral_constant<int, LL_BF16>{});
+      else cvt(std::integral_constant<int, LL_F32>{});
 #pragma unroll
       for (int b = 0; b < RB; ++b)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sc[b][i] = ll_scale_bits_to_f32(e_sc[b][i], decltype(dt)::value);
-    };
-    if (e8.s_ch_dtype == LL_F16) cvt(std::integral_constant<int, LL_F16>{});
-    else if (e8.s_ch_dtype == LL_BF16) cvt(std::integral_constant<int, LL_BF16>{});
-    else cvt(std::integral_constant<int, LL_F32>{});
-    lds_barrier();
-    if (wave >= 2) {
-#pragma unroll
-      for (int b = 0; b < RB; ++b)
-#pragma unroll
-        for (int t = 0; t < MB; ++t) {
-          const int cl = 16 * RB * (wave - 2) + 16 * b + 4 * j;
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            ub[(cl + i) * (16 * MB) + 16 * t + n] = (float)acc[b][t][i] * e_st[t] * sc[b][i];
-        }
-    }
-    lds_barrier();
-    if (wave < 2) {
-      // every output of the lane first (one wait for the scales and the LDS
-      // exchange), then the guarded stores, 4 channels per 8-byte store
-      TO y[RB][MB][4];
-#pragma unroll
-      for (int b = 0; b < RB; ++b) {
-        const int cl = 16 * RB * wave + 16 * b + 4 * j;
 #pragma unroll
         for (int t = 0; t < MB; ++t)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float gf = (float)acc[b][t][i] * e_st[t] * sc[b][i];
-            const float g = ll_to_f32(ll_from_f32<TO>(gf));
-            const float u = ll_to_f32(ll_from_f32<TO>(ub[(cl + i) * (16 * MB) + 16 * t + n]));
-            const TO sv = ll_from_f32<TO>(g / (1.0f + __expf(-g)));
-            y[b][t][i] = ll_from_f32<TO>(u * ll_to_f32(sv));
-          }
+          for (int i = 0; i < 4; ++i) vs[b][t][i] = (float)acc[b][t][i] * e_st[t] * sc[b][i];
+    } else {
+#pragma unroll
+      for (int b = 0; b < RB; ++b)
+#pragma unroll
+        for (int t = 0; t < MB; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) vs[b][t][i] = acc[b][t][i];
+    }
+    lds_barrier();  // every wave is done reading the last stage
+    float* dst = wave < 2 ? gbuf : ubuf;
+#pragma unroll
+    for (int b = 0; b < RB; ++b)
+#pragma unroll
+      for (int t = 0; t < MB; ++t) {
+        const int cl = 16 * RB * (wave & 1) + 16 * b + 4 * j;
+        *(f32x4*)(dst + (16 * t + n) * PITCH + cl) =
+            (f32x4){vs[b][t][0], vs[b][t][1], vs[b][t][2], vs[b][t][3]};
       }
-      TO* Yo = (TO*)e8.y;
-      const bool vec = ((I | e8.ldy) & 3) == 0;
+    lds_barrier();
+    TO* Yo = ES == 1 ? (TO*)e8.y : (TO*)Y;
+    const int64_t ly = ES == 1 ? e8.ldy : ldy;
+    const bool vec = ((I | ly) & 3) == 0;
+    constexpr int QPR = HALF / 4;     // channel quads per token row
+    constexpr int QUADS = XT * QPR;
 #pragma unroll
-      for (int b = 0; b < RB; ++b) {
-        const int c0 = blockIdx.x * HALF + 16 * RB * wave + 16 * b + 4 * j;
+    for (int r = 0; r < (QUADS + 255) / 256; ++r) {
+      const int q = r * 256 + (int)threadIdx.x;
+      if (QUADS % 256 != 0 && q >= QUADS) break;
+      const int tok = q / QPR, cq = (q - tok * QPR) * 4;
+      const f32x4 g4 = *(const f32x4*)(gbuf + tok * PITCH + cq);
+      const f32x4 u4 = *(const f32x4*)(ubuf + tok * PITCH + cq);
+      TO y[4];
 #pragma unroll
-        for (int t = 0; t < MB; ++t) {
-          const int tok = 16 * t + n;
-          if (tok >= M || c0 >= I) continue;
-          TO* yp = Yo + (int64_t)tok * e8.ldy + c0;
-          if (vec) {
-            typedef TO V4 __attribute__((ext_vector_type(4)));
-            *(V4*)yp = (V4){y[b][t][0], y[b][t][1], y[b][t][2], y[b][t][3]};
-          } else {
-            for (int i = 0; i < 4 && c0 + i < I; ++i) yp[i] = y[b][t][i];
-          }
+      for (int e = 0; e < 4; ++e) {
+        const float g = ll_to_f32(ll_from_f32<TO>(g4[e]));
+        const float u = ll_to_f32(ll_from_f32<TO>(u4[e]));
+        const TO sv = ll_from_f32<TO>(g / (1.0f + __expf(-g)));
+        y[e] = ll_from_f32<TO>(u * ll_to_f32(sv));
+      }
+      const int c0 = blockIdx.x * HALF + cq;
+      if (tok < M && c0 < I) {
+        TO* yp = Yo + (int64_t)tok * ly + c0;
+        if (vec) {
+          typedef TO V4 __attribute__((ext_vector_type(4)));
+          *(V4*)yp = (V4){y[0], y[1], y[2], y[3]};
+        } else {
+          for (int e = 0; e < 4 && c0 + e < I; ++e) yp[e] = y[e];
         }
       }
     }
@@ -318,43 +334,6 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, 
           *(i32x4*)pp = acc[b][t];
         } else {
           for (int i = 0; i < 4 && ch + i < N; ++i) pp[i] = acc[b][t][i];
-        }
-      }
-    }
-    return;
-  } else if constexpr (EPI == 1) {
-    // waves 2, 3 (up rows) hand their sums to waves 0, 1 (gate rows) through LDS
-    constexpr int HALF = TR / 2;  // gate channels of the tile
-    float* ub = (float*)smem;     // [HALF channels][16 * MB tokens]
-    lds_barrier();                // every wave is done reading the last stage
-    if (wave >= 2) {
-#pragma unroll
-      for (int b = 0; b < RB; ++b)
-#pragma unroll
-        for (int t = 0; t < MB; ++t)
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            ub[(16 * RB * (wave - 2) + 16 * b + 4 * j + i) * (16 * MB) + 16 * t + n] = acc[b][t][i];
-    }
-    lds_barrier();
-    if (wave < 2) {
-      const int I = N / 2;
-#pragma unroll
-      for (int b = 0; b < RB; ++b) {
-        const int cl = 16 * RB * wave + 16 * b + 4 * j;  // channel within the tile
-        const int c0 = blockIdx.x * HALF + cl;
-#pragma unroll
-        for (int t = 0; t < MB; ++t) {
-          const int tok = 16 * t + n;
-          if (tok >= M) continue;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            if (c0 + i >= I) continue;
-            const float g = ll_to_f32(ll_from_f32<T>(acc[b][t][i]));
-            const float u = ll_to_f32(ll_from_f32<T>(ub[(cl + i) * (16 * MB) + 16 * t + n]));
-            const T sv = ll_from_f32<T>(g / (1.0f + __expf(-g)));
-            Y[(int64_t)tok * ldy + c0 + i] = ll_from_f32<T>(u * ll_to_f32(sv));
-          }
         }
       }
     }
