@@ -335,6 +335,9 @@ extern "C" int ll_embedding(const void* table, int64_t table_row_stride, int64_t
 // (value, index) partial; pass 2 reduces the partials of each row. (Two
 // launches: an in-launch last-workgroup merge would need a device-scope
 // fence per workgroup, which flushes the XCD's whole L2 on gfx950.)
+static const int kArgmaxChunk = 8192;   // elements per workgroup of pass 1
+constexpr int kArgmaxChunkV = 8192;    // the same for the 16-byte-load pass
+
 __device__ __forceinline__ void argmax_merge(float& v, int& i, float ov, int oi) {
   if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
 }
@@ -378,6 +381,50 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const T* __restrict
   }
 }
 
+// Pass 1 with 16-byte loads (16-bit types, rows 16 B aligned, N % 8 == 0):
+// every thread issues the loads of its whole share of the chunk before the
+// first compare (clamped addresses, masked values), then merges them in index
+// order, so the first-index rule holds as in the scalar pass.
+template <typename T>
+__global__ __launch_bounds__(256) void argmax_partial_vec8_kernel(const T* __restrict__ x,
+                                                                  int64_t x_rs, int N,
+                                                                  float* __restrict__ pval,
+                                                                  int* __restrict__ pidx,
+                                                                  int64_t* __restrict__ out) {
+  typedef T V8 __attribute__((ext_vector_type(8)));
+  constexpr int PER = kArgmaxChunkV / (256 * 8);  // 16-byte loads per thread
+  __shared__ float sv[4];
+  __shared__ int si[4];
+  const int row = blockIdx.y, c = blockIdx.x, nchunk = gridDim.x;
+  const T* xr = x + (int64_t)row * x_rs;
+  const int beg = c * kArgmaxChunkV, end = min(N, beg + kArgmaxChunkV);
+  V8 v[PER];
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const int p = beg + (q * 256 + (int)threadIdx.x) * 8;
+    v[q] = *(const V8*)(xr + min(p, end - 8));
+  }
+  float best = -INFINITY;
+  int bi = 0x7fffffff;
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const int p = beg + (q * 256 + (int)threadIdx.x) * 8;
+    if (p < end) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) argmax_merge(best, bi, ll_to_f32(v[q][e]), p + e);
+    }
+  }
+  argmax_block_reduce(best, bi, sv, si);
+  if (threadIdx.x == 0) {
+    if (nchunk == 1) {
+      out[row] = (int64_t)(bi == 0x7fffffff ? 0 : bi);
+    } else {
+      pval[row * nchunk + c] = best;
+      pidx[row * nchunk + c] = bi;
+    }
+  }
+}
+
 __global__ __launch_bounds__(256) void argmax_final_kernel(const float* __restrict__ pval,
                                                            const int* __restrict__ pidx,
                                                            int nchunk, int64_t* __restrict__ out) {
@@ -392,7 +439,6 @@ __global__ __launch_bounds__(256) void argmax_final_kernel(const float* __restri
   if (threadIdx.x == 0) out[row] = (int64_t)(bi == 0x7fffffff ? 0 : bi);
 }
 
-static const int kArgmaxChunk = 8192;
 
 extern "C" int64_t ll_argmax_workspace_size(int64_t M, int64_t N) {
   const int64_t nchunk = (N + kArgmaxChunk - 1) / kArgmaxChunk;
@@ -414,9 +460,20 @@ extern "C" int ll_argmax(const void* x, int64_t x_row_stride, int64_t M, int64_t
     pval = (float*)workspace;
     pidx = (int*)(pval + M * nchunk);
   }
+  const bool vec = (dtype == LL_BF16 || dtype == LL_F16) && N % 8 == 0 && x_row_stride % 8 == 0 &&
+                   ((uintptr_t)x % 16) == 0;
   return LL_DISPATCH_DTYPE(dtype, T, [&]() -> int {
-    hipLaunchKernelGGL((argmax_partial_kernel<T>), dim3(nchunk, (unsigned)M), dim3(256), 0, stream,
-                       (const T*)x, x_row_stride, (int)N, kArgmaxChunk, pval, pidx, out);
+    if constexpr (sizeof(T) == 2) {
+      if (vec)
+        hipLaunchKernelGGL((argmax_partial_vec8_kernel<T>), dim3(nchunk, (unsigned)M), dim3(256),
+                           0, stream, (const T*)x, x_row_stride, (int)N, pval, pidx, out);
+      else
+        hipLaunchKernelGGL((argmax_partial_kernel<T>), dim3(nchunk, (unsigned)M), dim3(256), 0,
+                           stream, (const T*)x, x_row_stride, (int)N, kArgmaxChunk, pval, pidx, out);
+    } else {
+      hipLaunchKernelGGL((argmax_partial_kernel<T>), dim3(nchunk, (unsigned)M), dim3(256), 0,
+                         stream, (const T*)x, x_row_stride, (int)N, kArgmaxChunk, pval, pidx, out);
+    }
     if (nchunk > 1)
       hipLaunchKernelGGL(argmax_final_kernel, dim3((unsigned)M), dim3(256), 0, stream, pval, pidx,
                          nchunk, out);

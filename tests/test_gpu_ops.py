@@ -273,6 +273,18 @@ def test_embedding_and_argmax(cuda):
     assert got[3] == 100 and got[7] == 0
     got2 = _ops().argmax(logits[:, :5000].contiguous().to(cuda)).cpu()  # single-chunk path
     assert torch.equal(got2, O.argmax_first(logits[:, :5000].float()))
+    # ties inside one 16-byte load and across the 8192-wide chunk boundary,
+    # fp16, and a width that is not a multiple of 8 (the scalar pass)
+    lg = torch.randn(12, 20001, generator=g).half()
+    lg[5, 16:24] = 60.0
+    lg[9, 8191] = 70.0
+    lg[9, 8192] = 70.0
+    lg[10, 20000] = 80.0
+    for width in (20000, 20001):
+        sub = lg[:, :width].contiguous()
+        got3 = _ops().argmax(sub.to(cuda)).cpu()
+        assert torch.equal(got3, O.argmax_first(sub.float())), width
+    assert got3[5] == 16 and got3[9] == 8191 and got3[10] == 20000
 
 
 # ------------------------------------------------------------ GEMM
