@@ -530,3 +530,23 @@ def test_rope_kv_scatter_splitk(cuda):
     assert _maxdiff(q.view(T, H, D), q_ref) <= BF16_ATOL
     assert _maxdiff(pool[slots.long(), :KVH], k_ref) <= BF16_ATOL
     assert torch.equal(pool[slots.long(), KVH:].cpu().double(), qkv[:, (H + KVH) * D:].view(T, KVH, D))
+
+
+# ------------------------------------------------------------ slot table
+def test_assign_slots(cuda):
+    """ll_assign_slots: req_to_tokens[rows, cols] = slots (the table update of
+    PageCache.alloc_token_idxs, cache.py:238-248), over three rounds that
+    overwrite earlier entries."""
+    ops = _ops()
+    g = torch.Generator().manual_seed(41)
+    n = 40
+    ref = torch.zeros(50, 700, dtype=torch.int32)
+    r2t = ref.clone().to(cuda)
+    for _ in range(3):
+        rows = torch.randperm(50, generator=g)[:n].to(torch.int32)
+        cols = torch.randint(0, 700, (n,), generator=g, dtype=torch.int32)
+        slots = torch.randint(0, 1 << 20, (n,), generator=g, dtype=torch.int32)
+        ref[rows.long(), cols.long()] = slots
+        ops.assign_slots(r2t, torch.stack([slots, rows, cols]).to(cuda), n)
+    torch.cuda.synchronize()
+    assert torch.equal(r2t.cpu(), ref)
