@@ -21,6 +21,7 @@ from lite_lang_amd import ops
 from lite_lang_amd.models.cache import PageCache
 from lite_lang_amd.models.radix_cache import RadixTree
 from .decode_graph import DecodeGraph
+from ...tuning import use_prefill_gemm_solutions
 from .weights import (DeviceWeights, Qwen2Config, check_smoothquant_config, is_int8_checkpoint,
                       load_state_dict, random_state_dict)
 
@@ -91,7 +92,11 @@ class Qwen2Model:
             o = self._proj(attn.view(T, H * D), li, "wo")
             x2 = ops.rmsnorm(h, lw["ln2"], cfg.rms_norm_eps, residual=o)
             gu = self._proj(x2, li, "wgu")
-            act = ops.silu_and_mul(gu)
+            # a contiguous product (not the reference's in-place half view):
+            # the down projection then runs on the row layout its vendor GEMM
+            # solution was selected for
+            act = ops.silu_and_mul(gu, out=torch.empty((T, gu.shape[1] // 2), dtype=gu.dtype,
+                                                       device=gu.device))
             f = self._proj(act, li, "wdown")
         return f
 
@@ -363,6 +368,10 @@ class Qwen2ModelRunner:
                                   tp_rank=self.tp_rank_, tp_world_size=self.world_size_,
                                   kv_max_size=self.kv_max_size_arg_, device=self.device_)
         self.radix_cache = RadixTree() if self.use_radix_cache_ else None
+        if self.device_.type == "cuda":
+            # the prefill projections (vendor-library GEMMs) use the solutions
+            # selected offline for the benchmark shapes; other shapes are untouched
+            use_prefill_gemm_solutions()
         return self.kv_cache.kv_max_size_
 
     def _alloc_for_forward(self, model_inputs):
