@@ -47,6 +47,7 @@ struct PrefillArgs {
   const void* seq_len; int len64;
   const void* shared; int shared64;
   int H, G;
+  int nblk, B, KVH;  // MFMA path: query-row blocks per request, requests, KV heads
   float scale_log2;
   float sm_scale;
 };
@@ -60,10 +61,17 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_attn_mfma_kernel(PrefillA
   __shared__ __attribute__((aligned(16))) T vs[kTile * kVStride];
   __shared__ int slot_s[kTile];
 
-  const int mblk = blockIdx.x;
-  const int h = blockIdx.y;
-  const int b = blockIdx.z;
-  const int kvh = h / a.G;
+  // 1-D grid, XCD-aware: workgroups go round-robin over the 8 XCDs, so the G
+  // query heads of one (row block, request, KV head) unit take consecutive
+  // slots of the same XCD and read its K/V tiles through one L2; the longest
+  // (last) row blocks are dispatched first
+  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+  const int unit = (slot / a.G) * 8 + xcd;
+  if (unit >= a.nblk * a.B * a.KVH) return;
+  const int kvh = unit % a.KVH;
+  const int b = (unit / a.KVH) % a.B;
+  const int mblk = a.nblk - 1 - unit / (a.KVH * a.B);
+  const int h = kvh * a.G + slot % a.G;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int n = lane & 15;
@@ -303,7 +311,11 @@ extern "C" int ll_prefill_attention(const void* q, int64_t q_stride_tok, int64_t
       LL_RETURN_LAUNCH();
     });
   }
-  const dim3 grid((unsigned)ll_cdiv(max_input_len, kBlockM), (unsigned)q_heads, (unsigned)batch);
+  a.nblk = (int)ll_cdiv(max_input_len, kBlockM);
+  a.B = (int)batch;
+  a.KVH = (int)kv_heads;
+  const int64_t units = (int64_t)a.nblk * batch * kv_heads;
+  const dim3 grid((unsigned)(ll_cdiv(units, 8) * 8 * a.G));
   if (dtype == LL_BF16) {
     if (head_dim == 128)
       hipLaunchKernelGGL((prefill_attn_mfma_kernel<__bf16, 128>), grid, dim3(kWaves * 64), 0, stream, a);
