@@ -57,9 +57,8 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_attn_mfma_kernel(PrefillA
   typedef typename Vec8<T>::type V8;
   constexpr int DS = D / 32;
   constexpr int DB = D / 16;
-  __shared__ __attribute__((aligned(16))) T ks[kTile * kKStride];
-  __shared__ __attribute__((aligned(16))) T vs[kTile * kVStride];
-  __shared__ int slot_s[kTile];
+  __shared__ __attribute__((aligned(16))) T ks[2][kTile * kKStride];
+  __shared__ __attribute__((aligned(16))) T vs[2][kTile * kVStride];
 
   // 1-D grid, XCD-aware: workgroups go round-robin over the 8 XCDs, so the G
   // query heads of one (row block, request, KV head) unit take consecutive
@@ -112,38 +111,60 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_attn_mfma_kernel(PrefillA
   constexpr int VCH = D / 8;
   constexpr int ROWS_PER_PASS = (kWaves * 64) / VCH;
 
-  for (int64_t t0 = 0; t0 < kv_end; t0 += kTile) {
-    __syncthreads();  // previous tile fully consumed
-    if (threadIdx.x < kTile) {
-      const int64_t tok = t0 + threadIdx.x;
-      slot_s[threadIdx.x] = tok < kv_end ? slot_row[tok] : 0;
-    }
-    __syncthreads();
+  // Software pipeline over the 32-key tiles: the K/V rows of tile t+1 and the
+  // slot ids of tile t+2 are in flight (registers) while tile t is computed
+  // from one of two LDS buffers; one barrier per tile. Loads use clamped
+  // addresses (always a valid key) and rows past kv_end are zeroed on the
+  // LDS store.
+  constexpr int PASSES = (kTile + ROWS_PER_PASS - 1) / ROWS_PER_PASS;
+  const int ch = threadIdx.x % VCH, rr = threadIdx.x / VCH;
+  int32_t sl_cur[PASSES], sl_nxt[PASSES];
+  V8 kreg[PASSES], vreg[PASSES];
+  auto load_slots = [&](int64_t t0, int32_t (&s)[PASSES]) {
 #pragma unroll
-    for (int r0 = 0; r0 < kTile; r0 += ROWS_PER_PASS) {
-      const int r = r0 + threadIdx.x / VCH;
-      const int ch = threadIdx.x % VCH;
-      V8 kv, vv;
-      if (r < kTile && t0 + r < kv_end) {
-        const int64_t sl = slot_s[r];
-        kv = *(const V8*)(kbase + sl * a.k_st + ch * 8);
-        vv = *(const V8*)(vbase + sl * a.v_st + ch * 8);
-      } else {
-        for (int e = 0; e < 8; ++e) { kv[e] = (T)0.f; vv[e] = (T)0.f; }
-      }
+    for (int p = 0; p < PASSES; ++p)
+      s[p] = slot_row[min(t0 + p * ROWS_PER_PASS + rr, kv_end - 1)];
+  };
+  auto load_kv = [&](const int32_t (&s)[PASSES]) {
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+      kreg[p] = *(const V8*)(kbase + (int64_t)s[p] * a.k_st + ch * 8);
+      vreg[p] = *(const V8*)(vbase + (int64_t)s[p] * a.v_st + ch * 8);
+    }
+  };
+  load_slots(0, sl_cur);
+  load_kv(sl_cur);
+  load_slots(kTile, sl_nxt);
+  for (int64_t t0 = 0; t0 < kv_end; t0 += kTile) {
+    const int buf = (int)((t0 / kTile) & 1);
+    T* ksb = ks[buf];
+    T* vsb = vs[buf];
+    // this tile's rows into LDS (the buffer was last read two tiles ago,
+    // before the previous barrier)
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+      const int r = p * ROWS_PER_PASS + rr;
       if (r < kTile) {
-        *(V8*)(ks + r * kKStride + ch * 8) = kv;
-        *(V8*)(vs + r * kVStride + ch * 8) = vv;
+        const bool ok = t0 + r < kv_end;
+        V8 kv = kreg[p], vv = vreg[p];
+        if (!ok)
+          for (int e = 0; e < 8; ++e) { kv[e] = (T)0.f; vv[e] = (T)0.f; }
+        *(V8*)(ksb + r * kKStride + ch * 8) = kv;
+        *(V8*)(vsb + r * kVStride + ch * 8) = vv;
       }
     }
     __syncthreads();
+    if (t0 + kTile < kv_end) {
+      load_kv(sl_nxt);
+      load_slots(t0 + 2 * kTile, sl_nxt);
+    }
     if (t0 >= wave_kv_end) continue;  // every row of this wave is causally done
 
     f32x4 sA = {0.f, 0.f, 0.f, 0.f}, sB = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < DS; ++s) {
-      const V8 ka = *(const V8*)(ks + n * kKStride + 32 * s + 8 * j);
-      const V8 kb = *(const V8*)(ks + (16 + n) * kKStride + 32 * s + 8 * j);
+      const V8 ka = *(const V8*)(ksb + n * kKStride + 32 * s + 8 * j);
+      const V8 kb = *(const V8*)(ksb + (16 + n) * kKStride + 32 * s + 8 * j);
       sA = mfma16x16x32(ka, qb[s], sA);
       sB = mfma16x16x32(kb, qb[s], sB);
     }
@@ -177,7 +198,7 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_attn_mfma_kernel(PrefillA
     for (int c = 0; c < DB; ++c) {
       acc[c] *= alpha;
       V8 va;
-      const T* col = vs + 16 * c + n;
+      const T* col = vsb + 16 * c + n;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         va[i] = col[(4 * j + i) * kVStride];
