@@ -274,10 +274,18 @@ __host__ __device__ inline LLPartials ll_partials_f32(const float* p, int splits
 // Rotate-half RoPE of one (x_i, x_{i+D/2}) pair, rounded to T. The fused
 // multiply-adds are written out so every kernel rotating a pair rounds it the
 // same way: y0 = fma(a, c, -(b*s)), y1 = fma(a, s, b*c).
+// For fp16 the fp32 results are materialised before the conversion: otherwise
+// the compiler may fuse fma + fp16 conversion into one mixed-precision
+// instruction that rounds once, straight to fp16, where this sequence rounds
+// to fp32 first (a one-ulp difference in rare cases, and between kernels).
+// bf16 has no such fused instruction.
 template <typename T>
 __device__ __forceinline__ void ll_rope_pair(float a, float b, float c, float s, T& y0, T& y1) {
-  y0 = ll_from_f32<T>(__builtin_fmaf(a, c, -(b * s)));
-  y1 = ll_from_f32<T>(__builtin_fmaf(a, s, b * c));
+  float r0 = __builtin_fmaf(a, c, -(b * s));
+  float r1 = __builtin_fmaf(a, s, b * c);
+  if constexpr (sizeof(T) == 2 && !__is_same(T, __bf16)) asm volatile("" : "+v"(r0), "+v"(r1));
+  y0 = ll_from_f32<T>(r0);
+  y1 = ll_from_f32<T>(r1);
 }
 
 // ---------------------------------------------------------------- wave helpers

@@ -506,6 +506,31 @@ def test_silu_and_mul_splitk(cuda):
     assert _close_rel(out, O.silu_and_mul(gu, torch.bfloat16))
 
 
+@pytest.mark.parametrize("dtype,cs", [(torch.bfloat16, torch.float32), (torch.float16, torch.float16)])
+def test_rope_kv_scatter_vec_equals_scalar(cuda, dtype, cs):
+    """The 4-pairs-per-thread path (head_dim % 8 == 0, aligned rows) against the
+    one-pair path (forced by a row stride that is not a multiple of 4) on the
+    same inputs: q rows and pool bit-identical."""
+    g = torch.Generator().manual_seed(24)
+    T, H, KVH, D, P = 37, 16, 2, 128, 100
+    W = (H + 2 * KVH) * D
+    qkv = torch.randn(T, W, generator=g).to(dtype)
+    pos = torch.randint(0, 300, (T,), generator=g)
+    cos, sin = O.rope_table(320, D)
+    cos, sin = cos.to(cs).to(cuda), sin.to(cs).to(cuda)
+    slots = torch.from_numpy(np.random.RandomState(5).permutation(P)[:T].astype(np.int32)).to(cuda)
+    a = qkv.to(cuda)
+    wide = torch.zeros(T, W + 2, dtype=dtype)
+    wide[:, :W] = qkv
+    b = wide.to(cuda)[:, :W]  # row stride W + 2: the scalar path
+    pa = torch.zeros(P, 2 * KVH, D, dtype=dtype, device=cuda)
+    pb = torch.zeros_like(pa)
+    _ops().rope_kv_scatter(a, H, KVH, D, pos.to(cuda), cos, sin, slots, pa)
+    _ops().rope_kv_scatter(b, H, KVH, D, pos.to(cuda), cos, sin, slots, pb)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b) and torch.equal(pa, pb)
+
+
 def test_rope_kv_scatter_splitk(cuda):
     g = torch.Generator().manual_seed(44)
     T, H, KVH, D, P, S = 40, 16, 2, 128, 100, 4
