@@ -62,16 +62,22 @@ __global__ __launch_bounds__(256) void quant_row_vec_kernel(const T* __restrict_
                                                             const float* __restrict__ s_static) {
   typedef typename QVec8<T>::type V8;
   const T* row = X + (int64_t)blockIdx.x * ldx;
+  // every load issued before the first use (clamped addresses; columns past
+  // K are masked), one memory round trip for the row
   V8 v[VPT];
+#pragma unroll
+  for (int u = 0; u < VPT; ++u) {
+    const int k = (u * 256 + (int)threadIdx.x) * 8;
+    v[u] = *(const V8*)(row + min(k, K - 8));
+  }
   float m = 0.f;
 #pragma unroll
   for (int u = 0; u < VPT; ++u) {
     const int k = (u * 256 + (int)threadIdx.x) * 8;
-    if (k < K) {
-      v[u] = *(const V8*)(row + k);
+    float mu = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(ll_to_f32(v[u][e])));
-    }
+    for (int e = 0; e < 8; ++e) mu = fmaxf(mu, fabsf(ll_to_f32(v[u][e])));
+    m = k < K ? fmaxf(m, mu) : m;
   }
   float s;
   if constexpr (STATIC) {
