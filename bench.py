@@ -47,10 +47,11 @@ def log(msg):
 
 
 # ------------------------------------------------------------------ attention
-def bench_decode_attention(dev, iters=200, pools=28):
-    """Config 2: returns (avg seconds per launch, algorithmic bytes per launch)."""
+def bench_decode_attention(dev, iters=200, pools=28, L=600):
+    """Config 2 (context L): returns (avg seconds per launch, algorithmic bytes
+    per launch)."""
     from lite_lang_amd import ops
-    H, KVH, D, L = 12, 2, 128, 600
+    H, KVH, D = 12, 2, 128
     P = B * L
     g = torch.Generator(device=dev).manual_seed(0)
     q = torch.randn(B, H, D, generator=g, device=dev).bfloat16()
@@ -308,6 +309,13 @@ def main():
     attn_sec, attn_bytes = bench_decode_attention(dev)
     attn_gbs = attn_bytes / attn_sec / 1e9
     log(f"attention: {attn_sec * 1e6:.2f} us, {attn_gbs:.0f} GB/s")
+    # the same op at twice the context: the extra bytes over the extra time is
+    # the rate the op streams at beyond its fixed per-launch cost
+    sec2, bytes2 = bench_decode_attention(dev, L=2 * PROMPT)
+    marg_gbs = (bytes2 - attn_bytes) / (sec2 - attn_sec) / 1e9
+    fixed_us = (attn_sec - attn_bytes / (marg_gbs * 1e9)) * 1e6
+    log(f"attention at ctx {2 * PROMPT}: {sec2 * 1e6:.2f} us; marginal {marg_gbs:.0f} GB/s, "
+        f"fixed {fixed_us:.2f} us")
 
     log("building Qwen2.5-3B-shape runner (random init, bf16)")
     max_length = PROMPT + max(K, W) + 2
@@ -355,10 +363,16 @@ def main():
         "decode_tok_s": round(decode_tok_s, 1) if decode_tok_s else None,
         "decode_step": {"ms": round(step_sec * 1e3, 4), "bytes": int(step_bytes),
                         "hbm_frac": round(step_bytes / step_sec / 1e9 / HBM_PEAK_GBS, 4)},
-        "roofline": {"kernel": "decode_attn_dma_kernel + decode_attn_combine_kernel (config 2)", "bound": "hbm",
+        "roofline": {"kernel": "decode_attn_dma_kernel (config 2; split merge in the same launch)",
+                     "bound": "hbm",
                      "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "traffic": ATTN_TRAFFIC_BYTES,
-                     "avg_us": round(attn_sec * 1e6, 3), "bytes_per_launch": attn_bytes},
+                     "avg_us": round(attn_sec * 1e6, 3), "bytes_per_launch": attn_bytes,
+                     "marginal": {"ctx": [PROMPT, 2 * PROMPT],
+                                  "us": [round(attn_sec * 1e6, 3), round(sec2 * 1e6, 3)],
+                                  "gbs": round(marg_gbs, 1),
+                                  "frac": round(marg_gbs / HBM_PEAK_GBS, 4),
+                                  "fixed_us": round(fixed_us, 3)}},
         "cpu_baseline": cpu,
     }
     print(json.dumps(res), flush=True)

@@ -23,11 +23,13 @@
 //     length into that many tile-aligned chunks, so the grid does not depend
 //     on the lengths (graph safe);
 //   * the 8 waves merge in LDS; the splits of a (sequence, KV head) are merged
-//     by a second kernel, one wave per (sequence, head) with the partials of
-//     all splits in flight at once. Merging in the same launch (the last
-//     split to finish merges, signalled through a device-scope counter) was
-//     measured slower: the chain of device-scope store acknowledgement,
-//     counter atomic and coherent reloads costs more than the extra launch.
+//     by the last of them to finish, one wave per head with the partials of
+//     all splits in flight at once. All splits of a unit run on one XCD, so
+//     the ticket and the partials meet in that XCD's L2 (no device-scope
+//     write-back; a device-scope version was measured slower than a second
+//     launch). The quantising variant (one sequence's heads span units on
+//     different XCDs) and batches beyond kMergeUnits units merge in a second
+//     kernel instead.
 // A generic VALU path covers fp32 and head dims other than 64/128.
 #include "ll_common.h"
 
@@ -91,6 +93,7 @@ struct DecodeArgs {
   float scale_log2;   // sm_scale * log2(e)
   float* part_acc;    // [B*H*nsplit, D] unnormalised partial outputs
   float* part_ml;     // [B*H*nsplit, 2] running max (log2 domain) and sum
+  unsigned* merge_cnt;  // [units] split tickets (zero between calls), or null: separate combine
   // fused RoPE + new-token K/V write (ROPE kernels only)
   LLPartials qkv;          // [splits][B][(H + 2 KVH) * D] split-K partials (fp32, or int32 + scales)
   const void* qkv_bias;    // [(H + 2 KVH) * D] of the model dtype, or null
@@ -153,6 +156,59 @@ __device__ __forceinline__ void rope_job(const DecodeArgs& a, int64_t m, int64_t
       glb[i + HALF + e] = y1;
     }
   }
+}
+
+// Log-sum-exp merge of the split partials: one wave per (sequence, head),
+// lane l owns d = l + 64 q. Splits are taken 16 at a time with all their
+// loads issued before any is used (one memory round trip per 16 splits).
+// Merge of the partials of one (sequence, head) by one wave: lane l returns
+// out[d = l + 64 q] (unrounded).
+template <int D>
+__device__ __forceinline__ void combine_bh(const DecodeArgs& a, int bh, int lane, float (&o)[D / 64]) {
+  constexpr int DPL = D / 64;
+  constexpr int SB = 16;
+  const int ns = a.nsplit;
+  const int64_t p0 = (int64_t)bh * ns;  // partial rows of (b, h): p0 .. p0 + ns - 1
+  float M = -INFINITY, L = 0.f, A[DPL];
+#pragma unroll
+  for (int q = 0; q < DPL; ++q) A[q] = 0.f;
+  for (int s0 = 0; s0 < ns; s0 += SB) {
+    // lane s < SB holds (m, l) of split s0 + s; rows past the last split are
+    // clamped onto it and weighted 0
+    float av[SB][DPL];
+#pragma unroll
+    for (int u = 0; u < SB; ++u)
+#pragma unroll
+      for (int q = 0; q < DPL; ++q)
+        av[u][q] = a.part_acc[(p0 + min(s0 + u, ns - 1)) * D + lane + 64 * q];
+    const int sl = min(s0 + (lane & (SB - 1)), ns - 1);
+    const float m0 = a.part_ml[(p0 + sl) * 2];
+    const float l = a.part_ml[(p0 + sl) * 2 + 1];
+    // every load of this chunk is issued before the first use of any of them
+    __builtin_amdgcn_sched_barrier(0);
+    const float m = (lane < SB && s0 + lane < ns) ? m0 : -INFINITY;
+    float mc = m;
+#pragma unroll
+    for (int off = SB / 2; off > 0; off >>= 1) mc = fmaxf(mc, __shfl_xor(mc, off, 64));
+    mc = __shfl(mc, 0, 64);
+    const float Mn = fmaxf(M, mc);
+    if (Mn != -INFINITY) {
+      const float r = exp2f(M - Mn);
+      L *= r;
+#pragma unroll
+      for (int q = 0; q < DPL; ++q) A[q] *= r;
+#pragma unroll
+      for (int u = 0; u < SB; ++u) {
+        const float w = exp2f(__shfl(m, u, 64) - Mn);  // 0 for splits past the last
+        L += __shfl(l, u, 64) * w;
+#pragma unroll
+        for (int q = 0; q < DPL; ++q) A[q] += av[u][q] * w;
+      }
+    }
+    M = Mn;
+  }
+#pragma unroll
+  for (int q = 0; q < DPL; ++q) o[q] = L > 0.f ? A[q] / L : 0.f;
 }
 
 // XCD-aware unit mapping: workgroups are dispatched round-robin over the 8
@@ -472,59 +528,32 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
       }
     }
   }
-}
+  if (a.merge_cnt == nullptr) return;
 
-// Log-sum-exp merge of the split partials: one wave per (sequence, head),
-// lane l owns d = l + 64 q. Splits are taken 16 at a time with all their
-// loads issued before any is used (one memory round trip per 16 splits).
-// Merge of the partials of one (sequence, head) by one wave: lane l returns
-// out[d = l + 64 q] (unrounded).
-template <int D>
-__device__ __forceinline__ void combine_bh(const DecodeArgs& a, int bh, int lane, float (&o)[D / 64]) {
-  constexpr int DPL = D / 64;
-  constexpr int SB = 16;
-  const int ns = a.nsplit;
-  const int64_t p0 = (int64_t)bh * ns;  // partial rows of (b, h): p0 .. p0 + ns - 1
-  float M = -INFINITY, L = 0.f, A[DPL];
+  // ---- the last split of this (sequence, KV head) to finish merges all of
+  // them. Every split of a unit runs on one XCD (map_block; the dispatcher
+  // deals workgroup i to XCD i mod 8), so that XCD's L2 is where they meet:
+  // each thread's partial stores are acknowledged by L2 (the vector L1 is
+  // write-through) before the ticket is taken, and the merging workgroup
+  // drops its own L1 lines before reading the other splits' partials. The
+  // ticket wraps to zero on the last increment, so the counter is zero again
+  // for the next call.
+  __shared__ unsigned s_ticket;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0)
+    s_ticket = __builtin_amdgcn_atomic_inc32(a.merge_cnt + unit, (unsigned)(a.nsplit - 1),
+                                             __ATOMIC_RELAXED, "agent");
+  __syncthreads();
+  if (s_ticket != (unsigned)(a.nsplit - 1)) return;
+  asm volatile("buffer_inv sc0" ::: "memory");
+  for (int g = wave; g < G; g += kWaves) {
+    float o[D / 64];
+    combine_bh<D>(a, b * a.H + kvh * G + g, lane, o);
+    T* op = (T*)a.out + (int64_t)b * a.o_sb + (int64_t)(kvh * G + g) * a.o_sh;
 #pragma unroll
-  for (int q = 0; q < DPL; ++q) A[q] = 0.f;
-  for (int s0 = 0; s0 < ns; s0 += SB) {
-    // lane s < SB holds (m, l) of split s0 + s; rows past the last split are
-    // clamped onto it and weighted 0
-    float av[SB][DPL];
-#pragma unroll
-    for (int u = 0; u < SB; ++u)
-#pragma unroll
-      for (int q = 0; q < DPL; ++q)
-        av[u][q] = a.part_acc[(p0 + min(s0 + u, ns - 1)) * D + lane + 64 * q];
-    const int sl = min(s0 + (lane & (SB - 1)), ns - 1);
-    const float m0 = a.part_ml[(p0 + sl) * 2];
-    const float l = a.part_ml[(p0 + sl) * 2 + 1];
-    // every load of this chunk is issued before the first use of any of them
-    __builtin_amdgcn_sched_barrier(0);
-    const float m = (lane < SB && s0 + lane < ns) ? m0 : -INFINITY;
-    float mc = m;
-#pragma unroll
-    for (int off = SB / 2; off > 0; off >>= 1) mc = fmaxf(mc, __shfl_xor(mc, off, 64));
-    mc = __shfl(mc, 0, 64);
-    const float Mn = fmaxf(M, mc);
-    if (Mn != -INFINITY) {
-      const float r = exp2f(M - Mn);
-      L *= r;
-#pragma unroll
-      for (int q = 0; q < DPL; ++q) A[q] *= r;
-#pragma unroll
-      for (int u = 0; u < SB; ++u) {
-        const float w = exp2f(__shfl(m, u, 64) - Mn);  // 0 for splits past the last
-        L += __shfl(l, u, 64) * w;
-#pragma unroll
-        for (int q = 0; q < DPL; ++q) A[q] += av[u][q] * w;
-      }
-    }
-    M = Mn;
+    for (int q = 0; q < D / 64; ++q) op[lane + 64 * q] = ll_from_f32<T>(o[q]);
   }
-#pragma unroll
-  for (int q = 0; q < DPL; ++q) o[q] = L > 0.f ? A[q] / L : 0.f;
 }
 
 template <typename T, int D>
@@ -716,12 +745,19 @@ void launch_combine(const DecodeArgs& a, int dtype, hipStream_t stream) {
                        stream, a);
 }
 
+// Workspace layout when the sequences are split: [kMergeUnits split tickets]
+// [partial acc][partial (m, l)]. The tickets sit at a fixed offset so that
+// calls of every shape sharing one workspace find them at zero.
+constexpr int kMergeUnits = 4096;
+constexpr int64_t kTicketBytes = kMergeUnits * 4;
+
 int64_t workspace_bytes_for(int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
                             int64_t max_len) {
   const int ns = choose_nsplit((int)batch, (int)kv_heads, max_len, head_dim);
   if (ns <= 1) return 0;
   const int64_t parts = batch * q_heads * ns;
-  return align256(parts * head_dim * 4)  // partial acc
+  return kTicketBytes                      // split tickets
+         + align256(parts * head_dim * 4)  // partial acc
          + align256(parts * 2 * 4);        // partial (m, l)
 }
 
@@ -736,6 +772,9 @@ int launch_mfma(DecodeArgs& a, int64_t head_dim, int dtype, bool rope, int64_t m
                  "decode attention: workspace too small (need %lld bytes, got %lld)",
                  (long long)need, (long long)workspace_bytes);
     char* w = (char*)workspace;
+    // merge in the split stage unless the rows are quantised afterwards
+    a.merge_cnt = (a.qout == nullptr && a.units <= kMergeUnits) ? (unsigned*)w : nullptr;
+    w += kTicketBytes;
     const int64_t parts = (int64_t)a.B * a.H * a.nsplit;
     a.part_acc = (float*)w;
     w += align256(parts * head_dim * 4);
@@ -756,8 +795,10 @@ int launch_mfma(DecodeArgs& a, int64_t head_dim, int dtype, bool rope, int64_t m
     else launch_split_stage<64, false>(a, dtype, grid, lds, stream);
   }
   if (a.nsplit > 1) {
-    if (head_dim == 128) launch_combine<128>(a, dtype, stream);
-    else launch_combine<64>(a, dtype, stream);
+    if (a.merge_cnt == nullptr) {
+      if (head_dim == 128) launch_combine<128>(a, dtype, stream);
+      else launch_combine<64>(a, dtype, stream);
+    }
   } else if (a.qout != nullptr) {
     // one split: the split stage stored the rows; quantise them here
     const int64_t W = (int64_t)a.H * head_dim;

@@ -89,13 +89,20 @@ def test_decode_attention_shapes(cuda, dtype, H, KVH, D):
 
 
 def test_decode_attention_repeat_calls_are_identical(cuda):
-    # the split combine uses self-resetting tickets: calls must not interfere
-    print("case: decode repeat x3", flush=True)
+    # the last split of each (sequence, KV head) merges, picked by a ticket in
+    # the shared workspace that wraps back to zero: calls of different shapes
+    # and split counts in a row must not interfere, and leave the tickets at 0
+    print("case: decode repeat, interleaved shapes", flush=True)
     a, ref = _decode_case(cuda, 40, 16, 2, 128, [700] * 40, torch.bfloat16, 3)
+    c, cref = _decode_case(cuda, 2, 16, 2, 128, [40, 2000], torch.bfloat16, 4)
+    d, dref = _decode_case(cuda, 40, 12, 2, 128, [600] * 40, torch.bfloat16, 0)
+    e, eref = _decode_case(cuda, 64, 8, 8, 64, [300] * 64, torch.float16, 6)
     b, _ = _decode_case(cuda, 40, 16, 2, 128, [700] * 40, torch.bfloat16, 3)
-    c, _ = _decode_case(cuda, 2, 16, 2, 128, [40, 2000], torch.bfloat16, 4)
     assert torch.equal(a, b)
-    assert _maxdiff(a, ref) <= BF16_ATOL
+    for out, r in ((a, ref), (c, cref), (d, dref), (e, eref)):
+        assert _maxdiff(out, r) <= BF16_ATOL
+    ws = _ops()._WS[(0, "decode_attention")]
+    assert int(ws[:16384].count_nonzero()) == 0, "split tickets not back at zero"
 
 
 def test_decode_attention_reference_wrapper(cuda):
