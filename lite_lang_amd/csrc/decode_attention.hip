@@ -158,15 +158,14 @@ __device__ __forceinline__ void rope_job(const DecodeArgs& a, int64_t m, int64_t
   }
 }
 
-// Log-sum-exp merge of the split partials: one wave per (sequence, head),
-// lane l owns d = l + 64 q. Splits are taken 16 at a time with all their
-// loads issued before any is used (one memory round trip per 16 splits).
-// Merge of the partials of one (sequence, head) by one wave: lane l returns
-// out[d = l + 64 q] (unrounded).
-template <int D>
-__device__ __forceinline__ void combine_bh(const DecodeArgs& a, int bh, int lane, float (&o)[D / 64]) {
+// Log-sum-exp merge of the partials of one (sequence, head) by one wave:
+// lane l returns out[d = l + 64 q] (unrounded). Splits are taken SB at a time
+// with all their loads issued before any is used (one memory round trip per
+// SB splits).
+template <int D, int SB>
+__device__ __forceinline__ void combine_bh_sb(const DecodeArgs& a, int bh, int lane,
+                                              float (&o)[D / 64]) {
   constexpr int DPL = D / 64;
-  constexpr int SB = 16;
   const int ns = a.nsplit;
   const int64_t p0 = (int64_t)bh * ns;  // partial rows of (b, h): p0 .. p0 + ns - 1
   float M = -INFINITY, L = 0.f, A[DPL];
@@ -211,6 +210,15 @@ __device__ __forceinline__ void combine_bh(const DecodeArgs& a, int bh, int lane
   for (int q = 0; q < DPL; ++q) o[q] = L > 0.f ? A[q] / L : 0.f;
 }
 
+// SB = the split count rounded up to 4, 8 or 16 (rows past the last split
+// weigh 0, so every SB gives the same sums)
+template <int D>
+__device__ __forceinline__ void combine_bh(const DecodeArgs& a, int bh, int lane, float (&o)[D / 64]) {
+  if (a.nsplit <= 4) combine_bh_sb<D, 4>(a, bh, lane, o);
+  else if (a.nsplit <= 8) combine_bh_sb<D, 8>(a, bh, lane, o);
+  else combine_bh_sb<D, 16>(a, bh, lane, o);
+}
+
 // XCD-aware unit mapping: workgroups are dispatched round-robin over the 8
 // XCDs, so all splits of one (sequence, KV head) land on the same XCD.
 __device__ __forceinline__ void map_block(int bid, int nsplit, int& unit, int& split) {
@@ -228,7 +236,8 @@ template <int D> struct TileGeom {
   static constexpr int TILE_B = 2 * kTT * ROWB; // K rows then V rows
   static constexpr int ROWS_PER_BANKS = 256 / ROWB;  // rows sharing one 256 B bank window
   static constexpr int RING_B = kWaves * kRing * TILE_B;
-  static constexpr int MERGE_B = kWaves * 16 * (D + 1) * 4 + 2 * kWaves * 16 * 4;
+  static constexpr int CP = D + 4;  // floats per merge row (16 B aligned, staggers the banks)
+  static constexpr int MERGE_B = kWaves * 16 * CP * 4 + 2 * kWaves * 16 * 4;
   static constexpr int MAIN_B = RING_B > MERGE_B ? RING_B : MERGE_B;
   // LDS chunk position of global chunk c of tile row r (an involution)
   static __device__ __forceinline__ int swz(int c, int r) { return c ^ ((r / ROWS_PER_BANKS) & (CH - 1)); }
@@ -484,45 +493,51 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
   l_run += __shfl_xor(l_run, 32, 64);
 
   // ---- merge the waves of this workgroup (the tile rings are dead from here on)
-  typedef float CombAcc[16][D + 1];
+  typedef float CombAcc[16][TG::CP];
   CombAcc* comb_acc = (CombAcc*)smem;
-  float (*comb_m)[16] = (float (*)[16])(smem + kWaves * 16 * (D + 1) * 4);
-  float (*comb_l)[16] = (float (*)[16])(smem + kWaves * 16 * (D + 1) * 4 + kWaves * 16 * 4);
+  float (*comb_m)[16] = (float (*)[16])(smem + kWaves * 16 * TG::CP * 4);
+  float (*comb_l)[16] = (float (*)[16])(smem + kWaves * 16 * TG::CP * 4 + kWaves * 16 * 4);
+  const int G = a.G;
   __syncthreads();
-  // acc[c][i] holds O^T[d = 16c + 4j + i][head n]
+  // acc[c][i] holds O^T[d = 16c + 4j + i][head n]; only the G real heads are kept
+  if (n < G) {
 #pragma unroll
-  for (int c = 0; c < DB; ++c)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) comb_acc[wave][n][16 * c + 4 * j + i] = acc[c][i];
-  if (j == 0) {
-    comb_m[wave][n] = m_run;
-    comb_l[wave][n] = l_run;
+    for (int c = 0; c < DB; ++c) *(f32x4*)&comb_acc[wave][n][16 * c + 4 * j] = acc[c];
+    if (j == 0) {
+      comb_m[wave][n] = m_run;
+      comb_l[wave][n] = l_run;
+    }
   }
   __syncthreads();
 
-  const int G = a.G;
+  // four consecutive d of one head per thread
+  constexpr int DQ = D / 4;
   const int64_t pbase = ((int64_t)b * a.H + (int64_t)kvh * G) * a.nsplit;
-  for (int e = threadIdx.x; e < G * D; e += kWaves * 64) {
-    const int g = e / D, d = e - g * D;
+  for (int e = threadIdx.x; e < G * DQ; e += kWaves * 64) {
+    const int g = e / DQ, d0 = (e - g * DQ) * 4;
     float M = -INFINITY;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) M = fmaxf(M, comb_m[w][g]);
-    float L = 0.f, A = 0.f;
+    float L = 0.f;
+    f32x4 A = {0.f, 0.f, 0.f, 0.f};
     if (M != -INFINITY) {
 #pragma unroll
       for (int w = 0; w < kWaves; ++w) {
         const float sc = exp2f(comb_m[w][g] - M);
         L += comb_l[w][g] * sc;
-        A += comb_acc[w][g][d] * sc;
+        const f32x4 v = *(const f32x4*)&comb_acc[w][g][d0];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) A[i] += v[i] * sc;
       }
     }
     if (a.nsplit == 1) {
-      T* op = (T*)a.out + (int64_t)b * a.o_sb + (int64_t)(kvh * G + g) * a.o_sh;
-      op[d] = ll_from_f32<T>(L > 0.f ? A / L : 0.f);
+      T* op = (T*)a.out + (int64_t)b * a.o_sb + (int64_t)(kvh * G + g) * a.o_sh + d0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) op[i] = ll_from_f32<T>(L > 0.f ? A[i] / L : 0.f);
     } else {
       const int64_t p = pbase + (int64_t)g * a.nsplit + split;
-      a.part_acc[p * D + d] = A;
-      if (d == 0) {
+      *(f32x4*)&a.part_acc[p * D + d0] = A;
+      if (d0 == 0) {
         a.part_ml[p * 2] = M;
         a.part_ml[p * 2 + 1] = L;
       }
