@@ -237,8 +237,12 @@ template <int D> struct TileGeom {
   static constexpr int ROWS_PER_BANKS = 256 / ROWB;  // rows sharing one 256 B bank window
   static constexpr int RING_B = kWaves * kRing * TILE_B;
   static constexpr int CP = D + 4;  // floats per merge row (16 B aligned, staggers the banks)
-  static constexpr int MERGE_B = kWaves * 16 * CP * 4 + 2 * kWaves * 16 * 4;
-  static constexpr int MAIN_B = RING_B > MERGE_B ? RING_B : MERGE_B;
+  // a wave's merge rows (16 x CP accumulators, 16 maxima, 16 sums) sit in its
+  // own tile ring, which is idle once the wave has left its token loop
+  static constexpr int WAVE_B = kRing * TILE_B;
+  static constexpr int MERGE_WAVE_B = 16 * CP * 4 + 2 * 16 * 4;
+  static_assert(MERGE_WAVE_B <= WAVE_B, "merge rows must fit in a wave's ring");
+  static constexpr int MAIN_B = RING_B;
   // LDS chunk position of global chunk c of tile row r (an involution)
   static __device__ __forceinline__ int swz(int c, int r) { return c ^ ((r / ROWS_PER_BANKS) & (CH - 1)); }
 };
@@ -492,20 +496,20 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
   l_run += __shfl_xor(l_run, 16, 64);
   l_run += __shfl_xor(l_run, 32, 64);
 
-  // ---- merge the waves of this workgroup (the tile rings are dead from here on)
-  typedef float CombAcc[16][TG::CP];
-  CombAcc* comb_acc = (CombAcc*)smem;
-  float (*comb_m)[16] = (float (*)[16])(smem + kWaves * 16 * TG::CP * 4);
-  float (*comb_l)[16] = (float (*)[16])(smem + kWaves * 16 * TG::CP * 4 + kWaves * 16 * 4);
+  // ---- merge the waves of this workgroup. Each wave writes its rows into its
+  // own ring (its DMAs have landed and its LDS reads are done), so only the
+  // barrier after the writes is needed.
+  auto comb_acc = [&](int w, int g) { return (float*)(smem + w * TG::WAVE_B) + g * TG::CP; };
+  auto comb_m = [&](int w) { return (float*)(smem + w * TG::WAVE_B + 16 * TG::CP * 4); };
+  auto comb_l = [&](int w) { return (float*)(smem + w * TG::WAVE_B + 16 * TG::CP * 4 + 64); };
   const int G = a.G;
-  __syncthreads();
   // acc[c][i] holds O^T[d = 16c + 4j + i][head n]; only the G real heads are kept
   if (n < G) {
 #pragma unroll
-    for (int c = 0; c < DB; ++c) *(f32x4*)&comb_acc[wave][n][16 * c + 4 * j] = acc[c];
+    for (int c = 0; c < DB; ++c) *(f32x4*)(comb_acc(wave, n) + 16 * c + 4 * j) = acc[c];
     if (j == 0) {
-      comb_m[wave][n] = m_run;
-      comb_l[wave][n] = l_run;
+      comb_m(wave)[n] = m_run;
+      comb_l(wave)[n] = l_run;
     }
   }
   __syncthreads();
@@ -517,15 +521,15 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
     const int g = e / DQ, d0 = (e - g * DQ) * 4;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, comb_m[w][g]);
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, comb_m(w)[g]);
     float L = 0.f;
     f32x4 A = {0.f, 0.f, 0.f, 0.f};
     if (M != -INFINITY) {
 #pragma unroll
       for (int w = 0; w < kWaves; ++w) {
-        const float sc = exp2f(comb_m[w][g] - M);
-        L += comb_l[w][g] * sc;
-        const f32x4 v = *(const f32x4*)&comb_acc[w][g][d0];
+        const float sc = exp2f(comb_m(w)[g] - M);
+        L += comb_l(w)[g] * sc;
+        const f32x4 v = *(const f32x4*)(comb_acc(w, g) + d0);
 #pragma unroll
         for (int i = 0; i < 4; ++i) A[i] += v[i] * sc;
       }
