@@ -12,8 +12,10 @@
  *     negative LL_ERR_* code; ll_last_error() then holds the reason. Argument
  *     errors are raised before anything is launched.
  *   - workspaces are caller-owned device buffers of the size the matching
- *     *_workspace_size query returns (their contents need no initialisation);
- *     calls that share one workspace must not overlap in time.
+ *     *_workspace_size query returns; calls that share one workspace must
+ *     not overlap in time. Their contents need no initialisation, except the
+ *     decode attention workspace, which must be zero-filled once before its
+ *     first use (every call leaves it fit for the next).
  */
 #ifndef LITELANG_AMD_H
 #define LITELANG_AMD_H
@@ -43,7 +45,8 @@ const char* ll_last_error(void);
 
 /* ---------------------------------------------------------------- attention */
 
-/* Paged GQA decode attention, split-K (partials merged by a second kernel).
+/* Paged GQA decode attention, split-K (the last split of each (sequence,
+ * KV head) to finish merges the partials, in the same launch).
  * Replaces token_decode_attention_flash_decoding
  *   (litelang/kernel/develop_flash_attn/flash_decoding.py:262-312).
  * q [batch, q_heads, head_dim]; k_cache / v_cache [P, kv_heads, head_dim]
@@ -51,8 +54,10 @@ const char* ll_last_error(void);
  * int32 slot table; out [batch, q_heads, head_dim]. max_len_in_batch bounds
  * b_seq_len (it sizes the split count and the workspace; tokens beyond it are
  * ignored, as the reference's grid ignores them). workspace: at least
- * ll_decode_attention_workspace_size bytes (0 when no split is needed), any
- * contents; two calls in flight at once must not share it. */
+ * ll_decode_attention_workspace_size bytes (0 when no split is needed),
+ * zero-filled before its first use: its first 16 KiB hold the split tickets,
+ * which every call leaves at zero, so one buffer serves calls of any shape;
+ * two calls in flight at once must not share it. */
 int64_t ll_decode_attention_workspace_size(int64_t batch, int64_t q_heads, int64_t kv_heads,
                                            int64_t head_dim, int64_t max_len_in_batch);
 int ll_decode_attention(const void* q, int64_t q_stride_b, int64_t q_stride_h,

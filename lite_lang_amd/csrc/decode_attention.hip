@@ -219,13 +219,17 @@ __device__ __forceinline__ void combine_bh(const DecodeArgs& a, int bh, int lane
   else combine_bh_sb<D, 16>(a, bh, lane, o);
 }
 
-// XCD-aware unit mapping: workgroups are dispatched round-robin over the 8
-// XCDs, so all splits of one (sequence, KV head) land on the same XCD.
-__device__ __forceinline__ void map_block(int bid, int nsplit, int& unit, int& split) {
-  const int xcd = bid & 7;
-  const int slot = bid >> 3;
-  unit = (slot / nsplit) * 8 + xcd;
-  split = slot % nsplit;
+// XCD-aware mapping: the dispatcher deals workgroup i to XCD i mod 8, and
+// every workgroup of one sequence (all its KV heads and splits) is given an
+// index of the same residue, so they all run on one XCD and share its L2.
+__device__ __forceinline__ void map_block(int bid, int KVH, int nsplit, int& b, int& kvh,
+                                          int& split) {
+  const int xcd = bid & 7, slot = bid >> 3;
+  const int per_seq = KVH * nsplit;
+  const int k = slot / per_seq, r = slot - k * per_seq;
+  b = k * 8 + xcd;
+  kvh = r / nsplit;
+  split = r - kvh * nsplit;
 }
 
 template <int D> struct TileGeom {
@@ -264,11 +268,10 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
   extern __shared__ __attribute__((aligned(16))) char smem[];
   int32_t* s_slots = (int32_t*)(smem + TG::MAIN_B);
 
-  int unit, split;
-  map_block(blockIdx.x, a.nsplit, unit, split);
-  if (unit >= a.units) return;
-  const int b = unit / a.KVH;
-  const int kvh = unit - b * a.KVH;
+  int b, kvh, split;
+  map_block(blockIdx.x, a.KVH, a.nsplit, b, kvh, split);
+  if (b >= a.B) return;
+  const int unit = b * a.KVH + kvh;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int n = lane & 15;  // MFMA column (query head within the group) / row
@@ -550,29 +553,68 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
   if (a.merge_cnt == nullptr) return;
 
   // ---- the last split of this (sequence, KV head) to finish merges all of
-  // them. Every split of a unit runs on one XCD (map_block; the dispatcher
-  // deals workgroup i to XCD i mod 8), so that XCD's L2 is where they meet:
-  // each thread's partial stores are acknowledged by L2 (the vector L1 is
-  // write-through) before the ticket is taken, and the merging workgroup
-  // drops its own L1 lines before reading the other splits' partials. The
-  // ticket wraps to zero on the last increment, so the counter is zero again
-  // for the next call.
+  // them; with quantised output rows, the last workgroup of the sequence
+  // merges all its heads and quantises the row. All of them run on one XCD
+  // (map_block), so that XCD's L2 is where they meet: each thread's partial
+  // stores are acknowledged by L2 (the vector L1 is write-through) before the
+  // ticket is taken, and the merging workgroup drops its own L1 lines before
+  // reading the other workgroups' partials. The ticket wraps to zero on the
+  // last increment, so the counter is zero again for the next call.
   __shared__ unsigned s_ticket;
+  const bool whole_row = a.qout != nullptr;
+  const unsigned last = (unsigned)((whole_row ? a.KVH : 1) * a.nsplit - 1);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (threadIdx.x == 0)
-    s_ticket = __builtin_amdgcn_atomic_inc32(a.merge_cnt + unit, (unsigned)(a.nsplit - 1),
+    s_ticket = __builtin_amdgcn_atomic_inc32(a.merge_cnt + (whole_row ? b : unit), last,
                                              __ATOMIC_RELAXED, "agent");
   __syncthreads();
-  if (s_ticket != (unsigned)(a.nsplit - 1)) return;
+  if (s_ticket != last) return;
   asm volatile("buffer_inv sc0" ::: "memory");
-  for (int g = wave; g < G; g += kWaves) {
-    float o[D / 64];
-    combine_bh<D>(a, b * a.H + kvh * G + g, lane, o);
-    T* op = (T*)a.out + (int64_t)b * a.o_sb + (int64_t)(kvh * G + g) * a.o_sh;
+  if (!whole_row) {
+    for (int g = wave; g < G; g += kWaves) {
+      float o[D / 64];
+      combine_bh<D>(a, b * a.H + kvh * G + g, lane, o);
+      T* op = (T*)a.out + (int64_t)b * a.o_sb + (int64_t)(kvh * G + g) * a.o_sh;
 #pragma unroll
-    for (int q = 0; q < D / 64; ++q) op[lane + 64 * q] = ll_from_f32<T>(o[q]);
+      for (int q = 0; q < D / 64; ++q) op[lane + 64 * q] = ll_from_f32<T>(o[q]);
+    }
+    return;
   }
+  // the stored row is kept in LDS (the tile rings are idle) for the codes:
+  // by ll_quant_per_token's rule, or with the calibrated scale *a.qstatic
+  float* row = (float*)smem;
+  __shared__ float s_red[kWaves];
+  float amax = 0.f;
+  for (int h = wave; h < a.H; h += kWaves) {
+    float o[D / 64];
+    combine_bh<D>(a, b * a.H + h, lane, o);
+    T* op = (T*)a.out + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh;
+#pragma unroll
+    for (int q = 0; q < D / 64; ++q) {
+      const T v = ll_from_f32<T>(o[q]);
+      op[lane + 64 * q] = v;
+      const float y = ll_to_f32(v);
+      row[h * D + lane + 64 * q] = y;
+      amax = fmaxf(amax, fabsf(y));
+    }
+  }
+  amax = ll_wave_max(amax);
+  if (lane == 0) s_red[wave] = amax;
+  __syncthreads();
+  float sc;
+  if (a.qstatic != nullptr) {
+    sc = *a.qstatic;
+  } else {
+    float mx = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, s_red[w]);
+    sc = mx / 127.f;
+    if (!(sc > 0.f)) sc = 1.f;
+  }
+  if (threadIdx.x == 0) a.qscale[b] = sc;
+  int8_t* qrow = a.qout + (int64_t)b * a.ldq;
+  for (int i = threadIdx.x; i < a.H * D; i += kWaves * 64) qrow[i] = ll_quant1(row[i], sc);
 }
 
 template <typename T, int D>
@@ -791,8 +833,15 @@ int launch_mfma(DecodeArgs& a, int64_t head_dim, int dtype, bool rope, int64_t m
                  "decode attention: workspace too small (need %lld bytes, got %lld)",
                  (long long)need, (long long)workspace_bytes);
     char* w = (char*)workspace;
-    // merge in the split stage unless the rows are quantised afterwards
-    a.merge_cnt = (a.qout == nullptr && a.units <= kMergeUnits) ? (unsigned*)w : nullptr;
+    // merge in the split stage: per (sequence, KV head), or per sequence when
+    // the rows are quantised (the row must fit in the tile rings' LDS)
+    const int64_t row_b = (int64_t)a.H * head_dim * 4;
+    const bool fits = a.qout == nullptr
+                          ? a.units <= kMergeUnits
+                          : (a.B <= kMergeUnits &&
+                             row_b <= (head_dim == 128 ? TileGeom<128>::MAIN_B
+                                                       : TileGeom<64>::MAIN_B));
+    a.merge_cnt = fits ? (unsigned*)w : nullptr;
     w += kTicketBytes;
     const int64_t parts = (int64_t)a.B * a.H * a.nsplit;
     a.part_acc = (float*)w;
@@ -801,8 +850,8 @@ int launch_mfma(DecodeArgs& a, int64_t head_dim, int dtype, bool rope, int64_t m
   }
   const int64_t tiles = (max_len + kTT - 1) / kTT;
   a.slots_cap = (int)((tiles + a.nsplit - 1) / a.nsplit) * kTT;
-  const int groups = (a.units + 7) / 8;
-  const unsigned grid = (unsigned)(groups * 8 * a.nsplit);
+  const int groups = (a.B + 7) / 8;  // sequences per XCD
+  const unsigned grid = (unsigned)(groups * 8 * a.KVH * a.nsplit);
   const size_t extra = (size_t)a.slots_cap * 4 + (rope ? (size_t)(a.G + 2) * head_dim * 2 : 0);
   if (head_dim == 128) {
     const size_t lds = TileGeom<128>::MAIN_B + extra;
