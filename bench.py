@@ -35,11 +35,11 @@ import torch
 
 HBM_PEAK_GBS = 8000.0
 B, PROMPT = 40, 600
-# HBM bytes per config-2 attention op (split stage + combine), from
+# HBM bytes per config-2 attention op (one kernel, split merge included), from
 # rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of `bench.py --attention-only`,
 # scaled by what the counters read for a 256 MiB copy (fetch x2.0, write x1.0).
 # Measured on the current kernels; re-measure when they change.
-ATTN_TRAFFIC_BYTES = 26757837
+ATTN_TRAFFIC_BYTES = 26410793
 
 
 def log(msg):
