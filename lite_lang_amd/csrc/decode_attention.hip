@@ -617,6 +617,9 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
   for (int i = threadIdx.x; i < a.H * D; i += kWaves * 64) qrow[i] = ll_quant1(row[i], sc);
 }
 
+// Separate merge kernels, for the shapes the split stage cannot merge itself
+// (more than kMergeUnits units, or a quantised row larger than the tile
+// rings): one wave per (sequence, head).
 template <typename T, int D>
 __global__ __launch_bounds__(kCombWaves * 64) void decode_attn_combine_kernel(DecodeArgs a) {
   constexpr int DPL = D / 64;
@@ -822,7 +825,8 @@ int64_t workspace_bytes_for(int64_t batch, int64_t q_heads, int64_t kv_heads, in
          + align256(parts * 2 * 4);        // partial (m, l)
 }
 
-// Split stage (+ combine when the sequence is split) of the MFMA path; a has
+// Split stage of the MFMA path (which merges the splits itself, or is followed
+// by a separate merge kernel past kMergeUnits units); a has
 // every field but the split geometry and the workspace pointers set.
 int launch_mfma(DecodeArgs& a, int64_t head_dim, int dtype, bool rope, int64_t max_len,
                 void* workspace, int64_t workspace_bytes, hipStream_t stream) {
