@@ -47,16 +47,18 @@ def log(msg):
 
 
 # ------------------------------------------------------------------ attention
-def bench_decode_attention(dev, iters=200, pools=28, L=600):
+def bench_decode_attention(dev, iters=200, pools=28, L=600, identity=False):
     """Config 2 (context L): returns (avg seconds per launch, algorithmic bytes
-    per launch)."""
+    per launch). identity: slot table = arange instead of the seeded random
+    permutation."""
     from lite_lang_amd import ops
     H, KVH, D = 12, 2, 128
     P = B * L
     g = torch.Generator(device=dev).manual_seed(0)
     q = torch.randn(B, H, D, generator=g, device=dev).bfloat16()
     pool_list = [torch.randn(P, 2 * KVH, D, generator=g, device=dev).bfloat16() for _ in range(pools)]
-    perm = torch.from_numpy(np.random.RandomState(0).permutation(P).astype(np.int32)).view(B, L).to(dev)
+    order = np.arange(P) if identity else np.random.RandomState(0).permutation(P)
+    perm = torch.from_numpy(order.astype(np.int32)).view(B, L).to(dev)
     rids = torch.arange(B, dtype=torch.int32, device=dev)
     lens = torch.full((B,), L, dtype=torch.int64, device=dev)
     out = torch.empty_like(q)
@@ -276,6 +278,9 @@ def main():
     ap.add_argument("--config", type=int, default=4, choices=(3, 4, 5),
                     help="4: the headline line (default); 3: Qwen2-1.5B through the scheduler; "
                          "5: 3B W8A8 + radix cache")
+    ap.add_argument("--attention-sweep", action="store_true",
+                    help="time the config-2 decode attention at contexts 16..2400 (random "
+                         "slot table; identity table at 600 and 1200), one JSON line each")
     ap.add_argument("--attention-only", action="store_true",
                     help="run only the config-2 decode attention launches plus a 256 MiB "
                          "device copy of known size (for rocprofv3 --pmc traffic runs)")
@@ -299,6 +304,15 @@ def main():
         print(json.dumps(bench_config5(dev)), flush=True)
         return
 
+    if args.attention_sweep:
+        for L, ident in [(16, False), (64, False), (150, False), (300, False), (600, False),
+                         (1200, False), (2400, False), (600, True), (1200, True)]:
+            sec, nb = bench_decode_attention(dev, L=L, identity=ident)
+            print(json.dumps({"ctx": L, "slots": "identity" if ident else "random",
+                              "us": round(sec * 1e6, 3), "bytes": nb,
+                              "gbs": round(nb / sec / 1e9, 1)}), flush=True)
+            torch.cuda.empty_cache()
+        return
     if args.attention_only:
         src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)
