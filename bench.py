@@ -129,26 +129,28 @@ def run_window(runner, msgs, n_forwards, dev):
 
 
 # ------------------------------------------------------------------ CPU baseline
-def cpu_baseline(max_seconds=30.0):
+def cpu_baseline(seconds_per_depth=8.0, max_reps=20):
     """CPU oracle decode step at the 3B shape, batch 40, context 600.
 
-    Sample: one decode forward with 1 layer and one with 2 layers (same
-    weights shapes as Qwen2.5-3B, random KV pool of 600 tokens per request,
-    no prefill), extrapolated to 36 layers: t = t1 + 35 * (t2 - t1).
+    Sample: decode forwards with 1 layer and with 2 layers (same weight
+    shapes as Qwen2.5-3B, random KV pool of 600 tokens per request, no
+    prefill): one untimed warm-up forward each, then timed forwards until
+    seconds_per_depth (or max_reps) is reached; the medians t1, t2 are
+    extrapolated to 36 layers: t = t1 + 35 * (t2 - t1).
     """
     from oracle.qwen2 import Qwen2Cfg, Qwen2Oracle
     from oracle.runner_batch import Req
     from lite_lang_amd.models.qwen2.weights import Qwen2Config, random_state_dict
     cores = os.cpu_count() or 1
     torch.set_num_threads(cores)
-    times = {}
+    times, reps = {}, {}
     for nl in (1, 2):
         cfg = Qwen2Config(layer_nums=nl, hidden_size=2048, num_heads=16, num_key_value_heads=2,
                           intermediate_size=11008, vocab_size=151936)
         sd = random_state_dict(cfg, seed=0)
         oc = Qwen2Cfg(num_layers=nl, hidden=2048, heads=16, kv_heads=2, intermediate=11008,
                       vocab=151936)
-        orc = Qwen2Oracle(oc, sd, torch.bfloat16, B, PROMPT + 8, B * (PROMPT + 2))
+        orc = Qwen2Oracle(oc, sd, torch.bfloat16, B, PROMPT + 8, B * (PROMPT + max_reps + 4))
         del sd
         reqs = []
         for i in range(B):
@@ -157,16 +159,22 @@ def cpu_baseline(max_seconds=30.0):
             reqs.append(r)
         g = torch.Generator().manual_seed(1)
         orc.pool.normal_(generator=g)
-        t0 = time.perf_counter()
-        orc.forward(reqs, False, [1] * B)
-        times[nl] = time.perf_counter() - t0
+        orc.forward(reqs, False, [1] * B)  # warm-up (each forward takes one more slot)
+        ts = []
+        while len(ts) < max_reps and sum(ts) < seconds_per_depth:
+            t0 = time.perf_counter()
+            orc.forward(reqs, False, [1] * B)
+            ts.append(time.perf_counter() - t0)
+        times[nl] = float(np.median(ts))
+        reps[nl] = len(ts)
         del orc
     per_layer = max(times[2] - times[1], 1e-9)
     step = times[1] + 35 * per_layer
     return {"value": B / step, "unit": "tok/s", "cores": cores, "kind": "port",
             "sample": (f"CPU oracle (float64 math, bf16 storage emulation) decode forward of "
-                       f"the 3B shape at batch {B}, context {PROMPT}, no prefill; 1- and 2-layer "
-                       f"runs ({times[1]:.2f}s, {times[2]:.2f}s) extrapolated to 36 layers "
+                       f"the 3B shape at batch {B}, context {PROMPT}, no prefill; median 1- and "
+                       f"2-layer forwards ({times[1]:.3f}s over {reps[1]} runs, {times[2]:.3f}s "
+                       f"over {reps[2]} runs, one warm-up each) extrapolated to 36 layers "
                        f"= {step:.2f}s/step")}
 
 
