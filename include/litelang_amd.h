@@ -138,6 +138,14 @@ int ll_silu_and_mul(const void* x, int64_t x_row_stride, void* out, int64_t out_
 /* out[t, :] = table[ids[t], :].
  * Replaces torch.embedding in Qwen2PreLayer.Forward
  *   (litelang/models/qwen2/layer/pre_layer.py:15-19). */
+/* ll_embedding followed by ll_rmsnorm (no residual) in one launch, bit for
+ * bit: h[t] = table[ids[t]], out[t] = rmsnorm(h[t]) * gamma. Replaces
+ *   Qwen2PreLayer.Forward (pre_layer.py:15-19) + the first layer's rmsnorm
+ *   (transformer_layer.py:87). */
+int ll_embedding_rmsnorm(const void* table, int64_t table_row_stride, int64_t vocab,
+                         const void* ids, int ids_i64, void* h, int64_t h_row_stride,
+                         const void* gamma, void* out, int64_t out_row_stride, int64_t ntok,
+                         int64_t hidden, float eps, int dtype, hipStream_t stream);
 int ll_embedding(const void* table, int64_t table_row_stride, int64_t vocab, const void* ids,
                  int ids_i64, void* out, int64_t out_row_stride, int64_t ntok, int64_t hidden,
                  int dtype, hipStream_t stream);

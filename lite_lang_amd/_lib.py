@@ -35,6 +35,7 @@ SIGNATURES = {
                                  I64, I32, P]),
     "ll_kv_store": (I32, [P, I64, I64, I64, I64, P, P, I64, I64, I64, I32, P]),
     "ll_silu_and_mul": (I32, [P, I64, P, I64, I64, I64, I32, P]),
+    "ll_embedding_rmsnorm": (I32, [P, I64, I64, P, I32, P, I64, P, P, I64, I64, I64, F32, I32, P]),
     "ll_embedding": (I32, [P, I64, I64, P, I32, P, I64, I64, I64, I32, P]),
     "ll_argmax_workspace_size": (I64, [I64, I64]),
     "ll_argmax": (I32, [P, I64, I64, I64, P, P, I64, I32, P]),

@@ -31,15 +31,26 @@ extern "C" int ll_version(void) { return LL_ABI_VERSION; }
 // If `residual` is non-null the kernel first forms h = T(x + residual), stores
 // it back into x (the reference's `hidden_states.add_()` at
 // transformer_layer.py:69,76) and normalises h.
+// With table: x[row] is first gathered from table[ids[row]] (the embedding;
+// each thread re-reads only the elements it wrote).
 template <typename T, int BLOCK>
 __global__ __launch_bounds__(BLOCK) void rmsnorm_kernel(
     T* __restrict__ x, int64_t x_rs, const T* __restrict__ residual, int64_t r_rs,
-    const T* __restrict__ gamma, T* __restrict__ out, int64_t o_rs, int N, float eps) {
+    const T* __restrict__ gamma, T* __restrict__ out, int64_t o_rs, int N, float eps,
+    const T* __restrict__ table, int64_t tab_rs, const void* ids, int ids64) {
   const int row = blockIdx.x;
   T* xr = x + (int64_t)row * x_rs;
   T* orow = out + (int64_t)row * o_rs;
   float ss = 0.f;
-  if (residual != nullptr) {
+  if (table != nullptr) {
+    const T* src = table + ll_load_idx(ids, row, ids64) * tab_rs;
+    for (int i = threadIdx.x; i < N; i += BLOCK) {
+      const T h = src[i];
+      xr[i] = h;
+      float v = ll_to_f32(h);
+      ss += v * v;
+    }
+  } else if (residual != nullptr) {
     const T* rr = residual + (int64_t)row * r_rs;
     for (int i = threadIdx.x; i < N; i += BLOCK) {
       T h = ll_from_f32<T>(ll_to_f32(xr[i]) + ll_to_f32(rr[i]));
@@ -79,7 +90,27 @@ extern "C" int ll_rmsnorm(void* x, int64_t x_row_stride, const void* residual,
   return LL_DISPATCH_DTYPE(dtype, T, [&]() -> int {
     hipLaunchKernelGGL((rmsnorm_kernel<T, 256>), dim3((unsigned)M), dim3(256), 0, stream,
                        (T*)x, x_row_stride, (const T*)residual, residual_row_stride,
-                       (const T*)gamma, (T*)out, out_row_stride, (int)N, eps);
+                       (const T*)gamma, (T*)out, out_row_stride, (int)N, eps, (const T*)nullptr,
+                       (int64_t)0, (const void*)nullptr, 0);
+    LL_RETURN_LAUNCH();
+  });
+}
+
+// h[t] = table[ids[t]] and out[t] = rmsnorm(h[t]) * gamma in one launch: the
+// results of ll_embedding followed by ll_rmsnorm, bit for bit.
+extern "C" int ll_embedding_rmsnorm(const void* table, int64_t table_row_stride, int64_t vocab,
+                                    const void* ids, int ids_i64, void* h, int64_t h_row_stride,
+                                    const void* gamma, void* out, int64_t out_row_stride,
+                                    int64_t ntok, int64_t hidden, float eps, int dtype,
+                                    hipStream_t stream) {
+  LL_CHECK_ARG(table && ids && h && gamma && out, "ll_embedding_rmsnorm: null pointer");
+  LL_CHECK_ARG(vocab > 0 && ntok >= 0 && hidden > 0, "ll_embedding_rmsnorm: bad shape");
+  if (ntok == 0) return LL_OK;
+  return LL_DISPATCH_DTYPE(dtype, T, [&]() -> int {
+    hipLaunchKernelGGL((rmsnorm_kernel<T, 256>), dim3((unsigned)ntok), dim3(256), 0, stream,
+                       (T*)h, h_row_stride, (const T*)nullptr, (int64_t)0, (const T*)gamma,
+                       (T*)out, out_row_stride, (int)hidden, eps, (const T*)table,
+                       table_row_stride, ids, ids_i64);
     LL_RETURN_LAUNCH();
   });
 }

@@ -168,8 +168,9 @@ class Qwen2Model:
         H, KVH, D = cfg.num_heads, cfg.num_key_value_heads, cfg.head_dim
         B = ids.shape[0]
         pool, r2t = kv_cache.kv_cache_, kv_cache.req_to_tokens_
-        h = ops.embedding(self.w.embed, ids)
         if not self.fused_decode_ok(B):
+            h = ops.embedding(self.w.embed, ids)
+
             def attention(li, q, attn):
                 ops.decode_attention(q, r2t, rids, seq_len, max_len, pool[li, :, :KVH],
                                      pool[li, :, KVH:], attn)
@@ -183,11 +184,12 @@ class Qwen2Model:
         q = torch.empty((B, H * D), dtype=dt, device=dev)
         attn = torch.empty((B, H, D), dtype=dt, device=dev)
         act = torch.empty((B, cfg.intermediate_size), dtype=dt, device=dev)
-        x = ops.rmsnorm(h, w.layers[0]["ln1"], cfg.rms_norm_eps)
         nl = len(w.layers)
         if self.quant == "w8a8":
+            h = ops.embedding(w.embed, ids)
             return self._decode_w8a8(h, B, part, q, attn, act, positions, seq_len, rids, slots,
                                      pool, r2t, max_len, out)
+        h, x = ops.embedding_rmsnorm(w.embed, ids, w.layers[0]["ln1"], cfg.rms_norm_eps)
 
         def proj(xin, lw, pk, name):
             if pk.get(name) is not None:

@@ -217,6 +217,22 @@ def embedding(table, ids, out=None):
     return out
 
 
+def embedding_rmsnorm(table, ids, gamma, eps):
+    """(h, out): h = table[ids], out = rmsnorm(h) * gamma, in one launch."""
+    _dev(table, ids, gamma)
+    V, Hd = table.shape
+    T = ids.shape[0]
+    assert table.stride(1) == 1 and gamma.shape == (Hd,)
+    h = torch.empty((T, Hd), dtype=table.dtype, device=table.device)
+    out = torch.empty_like(h)
+    rc = _L.ll_embedding_rmsnorm(table.data_ptr(), table.stride(0), V, ids.data_ptr(),
+                                 _idx(ids, "ids"), h.data_ptr(), h.stride(0), gamma.data_ptr(),
+                                 out.data_ptr(), out.stride(0), T, Hd, float(eps),
+                                 dtype_code(table), _stream(table))
+    _lib.check(rc, "ll_embedding_rmsnorm")
+    return h, out
+
+
 def argmax(x, out=None):
     _dev(x, out)
     M, N = x.shape

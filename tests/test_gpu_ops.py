@@ -502,6 +502,24 @@ def test_add_rmsnorm_splitk(cuda):
     assert _maxdiff(out, O.rmsnorm(h_ref, gamma, 1e-6)) <= BF16_ATOL
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_embedding_rmsnorm_equals_two_calls(cuda, dtype):
+    """The decode step's fused gather + first RMSNorm equals ll_embedding then
+    ll_rmsnorm bit for bit (int64 and int32 ids, repeated ids)."""
+    ops = _ops()
+    g = torch.Generator().manual_seed(44)
+    table = torch.randn(1000, 2048, generator=g).to(dtype).to(cuda)
+    gamma = (torch.rand(2048, generator=g) + 0.5).to(dtype).to(cuda)
+    for ids in (torch.randint(0, 1000, (40,), generator=g),
+                torch.tensor([7, 7, 999, 0], dtype=torch.int32)):
+        ids = ids.to(cuda)
+        h, x = ops.embedding_rmsnorm(table, ids, gamma, 1e-6)
+        h2 = ops.embedding(table, ids)
+        x2 = ops.rmsnorm(h2, gamma, 1e-6)
+        torch.cuda.synchronize()
+        assert torch.equal(h, h2) and torch.equal(x, x2)
+
+
 def test_silu_and_mul_splitk(cuda):
     g = torch.Generator().manual_seed(43)
     M, N, S = 40, 1376, 2
