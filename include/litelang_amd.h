@@ -70,6 +70,17 @@ int ll_decode_attention(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                         int64_t max_len_in_batch, float sm_scale, int dtype, void* workspace,
                         int64_t workspace_bytes, hipStream_t stream);
 
+/* Launches a probe kernel on exactly the grid, block and LDS size of
+ * ll_decode_attention's split stage for this shape and writes, for every
+ * workgroup i, the XCD it ran on (hardware register XCC_ID) to out[i].
+ * Returns the grid size (> 0) or a negative LL_ERR_* code. The split merge in
+ * the same launch assumes out[i] == i % 8 (the XCD that deals the workgroup
+ * holds every split of a sequence in its own L2). No reference counterpart:
+ * it exists to check that premise on the machine. */
+int ll_decode_attention_xcc_probe(int64_t batch, int64_t q_heads, int64_t kv_heads,
+                                  int64_t head_dim, int64_t max_len_in_batch, int32_t* out,
+                                  int64_t out_len, hipStream_t stream);
+
 /* NoPad varlen causal prefill attention reading K/V through the slot table,
  * with an optional shared (prompt-cache) prefix per request.
  * b_shared_seq_len == NULL replaces context_attention_fwd_with_no_pad_and_kv_cache
@@ -135,17 +146,21 @@ int ll_kv_store(const void* src, int64_t src_tok_stride, int64_t src_head_stride
 int ll_silu_and_mul(const void* x, int64_t x_row_stride, void* out, int64_t out_row_stride,
                     int64_t M, int64_t N, int dtype, hipStream_t stream);
 
-/* out[t, :] = table[ids[t], :].
- * Replaces torch.embedding in Qwen2PreLayer.Forward
- *   (litelang/models/qwen2/layer/pre_layer.py:15-19). */
 /* ll_embedding followed by ll_rmsnorm (no residual) in one launch, bit for
  * bit: h[t] = table[ids[t]], out[t] = rmsnorm(h[t]) * gamma. Replaces
  *   Qwen2PreLayer.Forward (pre_layer.py:15-19) + the first layer's rmsnorm
- *   (transformer_layer.py:87). */
+ *   (transformer_layer.py:87). Ids are clamped into [0, vocab) as in
+ *   ll_embedding. */
 int ll_embedding_rmsnorm(const void* table, int64_t table_row_stride, int64_t vocab,
                          const void* ids, int ids_i64, void* h, int64_t h_row_stride,
                          const void* gamma, void* out, int64_t out_row_stride, int64_t ntok,
                          int64_t hidden, float eps, int dtype, hipStream_t stream);
+/* out[t, :] = table[ids[t], :].
+ * Replaces torch.embedding in Qwen2PreLayer.Forward
+ *   (litelang/models/qwen2/layer/pre_layer.py:15-19).
+ * An id outside [0, vocab) is clamped into it so the read stays inside the
+ * table (torch.embedding raises instead; the runner rejects such ids on the
+ * host when a request is admitted). */
 int ll_embedding(const void* table, int64_t table_row_stride, int64_t vocab, const void* ids,
                  int ids_i64, void* out, int64_t out_row_stride, int64_t ntok, int64_t hidden,
                  int dtype, hipStream_t stream);

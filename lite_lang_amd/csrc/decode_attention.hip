@@ -884,7 +884,40 @@ int launch_mfma(DecodeArgs& a, int64_t head_dim, int dtype, bool rope, int64_t m
   LL_RETURN_LAUNCH();
 }
 
+// The XCD (hardware register XCC_ID) each workgroup runs on, for the premise
+// of the same-launch split merge: workgroup i of a grid runs on XCD i mod 8.
+__global__ void xcc_probe_kernel(int32_t* __restrict__ out, int n) {
+  unsigned x;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+  if (threadIdx.x == 0 && (int)blockIdx.x < n) out[blockIdx.x] = (int32_t)(x & 0xf);
+}
+
 }  // namespace
+
+extern "C" int ll_decode_attention_xcc_probe(int64_t batch, int64_t q_heads, int64_t kv_heads,
+                                             int64_t head_dim, int64_t max_len_in_batch,
+                                             int32_t* out, int64_t out_len, hipStream_t stream) {
+  LL_CHECK_ARG(out != nullptr && batch > 0 && kv_heads > 0 && q_heads % kv_heads == 0 &&
+                   (head_dim == 64 || head_dim == 128) && max_len_in_batch > 0,
+               "ll_decode_attention_xcc_probe: bad arguments");
+  const int nsplit = choose_nsplit((int)batch, (int)kv_heads, max_len_in_batch, head_dim);
+  const int groups = (int)((batch + 7) / 8);
+  const int64_t grid = (int64_t)groups * 8 * kv_heads * nsplit;
+  LL_CHECK_ARG(out_len >= grid, "ll_decode_attention_xcc_probe: out holds %lld of %lld entries",
+               (long long)out_len, (long long)grid);
+  const int64_t tiles = (max_len_in_batch + kTT - 1) / kTT;
+  const size_t slots_cap = (size_t)((tiles + nsplit - 1) / nsplit) * kTT;
+  const size_t lds =
+      (head_dim == 128 ? TileGeom<128>::MAIN_B : TileGeom<64>::MAIN_B) + slots_cap * 4;
+  hipLaunchKernelGGL(xcc_probe_kernel, dim3((unsigned)grid), dim3(kWaves * 64), lds, stream, out,
+                     (int)grid);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    ll_set_error("HIP launch failed: %s", hipGetErrorString(e));
+    return LL_ERR_HIP;
+  }
+  return (int)grid;
+}
 
 extern "C" int64_t ll_decode_attention_workspace_size(int64_t batch, int64_t q_heads,
                                                       int64_t kv_heads, int64_t head_dim,

@@ -32,18 +32,21 @@ extern "C" int ll_version(void) { return LL_ABI_VERSION; }
 // it back into x (the reference's `hidden_states.add_()` at
 // transformer_layer.py:69,76) and normalises h.
 // With table: x[row] is first gathered from table[ids[row]] (the embedding;
-// each thread re-reads only the elements it wrote).
+// each thread re-reads only the elements it wrote); the id is clamped into
+// [0, vocab) so the read stays inside the table.
 template <typename T, int BLOCK>
 __global__ __launch_bounds__(BLOCK) void rmsnorm_kernel(
     T* __restrict__ x, int64_t x_rs, const T* __restrict__ residual, int64_t r_rs,
     const T* __restrict__ gamma, T* __restrict__ out, int64_t o_rs, int N, float eps,
-    const T* __restrict__ table, int64_t tab_rs, const void* ids, int ids64) {
+    const T* __restrict__ table, int64_t tab_rs, const void* ids, int ids64, int64_t vocab) {
   const int row = blockIdx.x;
   T* xr = x + (int64_t)row * x_rs;
   T* orow = out + (int64_t)row * o_rs;
   float ss = 0.f;
   if (table != nullptr) {
-    const T* src = table + ll_load_idx(ids, row, ids64) * tab_rs;
+    int64_t id = ll_load_idx(ids, row, ids64);
+    id = id < 0 ? 0 : (id >= vocab ? vocab - 1 : id);
+    const T* src = table + id * tab_rs;
     for (int i = threadIdx.x; i < N; i += BLOCK) {
       const T h = src[i];
       xr[i] = h;
@@ -91,7 +94,7 @@ extern "C" int ll_rmsnorm(void* x, int64_t x_row_stride, const void* residual,
     hipLaunchKernelGGL((rmsnorm_kernel<T, 256>), dim3((unsigned)M), dim3(256), 0, stream,
                        (T*)x, x_row_stride, (const T*)residual, residual_row_stride,
                        (const T*)gamma, (T*)out, out_row_stride, (int)N, eps, (const T*)nullptr,
-                       (int64_t)0, (const void*)nullptr, 0);
+                       (int64_t)0, (const void*)nullptr, 0, (int64_t)0);
     LL_RETURN_LAUNCH();
   });
 }
@@ -110,7 +113,7 @@ extern "C" int ll_embedding_rmsnorm(const void* table, int64_t table_row_stride,
     hipLaunchKernelGGL((rmsnorm_kernel<T, 256>), dim3((unsigned)ntok), dim3(256), 0, stream,
                        (T*)h, h_row_stride, (const T*)nullptr, (int64_t)0, (const T*)gamma,
                        (T*)out, out_row_stride, (int)hidden, eps, (const T*)table,
-                       table_row_stride, ids, ids_i64);
+                       table_row_stride, ids, ids_i64, vocab);
     LL_RETURN_LAUNCH();
   });
 }
@@ -395,9 +398,10 @@ extern "C" int ll_silu_and_mul(const void* x, int64_t x_row_stride, void* out,
 template <typename T>
 __global__ void embedding_kernel(const T* __restrict__ table, int64_t tab_rs,
                                  const void* __restrict__ ids, int ids64, T* __restrict__ out,
-                                 int64_t o_rs, int64_t ntok, int hidden) {
+                                 int64_t o_rs, int64_t ntok, int hidden, int64_t vocab) {
   const int64_t t = blockIdx.x;
-  const int64_t id = ll_load_idx(ids, t, ids64);
+  int64_t id = ll_load_idx(ids, t, ids64);
+  id = id < 0 ? 0 : (id >= vocab ? vocab - 1 : id);  // keep the read inside the table
   const T* src = table + id * tab_rs;
   T* dst = out + t * o_rs;
   for (int i = threadIdx.x; i < hidden; i += blockDim.x) dst[i] = src[i];
@@ -412,7 +416,7 @@ extern "C" int ll_embedding(const void* table, int64_t table_row_stride, int64_t
   return LL_DISPATCH_DTYPE(dtype, T, [&]() -> int {
     hipLaunchKernelGGL((embedding_kernel<T>), dim3((unsigned)ntok), dim3(256), 0, stream,
                        (const T*)table, table_row_stride, ids, ids_i64, (T*)out, out_row_stride,
-                       ntok, (int)hidden);
+                       ntok, (int)hidden, vocab);
     LL_RETURN_LAUNCH();
   });
 }

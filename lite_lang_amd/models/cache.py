@@ -79,7 +79,8 @@ class PageCache:
             free_b, _ = torch.cuda.mem_get_info(self.device)
             # cache.py:218-223: available MiB * mem_usage / 2, in slots
             kv_max_size = int((free_b / 1024**2 * mem_usage) / 2 * 1024**2 // 1024 // self.token_size_)
-        assert kv_max_size > 0, "GPU memory is not enough to allocate cache."
+        assert kv_max_size > 0, (f"no KV token slot fits the memory budget "
+                                 f"(mem_usage {mem_usage}, {self.token_size_:.1f} KiB per slot)")
         self.kv_max_size_ = int(kv_max_size)
         self.kv_cache_ = torch.empty(
             (num_layers, self.kv_max_size_, 2 * num_key_value_heads, head_dim),
@@ -127,8 +128,8 @@ class PageCache:
         lens = _host_ints(b_length)
         new = _host_ints(b_new_add_token_length)
         total = int(sum(new))
-        assert self.physical_free_token_start_ + total <= self.physical_free_token_end_, (
-            "No enough KV cache space")
+        free = self.physical_free_token_end_ - self.physical_free_token_start_
+        assert total <= free, f"KV pool exhausted: {total} slots requested, {free} free"
         s0 = self.physical_free_token_start_
         slots = self.physical_free_token_[s0:s0 + total].copy()
         self.physical_free_token_start_ += total
@@ -164,7 +165,8 @@ class PageCache:
         """Push slots back just below the stack window (cache.py:287-295)."""
         t = np.asarray(_host_ints(token_idxs), dtype=np.int32)
         n = t.shape[0]
-        assert self.physical_free_token_start_ - n >= 0, "page cache internal error"
+        assert self.physical_free_token_start_ - n >= 0, (
+            f"returning {n} slots would overfill the free-slot stack (double free?)")
         s = self.physical_free_token_start_
         self.physical_free_token_[s - n:s] = t
         self.physical_free_token_start_ -= n

@@ -16,8 +16,12 @@ decode forward for a fixed batch size is captured once into a HIP graph:
   * decode attention is captured with the runner's max_length as the length
     bound: its split count and workspace are fixed, and every sequence
     divides its own current length among the splits (ll_decode_attention).
-Workspaces are reserved before capture, so nothing is allocated by the
-library inside the graph; activations come from the graph's private pool.
+Every decode graph of a device is captured on one stream of this module's
+(_capture_stream), and the library workspaces that stream uses are reserved
+on it before capture, so nothing is allocated by the library inside the
+graph; activations come from the graph's private pool. The workspaces of
+that stream are never freed (a larger capture retires a buffer instead), so
+graphs captured earlier keep valid addresses.
 """
 from __future__ import annotations
 
@@ -48,10 +52,26 @@ def reserve_model_workspaces(model, batch, max_len):
             ops.reserve_workspace(model.device, "w8a8_part", model.w8a8_part_bytes(batch))
 
 
+_CAPTURE_STREAMS: dict[int, torch.cuda.Stream] = {}
+
+
+def _capture_stream(device) -> torch.cuda.Stream:
+    """The stream every decode graph of `device` is captured on (default priority)."""
+    idx = torch.device(device).index
+    idx = torch.cuda.current_device() if idx is None else idx
+    s = _CAPTURE_STREAMS.get(idx)
+    if s is None:
+        s = torch.cuda.Stream(device=idx)
+        _CAPTURE_STREAMS[idx] = s
+    return s
+
+
 class DecodeGraph:
     META_ROWS = 5  # slots, rids, cols, positions, seq_len
 
-    def __init__(self, model, kv_cache, batch_size: int, max_len: int):
+    def __init__(self, model, kv_cache, batch_size: int, max_len: int, reserve_upto: int = 0):
+        """reserve_upto: also size the workspaces for batches up to this size
+        (the runner's max batch), so later captures need no larger buffers."""
         self.model, self.kv_cache = model, kv_cache
         self.B = batch_size
         self.max_len = max_len
@@ -62,11 +82,14 @@ class DecodeGraph:
                                   pin_memory=True) for _ in range(2)]
         self._host_ev = [None, None]
         self._k = 0
-        reserve_model_workspaces(model, batch_size, max_len)
+        stream = _capture_stream(dev)
+        with torch.cuda.stream(stream):
+            for b in sorted({batch_size, min(reserve_upto, 64), reserve_upto} - {0}):
+                reserve_model_workspaces(model, b, max_len)
         # the slot table must never be written by the capture itself
         torch.cuda.synchronize(dev)
         self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
+        with torch.cuda.graph(self.graph, stream=stream):
             ops.assign_slots(kv_cache.req_to_tokens_, self.meta[0:3], batch_size)
             model.decode_tokens(self.ids, self.meta[3], self.meta[4], self.meta[1], self.meta[0],
                                 kv_cache, max_len, out=self.ids)

@@ -398,7 +398,8 @@ class Qwen2ModelRunner:
         B = len(lens)
         g = self._graphs.get(B)
         if g is None:
-            g = DecodeGraph(self.model_ins_, self.kv_cache, B, self.max_length_)
+            g = DecodeGraph(self.model_ins_, self.kv_cache, B, self.max_length_,
+                            reserve_upto=self.max_batch_size_)
             self._graphs[B] = g
         slots, rows, cols = self.kv_cache.plan_token_idxs(rids, [l - 1 for l in lens], [1] * B)
         out = g.run(model_inputs.output_token_ids, slots, rows, cols, pos, lens)

@@ -160,7 +160,8 @@ class RadixTree:
         if need_token_nums <= 0:
             return None
         if need_token_nums > self.all_taken_tokens_:
-            raise ValueError("need_token_nums is larger than all taken tokens")
+            raise ValueError(f"cannot evict {need_token_nums} tokens: the tree holds "
+                             f"{self.all_taken_tokens_}")
         freed, out = 0, []
         while len(self.evict_node_set_):
             node = self.evict_node_set_.pop(0)
@@ -174,7 +175,7 @@ class RadixTree:
         return torch.from_numpy(np.concatenate(out))
 
     def _del_node(self, node, out) -> int:
-        assert node.ref_count == 0, "can not del node while ref_count not equal 0"
+        assert node.ref_count == 0, f"evicting a node still referenced {node.ref_count} time(s)"
         out.append(node.page_cache_token_idxs)
         parent = node.parent_node
         del parent.child[int(node.token_ids[0])]

@@ -153,7 +153,19 @@ class RunnerBatch:
     @classmethod
     def create_batch(cls, req_messages, batch_id, is_prefill: bool = True, model_runner=None):
         """Admit requests (runner_batch.py:103-167): radix prefix match on all
-        but the last prompt token, request-row allocation, shared-slot refs."""
+        but the last prompt token, request-row allocation, shared-slot refs.
+
+        Every prompt id is checked against the vocabulary first (nothing is
+        admitted if one is out of range): the reference's torch.embedding
+        raises on such an id at the forward, and the embedding kernel here
+        would otherwise clamp it."""
+        vocab = getattr(getattr(model_runner, "config_", None), "vocab_size", None)
+        if vocab is not None:
+            for message in req_messages:
+                for t in message["input_tokens"]:
+                    if not 0 <= int(t) < vocab:
+                        raise ValueError(f"request {message['id']}: token id {int(t)} is outside "
+                                         f"the vocabulary [0, {vocab})")
         request_mapping = {}
         for message in req_messages:
             request_id = message["id"]

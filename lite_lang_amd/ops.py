@@ -42,20 +42,38 @@ def _dev(*ts: torch.Tensor) -> None:
 
 
 # ------------------------------------------------------------------ workspaces
-# Persistent, zero-initialised device buffers keyed by (device, name). Tickets
-# inside them are left at zero by the kernels, so they are zeroed only when a
-# buffer is (re)allocated. Calls on one device that share a buffer must not
-# overlap in time (the reference's single scheduler thread never does).
-_WS: dict[tuple[int, str], torch.Tensor] = {}
+# Persistent, zero-initialised device buffers keyed by (device, stream, name).
+# Tickets inside them are left at zero by the kernels, so they are zeroed only
+# when a buffer is allocated.
+#  * Per stream: work queued on two streams never shares a buffer, so a
+#    second stream gets buffers of its own instead of racing on the first
+#    one's. (Graphs are captured on torch's capture stream, so every captured
+#    decode step shares that stream's set; replays of them are issued one
+#    after another by the runner.)
+#  * Never freed: a HIP graph keeps the raw addresses it was captured with,
+#    so a buffer that grows is replaced by a larger one (twice the old size
+#    at least) and the old one is kept alive in _RETIRED, where graphs
+#    captured earlier still find it.
+_WS: dict[tuple[int, int, str], torch.Tensor] = {}
+_RETIRED: list[torch.Tensor] = []
+
+
+def _ws_key(device: torch.device, name: str):
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    return (idx, torch.cuda.current_stream(idx).cuda_stream, name)
 
 
 def workspace(device: torch.device, name: str, nbytes: int) -> torch.Tensor:
-    key = (device.index if device.index is not None else torch.cuda.current_device(), name)
+    key = _ws_key(device, name)
     buf = _WS.get(key)
     if buf is None or buf.numel() < nbytes:
         if buf is not None and torch.cuda.is_current_stream_capturing():
             raise RuntimeError(f"workspace '{name}' must be sized before graph capture")
-        buf = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
+        size = max(nbytes, 256)
+        if buf is not None:
+            size = max(size, 2 * buf.numel())
+            _RETIRED.append(buf)
+        buf = torch.zeros(size, dtype=torch.uint8, device=device)
         _WS[key] = buf
     return buf
 

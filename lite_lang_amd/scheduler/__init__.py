@@ -8,11 +8,12 @@ running one, swap-out under KV pressure. The model side is in-process
 process drives one GPU.
 """
 from .pause_strategy import STRATEGY_REGISTRY, select_swapped_reqs
-from .req_queue import ReadyQue, Req, ReqStatus, SchedulerRunnerQue
+from .request import Req, ReqStatus
+from .batching import LiveBatch, WaitingRoom, estimate_fits
 from .scheduler import Scheduler
 from .model_client import LocalModelClient, IdTokenizer
 from .tokenizer import Tokenizer
 
-__all__ = ["Scheduler", "Req", "ReqStatus", "ReadyQue", "SchedulerRunnerQue",
+__all__ = ["Scheduler", "Req", "ReqStatus", "LiveBatch", "WaitingRoom", "estimate_fits",
            "STRATEGY_REGISTRY", "select_swapped_reqs", "LocalModelClient", "IdTokenizer",
            "Tokenizer"]

@@ -1,154 +1,123 @@
-"""The scheduling loop (litelang/scheduler/scheduler.py:7-181)."""
+"""The continuous-batching loop (counterpart of litelang/scheduler/scheduler.py:7-181).
+
+One `forward()` is one scheduling round: admit a batch from the waiting room
+(prefill it, and merge it into the live batch if one is running), then decode
+the live batch for at most BURST_STEPS steps before the next admission
+attempt. The burst counter carries over between rounds (a batch that ends
+early leaves the rest of the burst to the next one), as in the reference.
+The model side is any object with the reference ModelClient's calls
+(init_model, add_batch, prefill, decode, merge_batch, filter_batch,
+swapped_reqs, remove_batch); LocalModelClient serves them in-process.
+"""
 from __future__ import annotations
 
 import queue
 import time
 
-from .req_queue import ReadyQue, Req, ReqStatus, SchedulerRunnerQue, new_batch_id
+from .batching import LiveBatch, WaitingRoom, new_batch_id
+from .request import Req, ReqStatus
+
+MAX_REQUEST_ID = 100000  # request ids wrap at this value (scheduler.py:40)
 
 
 class Scheduler:
-    """Continuous batching over one model client.
-
-    forward() is one scheduling round (scheduler.py:148-181): with no running
-    batch, admit a new one, prefill it and decode up to 10 steps; with a
-    running batch, admit, prefill and merge newcomers, then decode up to 10
-    steps. Finished requests are filtered out of the model-side batch after
-    every decode step; requests swapped out under KV pressure go back to the
-    front of the ready queue with their generated tokens appended to the
-    prompt."""
+    BURST_STEPS = 10
 
     def __init__(self, max_batch_size, tokenizer, max_total_length, max_output_length, max_reqs,
                  model_client, busy_scale, log=None):
-        self.model_client_ = model_client
-        max_sum_kv_tokens = self.model_client_.init_model()
-        self.ready_and_swapped_que_ = ReadyQue(max_reqs, max_total_length - max_output_length,
-                                               max_output_length, max_sum_kv_tokens,
-                                               max_batch_size, busy_scale)
-        self.running_que_ = SchedulerRunnerQue(max_batch_size, new_batch_id(), busy_scale,
-                                               max_sum_kv_tokens)
-        self.new_running_que_ = SchedulerRunnerQue(max_batch_size, new_batch_id(), busy_scale,
-                                                   max_sum_kv_tokens)
-        self.max_batch_size_ = max_batch_size
-        self.tokenizer_ = tokenizer
-        self.now_id = 0
-        self.max_id = 100000
-        self.max_total_length_ = max_total_length
-        self.max_output_length_ = max_output_length
-        self.now_decode_times_, self.every_decode_times_try_get_new_batch_ = 0, 10
-        self.log_ = log  # optional callable(str): the reference prints throughput lines
+        self.client = model_client
+        self.tokenizer = tokenizer
+        self.max_batch_size = max_batch_size
+        self.max_total_length = max_total_length
+        self.max_output_length = max_output_length
+        kv_budget = self.client.init_model()
+        self._room = WaitingRoom(max_reqs, max_batch_size, kv_budget, busy_scale)
+        self._kv_budget = kv_budget
+        self._live = LiveBatch(new_batch_id(), kv_budget)
+        self._burst = 0
+        self._submitted = 0
+        self._log = log  # optional callable(str) for throughput lines (the reference prints them)
 
     # ------------------------------------------------------------ requests
-    def add_req(self, prompt, top_p, top_k, temperature, do_sample):
-        # encode_single returns a batch of one sequence (tokenizer.py:15-24)
-        toks = self.tokenizer_.encode_single(prompt)[0]
-        toks = toks.tolist() if hasattr(toks, "tolist") else list(toks)
-        return self.add_req_tokens(toks, top_p, top_k, temperature, do_sample, prompt=prompt)
+    def add_req(self, prompt, top_p, top_k, temperature, do_sample) -> Req:
+        """Tokenise `prompt` and queue it; the caller reads the generated text
+        from the returned request's output_prompt_que."""
+        ids = self.tokenizer.encode_single(prompt)[0]  # a batch of one sequence
+        ids = ids.tolist() if hasattr(ids, "tolist") else list(ids)
+        return self.add_req_tokens(ids, top_p, top_k, temperature, do_sample, prompt=prompt)
 
-    def add_req_tokens(self, input_tokens, top_p=1.0, top_k=1, temperature=0.0,
-                       do_sample=False, prompt=""):
-        """add_req for callers that already hold token ids."""
+    def add_req_tokens(self, input_tokens, top_p=1.0, top_k=1, temperature=0.0, do_sample=False,
+                       prompt="") -> Req:
+        """add_req for callers that already hold token ids. A request arriving
+        while max_reqs are waiting is not queued (it never runs), as in the
+        reference."""
         toks = [int(t) for t in input_tokens]
-        req = Req(id=self.now_id % self.max_id, status=ReqStatus.READY, prompt=prompt,
-                  input_tokens=toks, output_tokens=[], max_total_length=self.max_total_length_,
-                  max_output_length=self.max_output_length_, output_prompt_que=queue.Queue(),
-                  top_p=top_p, top_k=top_k, temperature=temperature, do_sample=do_sample,
-                  input_length=len(toks), eos_token=self.tokenizer_.eos_token_id)
-        self.now_id += 1
-        self.ready_and_swapped_que_.add_req(req)
+        req = Req(id=self._submitted % MAX_REQUEST_ID, status=ReqStatus.READY, prompt=prompt,
+                  input_tokens=toks, output_tokens=[], max_total_length=self.max_total_length,
+                  max_output_length=self.max_output_length, output_prompt_que=queue.Queue(),
+                  temperature=temperature, top_p=top_p, top_k=top_k, do_sample=do_sample,
+                  input_length=len(toks), eos_token=self.tokenizer.eos_token_id)
+        self._submitted += 1
+        self._room.submit(req)
         return req
 
-    # ------------------------------------------------------------ batches
-    def construct_running_que(self):
-        self.running_que_ = self.ready_and_swapped_que_.try_generate_new_batch(self.running_que_)
-        return True
+    def has_work(self) -> bool:
+        """Whether a request is running or waiting."""
+        return not self._live.empty() or len(self._room) > 0
 
-    def try_construct_new_running_que(self):
-        self.new_running_que_ = self.ready_and_swapped_que_.try_generate_new_batch(self.running_que_)
-
-    def should_forward(self):
-        return not self.running_que_.is_empty()
-
-    def merge_runner_batch(self):
-        self.model_client_.merge_batch(self.running_que_.batch_id, self.new_running_que_.batch_id)
-        self.running_que_.update(self.new_running_que_)
-
-    def _log(self, what, n, t0):
-        if self.log_ is not None:
-            self.log_(f"{what} throughput: {n / max(time.perf_counter() - t0, 1e-9)} tokens/s")
-
-    def update_from_forward(self, output_token_ids, req_ids):
-        texts = self.tokenizer_.decode(output_token_ids)
-        return self.running_que_.update_from_forward(texts, output_token_ids, req_ids,
-                                                     self.tokenizer_.eos_token_id)
-
-    def model_prefill(self, batch_id):
-        t0 = time.perf_counter()
-        self.model_client_.add_batch(self.running_que_.get_transfer_data(), batch_id)
-        toks, req_ids = self.model_client_.prefill(batch_id)
-        self._filter_ended_at_prefill(batch_id, self.update_from_forward(toks, req_ids))
-        self._log("prefill", len(req_ids), t0)
-        return True
-
-    def _filter_ended_at_prefill(self, batch_id, stop):
-        # A request whose first token ends it leaves the scheduler's queue; the
-        # reference leaves it in the model-side batch, where the next decode
-        # returns an id the queue no longer holds (scheduler.py:97-103).
-        # Here it is filtered out of the model-side batch as well.
-        if stop:
-            self.model_client_.filter_batch(batch_id, [r.id for r in stop])
-
-    def model_decode(self, batch_id):
-        t0 = time.perf_counter()
-        swapped = self.running_que_.try_swapped_reqs()
-        if swapped:
-            self.model_client_.swapped_reqs(batch_id, [r.id for r in swapped])
-            for r in swapped:
-                r.input_tokens.extend(r.output_tokens)
-                r.output_tokens = []
-                r.is_prefill = True
-                r.status = ReqStatus.SWAPPED
-                self.ready_and_swapped_que_.add_swapped_req(r)
-        toks, req_ids = self.model_client_.decode(batch_id)
-        stop = self.update_from_forward(toks, req_ids)
-        if stop:
-            self.model_client_.filter_batch(batch_id, [r.id for r in stop])
-        self._log("decode", len(req_ids), t0)
-        return True
-
-    def new_update_from_forward(self, output_token_ids, req_ids):
-        texts = self.tokenizer_.decode(output_token_ids)
-        return self.new_running_que_.update_from_forward(texts, output_token_ids, req_ids,
-                                                         self.tokenizer_.eos_token_id)
-
-    def new_model_prefill(self, batch_id):
-        t0 = time.perf_counter()
-        self.model_client_.add_batch(self.new_running_que_.get_transfer_data(), batch_id)
-        toks, req_ids = self.model_client_.prefill(batch_id)
-        self._filter_ended_at_prefill(batch_id, self.new_update_from_forward(toks, req_ids))
-        self._log("prefill", len(req_ids), t0)
-        return True
-
-    def _decode_burst(self):
-        while not self.running_que_.is_end():
-            self.model_decode(self.running_que_.batch_id)
-            self.now_decode_times_ += 1
-            if self.now_decode_times_ >= self.every_decode_times_try_get_new_batch_:
-                self.now_decode_times_ = 0
-                break
-
-    def forward(self):
-        if self.running_que_.is_empty():
-            self.construct_running_que()
-            if self.running_que_.is_empty():
+    # ------------------------------------------------------------ one round
+    def forward(self) -> None:
+        if self._live.empty():
+            self._live = self._room.admit(self._live)
+            if self._live.empty():
                 return
-            self.model_prefill(self.running_que_.batch_id)
-            self._decode_burst()
+            self._prefill(self._live)
         else:
-            self.try_construct_new_running_que()
-            if not self.new_running_que_.is_empty():
-                self.new_model_prefill(self.new_running_que_.batch_id)
-                self.merge_runner_batch()
-            self._decode_burst()
-        if self.running_que_.is_end():
-            self.model_client_.remove_batch(self.running_que_.batch_id)
+            fresh = self._room.admit(self._live)
+            if not fresh.empty():
+                self._prefill(fresh)
+                self.client.merge_batch(self._live.batch_id, fresh.batch_id)
+                self._live.absorb(fresh)
+        while not self._live.finished:
+            self._decode_step()
+            self._burst += 1
+            if self._burst >= self.BURST_STEPS:
+                self._burst = 0
+                break
+        if self._live.finished:
+            self.client.remove_batch(self._live.batch_id)
+
+    # ------------------------------------------------------------ model calls
+    def _apply(self, batch: LiveBatch, tokens, req_ids):
+        """Hand a forward's tokens to the batch; drop finished requests from the
+        model-side batch. (A request that ends on its prefill token is dropped
+        too: the reference leaves it in the model-side batch, where its next
+        decode hands back an id the scheduler no longer holds,
+        scheduler.py:97-103.)"""
+        done = batch.record(self.tokenizer.decode(tokens), tokens, req_ids)
+        if done:
+            self.client.filter_batch(batch.batch_id, [r.id for r in done])
+
+    def _prefill(self, batch: LiveBatch) -> None:
+        t0 = time.perf_counter()
+        self.client.add_batch(batch.transfer_data(), batch.batch_id)
+        tokens, req_ids = self.client.prefill(batch.batch_id)
+        self._apply(batch, tokens, req_ids)
+        self._report("prefill", len(req_ids), t0)
+
+    def _decode_step(self) -> None:
+        t0 = time.perf_counter()
+        live = self._live
+        victims = live.swap_out_for_kv()
+        if victims:
+            self.client.swapped_reqs(live.batch_id, [r.id for r in victims])
+            for r in victims:
+                r.park()
+                self._room.return_swapped(r)
+        tokens, req_ids = self.client.decode(live.batch_id)
+        self._apply(live, tokens, req_ids)
+        self._report("decode", len(req_ids), t0)
+
+    def _report(self, what, n, t0):
+        if self._log is not None:
+            self._log(f"{what} throughput: {n / max(time.perf_counter() - t0, 1e-9)} tokens/s")

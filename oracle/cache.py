@@ -50,7 +50,7 @@ class PageCache:
         at columns b_length[r] .. b_length[r] + b_new[r] - 1 of its row
         (the bucketize mapping of cache.py:238-248)."""
         total = int(sum(int(n) for n in b_new))
-        assert self.start + total <= self.end, "No enough KV cache space"
+        assert self.start + total <= self.end, "KV pool exhausted"
         idxs = self.free[self.start:self.start + total].copy()
         self.start += total
         g = 0
@@ -73,7 +73,7 @@ class PageCache:
     def free_token_idxs(self, token_idxs):
         token_idxs = np.asarray(token_idxs, dtype=np.int32)
         n = token_idxs.shape[0]
-        assert self.start - n >= 0, "page cache internal error"
+        assert self.start - n >= 0, "free-slot stack overfilled"
         self.free[self.start - n:self.start] = token_idxs
         self.start -= n
 

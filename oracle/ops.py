@@ -3,18 +3,44 @@
 All arithmetic is float64 unless a function says otherwise; ``rnd`` emulates
 storing an intermediate in a low-precision dtype, at the points where the
 reference stores one. Reference paths are relative to the lite_lang root.
+
+``math_dtype(torch.float32)`` switches the float arithmetic to fp32 inside a
+``with`` block. It is used only where float64 would take minutes on the CPU
+(the full-width Qwen2 geometries and the CPU baseline); every pin in
+tests/test_oracle_*.py runs in float64. The integer paths (quantisers, int8
+GEMM) are exact in either mode.
 """
 from __future__ import annotations
 
+import contextlib
 import math
 
 import numpy as np
 import torch
 
 
+_MATH = [torch.float64]
+
+
+def compute_dtype() -> torch.dtype:
+    """The float type the oracle computes in (float64 unless math_dtype is active)."""
+    return _MATH[-1]
+
+
+@contextlib.contextmanager
+def math_dtype(dt: torch.dtype):
+    """Compute in `dt` (float32 or float64) inside the block."""
+    assert dt in (torch.float32, torch.float64)
+    _MATH.append(dt)
+    try:
+        yield
+    finally:
+        _MATH.pop()
+
+
 def rnd(x: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
-    """Round x to `dtype` storage (RNE) and come back to float64."""
-    return x.to(dtype).to(torch.float64)
+    """Round x to `dtype` storage (RNE) and come back to the compute dtype."""
+    return x.to(dtype).to(compute_dtype())
 
 
 # ---------------------------------------------------------------- RMSNorm
@@ -24,9 +50,9 @@ def rmsnorm(x: torch.Tensor, gamma: torch.Tensor, eps: float) -> torch.Tensor:
     Follows torch_rmsnorm, litelang/kernel/develop_rmsnorm/rms_norm.py:11-17
     (the kernel, rms_norm.py:37-53, does the same in fp32 and casts at the end).
     """
-    x = x.to(torch.float64)
+    x = x.to(compute_dtype())
     var = (x * x).sum(-1, keepdim=True) / x.shape[-1]
-    return x / torch.sqrt(var + eps) * gamma.to(torch.float64)
+    return x / torch.sqrt(var + eps) * gamma.to(compute_dtype())
 
 
 # ---------------------------------------------------------------- RoPE
@@ -45,11 +71,11 @@ def rotary(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tenso
 
     Follows torch_rotary_emb, litelang/kernel/develop_rope/rope.py:225-234.
     """
-    x = x.to(torch.float64)
+    x = x.to(compute_dtype())
     T, H, D = x.shape
     x0, x1 = x[..., : D // 2], x[..., D // 2:]
-    c = cos.to(torch.float64).view(T, 1, D // 2)
-    s = sin.to(torch.float64).view(T, 1, D // 2)
+    c = cos.to(compute_dtype()).view(T, 1, D // 2)
+    s = sin.to(compute_dtype()).view(T, 1, D // 2)
     return torch.cat((x0 * c - x1 * s, x0 * s + x1 * c), dim=-1)
 
 
@@ -61,7 +87,7 @@ def silu_and_mul(x: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
     the multiply (silu_and_mul.py:43-50; the reference rounds to fp16, its
     only runtime dtype; here to the model dtype).
     """
-    x = x.to(torch.float64)
+    x = x.to(compute_dtype())
     n = x.shape[-1] // 2
     g, u = x[:, :n], x[:, n:]
     s = rnd(g / (1.0 + torch.exp(-g)), dtype)
@@ -82,18 +108,18 @@ def decode_attention(q, req_to_tokens, b_req_idx, b_seq_len, k_pool, v_pool, sm_
     G = H // KVH
     if sm_scale is None:
         sm_scale = 1.0 / math.sqrt(D)
-    out = torch.zeros((B, H, D), dtype=torch.float64)
+    out = torch.zeros((B, H, D), dtype=compute_dtype())
     for b in range(B):
         L = int(b_seq_len[b])
         if L <= 0:
             continue
         slots = req_to_tokens[int(b_req_idx[b]), :L].long()
-        for h in range(H):
-            kv = h // G
-            k = k_pool[slots, kv].to(torch.float64)
-            v = v_pool[slots, kv].to(torch.float64)
-            s = (q[b, h].to(torch.float64) @ k.T) * sm_scale
-            out[b, h] = torch.softmax(s, -1) @ v
+        for kv in range(KVH):
+            k = k_pool[slots, kv].to(compute_dtype())
+            v = v_pool[slots, kv].to(compute_dtype())
+            for h in range(kv * G, (kv + 1) * G):
+                s = (q[b, h].to(compute_dtype()) @ k.T) * sm_scale
+                out[b, h] = torch.softmax(s, -1) @ v
     return out
 
 
@@ -113,7 +139,7 @@ def prefill_attention(q, k_pool, v_pool, b_req_idx, b_start_loc, b_seq_len, req_
     G = H // KVH
     if sm_scale is None:
         sm_scale = 1.0 / math.sqrt(D)
-    out = torch.zeros((T, H, D), dtype=torch.float64)
+    out = torch.zeros((T, H, D), dtype=compute_dtype())
     for b in range(len(b_seq_len)):
         L = int(b_seq_len[b])
         S = int(b_shared_seq_len[b]) if b_shared_seq_len is not None else 0
@@ -127,10 +153,11 @@ def prefill_attention(q, k_pool, v_pool, b_req_idx, b_start_loc, b_seq_len, req_
         mask = n <= m
         for h in range(H):
             kv = h // G
-            k = k_pool[slots, kv].to(torch.float64)
-            v = v_pool[slots, kv].to(torch.float64)
-            s = (q[st:st + nq, h].to(torch.float64) @ k.T) * sm_scale
-            s = torch.where(mask, s, torch.tensor(-math.inf, dtype=torch.float64))
+            if h % G == 0:
+                k = k_pool[slots, kv].to(compute_dtype())
+                v = v_pool[slots, kv].to(compute_dtype())
+            s = (q[st:st + nq, h].to(compute_dtype()) @ k.T) * sm_scale
+            s = torch.where(mask, s, torch.tensor(-math.inf, dtype=compute_dtype()))
             mx = s.max(-1, keepdim=True).values
             p = torch.exp(s - mx)
             l = p.sum(-1, keepdim=True)
@@ -149,9 +176,9 @@ def linear(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None = None) -
     product. Third-party arithmetic (cuBLAS) -- pinned by the closed form
     only.
     """
-    y = x.to(torch.float64) @ w.to(torch.float64).T
+    y = x.to(compute_dtype()) @ w.to(compute_dtype()).T
     if bias is not None:
-        y = y + bias.to(torch.float64)
+        y = y + bias.to(compute_dtype())
     return y
 
 
@@ -180,10 +207,13 @@ def quantize_weight_per_channel_absmax(w: torch.Tensor):
 
 
 def quantize_per_token_absmax(x: torch.Tensor):
-    """Dynamic per-token activation quantisation: s_t = max_k |x[t, k]| / 127,
-    x_q = clamp(round_half_even(x / s_t), -128, 127). Build-defined (the
-    reference has no activation quantisation at runtime; smooth_quant/layer.py
-    only fixes the weight side); parity unpinned beyond the closed form."""
+    """Dynamic per-token activation quantisation: s_t = max_k |x[t, k]| / 127
+    in fp32 (1 for an all-zero row), x_q = clamp(round_half_even(fp32(x) /
+    s_t), -128, 127). The rule is build-defined: the reference has no runtime
+    activation quantisation, and smooth_quant/layer.py:5-16 fixes only the
+    weight side, whose absmax / 127 rule this mirrors per token. Pinned by
+    hand-computed codes (ties to even, the absmax entry at +-127, the zero
+    row) in tests/test_oracle_ops.py."""
     x = x.to(torch.float32)
     s = x.abs().max(dim=1)[0] / 127
     s = torch.where(s > 0, s, torch.ones_like(s))
@@ -192,8 +222,14 @@ def quantize_per_token_absmax(x: torch.Tensor):
 
 
 def int8_gemm_i32(xq: torch.Tensor, wq: torch.Tensor) -> torch.Tensor:
-    """Exact int32 accumulators acc[t, o] = sum_k xq[t, k] * wq[o, k] (int64 math)."""
-    return (xq.to(torch.int64) @ wq.to(torch.int64).T).to(torch.int32)
+    """Exact int32 accumulators acc[t, o] = sum_k xq[t, k] * wq[o, k].
+
+    Evaluated as a float64 matrix product, which is exact here: every product
+    and every partial sum is an integer of magnitude <= 128 * 128 * K, below
+    2^53 for any K < 2^39, so no float64 operation rounds (and the int32
+    result holds for K <= 131071)."""
+    assert xq.shape[-1] < (1 << 17)
+    return (xq.to(torch.float64) @ wq.to(torch.float64).T).to(torch.int64).to(torch.int32)
 
 
 def quantize_static(x: torch.Tensor, s_a):

@@ -11,8 +11,9 @@ layer/post_layer.py:44-107, with the reference quirks kept:
   * o_proj bias ignored (transformer_layer.py:193);
   * residual adds stored in the model dtype (transformer_layer.py:69,76);
   * greedy argmax on the stored logits, first index on ties (post_layer.py:105-107).
-Compute is float64; `rnd` stores an intermediate in the model dtype wherever
-the reference stores a tensor.
+Compute is float64 (fp32 inside ops.math_dtype(torch.float32), used for the
+full-width geometries only); `rnd` stores an intermediate in the model dtype
+wherever the reference stores a tensor.
 
 Weights come in as a Hugging Face style state dict (the names read by
 layer_weights/load_weights.py:86-172 and pre/post_layer_weights.py).
@@ -101,14 +102,20 @@ class Qwen2Oracle:
                 for name in ("wq", "wk", "wv", "wo", "wg", "wu", "wd"):
                     w[name + "_i8"] = ops.quantize_weight_per_channel_absmax(w[name].to(dtype))
         D, KVH = cfg.head_dim, cfg.kv_heads
-        self.pool = torch.zeros((cfg.num_layers, kv_slots, 2 * KVH, D), dtype=torch.float64)
+        self.pool = torch.zeros((cfg.num_layers, kv_slots, 2 * KVH, D), dtype=ops.compute_dtype())
         self.cache = PageCache(max_batch, max_length, kv_slots)
         cos, sin = ops.rope_table(max_length, D, cfg.theta, cfg.table_dtype)
-        self.cos, self.sin = cos.to(torch.float64), sin.to(torch.float64)
+        self.cos, self.sin = cos.to(ops.compute_dtype()), sin.to(ops.compute_dtype())
 
     def _linear(self, x, w, names, bias=None):
         if self.quant != "w8a8":
-            wt = w[names[0]] if len(names) == 1 else torch.cat([w[n] for n in names], 0)
+            if len(names) == 1:
+                wt = w[names[0]]
+            else:  # the concatenated [gate; up] weight, built once
+                key = "+".join(names)
+                if key not in w:
+                    w[key] = torch.cat([w[n] for n in names], 0)
+                wt = w[key]
             return ops.linear(x, wt, bias)
         sa = w.get(names[0] + "_as")  # static input scale (o_proj, down_proj of a converted model)
         if sa is not None:
@@ -117,7 +124,7 @@ class Qwen2Oracle:
             xq, st = ops.quantize_per_token_absmax(x.to(self.dtype))
         wq = torch.cat([w[n + "_i8"][0] for n in names], 0)
         so = torch.cat([w[n + "_i8"][1] for n in names], 0)
-        y = ops.dequant_int32(ops.int8_gemm_i32(xq, wq), st, so).to(torch.float64)
+        y = ops.dequant_int32(ops.int8_gemm_i32(xq, wq), st, so).to(ops.compute_dtype())
         return y if bias is None else y + bias
 
     # ------------------------------------------------------------ one forward
@@ -167,9 +174,14 @@ class Qwen2Oracle:
         return ops.argmax_first(logits), logits
 
     # ------------------------------------------------------------ greedy loop
-    def generate(self, prompts, n_new: int, return_logits: bool = False):
+    def generate(self, prompts, n_new: int, return_logits: bool = False, feed=None):
         """Prefill all prompts as one NoPad batch, then n_new-1 decode steps
-        (the loop of test/generate_token.py:61-63). Returns [B, n_new] tokens."""
+        (the loop of test/generate_token.py:61-63). Returns [B, n_new] tokens.
+
+        feed [B, >= n_new-1] (optional): the tokens appended after each step
+        instead of this oracle's own argmax (teacher forcing), so that every
+        step is evaluated on the same context as the run that produced them;
+        the returned tokens are still this oracle's argmax at each step."""
         reqs = []
         for p in prompts:
             rid = self.cache.alloc_req()
@@ -177,10 +189,11 @@ class Qwen2Oracle:
         ids = [t for p in prompts for t in p]
         toks, logits = self.forward(reqs, True, ids)
         out, all_logits = [toks], [logits]
-        for _ in range(n_new - 1):
-            for r, t in zip(reqs, toks.tolist()):
+        for i in range(n_new - 1):
+            nxt = toks.tolist() if feed is None else [int(t) for t in feed[:, i]]
+            for r, t in zip(reqs, nxt):
                 r.output_tokens.append(t)
-            toks, logits = self.forward(reqs, False, toks.tolist())
+            toks, logits = self.forward(reqs, False, nxt)
             out.append(toks)
             all_logits.append(logits)
         res = torch.stack(out, 1)

@@ -126,7 +126,7 @@ class RadixOracle:
         if need <= 0:
             return None
         if need > self.all_taken:
-            raise ValueError("need_token_nums is larger than all taken tokens")
+            raise ValueError("eviction request exceeds the tokens held by the tree")
         freed, out = 0, []
         while self.evict:
             n = self.evict.pop(0)

@@ -116,6 +116,14 @@ SCENARIOS = [
 ]
 
 
+def _has_work(sch):
+    """A request is running or waiting (the product's Scheduler.has_work; the
+    reference scheduler exposes only its queues)."""
+    if hasattr(sch, "has_work"):
+        return sch.has_work()
+    return not sch.running_que_.is_empty() or bool(sch.ready_and_swapped_que_.reqs_)
+
+
 def run(scheduler_cls, scenario, as_tensor, max_rounds=400):
     name, kw, kv, lens, arrivals = scenario[:5]
     mod = scenario[5] if len(scenario) > 5 else 23
@@ -130,7 +138,7 @@ def run(scheduler_cls, scenario, as_tensor, max_rounds=400):
             prompt = " ".join(str(1 + (nxt * 7 + i) % 97) for i in range(L))
             reqs.append(sch.add_req(prompt, 1.0, 1, 0.0, False))
             nxt += 1
-        if not sch.running_que_.is_empty() or sch.ready_and_swapped_que_.reqs_ or rnd in arrivals:
+        if _has_work(sch) or rnd in arrivals:
             sch.forward()
         elif rnd > max(arrivals):
             break

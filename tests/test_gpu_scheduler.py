@@ -37,13 +37,13 @@ def test_scheduler_end_to_end_with_swaps(cuda):
     reqs = [sch.add_req_tokens(p) for p in prompts[:4]]
     rounds = 0
     swaps = 0
-    orig_swap = sch.model_client_.swapped_reqs
+    orig_swap = sch.client.swapped_reqs
 
     def count_swaps(bid, ids):
         nonlocal swaps
         swaps += len(ids)
         return orig_swap(bid, ids)
-    sch.model_client_.swapped_reqs = count_swaps
+    sch.client.swapped_reqs = count_swaps
     while rounds < 200 and (not all(r.is_end for r in reqs) or len(reqs) < len(prompts)):
         if rounds == 3:
             reqs += [sch.add_req_tokens(p) for p in prompts[4:]]

@@ -214,3 +214,63 @@ def test_oracle_weight_quantiser_pinned():
         assert int(q[r].abs().max()) == 127
         err = (q[r].float() * sf[r] - wf[r]).abs()
         assert float(err.max()) <= float(sf[r]) / 2 + 1e-7
+
+
+def test_oracle_token_quantiser_pinned():
+    """quantize_per_token_absmax against hand-computed codes: s_t =
+    max_k |x[t, k]| / 127 in fp32; codes round half to even; the row's
+    largest magnitude codes to +-127; an all-zero row gets scale 1 and codes
+    0; no code can fall below -127 (|x| <= absmax, so |x / s| <= 127 up to
+    one rounding), so the -128 clamp only matters for a static scale, whose
+    clamping is pinned here too. Inputs arrive in the model dtype (bf16 and
+    fp16 hold every value below exactly)."""
+    from oracle.ops import quantize_per_token_absmax, quantize_static
+    rows = [
+        [127.0, 63.5, -0.5, 1.5, 2.5, -127.0, 0.25, -63.5],   # s = 1
+        [0.0] * 8,                                             # s = 1 by definition
+        [-254.0, 5.0, -3.0, 1.0, 127.0, 0.0, 3.0, -1.0],       # s = 2
+        [0.75, -0.375, 0.1875, 0.0, 0.0, 0.0, 0.0, -0.09375],  # s = 0.75 / 127
+    ]
+    want = [
+        [127, 64, 0, 2, 2, -127, 0, -64],
+        [0] * 8,
+        [-127, 2, -2, 0, 64, 0, 2, 0],
+        # 0.375 * 127 / 0.75 = 63.5 -> 64 (even); 0.1875 -> 31.75 -> 32;
+        # 0.09375 -> 15.875 -> 16
+        [127, -64, 32, 0, 0, 0, 0, -16],
+    ]
+    for dt in (torch.bfloat16, torch.float16, torch.float32):
+        q, s = quantize_per_token_absmax(torch.tensor(rows, dtype=dt))
+        assert q.dtype == torch.int8 and s.dtype == torch.float32
+        assert q.tolist() == want, dt
+        assert s[:3].tolist() == [1.0, 1.0, 2.0]
+        assert float(s[3]) == float(torch.tensor(0.75, dtype=torch.float32) / 127)
+    # random rows: the absmax entry codes to +-127 and every code is within
+    # half a step of x / s (no code is clamped)
+    g = torch.Generator().manual_seed(71)
+    x = (torch.randn(16, 96, generator=g) * torch.rand(16, 1, generator=g) * 3).bfloat16()
+    q, s = quantize_per_token_absmax(x)
+    xd, sd = x.double(), s.double()
+    for r in range(16):
+        assert int(q[r].abs().max()) == 127 and int(q[r].min()) >= -127
+        # exact error of the code; the fp32 division x / s may move a value
+        # by 127 * 2^-24 of a step across the half-way point
+        err = (q[r].double() * sd[r] - xd[r]).abs()
+        assert float(err.max()) <= float(sd[r]) * (0.5 + 1e-5)
+    # static scale: the clamp at both ends, ties to even
+    qs, ss = quantize_static(torch.tensor([[-1000.0, 1000.0, 2.5, -2.5, 127.5, -128.5]]), 1.0)
+    assert qs.tolist() == [[-128, 127, 2, -2, 127, -128]] and ss.tolist() == [1.0]
+
+
+def test_oracle_dequant_pinned():
+    """dequant_int32 = (fp32(acc) * s_tok[m]) * fp32(s_ch[n]) on hand-computed
+    exact cases, including the fp32 conversion of an int32 sum above 2^24
+    (16777217 rounds to even, 16777216) and 16-bit channel scales."""
+    from oracle.ops import dequant_int32
+    acc = torch.tensor([[100, -7], [0, 1 << 20], [16777217, 16777219]], dtype=torch.int32)
+    s_tok = torch.tensor([0.5, 2.0 ** -10, 1.0], dtype=torch.float32)
+    for dt in (torch.float16, torch.bfloat16, torch.float32):
+        s_ch = torch.tensor([0.25, 3.0], dtype=dt)
+        y = dequant_int32(acc, s_tok, s_ch)
+        assert y.dtype == torch.float32
+        assert y.tolist() == [[12.5, -10.5], [0.0, 3072.0], [4194304.0, 50331660.0]]

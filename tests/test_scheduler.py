@@ -19,8 +19,9 @@ import pytest
 sys.path.insert(0, os.path.join(os.path.dirname(__file__), "golden"))
 import sched_scenarios  # noqa: E402
 
-from lite_lang_amd.scheduler import (STRATEGY_REGISTRY, ReadyQue, Req, ReqStatus,  # noqa: E402
-                                     Scheduler, SchedulerRunnerQue, select_swapped_reqs)
+from lite_lang_amd.scheduler import (STRATEGY_REGISTRY, LiveBatch, Req, ReqStatus,  # noqa: E402
+                                     Scheduler, WaitingRoom, estimate_fits,
+                                     select_swapped_reqs)
 
 GOLD = os.path.join(os.path.dirname(__file__), "golden", "scheduler_traces.json")
 
@@ -54,31 +55,66 @@ def _req(i, inp, out=0, max_total=100, max_out=50):
 
 def test_admission_estimate_closed_form():
     """Admit iff max_j (sum_{i<=j} held_i + rem_j * j) <= budget over requests
-    sorted by expected remaining tokens, descending (req_queue.py:219-232)."""
-    rq = ReadyQue(64, 100, 50, 1000, 8, 0.8)
-    rq.cache_len_list_ = [[30, 50.0], [10, 20.0]]
+    sorted by expected remaining tokens, descending (req_queue.py:219-232);
+    the expected counts are truncated to integers as the reference's int64
+    array does."""
     new = _req(5, 40)  # idle system: expects 0.6 * 50 = 30 more
+    assert new.forecast(False) == (40, 50 * 0.6)
     # sorted by remaining: (30, 50), (40, 30), (10, 20) -> 30+50*1, 70+30*2, 80+20*3 -> max 140
-    assert rq._can_add_new_req(new, False)
-    rq2 = ReadyQue(64, 100, 50, 139, 8, 0.8)
-    rq2.cache_len_list_ = [[30, 50.0], [10, 20.0]]
-    assert not rq2._can_add_new_req(new, False)
+    rows = [(30, 50.0), (10, 20.0), new.forecast(False)]
+    assert estimate_fits(rows, 140) and not estimate_fits(rows, 139)
+    # truncation: 7 * 0.6 = 4.2 counts as 4 -> (10 + 4) = 14
+    assert estimate_fits([(10, 4.2)], 14) and not estimate_fits([(10, 4.9)], 13)
+    # equal expectations in any order give the same worst prefix
+    a, b = [(5, 10), (30, 10), (1, 3)], [(30, 10), (5, 10), (1, 3)]
+    assert estimate_fits(a, 55) and estimate_fits(b, 55) and not estimate_fits(a, 54)
+    assert not estimate_fits(b, 54)
+    # the waiting room admits in order while the estimate fits and the batch has room
+    room = WaitingRoom(max_reqs=8, max_batch_size=3, kv_budget=140, busy_scale=0.8)
+    live = LiveBatch("live", 140)
+    for r in (_req(0, 30), _req(1, 40), _req(2, 40), _req(3, 10)):
+        assert room.submit(r)
+    fresh = room.admit(live)
+    # 30+30 = 60; (30,30),(40,30): 70+60 = 130; a third (40, 30): 110+90 > 140
+    assert list(fresh.members) == [0, 1] and len(room) == 2
+    assert all(r.status == ReqStatus.RUNNER for r in fresh.members.values())
 
 
 def test_need_tokens_and_end_rule():
     r = _req(1, 10, out=0, max_total=30, max_out=15)
-    assert r.need_tokens(False) == [10, 15 * 0.6] and r.need_tokens(True) == [10, 15]
+    assert r.forecast(False) == (10, 15 * 0.6) and r.forecast(True) == (10, 15)
     r.output_length = 9
-    assert r.need_tokens(False) == [19, 15]  # past 60% of the cap: assume the full cap
+    assert r.forecast(False) == (19, 15)  # past 60% of the cap: assume the full cap
     r = _req(2, 10, max_total=20, max_out=15)
     for k in range(14):
-        r.Add("t", 7)
-        assert not r.is_end  # total reached at 10 outputs, but output cap not yet
-    r.Add("t", 7)
+        assert not r.accept("t", 7)  # total reached at 10 outputs, but output cap not yet
+    assert r.accept("t", 7)
     assert r.is_end and r.output_length == 15
+    assert [r.output_prompt_que.get()[1] for _ in range(15)] == [False] * 14 + [True]
     r = _req(3, 5)
-    r.Add("t", 0)
-    assert r.is_end  # EOS
+    assert r.accept("t", 0) and r.is_end  # EOS
+
+
+def test_swap_out_under_kv_pressure():
+    """A live batch whose next step overruns the budget swaps out requests in
+    the strategy's order until more than the excess is freed; they return to
+    the front of the waiting queue with their tokens folded into the prompt."""
+    live = LiveBatch("b", 100)
+    reqs = [_req(i, n) for i, n in enumerate([30, 20, 40])]
+    for r in reqs:
+        r.is_prefill = False
+        r.output_tokens = [9, 9]
+        live.add(r)
+    live.kv_in_use = 98  # + 3 new tokens -> 1 over
+    assert live.kv_excess() == 1
+    victims = live.swap_out_for_kv()
+    assert [v.id for v in victims] == [1]  # shortest first under LongestFirstStrategy
+    room = WaitingRoom(8, 4, 100, 0.5)
+    room.submit(_req(7, 5))
+    victims[0].park()
+    room.return_swapped(victims[0])
+    assert [r.id for r in room.waiting] == [1, 7] and victims[0].status == ReqStatus.SWAPPED
+    assert victims[0].input_tokens == [1] * 20 + [9, 9] and victims[0].is_prefill
 
 
 def test_swap_selection_strategies():
