@@ -74,9 +74,10 @@ int ll_decode_attention(const void* q, int64_t q_stride_b, int64_t q_stride_h,
  * ll_decode_attention's split stage for this shape and writes, for every
  * workgroup i, the XCD it ran on (hardware register XCC_ID) to out[i].
  * Returns the grid size (> 0) or a negative LL_ERR_* code. The split merge in
- * the same launch assumes out[i] == i % 8 (the XCD that deals the workgroup
- * holds every split of a sequence in its own L2). No reference counterpart:
- * it exists to check that premise on the machine. */
+ * the same launch assumes (out[i] - i) mod 8 is the same for every i of a
+ * launch (round-robin dealing, from whichever XCD the previous launch left
+ * off at), so that every split of a sequence meets in one XCD's L2. No
+ * reference counterpart: it exists to check that premise on the machine. */
 int ll_decode_attention_xcc_probe(int64_t batch, int64_t q_heads, int64_t kv_heads,
                                   int64_t head_dim, int64_t max_len_in_batch, int32_t* out,
                                   int64_t out_len, hipStream_t stream);

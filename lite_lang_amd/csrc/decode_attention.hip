@@ -219,7 +219,9 @@ __device__ __forceinline__ void combine_bh(const DecodeArgs& a, int bh, int lane
   else combine_bh_sb<D, 16>(a, bh, lane, o);
 }
 
-// XCD-aware mapping: the dispatcher deals workgroup i to XCD i mod 8, and
+// XCD-aware mapping: the dispatcher deals the workgroups of a launch to the
+// 8 XCDs round-robin, workgroup i to XCD (i + r) mod 8 for one r per launch
+// (the round-robin continues from the previous launch, so r varies), and
 // every workgroup of one sequence (all its KV heads and splits) is given an
 // index of the same residue, so they all run on one XCD and share its L2.
 __device__ __forceinline__ void map_block(int bid, int KVH, int nsplit, int& b, int& kvh,
@@ -885,7 +887,8 @@ int launch_mfma(DecodeArgs& a, int64_t head_dim, int dtype, bool rope, int64_t m
 }
 
 // The XCD (hardware register XCC_ID) each workgroup runs on, for the premise
-// of the same-launch split merge: workgroup i of a grid runs on XCD i mod 8.
+// of the same-launch split merge: workgroup i of a grid runs on XCD
+// (i + r) mod 8 with one r for the whole launch.
 __global__ void xcc_probe_kernel(int32_t* __restrict__ out, int n) {
   unsigned x;
   asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));

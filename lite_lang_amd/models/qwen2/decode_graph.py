@@ -93,6 +93,7 @@ class DecodeGraph:
             ops.assign_slots(kv_cache.req_to_tokens_, self.meta[0:3], batch_size)
             model.decode_tokens(self.ids, self.meta[3], self.meta[4], self.meta[1], self.meta[0],
                                 kv_cache, max_len, out=self.ids)
+        self.logits = model.last_logits  # the graph's own logits buffer
         torch.cuda.synchronize(dev)
 
     def run(self, in_ids: torch.Tensor, slots, rids, cols, positions, seq_len) -> torch.Tensor:
@@ -111,4 +112,5 @@ class DecodeGraph:
         if in_ids.data_ptr() != self.ids.data_ptr():
             self.ids.copy_(in_ids.view(-1))
         self.graph.replay()
+        self.model.last_logits = self.logits
         return self.ids

@@ -350,6 +350,12 @@ class Qwen2ModelRunner:
         self._graphs = {}
 
     def init_model(self):
+        """Load the weights, allocate the KV pool; returns its size in token
+        slots. A second call returns the same size and changes nothing (the
+        weights a state dict supplied are not kept, so they could not be
+        loaded again)."""
+        if self.kv_cache is not None:
+            return self.kv_cache.kv_max_size_
         if self.state_dict_ is not None:
             sd = self.state_dict_
         elif self.model_path_:

@@ -174,19 +174,35 @@ class Qwen2Oracle:
         return ops.argmax_first(logits), logits
 
     # ------------------------------------------------------------ greedy loop
-    def generate(self, prompts, n_new: int, return_logits: bool = False, feed=None):
+    def generate(self, prompts, n_new: int, return_logits: bool = False, feed=None, prefix=None):
         """Prefill all prompts as one NoPad batch, then n_new-1 decode steps
         (the loop of test/generate_token.py:61-63). Returns [B, n_new] tokens.
 
         feed [B, >= n_new-1] (optional): the tokens appended after each step
         instead of this oracle's own argmax (teacher forcing), so that every
         step is evaluated on the same context as the run that produced them;
-        the returned tokens are still this oracle's argmax at each step."""
+        the returned tokens are still this oracle's argmax at each step.
+
+        prefix (optional): a token list prefilled first as a request of its
+        own; every prompt that extends it then starts from its slots as a
+        shared prefix and prefills only its suffix (prompt-cache prefill,
+        flash_attn_v2.py:699-762), which equals the full causal prefill of the
+        prompt because a prefix token's K/V depend on the prefix alone."""
+        pslots = None
+        if prefix is not None:
+            pre = Req(rid=self.cache.alloc_req(), input_tokens=list(prefix))
+            self.forward([pre], True, list(prefix))
+            pslots = self.cache.req_to_tokens_[pre.rid, :len(prefix)].copy()
         reqs = []
         for p in prompts:
             rid = self.cache.alloc_req()
-            reqs.append(Req(rid=rid, input_tokens=list(p)))
-        ids = [t for p in prompts for t in p]
+            p = list(p)
+            if pslots is not None and len(p) > len(prefix) and p[:len(prefix)] == list(prefix):
+                self.cache.add_refs(rid, pslots)
+                reqs.append(Req(rid=rid, input_tokens=p[len(prefix):], shared_tokens=list(prefix)))
+            else:
+                reqs.append(Req(rid=rid, input_tokens=p))
+        ids = [t for r in reqs for t in r.input_tokens]
         toks, logits = self.forward(reqs, True, ids)
         out, all_logits = [toks], [logits]
         for i in range(n_new - 1):

@@ -102,4 +102,4 @@ def test_scheduler_text_matches_hf(cuda, ckpt):
             ref_ids = ref_ids[: ref_ids.index(EOS) + 1]
         assert r.output_tokens == ref_ids, f"request {r.id}"
         want = ref_tok.decode(ref_ids, skip_special_tokens=True, clean_up_tokenization_spaces=False)
-        assert sch.tokenizer_.decode([r.output_tokens]) == [want]
+        assert sch.tokenizer.decode([r.output_tokens]) == [want]

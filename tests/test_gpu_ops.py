@@ -101,7 +101,7 @@ def test_decode_attention_repeat_calls_are_identical(cuda):
     assert torch.equal(a, b)
     for out, r in ((a, ref), (c, cref), (d, dref), (e, eref)):
         assert _maxdiff(out, r) <= BF16_ATOL
-    ws = _ops()._WS[(0, "decode_attention")]
+    ws = _ops()._WS[_ops()._ws_key(cuda, "decode_attention")]
     assert int(ws[:16384].count_nonzero()) == 0, "split tickets not back at zero"
 
 
