@@ -70,6 +70,30 @@ int ll_decode_attention(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                         int64_t max_len_in_batch, float sm_scale, int dtype, void* workspace,
                         int64_t workspace_bytes, hipStream_t stream);
 
+/* ll_decode_attention without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference.
+ * The split tickets and partials live in a library-owned device array of
+ * ll_decode_attention_noalloc_max_bytes() bytes (4 MiB) that each GPU the
+ * library runs on holds until the process ends; a shape whose partials need
+ * more is rejected with LL_ERR_ARG (use ll_decode_attention with a
+ * workspace). Nothing is allocated. Every call on one GPU shares that GPU's
+ * array: two calls that overlap in time on one GPU (two streams, two threads)
+ * race and give wrong results. The first call on a device looks the array up
+ * and clears its tickets on `stream`; results are identical to
+ * ll_decode_attention's. */
+int64_t ll_decode_attention_noalloc_max_bytes(void);
+int ll_decode_attention_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                const void* k_cache, int64_t k_stride_tok,
+                                int64_t k_stride_head, const void* v_cache,
+                                int64_t v_stride_tok, int64_t v_stride_head,
+                                const int32_t* req_to_tokens, int64_t req_to_tokens_stride,
+                                const void* b_req_idx, int req_idx_i64, const void* b_seq_len,
+                                int seq_len_i64, void* out, int64_t out_stride_b,
+                                int64_t out_stride_h, int64_t batch, int64_t q_heads,
+                                int64_t kv_heads, int64_t head_dim, int64_t max_len_in_batch,
+                                float sm_scale, int dtype, hipStream_t stream);
+
 /* Launches a probe kernel on exactly the grid, block and LDS size of
  * ll_decode_attention's split stage for this shape and writes, for every
  * workgroup i, the XCD it ran on (hardware register XCC_ID) to out[i].

@@ -24,6 +24,10 @@ SIGNATURES = {
     "ll_last_error": (ctypes.c_char_p, []),
     "ll_decode_attention_workspace_size": (I64, [I64, I64, I64, I64, I64]),
     "ll_decode_attention_xcc_probe": (I32, [I64, I64, I64, I64, I64, P, I64, P]),
+    "ll_decode_attention_noalloc_max_bytes": (I64, []),
+    "ll_decode_attention_noalloc": (I32, [P, I64, I64, P, I64, I64, P, I64, I64, P, I64, P, I32,
+                                          P, I32, P, I64, I64, I64, I64, I64, I64, I64, F32, I32,
+                                          P]),
     "ll_decode_attention": (I32, [P, I64, I64, P, I64, I64, P, I64, I64, P, I64, P, I32, P, I32,
                                   P, I64, I64, I64, I64, I64, I64, I64, F32, I32, P, I64, P]),
     "ll_prefill_attention": (I32, [P, I64, I64, P, I64, I64, P, I64, I64, P, I64, I64, P, I64,

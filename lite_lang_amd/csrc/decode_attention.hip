@@ -33,6 +33,8 @@
 // A generic VALU path covers fp32 and head dims other than 64/128.
 #include "ll_common.h"
 
+#include <mutex>
+
 namespace {
 
 constexpr int kTT = 16;     // tokens per tile
@@ -981,6 +983,95 @@ extern "C" int ll_decode_attention(const void* q, int64_t q_stride_b, int64_t q_
 
   return launch_mfma(a, head_dim, dtype, false, max_len_in_batch, workspace, workspace_bytes,
                      stream);
+}
+
+// ---------------------------------------------------------------- no-allocation variant
+// ll_decode_attention_noalloc runs ll_decode_attention with a library-owned
+// scratch buffer in place of the caller's workspace: a file-scope device array
+// that every GPU the library runs on holds until the process ends. In host
+// code `scratch` names a host-side stand-in, not the device array, so the
+// device address is looked up once per device (hipGetSymbolAddress, with that
+// device current) and only that address is ever passed to kernels.
+namespace {
+
+constexpr int64_t kNoAllocScratchBytes = 4 << 20;  // split tickets + partials
+constexpr int kMaxDevices = 64;
+
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Zeroes the split-ticket words (every call leaves them at zero again).
+__global__ void zero_words_kernel(uint32_t* p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+// The device address of this device's scratch array, looked up (and its
+// tickets cleared on `stream`) on the first call on the device.
+int scratch_for_current_device(hipStream_t stream, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    ll_set_error("ll_decode_attention_noalloc: no usable current device (%s)",
+                 hipGetErrorString(e));
+    return LL_ERR_HIP;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      ll_set_error("ll_decode_attention_noalloc: hipGetSymbolAddress(scratch) failed: %s",
+                   hipGetErrorString(e));
+      return LL_ERR_HIP;
+    }
+    const int words = (int)(kTicketBytes / 4);
+    hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0,
+                       stream, (uint32_t*)ptr, words);
+    e = hipGetLastError();
+    if (e != hipSuccess) {
+      ll_set_error("ll_decode_attention_noalloc: clearing the scratch tickets failed: %s",
+                   hipGetErrorString(e));
+      return LL_ERR_HIP;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return LL_OK;
+}
+
+}  // namespace
+
+extern "C" int64_t ll_decode_attention_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
+
+extern "C" int ll_decode_attention_noalloc(
+    const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_cache,
+    int64_t k_stride_tok, int64_t k_stride_head, const void* v_cache, int64_t v_stride_tok,
+    int64_t v_stride_head, const int32_t* req_to_tokens, int64_t req_to_tokens_stride,
+    const void* b_req_idx, int req_idx_i64, const void* b_seq_len, int seq_len_i64, void* out,
+    int64_t out_stride_b, int64_t out_stride_h, int64_t batch, int64_t q_heads, int64_t kv_heads,
+    int64_t head_dim, int64_t max_len_in_batch, float sm_scale, int dtype, hipStream_t stream) {
+  LL_CHECK_ARG(batch >= 0 && kv_heads > 0 && q_heads > 0 && head_dim > 0,
+               "ll_decode_attention_noalloc: bad shape");
+  const int64_t need =
+      batch == 0 ? 0 : workspace_bytes_for(batch, q_heads, kv_heads, head_dim, max_len_in_batch);
+  LL_CHECK_ARG(need <= kNoAllocScratchBytes,
+               "ll_decode_attention_noalloc: this shape needs %lld bytes of split partials, more "
+               "than the %lld-byte scratch; use ll_decode_attention with a workspace",
+               (long long)need, (long long)kNoAllocScratchBytes);
+  void* ws = nullptr;
+  if (need > 0) {
+    const int rc = scratch_for_current_device(stream, &ws);
+    if (rc != LL_OK) return rc;
+  }
+  return ll_decode_attention(q, q_stride_b, q_stride_h, k_cache, k_stride_tok, k_stride_head,
+                             v_cache, v_stride_tok, v_stride_head, req_to_tokens,
+                             req_to_tokens_stride, b_req_idx, req_idx_i64, b_seq_len, seq_len_i64,
+                             out, out_stride_b, out_stride_h, batch, q_heads, kv_heads, head_dim,
+                             max_len_in_batch, sm_scale, dtype, ws, need > 0 ? kNoAllocScratchBytes : 0,
+                             stream);
 }
 
 namespace {
