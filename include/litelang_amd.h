@@ -205,6 +205,55 @@ int ll_assign_slots(int32_t* req_to_tokens, int64_t req_to_tokens_stride, const 
 
 /* ------------------------------------------------------------------- GEMM */
 
+/* Prefill tile GEMMs (256 x 256 output tiles on MFMA, see gemm_tiles.hip).
+ * ll_gemm_tiled: Y[M, N] = T(X[M, K] . W[N, K]^T + bias[N]) in bf16/fp16 with
+ * fp32 accumulation; needs N % 4 == 0, K % 32 == 0 and 16-byte aligned rows.
+ * Replaces torch.addmm / torch.mm of the reference's prefill projections
+ * (transformer_layer.py:80,82,95-109,193); ll_gemm uses it for M > 64.
+ * ll_gemm_tiled_supported returns 1 when ll_gemm_tiled takes the shape. */
+int ll_gemm_tiled_supported(int64_t M, int64_t N, int64_t K, int dtype);
+int ll_gemm_tiled(const void* X, int64_t ldx, const void* W, int64_t ldw, const void* bias,
+                  void* Y, int64_t ldy, int64_t M, int64_t N, int64_t K, int dtype,
+                  hipStream_t stream);
+
+/* Copy of a [gate; up] weight ([2I, K], I % 128 == 0, elem_bytes 2 or 1)
+ * with its rows interleaved in 64-row blocks (gate c..c+63, up c..c+63,
+ * ...), the layout ll_gemm_gate_up_silu_tiled and
+ * ll_gemm_i8_gate_up_silu_tiled read. No reference counterpart (a layout of
+ * the weights load_weights.py:110,160 concatenates). */
+int ll_gemm_interleave_gate_up(const void* W, int64_t ldw, int64_t I, int64_t K,
+                               int64_t elem_bytes, void* out, hipStream_t stream);
+
+/* Y[M, I] = T(up) * T(silu(T(gate))) (the rounding of ll_silu_and_mul) of
+ * gate = X . Wg^T, up = X . Wu^T from the interleaved weight, in one launch:
+ * the prefill gate/up projection and silu_and_mul_fwd
+ * (transformer_layer.py:80-81, silu_and_mul.py:54-78) without the [M, 2I]
+ * intermediate. */
+int ll_gemm_gate_up_silu_tiled(const void* X, int64_t ldx, const void* W_il, int64_t M,
+                               int64_t I, int64_t K, int dtype, void* Y, int64_t ldy,
+                               hipStream_t stream);
+
+/* W8A8 prefill: Y[M, N] = out(fp32(int8(X) . int8(W)^T) * s_tok[m] *
+ * fp32(s_ch[n]) (+ bias[n])), the exact int32 sums dequantised as
+ * ll_dequant_splitk does; out_dtype bf16/fp16 (bias allowed, in that dtype)
+ * or fp32. K % 64 == 0. No reference counterpart (the reference's
+ * SmoothQuant layer, quantize/smooth_quant/layer.py:19-59, has no forward). */
+int ll_gemm_i8_tiled(const int8_t* Xq, int64_t ldx, const float* s_tok, const int8_t* Wq,
+                     int64_t ldw, const void* s_ch, int s_ch_dtype, const void* bias, void* Y,
+                     int64_t ldy, int64_t M, int64_t N, int64_t K, int out_dtype,
+                     hipStream_t stream);
+/* The raw int32 sums of the same product (Y int32 [M, N]). */
+int ll_gemm_i8_i32_tiled(const int8_t* Xq, int64_t ldx, const int8_t* Wq, int64_t ldw,
+                         int32_t* Y, int64_t ldy, int64_t M, int64_t N, int64_t K,
+                         hipStream_t stream);
+/* ll_gemm_gate_up_silu_tiled for the W8A8 runtime: both halves dequantised
+ * as in ll_gemm_i8_tiled (s_ch holds the [gate; up] channel scales in the
+ * original order), then SiLU_and_Mul into Y (bf16/fp16). */
+int ll_gemm_i8_gate_up_silu_tiled(const int8_t* Xq, int64_t ldx, const float* s_tok,
+                                  const int8_t* Wq_il, const void* s_ch, int s_ch_dtype,
+                                  int64_t M, int64_t I, int64_t K, int out_dtype, void* Y,
+                                  int64_t ldy, hipStream_t stream);
+
 /* Y[M, N] = X[M, K] . W[N, K]^T (+ bias[N]) with fp32 accumulation.
  * W is the nn.Linear layout [out, in]. Replaces the torch.addmm / torch.mm /
  * matmul projections of transformer_layer.py:80,82,95-109,193 and the lm_head

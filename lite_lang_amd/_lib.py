@@ -45,6 +45,14 @@ SIGNATURES = {
     "ll_argmax_workspace_size": (I64, [I64, I64]),
     "ll_argmax": (I32, [P, I64, I64, I64, P, P, I64, I32, P]),
     "ll_assign_slots": (I32, [P, I64, P, P, P, I64, P]),
+    "ll_gemm_tiled_supported": (I32, [I64, I64, I64, I32]),
+    "ll_gemm_tiled": (I32, [P, I64, P, I64, P, P, I64, I64, I64, I64, I32, P]),
+    "ll_gemm_interleave_gate_up": (I32, [P, I64, I64, I64, I64, P, P]),
+    "ll_gemm_gate_up_silu_tiled": (I32, [P, I64, P, I64, I64, I64, I32, P, I64, P]),
+    "ll_gemm_i8_tiled": (I32, [P, I64, P, P, I64, P, I32, P, P, I64, I64, I64, I64, I32, P]),
+    "ll_gemm_i8_i32_tiled": (I32, [P, I64, P, I64, P, I64, I64, I64, I64, P]),
+    "ll_gemm_i8_gate_up_silu_tiled": (I32, [P, I64, P, P, P, I32, I64, I64, I64, I32, P, I64,
+                                            P]),
     "ll_gemm_workspace_size": (I64, [I64, I64, I64]),
     "ll_gemm": (I32, [P, I64, P, I64, P, P, I64, I64, I64, I64, I32, P, I64, P]),
     "ll_gemm_splitk_count": (I32, [I64, I64, I64]),

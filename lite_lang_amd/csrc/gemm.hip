@@ -775,6 +775,12 @@ int launch_gemm(const T* X, int64_t ldx, const T* W, int64_t ldw, const T* bias,
     }
     LL_RETURN_LAUNCH();
   }
+  // above 64 rows: the 256 x 256 MFMA tile kernel (gemm_tiles.hip) wherever
+  // its layout constraints hold, else the 128 x 128 kernel below
+  constexpr int dt = sizeof(T) == 2 && !__is_same(T, __bf16) ? LL_F16 : LL_BF16;
+  if (ll_gemm_tiled_supported(M, N, K, dt) && ldy % 4 == 0 && ((uintptr_t)Y) % 8 == 0 &&
+      (ldx * 2) % 16 == 0 && (ldw * 2) % 16 == 0 && (((uintptr_t)X | (uintptr_t)W) % 16) == 0)
+    return ll_gemm_tiled(X, ldx, W, ldw, bias, Y, ldy, M, N, K, dt, stream);
   const dim3 grid((unsigned)ll_cdiv(N, kBN), (unsigned)ll_cdiv(M, kBM));
   hipLaunchKernelGGL((gemm_tiled_kernel<T>), grid, dim3(256), 0, stream, X, ldx, W, ldw, bias, Y,
                      ldy, (int)M, (int)N, (int)K);

@@ -1,0 +1,481 @@
+// Prefill projections (M > 64 rows): Y[M, N] = X[M, K] . W[N, K]^T on MFMA,
+// gfx950. Replaces the torch.addmm / torch.mm products of the reference's
+// prefill (litelang/models/qwen2/layer/transformer_layer.py:80,82,95-109,193)
+// for bf16/fp16, and is the int8 x int8 -> int32 product of the W8A8 runtime
+// (the reference's SmoothQuant module has no forward, quantize/smooth_quant/
+// layer.py:19-59).
+//
+// One workgroup (4 waves, one per SIMD) computes a 256 x 256 output tile:
+//   * stages of 64 bytes of K per row (32 bf16/fp16 or 64 int8) for the
+//     tile's 256 weight rows and 256 activation rows (32 KB) are copied
+//     global -> LDS with global_load_lds_dwordx4 (no VGPR staging) into a
+//     ring of five stage buffers (160 KB), three stages in flight ahead of
+//     the one being multiplied, one barrier per stage, placed between the stage's
+//     two MFMA k-steps so that the operand reads of the next stage overlap
+//     the multiplications of this one;
+//   * the 16-byte chunks of every LDS row are XOR-swizzled (tile_swz) so
+//     the MFMA operand reads (16 rows x 16 B per 16 lanes) hit distinct
+//     banks;
+//   * each wave multiplies a 128 x 128 quarter with v_mfma_f32_32x32x16_bf16
+//     (v_mfma_i32_32x32x32_i8 for int8) as C^T = W . X^T: the weight rows are
+//     the MFMA's row operand, so every lane ends with runs of 4 consecutive
+//     output columns of one token row (8-byte stores) in 16 accumulator
+//     blocks of 32 x 32;
+//   * the grid is XCD-aware: the workgroups the dispatcher deals to one XCD
+//     take a contiguous range of tiles in 4-row-tile groups, so tiles sharing
+//     activation or weight rows run together on one L2.
+// Epilogues: the model dtype with an optional bias; SiLU_and_Mul of a
+// gate/up weight interleaved in 64-row blocks (ll_gemm_interleave_gate_up),
+// with the rounding sequence of ll_silu_and_mul; int8 sums dequantised as
+// fp32(acc) * s_tok[m] * fp32(s_ch[n]) (+ bias) as ll_dequant_splitk does;
+// raw int32 sums.
+#include "ll_common.h"
+
+namespace {
+
+constexpr int kT = 256;        // output tile: 256 activation rows x 256 weight rows
+constexpr int kRB = 64;        // bytes of K per row per stage
+constexpr int kStageB = 2 * kT * kRB;  // 32 KB: weight rows, then activation rows
+constexpr int kNst = 5;        // stage buffers (160 KB of LDS)
+constexpr int kGroupM = 4;     // row tiles per group of the tile order
+
+enum { EPI_STORE = 0, EPI_SILU = 1, EPI_DEQ = 2, EPI_DEQ_SILU = 3, EPI_I32 = 4 };
+
+typedef float f32x16v __attribute__((ext_vector_type(16)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+template <typename T> struct TileOp;
+template <> struct TileOp<__bf16> { typedef bf16x8 V; typedef f32x16v Acc; };
+template <> struct TileOp<_Float16> { typedef f16x8 V; typedef f32x16v Acc; };
+template <> struct TileOp<int8_t> { typedef i32x4 V; typedef i32x16 Acc; };
+
+// 32 x 32 output block, 16 bf16/fp16 (32 int8) of K per instruction: lane l
+// supplies row (or column) l % 32 and the 16-byte K chunk l / 32
+__device__ __forceinline__ f32x16v tile_mma(bf16x8 a, bf16x8 b, f32x16v c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16v tile_mma(f16x8 a, f16x8 b, f32x16v c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ i32x16 tile_mma(i32x4 a, i32x4 b, i32x16 c) {
+  return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+}
+
+// 16 B global -> LDS copy of one lane (lane i lands at lds + 16 i); kept out of
+// the templates (a dependent call of this builtin drops the host launch stub).
+__device__ __forceinline__ void tile_dma16(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0);
+}
+
+template <int N_> __device__ __forceinline__ void tile_vm_wait() {
+  static_assert(N_ >= 0 && N_ < 64, "vmcnt is a 6-bit counter");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N_) : "memory");
+}
+
+// Barrier that waits for this wave's LDS reads only (its own copies were
+// waited for with tile_vm_wait; __syncthreads would also drain the copies of
+// the stages in flight).
+__device__ __forceinline__ void tile_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+struct TileArgs {
+  const char* X; int64_t ldx_b;   // activation rows (K contiguous), row stride in bytes
+  const char* W; int64_t ldw_b;   // weight rows [N][K] (EPI_SILU*: interleaved gate/up)
+  int M, N, K_b;                  // K in bytes
+  int tiles_m, tiles_n;
+  void* Y; int64_t ldy;           // output, row stride in elements of the output type
+  const void* bias;               // [N] in the model dtype, or null
+  const float* s_tok;             // int8: activation scale per row [M]
+  const void* s_ch; int s_ch_dtype;  // int8: weight scale per channel [N]
+};
+
+// Swizzle of the 16-byte chunks of LDS row r (an involution on 0..3): the
+// operand reads of 16 lanes (rows r0..r0+15, one logical chunk) hit 16
+// distinct 16-byte bank groups of a 256-byte bank row, and so do those of
+// every 8 lanes within a 128-byte bank row.
+__device__ __forceinline__ int tile_swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+// LDS byte offset of chunk c (16 B) of tile row r within a stage half
+__device__ __forceinline__ int tile_lds_off(int r, int c) { return r * kRB + ((c ^ tile_swz(r)) << 4); }
+
+template <typename T, typename TO, int EPI>
+__global__ __launch_bounds__(256, 1) void gemm_tile_kernel(TileArgs a) {
+  typedef typename TileOp<T>::V V;
+  typedef typename TileOp<T>::Acc Acc;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+
+  // ---- tile of this workgroup: XCD x (= blockIdx % 8, up to a launch-wide
+  // rotation) takes tiles x * per .. x * per + per - 1 of the grouped order
+  const int tiles = a.tiles_m * a.tiles_n;
+  const int per = (tiles + 7) / 8;
+  const int t = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
+  if (t >= tiles) return;
+  const int gsz = kGroupM * a.tiles_n;
+  const int grp = t / gsz, rin = t - grp * gsz;
+  const int gm = min(kGroupM, a.tiles_m - grp * kGroupM);
+  const int tm = grp * kGroupM + rin % gm, tn = rin / gm;
+  const int m0 = tm * kT, n0 = tn * kT;
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int wn = wave & 1, wm = wave >> 1;
+
+  // ---- copy geometry: instruction u of this wave covers LDS rows
+  // 16 * (4 * wave + u) .. + 15 of the weight half (u < 4) or the
+  // activation half (u >= 4); lane -> row + l/4, LDS chunk l % 4
+  const int crow = lane >> 2;
+  uint32_t soff[8];  // byte offsets of this lane's copy sources (rows clamped into range)
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const int r = 16 * (4 * wave + (u & 3)) + crow;
+    const int gch = (lane & 3) ^ tile_swz(r);
+    if (u < 4) soff[u] = (uint32_t)((int64_t)min(n0 + r, a.N - 1) * a.ldw_b + gch * 16);
+    else soff[u] = (uint32_t)((int64_t)min(m0 + r, a.M - 1) * a.ldx_b + gch * 16);
+  }
+  const int nk = a.K_b / kRB;
+  auto issue = [&](int ks) {
+    char* base = smem + (ks % kNst) * kStageB + wave * 4096;
+    const char* wk = a.W + (int64_t)ks * kRB;
+    const char* xk = a.X + (int64_t)ks * kRB;
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      tile_dma16((u < 4 ? wk : xk) + soff[u], base + (u >> 2) * (kT * kRB) + (u & 3) * 1024);
+  };
+
+  Acc acc[4][4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[p][q][e] = 0;
+
+  // Schedule per stage ks (two MFMA k-steps of 16 bytes per row): the
+  // fragments of k-step 0 were read during the previous stage; k-step 1's
+  // are read while k-step 0 is multiplied; then the barrier publishes stage
+  // ks + 1 (and certifies that every wave has left stage ks - 1, whose
+  // buffer the copy of stage ks + 3 refills) and k-step 0 of stage ks + 1 is
+  // read while k-step 1 of stage ks is multiplied.
+  const int lr = lane & 31, lc = lane >> 5;
+  const int wrow = wn * 128 + lr, xrow = wm * 128 + lr;
+  V w0[4], x0[4], w1[4], x1[4];
+  auto load_k = [&](int ks, int kstep, V (&wf)[4], V (&xf)[4]) {
+    const char* wb = smem + (ks % kNst) * kStageB;
+    const char* xb = wb + kT * kRB;
+    const int c = 2 * kstep + lc;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) wf[p] = *(const V*)(wb + tile_lds_off(wrow + 32 * p, c));
+#pragma unroll
+    for (int q = 0; q < 4; ++q) xf[q] = *(const V*)(xb + tile_lds_off(xrow + 32 * q, c));
+  };
+  // wait until a stage has landed while `younger` later stages stay in flight
+  auto wait_stage = [&](int younger) {
+    if (younger >= 3) tile_vm_wait<24>();
+    else if (younger == 2) tile_vm_wait<16>();
+    else if (younger == 1) tile_vm_wait<8>();
+    else tile_vm_wait<0>();
+  };
+  static_assert(kNst >= 3 && kNst <= 5, "stage ring of 3 to 5 buffers");
+#pragma unroll
+  for (int st = 0; st < kNst - 1; ++st)
+    if (st < nk) issue(st);
+  wait_stage(min(kNst - 2, nk - 1));
+  tile_barrier();
+  load_k(0, 0, w0, x0);
+  // Per k-step the 16 MFMAs are issued in program order with one memory
+  // instruction after each of the first 8 (k-step 0: the reads of k-step 1;
+  // k-step 1: the stage copies, then the reads of the next stage's k-step 0
+  // after the next 8), and sched_barrier keeps that order: the wave issues
+  // its memory work while the MFMA pipe is busy instead of draining it.
+  const int c0 = lc, c1 = 2 + lc;  // LDS chunks of k-step 0 and 1 for this lane
+  auto frag_w = [&](int ks, int c, int p) {
+    return *(const V*)(smem + (ks % kNst) * kStageB + tile_lds_off(wrow + 32 * p, c));
+  };
+  auto frag_x = [&](int ks, int c, int q) {
+    return *(const V*)(smem + (ks % kNst) * kStageB + kT * kRB + tile_lds_off(xrow + 32 * q, c));
+  };
+  for (int ks = 0; ks < nk; ++ks) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      acc[i >> 2][i & 3] = tile_mma(w0[i >> 2], x0[i & 3], acc[i >> 2][i & 3]);
+      if (i < 4) w1[i] = frag_w(ks, c1, i);
+      else if (i < 8) x1[i - 4] = frag_x(ks, c1, i - 4);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    const bool more = ks + 1 < nk;
+    if (more) {
+      // stage ks + 1 landed; stages up to ks + kNst - 2 may stay in flight
+      wait_stage(min(kNst - 3, nk - 2 - ks));
+      tile_barrier();
+    }
+    const bool refill = ks + kNst - 1 < nk;  // into the buffer of stage ks - 1
+    char* rbase = smem + ((ks + kNst - 1) % kNst) * kStageB + wave * 4096;
+    const char* wk = a.W + (int64_t)(ks + kNst - 1) * kRB;
+    const char* xk = a.X + (int64_t)(ks + kNst - 1) * kRB;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      acc[i >> 2][i & 3] = tile_mma(w1[i >> 2], x1[i & 3], acc[i >> 2][i & 3]);
+      if (i < 8) {
+        if (refill)
+          tile_dma16((i < 4 ? wk : xk) + soff[i], rbase + (i >> 2) * (kT * kRB) + (i & 3) * 1024);
+      } else if (more) {
+        if (i < 12) w0[i - 8] = frag_w(ks + 1, c0, i - 8);
+        else x0[i - 12] = frag_x(ks + 1, c0, i - 12);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  // ---- epilogue: acc[p][q][4g + i] = C[m][n] with
+  //   m = m0 + wm*128 + 32q + l % 32,  n = n0 + wn*128 + 32p + 8g + 4(l / 32) + i
+  const int mrow = m0 + wm * 128 + lr;
+  if constexpr (EPI == EPI_STORE || EPI == EPI_DEQ || EPI == EPI_I32) {
+    const int ncol = n0 + wn * 128 + 4 * lc;
+    float st[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      st[q] = 1.f;
+      if constexpr (EPI == EPI_DEQ) st[q] = a.s_tok[min(mrow + 32 * q, a.M - 1)];
+    }
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int n = ncol + 32 * p + 8 * g;
+        if (n >= a.N) continue;
+        float sch[4], bv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          sch[i] = 1.f;
+          bv[i] = 0.f;
+          if constexpr (EPI == EPI_DEQ) sch[i] = ll_load_scale(a.s_ch, a.s_ch_dtype, n + i);
+          if constexpr (EPI != EPI_I32) {
+            if (a.bias != nullptr) bv[i] = ll_to_f32(((const TO*)a.bias)[n + i]);
+          }
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int m = mrow + 32 * q;
+          if (m >= a.M) continue;
+          TO o[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            if constexpr (EPI == EPI_I32) {
+              o[i] = (TO)acc[p][q][4 * g + i];
+            } else if constexpr (EPI == EPI_DEQ) {
+              // the product is rounded before the bias is added (no fused
+              // multiply-add), as in ll_dequant_splitk followed by the add
+              float v = (float)acc[p][q][4 * g + i] * st[q] * sch[i];
+              asm volatile("" : "+v"(v));
+              if (a.bias != nullptr) v += bv[i];
+              o[i] = ll_from_f32<TO>(v);
+            } else {
+              o[i] = ll_from_f32<TO>(acc[p][q][4 * g + i] + bv[i]);
+            }
+          }
+          typedef TO V4 __attribute__((ext_vector_type(4)));
+          *(V4*)((TO*)a.Y + (int64_t)m * a.ldy + n) = (V4){o[0], o[1], o[2], o[3]};
+        }
+      }
+  } else {
+    // gate/up interleaved in 64-row blocks: this wave's rows 0..63 (p < 2)
+    // are gate channels c, rows 64..127 (p >= 2) the up channels c, with
+    // c = n0 / 2 + wn * 64 + 32 (p % 2) + 8g + 4(l / 32) + i; N = 2 I
+    const int I = a.N / 2;
+    const int cbase = n0 / 2 + wn * 64 + 4 * lc;
+    float st[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      st[q] = 1.f;
+      if constexpr (EPI == EPI_DEQ_SILU) st[q] = a.s_tok[min(mrow + 32 * q, a.M - 1)];
+    }
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int c = cbase + 32 * p + 8 * g;
+        if (c >= I) continue;
+        float sg[4], su[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          sg[i] = su[i] = 1.f;
+          if constexpr (EPI == EPI_DEQ_SILU) {
+            sg[i] = ll_load_scale(a.s_ch, a.s_ch_dtype, c + i);
+            su[i] = ll_load_scale(a.s_ch, a.s_ch_dtype, I + c + i);
+          }
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int m = mrow + 32 * q;
+          if (m >= a.M) continue;
+          TO o[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            float gs, us;
+            if constexpr (EPI == EPI_DEQ_SILU) {
+              gs = (float)acc[p][q][4 * g + i] * st[q] * sg[i];
+              us = (float)acc[p + 2][q][4 * g + i] * st[q] * su[i];
+            } else {
+              gs = acc[p][q][4 * g + i];
+              us = acc[p + 2][q][4 * g + i];
+            }
+            const float gv = ll_to_f32(ll_from_f32<TO>(gs));
+            const float u = ll_to_f32(ll_from_f32<TO>(us));
+            const TO sv = ll_from_f32<TO>(gv / (1.0f + __expf(-gv)));
+            o[i] = ll_from_f32<TO>(u * ll_to_f32(sv));
+          }
+          typedef TO V4 __attribute__((ext_vector_type(4)));
+          *(V4*)((TO*)a.Y + (int64_t)m * a.ldy + c) = (V4){o[0], o[1], o[2], o[3]};
+        }
+      }
+  }
+}
+
+// Interleave a [gate; up] weight ([2I, K], I % 128 == 0) into 64-row blocks:
+// out row R of tile R / 256: block (R % 256) / 64 alternates gate and up rows
+// of channels (R / 256) * 128 + ((R % 256) / 128) * 64 + R % 64.
+__global__ void interleave_gate_up_kernel(const u32x4* __restrict__ W, int64_t ldw16,
+                                          u32x4* __restrict__ out, int64_t row16, int I,
+                                          int64_t total) {
+  const int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (u >= total) return;
+  const int64_t R = u / row16, c = u - R * row16;
+  const int64_t t = R / 256, r = R % 256;
+  const int64_t blk = r / 64, ch = t * 128 + (blk / 2) * 64 + (r % 64);
+  const int64_t src = (blk % 2 == 0) ? ch : I + ch;
+  out[u] = W[src * ldw16 + c];
+}
+
+template <typename T, typename TO, int EPI>
+int launch_tiles(const TileArgs& a0, hipStream_t stream) {
+  TileArgs a = a0;
+  a.tiles_m = ll_cdiv(a.M, kT);
+  a.tiles_n = ll_cdiv(a.N, kT);
+  const int tiles = a.tiles_m * a.tiles_n;
+  const int grid = 8 * ((tiles + 7) / 8);
+  hipLaunchKernelGGL((gemm_tile_kernel<T, TO, EPI>), dim3((unsigned)grid), dim3(256),
+                     (size_t)kNst * kStageB, stream, a);
+  LL_RETURN_LAUNCH();
+}
+
+int check_tile_args(const char* name, const void* X, int64_t ldx, const void* W, int64_t ldw,
+                    const void* Y, int64_t M, int64_t N, int64_t K_b, int64_t es) {
+  LL_CHECK_ARG(X && W && Y, "%s: null pointer", name);
+  LL_CHECK_ARG(M > 0 && N > 0 && N % 4 == 0 && K_b > 0 && K_b % kRB == 0,
+               "%s: needs M > 0, N %% 4 == 0 and K a multiple of %lld (M=%lld N=%lld K=%lld)", name,
+               (long long)(kRB / es), (long long)M, (long long)N, (long long)(K_b / es));
+  LL_CHECK_ARG((ldx * es) % 16 == 0 && (ldw * es) % 16 == 0 &&
+                   (((uintptr_t)X | (uintptr_t)W) % 16) == 0,
+               "%s: X and W rows must be 16 B aligned", name);
+  LL_CHECK_ARG(M <= INT32_MAX && N <= INT32_MAX && K_b <= INT32_MAX, "%s: shape too large", name);
+  return LL_OK;
+}
+
+TileArgs make_args(const void* X, int64_t ldx_b, const void* W, int64_t ldw_b, int64_t M,
+                   int64_t N, int64_t K_b, void* Y, int64_t ldy) {
+  TileArgs a = {};
+  a.X = (const char*)X; a.ldx_b = ldx_b;
+  a.W = (const char*)W; a.ldw_b = ldw_b;
+  a.M = (int)M; a.N = (int)N; a.K_b = (int)K_b;
+  a.Y = Y; a.ldy = ldy;
+  return a;
+}
+
+}  // namespace
+
+extern "C" int ll_gemm_tiled_supported(int64_t M, int64_t N, int64_t K, int dtype) {
+  if (dtype != LL_BF16 && dtype != LL_F16) return 0;
+  return M > 0 && N > 0 && N % 4 == 0 && K > 0 && (K * 2) % kRB == 0;
+}
+
+extern "C" int ll_gemm_tiled(const void* X, int64_t ldx, const void* W, int64_t ldw,
+                             const void* bias, void* Y, int64_t ldy, int64_t M, int64_t N,
+                             int64_t K, int dtype, hipStream_t stream) {
+  LL_CHECK_ARG(dtype == LL_BF16 || dtype == LL_F16, "ll_gemm_tiled: bf16 or fp16 only");
+  const int rc = check_tile_args("ll_gemm_tiled", X, ldx, W, ldw, Y, M, N, K * 2, 2);
+  if (rc != LL_OK) return rc;
+  LL_CHECK_ARG(ldy % 4 == 0 && ((uintptr_t)Y) % 8 == 0, "ll_gemm_tiled: Y rows must be 8 B aligned");
+  TileArgs a = make_args(X, ldx * 2, W, ldw * 2, M, N, K * 2, Y, ldy);
+  a.bias = bias;
+  if (dtype == LL_BF16) return launch_tiles<__bf16, __bf16, EPI_STORE>(a, stream);
+  return launch_tiles<_Float16, _Float16, EPI_STORE>(a, stream);
+}
+
+extern "C" int ll_gemm_interleave_gate_up(const void* W, int64_t ldw, int64_t I, int64_t K,
+                                          int64_t elem_bytes, void* out, hipStream_t stream) {
+  LL_CHECK_ARG(W && out, "ll_gemm_interleave_gate_up: null pointer");
+  LL_CHECK_ARG(I > 0 && I % 128 == 0 && K > 0 && (K * elem_bytes) % 16 == 0 &&
+                   (ldw * elem_bytes) % 16 == 0 && (elem_bytes == 1 || elem_bytes == 2),
+               "ll_gemm_interleave_gate_up: needs I %% 128 == 0 and 16 B rows");
+  const int64_t row16 = K * elem_bytes / 16, total = 2 * I * row16;
+  hipLaunchKernelGGL(interleave_gate_up_kernel, dim3((unsigned)ll_cdiv(total, 256)), dim3(256), 0,
+                     stream, (const u32x4*)W, ldw * elem_bytes / 16, (u32x4*)out, row16, (int)I,
+                     total);
+  LL_RETURN_LAUNCH();
+}
+
+extern "C" int ll_gemm_gate_up_silu_tiled(const void* X, int64_t ldx, const void* W_il,
+                                          int64_t M, int64_t I, int64_t K, int dtype, void* Y,
+                                          int64_t ldy, hipStream_t stream) {
+  LL_CHECK_ARG(dtype == LL_BF16 || dtype == LL_F16, "ll_gemm_gate_up_silu_tiled: bf16 or fp16 only");
+  LL_CHECK_ARG(I % 128 == 0, "ll_gemm_gate_up_silu_tiled: I must be a multiple of 128");
+  const int rc = check_tile_args("ll_gemm_gate_up_silu_tiled", X, ldx, W_il, K, Y, M, 2 * I, K * 2, 2);
+  if (rc != LL_OK) return rc;
+  LL_CHECK_ARG(ldy % 4 == 0 && ((uintptr_t)Y) % 8 == 0,
+               "ll_gemm_gate_up_silu_tiled: Y rows must be 8 B aligned");
+  TileArgs a = make_args(X, ldx * 2, W_il, K * 2, M, 2 * I, K * 2, Y, ldy);
+  if (dtype == LL_BF16) return launch_tiles<__bf16, __bf16, EPI_SILU>(a, stream);
+  return launch_tiles<_Float16, _Float16, EPI_SILU>(a, stream);
+}
+
+extern "C" int ll_gemm_i8_tiled(const int8_t* Xq, int64_t ldx, const float* s_tok,
+                                const int8_t* Wq, int64_t ldw, const void* s_ch, int s_ch_dtype,
+                                const void* bias, void* Y, int64_t ldy, int64_t M, int64_t N,
+                                int64_t K, int out_dtype, hipStream_t stream) {
+  const int rc = check_tile_args("ll_gemm_i8_tiled", Xq, ldx, Wq, ldw, Y, M, N, K, 1);
+  if (rc != LL_OK) return rc;
+  LL_CHECK_ARG(out_dtype == LL_BF16 || out_dtype == LL_F16 || out_dtype == LL_F32,
+               "ll_gemm_i8_tiled: bad output dtype %d", out_dtype);
+  LL_CHECK_ARG(s_tok && s_ch && (s_ch_dtype == LL_F32 || s_ch_dtype == LL_F16 ||
+                                 s_ch_dtype == LL_BF16),
+               "ll_gemm_i8_tiled: needs s_tok and s_ch (fp32/fp16/bf16)");
+  LL_CHECK_ARG(bias == nullptr || out_dtype != LL_F32,
+               "ll_gemm_i8_tiled: a bias needs a 16-bit output dtype");
+  LL_CHECK_ARG(ldy % 4 == 0 && ((uintptr_t)Y) % 16 == 0, "ll_gemm_i8_tiled: Y rows must be 16 B aligned");
+  TileArgs a = make_args(Xq, ldx, Wq, ldw, M, N, K, Y, ldy);
+  a.bias = bias; a.s_tok = s_tok; a.s_ch = s_ch; a.s_ch_dtype = s_ch_dtype;
+  if (out_dtype == LL_BF16) return launch_tiles<int8_t, __bf16, EPI_DEQ>(a, stream);
+  if (out_dtype == LL_F16) return launch_tiles<int8_t, _Float16, EPI_DEQ>(a, stream);
+  return launch_tiles<int8_t, float, EPI_DEQ>(a, stream);
+}
+
+extern "C" int ll_gemm_i8_i32_tiled(const int8_t* Xq, int64_t ldx, const int8_t* Wq, int64_t ldw,
+                                    int32_t* Y, int64_t ldy, int64_t M, int64_t N, int64_t K,
+                                    hipStream_t stream) {
+  const int rc = check_tile_args("ll_gemm_i8_i32_tiled", Xq, ldx, Wq, ldw, Y, M, N, K, 1);
+  if (rc != LL_OK) return rc;
+  LL_CHECK_ARG(ldy % 4 == 0 && ((uintptr_t)Y) % 16 == 0,
+               "ll_gemm_i8_i32_tiled: Y rows must be 16 B aligned");
+  TileArgs a = make_args(Xq, ldx, Wq, ldw, M, N, K, Y, ldy);
+  return launch_tiles<int8_t, int32_t, EPI_I32>(a, stream);
+}
+
+extern "C" int ll_gemm_i8_gate_up_silu_tiled(const int8_t* Xq, int64_t ldx, const float* s_tok,
+                                             const int8_t* Wq_il, const void* s_ch,
+                                             int s_ch_dtype, int64_t M, int64_t I, int64_t K,
+                                             int out_dtype, void* Y, int64_t ldy,
+                                             hipStream_t stream) {
+  LL_CHECK_ARG(I % 128 == 0, "ll_gemm_i8_gate_up_silu_tiled: I must be a multiple of 128");
+  const int rc = check_tile_args("ll_gemm_i8_gate_up_silu_tiled", Xq, ldx, Wq_il, K, Y, M, 2 * I,
+                                 K, 1);
+  if (rc != LL_OK) return rc;
+  LL_CHECK_ARG(out_dtype == LL_BF16 || out_dtype == LL_F16,
+               "ll_gemm_i8_gate_up_silu_tiled: bf16 or fp16 output");
+  LL_CHECK_ARG(s_tok && s_ch && (s_ch_dtype == LL_F32 || s_ch_dtype == LL_F16 ||
+                                 s_ch_dtype == LL_BF16),
+               "ll_gemm_i8_gate_up_silu_tiled: needs s_tok and s_ch (fp32/fp16/bf16)");
+  LL_CHECK_ARG(ldy % 4 == 0 && ((uintptr_t)Y) % 8 == 0,
+               "ll_gemm_i8_gate_up_silu_tiled: Y rows must be 8 B aligned");
+  TileArgs a = make_args(Xq, ldx, Wq_il, K, M, 2 * I, K, Y, ldy);
+  a.s_tok = s_tok; a.s_ch = s_ch; a.s_ch_dtype = s_ch_dtype;
+  if (out_dtype == LL_BF16) return launch_tiles<int8_t, __bf16, EPI_DEQ_SILU>(a, stream);
+  return launch_tiles<int8_t, _Float16, EPI_DEQ_SILU>(a, stream);
+}

@@ -288,6 +288,104 @@ def gemm(x, w, bias=None, out=None):
     return out
 
 
+def gemm_tiled(x, w, bias=None, out=None):
+    """out[M, N] = x @ w^T (+ bias) on the 256 x 256 MFMA tile kernel (prefill)."""
+    _dev(x, w, bias, out)
+    M, K = x.shape
+    N = w.shape[0]
+    assert w.shape[1] == K and x.stride(1) == 1 and w.stride(1) == 1 and x.dtype == w.dtype
+    if out is None:
+        out = torch.empty((M, N), dtype=x.dtype, device=x.device)
+    assert out.shape == (M, N) and out.stride(1) == 1
+    rc = _L.ll_gemm_tiled(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0),
+                          bias.data_ptr() if bias is not None else None, out.data_ptr(),
+                          out.stride(0), M, N, K, dtype_code(x), _stream(x))
+    _lib.check(rc, "ll_gemm_tiled")
+    return out
+
+
+def gemm_tiled_supported(M, N, K, dtype) -> bool:
+    return dtype in (torch.bfloat16, torch.float16) and bool(
+        _L.ll_gemm_tiled_supported(M, N, K, _DTYPES[dtype]))
+
+
+def interleave_gate_up(w):
+    """[gate; up] weight [2I, K] (16-bit or int8) -> the 64-row interleaved copy
+    the fused gate/up + SiLU tile kernels read, or None when I % 128 != 0."""
+    _dev(w)
+    N2, K = w.shape
+    I = N2 // 2
+    es = w.element_size()
+    if N2 % 2 or I % 128 or (K * es) % 16 or w.stride(1) != 1:
+        return None
+    out = torch.empty_like(w, memory_format=torch.contiguous_format)
+    rc = _L.ll_gemm_interleave_gate_up(w.data_ptr(), w.stride(0), I, K, es, out.data_ptr(),
+                                       _stream(w))
+    _lib.check(rc, "ll_gemm_interleave_gate_up")
+    return out
+
+
+def gate_up_silu_tiled(x, w_il, out=None):
+    """silu(x @ gate^T) * (x @ up^T) from the interleaved weight (prefill)."""
+    _dev(x, w_il, out)
+    M, K = x.shape
+    I = w_il.shape[0] // 2
+    assert w_il.shape[1] == K and x.stride(1) == 1 and x.dtype == w_il.dtype
+    if out is None:
+        out = torch.empty((M, I), dtype=x.dtype, device=x.device)
+    assert out.shape == (M, I) and out.stride(1) == 1
+    rc = _L.ll_gemm_gate_up_silu_tiled(x.data_ptr(), x.stride(0), w_il.data_ptr(), M, I, K,
+                                       dtype_code(x), out.data_ptr(), out.stride(0), _stream(x))
+    _lib.check(rc, "ll_gemm_gate_up_silu_tiled")
+    return out
+
+
+def gemm_i8_tiled(xq, s_tok, wq, s_ch, bias=None, out_dtype=torch.bfloat16, out=None):
+    """dequantised W8A8 product out[M, N] (prefill tile kernel)."""
+    _dev(xq, s_tok, wq, s_ch, bias, out)
+    M, K = xq.shape
+    N = wq.shape[0]
+    assert wq.shape[1] == K and xq.dtype == torch.int8 and wq.dtype == torch.int8
+    assert s_tok.dtype == torch.float32 and s_ch.numel() == N
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype, device=xq.device)
+    rc = _L.ll_gemm_i8_tiled(xq.data_ptr(), xq.stride(0), s_tok.data_ptr(), wq.data_ptr(),
+                             wq.stride(0), s_ch.data_ptr(), dtype_code(s_ch),
+                             bias.data_ptr() if bias is not None else None, out.data_ptr(),
+                             out.stride(0), M, N, K, dtype_code(out), _stream(xq))
+    _lib.check(rc, "ll_gemm_i8_tiled")
+    return out
+
+
+def gemm_i8_i32_tiled(xq, wq, out=None):
+    """exact int32 sums int8(x) @ int8(w)^T on the prefill tile kernel."""
+    _dev(xq, wq, out)
+    M, K = xq.shape
+    N = wq.shape[0]
+    assert wq.shape[1] == K and xq.dtype == torch.int8 and wq.dtype == torch.int8
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.int32, device=xq.device)
+    rc = _L.ll_gemm_i8_i32_tiled(xq.data_ptr(), xq.stride(0), wq.data_ptr(), wq.stride(0),
+                                 out.data_ptr(), out.stride(0), M, N, K, _stream(xq))
+    _lib.check(rc, "ll_gemm_i8_i32_tiled")
+    return out
+
+
+def gemm_i8_gate_up_silu_tiled(xq, s_tok, wq_il, s_ch, out_dtype=torch.bfloat16, out=None):
+    """W8A8 gate/up + SiLU_and_Mul from the interleaved int8 weight (prefill)."""
+    _dev(xq, s_tok, wq_il, s_ch, out)
+    M, K = xq.shape
+    I = wq_il.shape[0] // 2
+    if out is None:
+        out = torch.empty((M, I), dtype=out_dtype, device=xq.device)
+    rc = _L.ll_gemm_i8_gate_up_silu_tiled(xq.data_ptr(), xq.stride(0), s_tok.data_ptr(),
+                                          wq_il.data_ptr(), s_ch.data_ptr(), dtype_code(s_ch),
+                                          M, I, K, dtype_code(out), out.data_ptr(), out.stride(0),
+                                          _stream(xq))
+    _lib.check(rc, "ll_gemm_i8_gate_up_silu_tiled")
+    return out
+
+
 # ------------------------------------------------------------------ slot table
 def assign_slots(req_to_tokens, packed, n):
     """req_to_tokens[rows, cols] = slots with packed = int32 [3, n] (slots, rows, cols)."""
