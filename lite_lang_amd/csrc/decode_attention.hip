@@ -282,8 +282,8 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
   const int j = lane >> 4;  // lane group
 
   // Q^T as the B operand: column n = head kvh*G + n, k-slots = d 32*s + 8*j + 0..7.
-  // Loaded first (it does not depend on the lengths); columns n >= G read a
-  // valid head and are zeroed once the loads have landed.
+  // Loaded first (it does not depend on the lengths); columns n >= G read
+  // head G - 1.
   V8 qb[DS];
   T* s_q = (T*)(smem + TG::MAIN_B + (size_t)a.slots_cap * 4);  // ROPE: [G][D] rotated q
   T* s_kv = s_q + a.G * D;                                     // ROPE: new token's K, V
@@ -323,28 +323,52 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
   const int64_t tok0 = (int64_t)tb * kTT;
   const int ntok = (int)(min(len, (int64_t)te * kTT) - tok0);  // tokens of this split (may be 0)
 
-  // slot ids of the split -> LDS (tail entries point at slot 0, masked later);
-  // four loads per thread in flight per round, the first round's issued
-  // before the RoPE jobs
-  const int nslots = (te - tb) * kTT;
-  auto load_slots = [&](int i0, int32_t (&v)[4]) {
+  const char* kbase = (const char*)((const T*)a.k + (int64_t)kvh * a.k_sh);
+  const char* vbase = (const char*)((const T*)a.v + (int64_t)kvh * a.v_sh);
+  const int64_t kst = a.k_st * (int64_t)sizeof(T), vst = a.v_st * (int64_t)sizeof(T);
+  char* ring = smem + wave * kRing * TG::TILE_B;
+  const int nw = (te - tb - wave + kWaves - 1) / kWaves;  // tiles of this wave (may be <= 0)
+
+  // slot ids of this wave's tiles (wave, wave + kWaves, ... of the split) ->
+  // LDS, up to 16 tiles per round with every load of a round in flight
+  // together; tail entries point at slot 0 (masked later). Only this wave reads them
+  // (K/V copy addresses, the writer's patch test), and a wave's LDS accesses
+  // are ordered, so no barrier stands between the slot loads and the wave's
+  // first K/V copies.
+  for (int r0 = 0; 4 * r0 < nw; r0 += 4) {  // rounds of 16 tiles, loads in flight together
+    int32_t sl[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int i = i0 + u * kWaves * 64 + threadIdx.x;
+      const int i = (wave + kWaves * (4 * (r0 + u) + (lane >> 4))) * kTT + (lane & 15);
       const int64_t t = min(tok0 + i, len > 0 ? len - 1 : (int64_t)0);  // always a valid entry
-      const int32_t sl = slot_row[t];
-      v[u] = (i < ntok) ? sl : 0;
+      sl[u] = slot_row[t];
     }
-  };
-  auto store_slots = [&](int i0, const int32_t (&v)[4]) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int i = i0 + u * kWaves * 64 + threadIdx.x;
-      if (i < nslots) s_slots[i] = v[u];
+      const int tw = wave + kWaves * (4 * (r0 + u) + (lane >> 4));  // tile within the split
+      const int i = tw * kTT + (lane & 15);                         // token within the split
+      if (tw < te - tb) s_slots[i] = (i < ntok) ? sl[u] : 0;
+    }
+  }
+
+  // DMA lane geometry: lane -> (row within an instruction's rows, LDS chunk position)
+  const int dr = lane / TG::CH, dp = lane % TG::CH;
+  auto issue = [&](int k) {
+    const int t0 = (wave + k * kWaves) * kTT;  // token offset of the tile within the split
+    char* buf = ring + (k % kRing) * TG::TILE_B;
+#pragma unroll
+    for (int i = 0; i < TG::IPT; ++i) {
+      const int r = i * TG::RPI + dr;
+      const int64_t slot = s_slots[t0 + r];
+      const int c = TG::swz(dp, r);
+      dma16(kbase + slot * kst + c * 16, buf + i * 1024);
+      dma16(vbase + slot * vst + c * 16, buf + kTT * TG::ROWB + i * 1024);
     }
   };
-  int32_t v0[4];
-  load_slots(0, v0);
+  // the first tiles' copies go out before the RoPE jobs and the q barrier
+#pragma unroll
+  for (int k = 0; k < kRing - 1; ++k)
+    if (k < nw) issue(k);
 
   // ROPE: q of the group's heads into LDS; the split holding the last tile
   // (split 0 for an empty sequence) also writes the new token's K and V (the
@@ -369,45 +393,13 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
       rope_job<T, D>(a, b, qkv_row, (a.H + (isv ? a.KVH : 0) + kvh) * D, i, cs, sn,
                      !isv, s_kv + (isv ? D : 0), glb);
     }
-  }
-  store_slots(0, v0);
-  for (int i0 = 4 * kWaves * 64; i0 < nslots; i0 += 4 * kWaves * 64) {
-    int32_t v[4];
-    load_slots(i0, v);
-    store_slots(i0, v);
-  }
-  if constexpr (ROPE) {
-    __syncthreads();  // s_q, s_kv and the slot table are complete
+    __syncthreads();  // s_q and s_kv are complete
     const T* qs = s_q + min(n, a.G - 1) * D;
 #pragma unroll
     for (int s = 0; s < DS; ++s) qb[s] = *(const V8*)(qs + 32 * s + 8 * j);
   }
-  if (n >= a.G) {
-#pragma unroll
-    for (int s = 0; s < DS; ++s)
-      for (int e = 0; e < 8; ++e) qb[s][e] = (T)0.f;
-  }
-  if constexpr (!ROPE) __syncthreads();
-
-  const char* kbase = (const char*)((const T*)a.k + (int64_t)kvh * a.k_sh);
-  const char* vbase = (const char*)((const T*)a.v + (int64_t)kvh * a.v_sh);
-  const int64_t kst = a.k_st * (int64_t)sizeof(T), vst = a.v_st * (int64_t)sizeof(T);
-  char* ring = smem + wave * kRing * TG::TILE_B;
-  const int nw = (te - tb - wave + kWaves - 1) / kWaves;  // tiles of this wave (may be <= 0)
-  // DMA lane geometry: lane -> (row within an instruction's rows, LDS chunk position)
-  const int dr = lane / TG::CH, dp = lane % TG::CH;
-  auto issue = [&](int k) {
-    const int t0 = (wave + k * kWaves) * kTT;  // token offset of the tile within the split
-    char* buf = ring + (k % kRing) * TG::TILE_B;
-#pragma unroll
-    for (int i = 0; i < TG::IPT; ++i) {
-      const int r = i * TG::RPI + dr;
-      const int64_t slot = s_slots[t0 + r];
-      const int c = TG::swz(dp, r);
-      dma16(kbase + slot * kst + c * 16, buf + i * 1024);
-      dma16(vbase + slot * vst + c * 16, buf + kTT * TG::ROWB + i * 1024);
-    }
-  };
+  // (columns n >= G hold a copy of head G - 1: their scores and sums are
+  // finite and their outputs are never stored)
 
   f32x4 acc[DB];
 #pragma unroll
@@ -415,9 +407,6 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
   float m_run = -INFINITY;  // running max of head n (log2 domain)
   float l_run = 0.f;        // this lane's share of the running sum
 
-#pragma unroll
-  for (int k = 0; k < kRing - 1; ++k)
-    if (k < nw) issue(k);
   for (int k = 0; k < nw; ++k) {
     if (k + kRing - 1 < nw) {
       issue(k + kRing - 1);
