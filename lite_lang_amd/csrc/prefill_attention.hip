@@ -8,32 +8,42 @@
 //   litelang/kernel/develop_flash_attn/flash_attn_v2.py:569-762 (prompt cache)
 // including the rounding of the probabilities to the KV dtype before P.V.
 //
-// Design: one workgroup = 4 waves = 64 query rows of one head; every wave owns
-// 16 rows. Per 32-key tile the workgroup stages K and V in LDS once (16 B per
-// lane, rows fetched through the slot table) and each wave computes
-// S^T = K . Q^T and O^T += V^T . P^T on bf16/fp16 MFMA (v_mfma_f32_16x16x32),
-// the same operand arrangement as the decode kernel with query rows in place
-// of query heads. Online softmax in the exp2 domain, fp32 state.
+// Design: one workgroup = 8 waves of 32 query rows, two per SIMD (so that one
+// wave's softmax overlaps the other's MFMAs, with the register budget of two
+// waves). WPH waves take query rows row0 .. row0 + 32 WPH - 1 of one head and
+// the workgroup takes 8 / WPH heads of one KV head (WPH = 2 when the group
+// size is a multiple of 4, else 4), so every K/V tile staged in LDS serves 256
+// query rows. Per 64-key tile:
+//   * K and V rows are loaded through the slot table into registers while the
+//     previous tile is computed, then stored to LDS: K with its 16-byte chunks
+//     XOR-swizzled by row so that the MFMA operand reads are bank-conflict
+//     free, V transposed (4 keys x 8 d per thread) as V^T [d][key], the keys
+//     of every 16-key group permuted so that the 8 keys one MFMA lane needs
+//     form one 16-byte chunk (no copy into LDS is in flight while the tile is
+//     computed, so its LDS reads wait for no global load);
+//   * each wave computes S^T = K . Q^T (2 key blocks of 32, Q^T fragments in
+//     registers, v_mfma_f32_32x32x16), the online softmax in the exp2 domain
+//     with fp32 state, and O^T += V^T . P^T with P rounded to the KV dtype;
+//     the reference max is raised (and the output rows rescaled) only when a
+//     probability would exceed 2^8, outside the inner loop;
+//   * two LDS stages, one barrier per tile.
+#include <type_traits>
+
 #include "ll_common.h"
 
 namespace {
 
-constexpr int kTile = 32;
-constexpr int kWaves = 4;
-constexpr int kRowsPerWave = 16;
-constexpr int kBlockM = kWaves * kRowsPerWave;  // 64 query rows per workgroup
-constexpr int kKStride = 136;  // K tile row stride (elements), 16 B aligned
-constexpr int kVStride = 136;  // V tile row stride, conflict-free transposed reads
+constexpr int kBK = 64;   // keys per tile
 
 template <typename T> struct Vec8;
 template <> struct Vec8<__bf16> { typedef bf16x8 type; };
 template <> struct Vec8<_Float16> { typedef f16x8 type; };
 
-__device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
-__device__ __forceinline__ f32x4 mfma16x16x32(f16x8 a, f16x8 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+__device__ __forceinline__ f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
 struct PrefillArgs {
@@ -52,170 +62,335 @@ struct PrefillArgs {
   float sm_scale;
 };
 
-template <typename T, int D>
-__global__ __launch_bounds__(kWaves * 64) void prefill_attn_mfma_kernel(PrefillArgs a) {
-  typedef typename Vec8<T>::type V8;
-  constexpr int DS = D / 32;
-  constexpr int DB = D / 16;
-  __shared__ __attribute__((aligned(16))) T ks[2][kTile * kKStride];
-  __shared__ __attribute__((aligned(16))) T vs[2][kTile * kVStride];
+template <int D> struct FaGeom {
+  static constexpr int ROWB = D * 2;            // bytes of a K row
+  static constexpr int CH = ROWB / 16;          // 16 B chunks per K row
+  static constexpr int VTB = kBK * 2;           // bytes of a V^T row
+  static constexpr int K_B = kBK * ROWB;        // K tile
+  static constexpr int STAGE_B = K_B + D * VTB; // K tile, then V^T
+  static constexpr int VDG = D / 8;             // 8-wide d groups of a V row
+  // LDS chunk position of K chunk c of row r (an involution): the operand
+  // reads of 16 lanes (16 rows, one chunk) hit 16 distinct 16 B bank slots
+  static __device__ __forceinline__ int kswz(int c, int r) {
+    return ROWB == 256 ? (c ^ (r & 15)) : (c ^ ((r >> 1) & 7));
+  }
+  // V^T row d: chunk c of the (permuted) key positions. Rows are 128 B: the
+  // reads of 8 lanes (rows d..d+7, one chunk) hit 8 distinct chunks of a
+  // 128 B bank row, and those of 16 lanes 16 distinct slots of 256 B.
+  static __device__ __forceinline__ int vswz(int c, int d) { return c ^ (d & 7) ^ ((d >> 3) & 1); }
+};
 
-  // 1-D grid, XCD-aware: workgroups go round-robin over the 8 XCDs, so the G
-  // query heads of one (row block, request, KV head) unit take consecutive
+// position of tile key k in a V^T row: within each 16-key group, keys
+// 0-3, 8-11 | 4-7, 12-15, so MFMA lane half h reads keys 4h..4h+3 and
+// 8+4h..8+4h+3 of the group as one 16-byte chunk
+__device__ __forceinline__ int vt_pos(int k) {
+  const int k16 = k & 15;
+  return (k & ~15) | (((k16 >> 2) & 1) << 3) | (((k16 >> 3) & 1) << 2) | (k16 & 3);
+}
+
+// WPH: waves (of 32 query rows each) per head; the 8 waves of a workgroup
+// take 8 / WPH heads of one KV head and 32 * WPH query rows of each
+template <int WPH_> struct FaShape {
+  static constexpr int WPH = WPH_;
+  static constexpr int NW = 8;           // waves per workgroup (two per SIMD)
+  static constexpr int HPW = NW / WPH;   // heads per workgroup
+  static constexpr int RW = 32;          // query rows per wave
+  static constexpr int BQ = WPH * RW;    // query rows of one head per workgroup
+};
+
+template <typename T, int D, int WPH>
+__global__ __launch_bounds__(512) void prefill_attn_fa_kernel(PrefillArgs a) {
+  typedef typename Vec8<T>::type V8;
+  typedef FaGeom<D> FG;
+  typedef FaShape<WPH> SH;
+  constexpr int QB = 1;  // 32-row query blocks per wave
+  constexpr int DS = D / 16;  // k-steps of S^T = K . Q^T
+  constexpr int DB = D / 32;  // 32-row d blocks of O^T
+  constexpr int NT = 64 * SH::NW;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+
+  // 1-D grid, XCD-aware: workgroups go round-robin over the 8 XCDs, so the
+  // head groups of one (row block, request, KV head) unit take consecutive
   // slots of the same XCD and read its K/V tiles through one L2; the longest
   // (last) row blocks are dispatched first
+  const int HP = (a.G + SH::HPW - 1) / SH::HPW;  // head groups per KV head
   const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
-  const int unit = (slot / a.G) * 8 + xcd;
+  const int unit = (slot / HP) * 8 + xcd;
   if (unit >= a.nblk * a.B * a.KVH) return;
+  const int hp = slot % HP;
   const int kvh = unit % a.KVH;
   const int b = (unit / a.KVH) % a.B;
   const int mblk = a.nblk - 1 - unit / (a.KVH * a.B);
-  const int h = kvh * a.G + slot % a.G;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int n = lane & 15;
-  const int j = lane >> 4;
+  const int l32 = lane & 31, hf = lane >> 5;
+  const int gh = SH::HPW * hp + wave / SH::WPH;  // head within the KV head's group
+  const bool head_ok = gh < a.G;
+  const int h = kvh * a.G + (head_ok ? gh : 0);
 
   const int64_t L = ll_load_idx(a.seq_len, b, a.len64);
   const int64_t S = a.shared ? ll_load_idx(a.shared, b, a.shared64) : 0;
   const int64_t qlen = L - S;
-  const int64_t row0 = (int64_t)mblk * kBlockM;
-  if (row0 >= qlen) return;
+  const int64_t blk0 = (int64_t)mblk * SH::BQ;
+  if (blk0 >= qlen) return;
   const int64_t start = ll_load_idx(a.start_loc, b, a.start64);
   const int64_t rid = ll_load_idx(a.req_idx, b, a.req64);
   const int32_t* slot_row = a.r2t + rid * a.r2t_s;
+  // token indices within a request fit in 32 bits (lengths below 2^31)
+  const int row0 = (int)blk0 + SH::RW * (wave % SH::WPH);  // this wave's first query row
+  const bool wave_ok = head_ok && row0 < qlen;
+  const int kv_end = (int)min(L, blk0 + SH::BQ + S);     // keys of the workgroup
+  const int wave_kv_end = (int)min(L, (int64_t)row0 + SH::RW + S);  // keys of this wave's rows
+  const int Si = (int)S, Lm1 = (int)L - 1, qlast = (int)qlen - 1;
 
-  // this wave's 16 query rows: m = row0 + 16*wave + n (column n of S^T)
-  const int64_t m_row = row0 + kRowsPerWave * wave + n;
-  const bool row_ok = m_row < qlen;
-  V8 qb[DS];
+  // Q^T fragments (B operand: column = query row row0 + l32, clamped into the
+  // request; k-slots = d 16 s + 8 hf .. +7), in registers for the whole loop
+  V8 qreg[DS];
   {
-    const T* qp = (const T*)a.q + (start + (row_ok ? m_row : 0)) * a.q_st + (int64_t)h * a.q_sh;
+    const int r = min(row0 + l32, qlast);
+    const T* qp = (const T*)a.q + (start + r) * a.q_st + (int64_t)h * a.q_sh + 8 * hf;
 #pragma unroll
-    for (int s = 0; s < DS; ++s) {
-      if (row_ok) qb[s] = *(const V8*)(qp + 32 * s + 8 * j);
-      else for (int e = 0; e < 8; ++e) qb[s][e] = (T)0.f;
-    }
+    for (int s = 0; s < DS; ++s) qreg[s] = *(const V8*)(qp + 16 * s);
   }
-  // keys needed by the workgroup: [0, min(L, row0 + 64 + S))
-  const int64_t kv_end = min(L, row0 + kBlockM + S);
-  // keys needed by this wave's rows: [0, min(L, row0 + 16*wave + 16 + S))
-  const int64_t wave_kv_end = min(L, row0 + kRowsPerWave * (wave + 1) + S);
 
-  f32x4 acc[DB];
-#pragma unroll
-  for (int c = 0; c < DB; ++c) acc[c] = (f32x4){0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY, l_run = 0.f;
+  // K and V tiles are staged through registers (global loads, then LDS
+  // stores after the current tile's compute): with no copy into LDS in
+  // flight, the compute's LDS reads need no wait on the global loads.
   const T* kbase = (const T*)a.k + (int64_t)kvh * a.k_sh;
   const T* vbase = (const T*)a.v + (int64_t)kvh * a.v_sh;
-  constexpr int VCH = D / 8;
-  constexpr int ROWS_PER_PASS = (kWaves * 64) / VCH;
-
-  // Software pipeline over the 32-key tiles: the K/V rows of tile t+1 and the
-  // slot ids of tile t+2 are in flight (registers) while tile t is computed
-  // from one of two LDS buffers; one barrier per tile. Loads use clamped
-  // addresses (always a valid key) and rows past kv_end are zeroed on the
-  // LDS store.
-  constexpr int PASSES = (kTile + ROWS_PER_PASS - 1) / ROWS_PER_PASS;
-  const int ch = threadIdx.x % VCH, rr = threadIdx.x / VCH;
-  int32_t sl_cur[PASSES], sl_nxt[PASSES];
-  V8 kreg[PASSES], vreg[PASSES];
-  auto load_slots = [&](int64_t t0, int32_t (&s)[PASSES]) {
+  // K geometry: thread -> rows kr + KRS u (u < KR), 16-byte chunk kc; the
+  // lanes of one row write its whole LDS row (a permutation of the chunks)
+  constexpr int KR = kBK * FG::CH / NT;  // K chunks per thread per tile
+  constexpr int KRS = NT / FG::CH;       // rows covered per pass
+  const int kc = threadIdx.x % FG::CH, kr = threadIdx.x / FG::CH;
+  // V geometry: thread -> 4 keys x 8 d, the 16 key groups of a tile over
+  // consecutive lanes (so the 16 lanes writing one V^T row cover its 128 bytes
+  // once); threads past 16 * VDG idle
+  const int vkg = threadIdx.x & 15, vdg = threadIdx.x >> 4;
+  const bool v_on = vdg < FG::VDG;
+  int32_t ksl[KR], vsl[4];  // slot ids of the next tile's K rows / V rows
+  auto load_slots = [&](int t0) {
 #pragma unroll
-    for (int p = 0; p < PASSES; ++p)
-      s[p] = slot_row[min(t0 + p * ROWS_PER_PASS + rr, kv_end - 1)];
-  };
-  auto load_kv = [&](const int32_t (&s)[PASSES]) {
+    for (int u = 0; u < KR; ++u) ksl[u] = slot_row[min(t0 + kr + KRS * u, kv_end - 1)];
+    if (v_on) {
 #pragma unroll
-    for (int p = 0; p < PASSES; ++p) {
-      kreg[p] = *(const V8*)(kbase + (int64_t)s[p] * a.k_st + ch * 8);
-      vreg[p] = *(const V8*)(vbase + (int64_t)s[p] * a.v_st + ch * 8);
+      for (int i = 0; i < 4; ++i) vsl[i] = slot_row[min(t0 + 4 * vkg + i, kv_end - 1)];
     }
   };
-  load_slots(0, sl_cur);
-  load_kv(sl_cur);
-  load_slots(kTile, sl_nxt);
-  for (int64_t t0 = 0; t0 < kv_end; t0 += kTile) {
-    const int buf = (int)((t0 / kTile) & 1);
-    T* ksb = ks[buf];
-    T* vsb = vs[buf];
-    // this tile's rows into LDS (the buffer was last read two tiles ago,
-    // before the previous barrier)
+  V8 kreg[KR], vreg[4];
+  auto issue = [&]() {  // global loads of the tile whose slots are in ksl/vsl
 #pragma unroll
-    for (int p = 0; p < PASSES; ++p) {
-      const int r = p * ROWS_PER_PASS + rr;
-      if (r < kTile) {
-        const bool ok = t0 + r < kv_end;
-        V8 kv = kreg[p], vv = vreg[p];
-        if (!ok)
-          for (int e = 0; e < 8; ++e) { kv[e] = (T)0.f; vv[e] = (T)0.f; }
-        *(V8*)(ksb + r * kKStride + ch * 8) = kv;
-        *(V8*)(vsb + r * kVStride + ch * 8) = vv;
-      }
-    }
-    __syncthreads();
-    if (t0 + kTile < kv_end) {
-      load_kv(sl_nxt);
-      load_slots(t0 + 2 * kTile, sl_nxt);
-    }
-    if (t0 >= wave_kv_end) continue;  // every row of this wave is causally done
-
-    f32x4 sA = {0.f, 0.f, 0.f, 0.f}, sB = {0.f, 0.f, 0.f, 0.f};
+    for (int u = 0; u < KR; ++u) kreg[u] = *(const V8*)(kbase + (int64_t)ksl[u] * a.k_st + 8 * kc);
+    if (v_on) {
 #pragma unroll
-    for (int s = 0; s < DS; ++s) {
-      const V8 ka = *(const V8*)(ksb + n * kKStride + 32 * s + 8 * j);
-      const V8 kb = *(const V8*)(ksb + (16 + n) * kKStride + 32 * s + 8 * j);
-      sA = mfma16x16x32(ka, qb[s], sA);
-      sB = mfma16x16x32(kb, qb[s], sB);
+      for (int i = 0; i < 4; ++i) vreg[i] = *(const V8*)(vbase + (int64_t)vsl[i] * a.v_st + 8 * vdg);
     }
-    // causal + length mask: key t0+4j+i (A) / t0+16+4j+i (B) vs query row m_row
-    const int64_t lim = min(m_row + S, L - 1);  // last key this row may see
-    float x[8];
+  };
+  auto store = [&](int buf) {  // the loaded rows into LDS: K swizzled, V transposed
+    char* kl = smem + buf * FG::STAGE_B;
+#pragma unroll
+    for (int u = 0; u < KR; ++u) {
+      const int r = kr + KRS * u;
+      *(V8*)(kl + r * FG::ROWB + FG::kswz(kc, r) * 16) = kreg[u];
+    }
+    if (!v_on) return;
+    char* vt = kl + FG::K_B;
+    const int pk = vt_pos(4 * vkg);  // positions pk .. pk+3 (one 8-byte half chunk)
+    uint32_t w[4][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      x[i] = (t0 + 4 * j + i <= lim) ? sA[i] * a.scale_log2 : -INFINITY;
-      x[4 + i] = (t0 + 16 + 4 * j + i <= lim) ? sB[i] * a.scale_log2 : -INFINITY;
+      const u32x4 u = __builtin_bit_cast(u32x4, vreg[i]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) w[i][e] = u[e];
     }
-    float tmax = x[0];
 #pragma unroll
-    for (int i = 1; i < 8; ++i) tmax = fmaxf(tmax, x[i]);
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const float m_new = fmaxf(m_run, tmax);
-    // m_new is finite: key 0 is visible to every row and tiles run in order
-    const float alpha = exp2f(m_run - m_new);
-    V8 pb;
-    float psum = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float p = exp2f(x[i] - m_new);
-      psum += p;
-      pb[i] = (T)p;
+    for (int dd = 0; dd < 8; ++dd) {
+      const int d = 8 * vdg + dd;
+      const int e = dd >> 1, sh = (dd & 1) * 16;
+      const uint32_t lo = ((w[0][e] >> sh) & 0xffffu) | (((w[1][e] >> sh) & 0xffffu) << 16);
+      const uint32_t hi = ((w[2][e] >> sh) & 0xffffu) | (((w[3][e] >> sh) & 0xffffu) << 16);
+      typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+      *(u32x2*)(vt + d * FG::VTB + FG::vswz(pk >> 3, d) * 16 + (pk & 7) * 2) = (u32x2){lo, hi};
     }
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
+  };
+
+  f32x16 acc[DB][QB];
 #pragma unroll
-    for (int c = 0; c < DB; ++c) {
-      acc[c] *= alpha;
-      V8 va;
-      const T* col = vsb + 16 * c + n;
+  for (int db = 0; db < DB; ++db)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        va[i] = col[(4 * j + i) * kVStride];
-        va[4 + i] = col[(16 + 4 * j + i) * kVStride];
-      }
-      acc[c] = mfma16x16x32(va, pb, acc[c]);
-    }
+    for (int qb = 0; qb < QB; ++qb) acc[db][qb] = (f32x16){};
+  float m_run[QB], l_run[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    m_run[qb] = -INFINITY;
+    l_run[qb] = 0.f;
   }
-  l_run += __shfl_xor(l_run, 16, 64);
-  l_run += __shfl_xor(l_run, 32, 64);
-  if (!row_ok) return;
-  T* op = (T*)a.o + (start + m_row) * a.o_st + (int64_t)h * a.o_sh;
-  const float inv = 1.0f / l_run;
+
+  // tile 0 into stage 0; the slot ids of tile 1 are loaded behind it
+  load_slots(0);
+  issue();
+  store(0);
+  if (kBK < kv_end) load_slots(kBK);
+  __syncthreads();
+
+  // S^T[key 32 kb + 8 g + 4 hf + i][query 32 qb + l32] of the current tile in
+  // sacc[kb][qb][4 g + i]; the row maxima it proposes in m_cand
+  f32x16 sacc[2][QB];
+  float m_cand[QB];
+  auto scores = [&](int t0, int buf) {
+    const char* kl = smem + buf * FG::STAGE_B;
 #pragma unroll
-  for (int c = 0; c < DB; ++c)
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) op[16 * c + 4 * j + i] = ll_from_f32<T>(acc[c][i] * inv);
+      for (int qb = 0; qb < QB; ++qb) sacc[kb][qb] = (f32x16){};
+#pragma unroll
+    for (int s = 0; s < DS; ++s) {
+      V8 qf[QB], ka[2];
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        const int r = 32 * x + l32;
+        ka[x] = *(const V8*)(kl + r * FG::ROWB + FG::kswz(2 * s + hf, r) * 16);
+      }
+      qf[0] = qreg[s];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) sacc[kb][qb] = mfma32(ka[kb], qf[qb], sacc[kb][qb]);
+    }
+    // the causal + length mask only where a key can pass the wave's first
+    // row's limit (masked keys -> -inf), then the tile's row maxima in the
+    // exp2 domain (finite: key 0 is visible to every row, scale_log2 > 0)
+    const bool need_mask = t0 + kBK - 1 > min(row0 + Si, Lm1);
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      if (need_mask) {
+        // last key this row sees, relative to the tile (rows past the
+        // request see every key of it)
+        const int lim = min(row0 + 32 * qb + l32 + Si, Lm1) - t0;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int key = 32 * kb + 8 * (e >> 2) + 4 * hf + (e & 3);
+            if (key > lim) sacc[kb][qb][e] = -INFINITY;
+          }
+      }
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) tmax = fmaxf(tmax, sacc[kb][qb][e]);
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      m_cand[qb] = fmaxf(m_run[qb], tmax * a.scale_log2);
+    }
+  };
+  // p = 2^(s * scale_log2 - m_run) rounded to T as the P^T fragments of the 4
+  // key steps (step s = keys 16 s + {4hf..4hf+3, 8+4hf..8+4hf+3}: S^T block
+  // kb = s / 2, g = 2 (s % 2) and g + 1), the row sums into l_run, then
+  // O^T[d 32 db + 8 g + 4 hf + i][query 32 qb + l32] += V^T . P^T
+  auto accumulate = [&](int buf) {
+    const char* vt = smem + buf * FG::STAGE_B + FG::K_B;
+    V8 pf[QB][4];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      float psum = 0.f;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int kb = s >> 1, e0 = 8 * (s & 1);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float p = __builtin_amdgcn_exp2f(
+              __builtin_fmaf(sacc[kb][qb][e0 + e], a.scale_log2, -m_run[qb]));
+          psum += p;
+          pf[qb][s][e] = (T)p;
+        }
+      }
+      psum += __shfl_xor(psum, 32, 64);
+      l_run[qb] += psum;
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const int d = 32 * db + l32;
+        const V8 va = *(const V8*)(vt + d * FG::VTB + FG::vswz(2 * s + hf, d) * 16);
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) acc[db][qb] = mfma32(va, pf[qb][s], acc[db][qb]);
+      }
+  };
+
+  // The reference max m_run of the exponentials is raised only on the first
+  // tile and when some row of a query block would otherwise see a
+  // probability above 2^8 (p <= 2^8 is rounded to T at the same relative
+  // precision). Raising it rescales the output rows, which leaves the inner
+  // loop (with the tile's scores kept): inside it the accumulators are only
+  // touched by MFMAs and stay in the accumulation registers.
+  int t0 = 0, buf = 0;
+  bool issued = false;  // the next tile's loads went out before leaving the inner loop
+  for (;;) {
+    bool raise = false;
+    for (; t0 < kv_end; t0 += kBK, buf ^= 1) {
+      const bool has_next = t0 + kBK < kv_end;
+      if (has_next && !issued) {
+        issue();
+        if (t0 + 2 * kBK < kv_end) load_slots(t0 + 2 * kBK);
+      }
+      issued = false;
+      if (wave_ok && t0 < wave_kv_end) {
+        scores(t0, buf);
+        bool up = false;
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) up = up || m_cand[qb] > m_run[qb] + 8.f;
+        if (t0 == 0) {
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) m_run[qb] = m_cand[qb];  // acc and l_run are zero
+        } else if (__builtin_amdgcn_ballot_w64(up)) {
+          raise = true;
+          issued = has_next;
+          break;
+        }
+        accumulate(buf);
+      }
+      if (has_next) store(buf ^ 1);
+      // the next tile's K rows and V^T rows are in LDS, every wave is done
+      // reading this tile's stage
+      __syncthreads();
+    }
+    if (!raise) break;
+    // raise the reference maxima, rescale, and finish tile t0
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - m_cand[qb]);
+      m_run[qb] = m_cand[qb];
+      l_run[qb] *= alpha;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) acc[db][qb] *= alpha;
+    }
+    accumulate(buf);
+    if (t0 + kBK < kv_end) store(buf ^ 1);
+    __syncthreads();
+    t0 += kBK;
+    buf ^= 1;
+  }
+  if (!wave_ok) return;
+  // acc[db][qb][4 g + i] = O^T[d = 32 db + 8 g + 4 hf + i][query row0 + 32 qb + l32]
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    const int r = row0 + 32 * qb + l32;
+    if (r > qlast) continue;
+    const float inv = 1.0f / l_run[qb];
+    T* op = (T*)a.o + (start + r) * a.o_st + (int64_t)h * a.o_sh + 4 * hf;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        typedef T T4 __attribute__((ext_vector_type(4)));
+        T4 y;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) y[i] = ll_from_f32<T>(acc[db][qb][4 * g + i] * inv);
+        *(T4*)(op + 32 * db + 8 * g) = y;
+      }
+  }
 }
 
 // Generic path: one wave per (query row, head), keys spread over the lanes.
@@ -332,21 +507,28 @@ extern "C" int ll_prefill_attention(const void* q, int64_t q_stride_tok, int64_t
       LL_RETURN_LAUNCH();
     });
   }
-  a.nblk = (int)ll_cdiv(max_input_len, kBlockM);
+  // four heads of 64 rows per workgroup when the group size allows, else two
+  // heads of 128 rows (fewer idle head slots for G = 6 or 7)
+  const int wph = (a.G % 4 == 0) ? 2 : 4;
+  a.nblk = (int)ll_cdiv(max_input_len, 32 * wph);
   a.B = (int)batch;
   a.KVH = (int)kv_heads;
   const int64_t units = (int64_t)a.nblk * batch * kv_heads;
-  const dim3 grid((unsigned)(ll_cdiv(units, 8) * 8 * a.G));
+  const dim3 grid((unsigned)(ll_cdiv(units, 8) * 8 * ll_cdiv(a.G, 8 / wph)));
+  const dim3 block(512);
+  auto launch = [&](auto tag, auto dtag) {
+    typedef decltype(tag) T;
+    constexpr int D = decltype(dtag)::value;
+    constexpr size_t lds = 2 * FaGeom<D>::STAGE_B;
+    if (wph == 2) hipLaunchKernelGGL((prefill_attn_fa_kernel<T, D, 2>), grid, block, lds, stream, a);
+    else hipLaunchKernelGGL((prefill_attn_fa_kernel<T, D, 4>), grid, block, lds, stream, a);
+  };
+  typedef std::integral_constant<int, 128> D128;
+  typedef std::integral_constant<int, 64> D64;
   if (dtype == LL_BF16) {
-    if (head_dim == 128)
-      hipLaunchKernelGGL((prefill_attn_mfma_kernel<__bf16, 128>), grid, dim3(kWaves * 64), 0, stream, a);
-    else
-      hipLaunchKernelGGL((prefill_attn_mfma_kernel<__bf16, 64>), grid, dim3(kWaves * 64), 0, stream, a);
+    if (head_dim == 128) launch(__bf16{}, D128{}); else launch(__bf16{}, D64{});
   } else {
-    if (head_dim == 128)
-      hipLaunchKernelGGL((prefill_attn_mfma_kernel<_Float16, 128>), grid, dim3(kWaves * 64), 0, stream, a);
-    else
-      hipLaunchKernelGGL((prefill_attn_mfma_kernel<_Float16, 64>), grid, dim3(kWaves * 64), 0, stream, a);
+    if (head_dim == 128) launch(_Float16{}, D128{}); else launch(_Float16{}, D64{});
   }
   LL_RETURN_LAUNCH();
 }

@@ -170,6 +170,16 @@ def test_prefill_attention_varlen(cuda, dtype, H, KVH, D):
     assert _maxdiff(out, ref) <= _tol(dtype)
 
 
+@pytest.mark.parametrize("H,KVH,lens,shared", [
+    (28, 4, [600, 129, 1, 257], [0, 0, 0, 0]),     # odd group (7 q heads per KV head)
+    (12, 2, [700, 333, 64], [0, 0, 0]),           # 1.5B geometry, several 128-row blocks
+    (16, 2, [650, 400, 90], [520, 17, 89])])      # long cached prefixes, one-row query
+def test_prefill_attention_long_and_odd_groups(cuda, H, KVH, lens, shared):
+    print(f"case: prefill H={H} KVH={KVH} lens={lens} shared={shared}", flush=True)
+    out, ref = _prefill_case(cuda, H, KVH, 128, lens, shared, torch.bfloat16, 12)
+    assert _maxdiff(out, ref) <= _tol(torch.bfloat16)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_prefill_attention_prompt_cache(cuda, dtype):
     # shapes of test_context_attention_with_kv_cache_and_prompt_cache
