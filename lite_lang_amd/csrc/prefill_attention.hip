@@ -24,8 +24,6 @@
 //   * each wave computes S^T = K . Q^T (2 key blocks of 32, Q^T fragments in
 //     registers, v_mfma_f32_32x32x16), the online softmax in the exp2 domain
 //     with fp32 state, and O^T += V^T . P^T with P rounded to the KV dtype;
-//     the reference max is raised (and the output rows rescaled) only when a
-//     probability would exceed 2^8, outside the inner loop;
 //   * two LDS stages, one barrier per tile.
 #include <type_traits>
 
@@ -319,58 +317,33 @@ __global__ __launch_bounds__(512) void prefill_attn_fa_kernel(PrefillArgs a) {
       }
   };
 
-  // The reference max m_run of the exponentials is raised only on the first
-  // tile and when some row of a query block would otherwise see a
-  // probability above 2^8 (p <= 2^8 is rounded to T at the same relative
-  // precision). Raising it rescales the output rows, which leaves the inner
-  // loop (with the tile's scores kept): inside it the accumulators are only
-  // touched by MFMAs and stay in the accumulation registers.
-  int t0 = 0, buf = 0;
-  bool issued = false;  // the next tile's loads went out before leaving the inner loop
-  for (;;) {
-    bool raise = false;
-    for (; t0 < kv_end; t0 += kBK, buf ^= 1) {
-      const bool has_next = t0 + kBK < kv_end;
-      if (has_next && !issued) {
-        issue();
-        if (t0 + 2 * kBK < kv_end) load_slots(t0 + 2 * kBK);
-      }
-      issued = false;
-      if (wave_ok && t0 < wave_kv_end) {
-        scores(t0, buf);
-        bool up = false;
+  int buf = 0;
+  for (int t0 = 0; t0 < kv_end; t0 += kBK, buf ^= 1) {
+    const bool has_next = t0 + kBK < kv_end;
+    if (has_next) {
+      issue();
+      if (t0 + 2 * kBK < kv_end) load_slots(t0 + 2 * kBK);
+    }
+    if (wave_ok && t0 < wave_kv_end) {
+      scores(t0, buf);
+      // running maxima; the output rows are rescaled when a row's max rises
+      // (every lane of a block skips the multiply when none does)
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb) up = up || m_cand[qb] > m_run[qb] + 8.f;
-        if (t0 == 0) {
+      for (int qb = 0; qb < QB; ++qb) {
+        const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - m_cand[qb]);
+        m_run[qb] = m_cand[qb];
+        l_run[qb] *= alpha;
+        if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
 #pragma unroll
-          for (int qb = 0; qb < QB; ++qb) m_run[qb] = m_cand[qb];  // acc and l_run are zero
-        } else if (__builtin_amdgcn_ballot_w64(up)) {
-          raise = true;
-          issued = has_next;
-          break;
+          for (int db = 0; db < DB; ++db) acc[db][qb] *= alpha;
         }
-        accumulate(buf);
       }
-      if (has_next) store(buf ^ 1);
-      // the next tile's K rows and V^T rows are in LDS, every wave is done
-      // reading this tile's stage
-      __syncthreads();
+      accumulate(buf);
     }
-    if (!raise) break;
-    // raise the reference maxima, rescale, and finish tile t0
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-      const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - m_cand[qb]);
-      m_run[qb] = m_cand[qb];
-      l_run[qb] *= alpha;
-#pragma unroll
-      for (int db = 0; db < DB; ++db) acc[db][qb] *= alpha;
-    }
-    accumulate(buf);
-    if (t0 + kBK < kv_end) store(buf ^ 1);
+    if (has_next) store(buf ^ 1);
+    // the next tile's K rows and V^T rows are in LDS, every wave is done
+    // reading this tile's stage
     __syncthreads();
-    t0 += kBK;
-    buf ^= 1;
   }
   if (!wave_ok) return;
   // acc[db][qb][4 g + i] = O^T[d = 32 db + 8 g + 4 hf + i][query row0 + 32 qb + l32]

@@ -180,6 +180,42 @@ def test_prefill_attention_long_and_odd_groups(cuda, H, KVH, lens, shared):
     assert _maxdiff(out, ref) <= _tol(torch.bfloat16)
 
 
+@pytest.mark.parametrize("H,KVH", [(16, 2), (12, 2)])
+def test_prefill_attention_growing_scores(cuda, H, KVH):
+    """Keys scaled up tile after tile, so the running maxima jump by far more
+    than 2^8 in the exp2 domain at several tiles (the kernel's rescale path),
+    with rows that also see a prompt-cache prefix."""
+    g = torch.Generator().manual_seed(13)
+    lens, shared = [700, 300, 64], [100, 0, 0]
+    B = len(lens)
+    qlens = [l - s for l, s in zip(lens, shared)]
+    starts = np.concatenate([[0], np.cumsum(qlens)[:-1]]).tolist()
+    P = sum(lens) + 5
+    q = torch.randn(sum(qlens), H, 128, generator=g).bfloat16()
+    pool = torch.randn(P, 2 * KVH, 128, generator=g)
+    r2t = torch.zeros(B, max(lens), dtype=torch.int32)
+    o = 0
+    for b in range(B):
+        r2t[b, :lens[b]] = torch.arange(o, o + lens[b], dtype=torch.int32)
+        # key j of the request (tile j // 64) scaled by 1 + 2 (j // 64)
+        pool[o:o + lens[b], :KVH] *= (1 + 2 * (torch.arange(lens[b]) // 64)).float()[:, None, None]
+        o += lens[b]
+    pool = pool.bfloat16()
+    rids = list(range(B))
+    ref = O.prefill_attention(q, pool[:, :KVH], pool[:, KVH:], rids, starts, lens, r2t,
+                              b_shared_seq_len=shared, p_dtype=torch.bfloat16)
+    pd = pool.to(cuda)
+    out = torch.empty_like(q, device=cuda)
+    print(f"case: prefill growing scores H={H} KVH={KVH}", flush=True)
+    _ops().prefill_attention(q.to(cuda), pd[:, :KVH], pd[:, KVH:], out,
+                             torch.tensor(rids, dtype=torch.int32, device=cuda),
+                             torch.tensor(starts, dtype=torch.int64, device=cuda),
+                             torch.tensor(lens, dtype=torch.int64, device=cuda), max(lens),
+                             r2t.to(cuda), b_shared_seq_len=torch.tensor(shared, device=cuda))
+    torch.cuda.synchronize()
+    assert _maxdiff(out, ref) <= _tol(torch.bfloat16)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_prefill_attention_prompt_cache(cuda, dtype):
     # shapes of test_context_attention_with_kv_cache_and_prompt_cache

@@ -4,13 +4,12 @@ weight_scale, static quant_scale on o_proj/down_proj, pytorch_model.bin)
 loaded through model_path -- the runner detects the int8 checkpoint and runs
 its W8A8 runtime -- against the CPU oracle reading the same files.
 
-Bars as for the W8A8 runtime on float checkpoints: fp32 storage gives the
-oracle's greedy tokens exactly (the int32 products are exact and the
-dequantisation is evaluated in the same fp32 order); fp16 storage, the
-checkpoint's own dtype, is held to max-abs 4e-2 on the logits of a prefill
-and decode steps (a single activation rounding can flip across a
-quantisation step, the same bar as the bf16 W8A8 model test). Both the
-static quantiser (quant_scale) and the per-token one run in every layer.
+fp32 storage gives the oracle's greedy tokens exactly (the int32 products
+are exact and the dequantisation is evaluated in the same fp32 order); fp16
+storage, the checkpoint's own dtype, is compared teacher-forced on the logits
+of a prefill and decode steps (see that test for the bars: an activation
+rounding can flip an int8 code). Both the static quantiser (quant_scale) and
+the per-token one run in every layer.
 """
 import pytest
 import torch
@@ -71,14 +70,34 @@ def test_int8_checkpoint_fp32_tokens_identical(cuda, ckpt, graph):
 
 
 def test_int8_checkpoint_fp16_logits(cuda, ckpt):
+    """fp16 storage. The oracle is teacher-forced with the product's tokens,
+    so both evaluate every step on the same context. The static and per-token
+    quantisers are step functions of their fp16 inputs: a one-ulp difference
+    in an activation (another summation order in any kernel) can move an int8
+    code by one step, and in this 256-wide model one such flip in the first
+    layer's attention output moved a prompt's logits by 0.67 (two prefill
+    attention kernels, both within 0.0016 of the oracle's attention, one
+    flipping and one not). So: every (prompt, step) within 1.0 (a broken
+    kernel moves logits by whole units), the median within 4e-2, and the
+    product's token equal to the oracle's argmax wherever the oracle's top-1
+    margin exceeds 4x the logits difference of that step."""
+    from oracle.qwen2 import Qwen2Cfg, Qwen2Oracle
     sq, sd, prompts = ckpt
     print("case: SmoothQuant checkpoint fp16", flush=True)
-    got, lg = _product(sq, prompts, 6, torch.float16, cuda, True)
-    ref, lr = _oracle(sd, prompts, 6, torch.float16)
-    # logits compared while the two greedy paths agree (a flip changes the next inputs)
+    n_new = 6
+    got, lg = _product(sq, prompts, n_new, torch.float16, cuda, True)
+    oc = Qwen2Cfg(num_layers=2, hidden=256, heads=4, kv_heads=2, intermediate=688, vocab=1024)
+    ref, lr = Qwen2Oracle(oc, sd, torch.float16, 8, 128, 1024, quant="w8a8").generate(
+        prompts, n_new, return_logits=True, feed=got)
+    errs = []
     for b in range(len(prompts)):
-        for s in range(6):
+        for s in range(n_new):
             err = float((lg[b, s].double() - lr[b, s].double()).abs().max())
-            assert err <= 4e-2, f"prompt {b} step {s}: {err}"
-            if got[b, s] != ref[b, s]:
-                break
+            errs.append(err)
+            assert err <= 1.0, f"prompt {b} step {s}: {err}"
+            top2 = lr[b, s].double().topk(2).values
+            if float(top2[0] - top2[1]) > 4 * err:
+                assert int(got[b, s]) == int(ref[b, s]), f"prompt {b} step {s}: token differs"
+    errs.sort()
+    assert errs[len(errs) // 2] <= 4e-2, f"median logits difference {errs[len(errs) // 2]}"
+    print(f"fp16 W8A8: logits diff median {errs[len(errs) // 2]:.4f}, max {errs[-1]:.4f}", flush=True)
