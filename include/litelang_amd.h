@@ -246,6 +246,12 @@ int ll_gemm_i8_tiled(const int8_t* Xq, int64_t ldx, const float* s_tok, const in
 int ll_gemm_i8_i32_tiled(const int8_t* Xq, int64_t ldx, const int8_t* Wq, int64_t ldw,
                          int32_t* Y, int64_t ldy, int64_t M, int64_t N, int64_t K,
                          hipStream_t stream);
+/* The same int32 sums for any shape: the tile kernel where its layout holds
+ * (K % 64 == 0, N % 4 == 0, 16 B aligned rows), else a plain int8
+ * dot-product kernel. The int8 x int8 -> int32 product of the W8A8 prefill
+ * (no reference counterpart, as ll_gemm_i8_tiled). */
+int ll_gemm_i8_i32(const int8_t* Xq, int64_t ldx, const int8_t* Wq, int64_t ldw, int32_t* Y,
+                   int64_t ldy, int64_t M, int64_t N, int64_t K, hipStream_t stream);
 /* ll_gemm_gate_up_silu_tiled for the W8A8 runtime: both halves dequantised
  * as in ll_gemm_i8_tiled (s_ch holds the [gate; up] channel scales in the
  * original order), then SiLU_and_Mul into Y (bf16/fp16). */

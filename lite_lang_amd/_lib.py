@@ -51,6 +51,7 @@ SIGNATURES = {
     "ll_gemm_gate_up_silu_tiled": (I32, [P, I64, P, I64, I64, I64, I32, P, I64, P]),
     "ll_gemm_i8_tiled": (I32, [P, I64, P, P, I64, P, I32, P, P, I64, I64, I64, I64, I32, P]),
     "ll_gemm_i8_i32_tiled": (I32, [P, I64, P, I64, P, I64, I64, I64, I64, P]),
+    "ll_gemm_i8_i32": (I32, [P, I64, P, I64, P, I64, I64, I64, I64, P]),
     "ll_gemm_i8_gate_up_silu_tiled": (I32, [P, I64, P, P, P, I32, I64, I64, I64, I32, P, I64,
                                             P]),
     "ll_gemm_workspace_size": (I64, [I64, I64, I64]),

@@ -458,6 +458,30 @@ extern "C" int ll_gemm_i8_i32_tiled(const int8_t* Xq, int64_t ldx, const int8_t*
   return launch_tiles<int8_t, int32_t, EPI_I32>(a, stream);
 }
 
+// Shapes outside the tile kernel's layout (K not a multiple of 64, unaligned
+// rows; small test models): one thread per output, the int8 dot product over
+// K in 4-byte steps where the rows allow (v_dot4_i32_i8), exact int32 sums.
+__global__ __launch_bounds__(256) void gemm_i8_plain_kernel(const int8_t* __restrict__ X,
+                                                            int64_t ldx,
+                                                            const int8_t* __restrict__ W,
+                                                            int64_t ldw, int32_t* __restrict__ Y,
+                                                            int64_t ldy, int M, int N, int K,
+                                                            int vec4) {
+  const int n = blockIdx.x * 64 + (threadIdx.x & 63);
+  const int m = blockIdx.y * 4 + (threadIdx.x >> 6);
+  if (m >= M || n >= N) return;
+  const int8_t* xr = X + (int64_t)m * ldx;
+  const int8_t* wr = W + (int64_t)n * ldw;
+  int32_t acc = 0;
+  int k = 0;
+  if (vec4) {
+    for (; k + 4 <= K; k += 4)
+      acc = __builtin_amdgcn_sdot4(*(const int32_t*)(xr + k), *(const int32_t*)(wr + k), acc, false);
+  }
+  for (; k < K; ++k) acc += (int32_t)xr[k] * (int32_t)wr[k];
+  Y[(int64_t)m * ldy + n] = acc;
+}
+
 extern "C" int ll_gemm_i8_gate_up_silu_tiled(const int8_t* Xq, int64_t ldx, const float* s_tok,
                                              const int8_t* Wq_il, const void* s_ch,
                                              int s_ch_dtype, int64_t M, int64_t I, int64_t K,
@@ -478,4 +502,23 @@ extern "C" int ll_gemm_i8_gate_up_silu_tiled(const int8_t* Xq, int64_t ldx, cons
   a.s_tok = s_tok; a.s_ch = s_ch; a.s_ch_dtype = s_ch_dtype;
   if (out_dtype == LL_BF16) return launch_tiles<int8_t, __bf16, EPI_DEQ_SILU>(a, stream);
   return launch_tiles<int8_t, _Float16, EPI_DEQ_SILU>(a, stream);
+}
+
+extern "C" int ll_gemm_i8_i32(const int8_t* Xq, int64_t ldx, const int8_t* Wq, int64_t ldw,
+                              int32_t* Y, int64_t ldy, int64_t M, int64_t N, int64_t K,
+                              hipStream_t stream) {
+  LL_CHECK_ARG(Xq && Wq && Y, "ll_gemm_i8_i32: null pointer");
+  LL_CHECK_ARG(M >= 0 && N > 0 && K > 0 && ldx >= K && ldw >= K && ldy >= N,
+               "ll_gemm_i8_i32: bad shape (M=%lld N=%lld K=%lld)", (long long)M, (long long)N,
+               (long long)K);
+  LL_CHECK_ARG(M <= INT32_MAX && N <= INT32_MAX && K <= INT32_MAX, "ll_gemm_i8_i32: shape too large");
+  if (M == 0) return LL_OK;
+  const bool tile = N % 4 == 0 && K % kRB == 0 && ldx % 16 == 0 && ldw % 16 == 0 &&
+                    (((uintptr_t)Xq | (uintptr_t)Wq) % 16) == 0 && ldy % 4 == 0 &&
+                    ((uintptr_t)Y) % 16 == 0;
+  if (tile) return ll_gemm_i8_i32_tiled(Xq, ldx, Wq, ldw, Y, ldy, M, N, K, stream);
+  const int vec4 = ldx % 4 == 0 && ldw % 4 == 0 && (((uintptr_t)Xq | (uintptr_t)Wq) % 4) == 0;
+  hipLaunchKernelGGL(gemm_i8_plain_kernel, dim3((unsigned)ll_cdiv(N, 64), (unsigned)ll_cdiv(M, 4)),
+                     dim3(256), 0, stream, Xq, ldx, Wq, ldw, Y, ldy, (int)M, (int)N, (int)K, vec4);
+  LL_RETURN_LAUNCH();
 }

@@ -21,7 +21,6 @@ from lite_lang_amd import ops
 from lite_lang_amd.models.cache import PageCache
 from lite_lang_amd.models.radix_cache import RadixTree
 from .decode_graph import DecodeGraph
-from ...tuning import use_prefill_gemm_solutions
 from .weights import (DeviceWeights, Qwen2Config, check_smoothquant_config, is_int8_checkpoint,
                       load_state_dict, random_state_dict)
 
@@ -38,14 +37,9 @@ def rope_tables(max_length: int, head_dim: int, theta: float, device):
 
 
 def dense(x, w, bias=None):
-    """Projection of the generic (prefill) path. Above 64 rows in bf16/fp16
-    this is a plain GEMM with nothing to fuse, so it goes to the vendor
-    library (hipBLASLt through torch.matmul/addmm: 1.1-1.4 PFLOP/s at the 3B
-    prefill shapes against 0.7 for ll_gemm's tiled kernel); the decode
-    projections (<= 64 rows) are this library's weight-streaming kernels."""
-    if x.shape[0] > 64 and x.dtype in (torch.bfloat16, torch.float16) and x.is_cuda:
-        # addmm adds the bias to the fp32 sums and rounds once, as ll_gemm does
-        return torch.addmm(bias, x, w.t()) if bias is not None else torch.matmul(x, w.t())
+    """Projection of the generic (prefill) path: ll_gemm, which runs the
+    256 x 256 MFMA tile kernel above 64 rows and the weight-streaming kernel
+    at or below (transformer_layer.py:80,82,95-109)."""
     return ops.gemm(x, w, bias)
 
 
@@ -74,6 +68,28 @@ class Qwen2Model:
             return ops.linear_w8a8(x, self.w.packed[li][name + "_i8"], bias)
         return dense(x, self.w.layers[li][name], bias)
 
+    def _gate_up_silu(self, x, li):
+        """silu(x @ gate^T) * (x @ up^T) (transformer_layer.py:95-109). Above
+        64 rows, when the weights have an interleaved copy, in one tile GEMM
+        whose epilogue applies SiLU_and_Mul (bit-identical to the product
+        followed by silu_and_mul); otherwise the [M, 2I] product, then
+        silu_and_mul into a contiguous [M, I] buffer."""
+        T = x.shape[0]
+        if T > 64:
+            if self.quant == "w8a8":
+                qw = self.w.packed[li]["wgu_i8"]
+                if qw.q_il is not None and x.dtype in (torch.bfloat16, torch.float16):
+                    xq, st = ops.quant_input(x, qw)
+                    return ops.gemm_i8_gate_up_silu_tiled(xq, st, qw.q_il, qw.scale,
+                                                          out_dtype=x.dtype)
+            else:
+                w_il = self.w.layers[li].get("wgu_il")
+                if w_il is not None:
+                    return ops.gate_up_silu_tiled(x, w_il)
+        gu = self._proj(x, li, "wgu")
+        return ops.silu_and_mul(gu, out=torch.empty((T, gu.shape[1] // 2), dtype=gu.dtype,
+                                                    device=gu.device))
+
     # ------------------------------------------------------------ layer stack
     def _layers(self, h, T, slots, positions, pool, attention):
         """The L transformer layers (transformer_layer.py:46-77) over hidden
@@ -91,12 +107,7 @@ class Qwen2Model:
             attention(li, q, attn)
             o = self._proj(attn.view(T, H * D), li, "wo")
             x2 = ops.rmsnorm(h, lw["ln2"], cfg.rms_norm_eps, residual=o)
-            gu = self._proj(x2, li, "wgu")
-            # a contiguous product (not the reference's in-place half view):
-            # the down projection then runs on the row layout its vendor GEMM
-            # solution was selected for
-            act = ops.silu_and_mul(gu, out=torch.empty((T, gu.shape[1] // 2), dtype=gu.dtype,
-                                                       device=gu.device))
+            act = self._gate_up_silu(x2, li)
             f = self._proj(act, li, "wdown")
         return f
 
@@ -376,10 +387,6 @@ class Qwen2ModelRunner:
                                   tp_rank=self.tp_rank_, tp_world_size=self.world_size_,
                                   kv_max_size=self.kv_max_size_arg_, device=self.device_)
         self.radix_cache = RadixTree() if self.use_radix_cache_ else None
-        if self.device_.type == "cuda":
-            # the prefill projections (vendor-library GEMMs) use the solutions
-            # selected offline for the benchmark shapes; other shapes are untouched
-            use_prefill_gemm_solutions()
         return self.kv_cache.kv_max_size_
 
     def _alloc_for_forward(self, model_inputs):

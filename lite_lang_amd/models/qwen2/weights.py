@@ -12,6 +12,9 @@ configurations -- and are packed once into the device layout:
   wo         [hidden, H * D]             (o_proj bias is ignored, as the
                                           reference does: transformer_layer.py:193)
   wgu        [2 * I, hidden]             rows: gate then up
+  wgu_il     [2 * I, hidden]             the same rows in 64-row blocks that
+                                         alternate gate and up (the prefill
+                                         gate/up + SiLU tile kernel's layout)
   wdown      [hidden, I]
   ln1, ln2   [hidden]
   norm       [hidden]
@@ -246,6 +249,10 @@ class DeviceWeights:
                 for name in ("wqkv", "wo", "wdown"):
                     pk[name] = ops.pack_weight(lw[name])
                 pk["wgu_silu"] = ops.pack_gate_up(lw["wgu"])
+                # the prefill gate/up + SiLU tile kernel's interleaved copy
+                K = lw["wgu"].shape[1]
+                if ops.gemm_tiled_supported(65, lw["wgu"].shape[0], K, dtype):
+                    lw["wgu_il"] = ops.interleave_gate_up(lw["wgu"])
             self.lm_head_p = ops.pack_weight(self.lm_head)
 
     def nbytes_streamed_per_decode(self) -> int:
@@ -254,6 +261,8 @@ class DeviceWeights:
         n = (self.norm.numel() + self.lm_head.numel()) * es
         for lw, pk in zip(self.layers, self.packed):
             for name, v in lw.items():
+                if name == "wgu_il":  # prefill-only copy
+                    continue
                 qw = pk.get(name + "_i8")
                 if qw is not None:
                     n += qw.q.numel() + qw.scale.numel() * qw.scale.element_size()

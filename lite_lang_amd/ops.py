@@ -371,6 +371,28 @@ def gemm_i8_i32_tiled(xq, wq, out=None):
     return out
 
 
+def gemm_i8_i32(xq, wq, out=None):
+    """exact int32 sums int8(x) @ int8(w)^T for any shape (the tile kernel
+    where its layout holds, else a plain dot-product kernel)."""
+    _dev(xq, wq, out)
+    M, K = xq.shape
+    N = wq.shape[0]
+    assert wq.shape[1] == K and xq.dtype == torch.int8 and wq.dtype == torch.int8
+    assert xq.stride(1) == 1 and wq.stride(1) == 1
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.int32, device=xq.device)
+    assert out.shape == (M, N) and out.stride(1) == 1 and out.dtype == torch.int32
+    rc = _L.ll_gemm_i8_i32(xq.data_ptr(), xq.stride(0), wq.data_ptr(), wq.stride(0),
+                           out.data_ptr(), out.stride(0), M, N, K, _stream(xq))
+    _lib.check(rc, "ll_gemm_i8_i32")
+    return out
+
+
+def gemm_i8_tiled_supported(M, N, K) -> bool:
+    """Shapes the int8 tile kernel takes (K % 64 == 0, N % 4 == 0)."""
+    return M > 0 and N % 4 == 0 and K % 64 == 0
+
+
 def gemm_i8_gate_up_silu_tiled(xq, s_tok, wq_il, s_ch, out_dtype=torch.bfloat16, out=None):
     """W8A8 gate/up + SiLU_and_Mul from the interleaved int8 weight (prefill)."""
     _dev(xq, s_tok, wq_il, s_ch, out)
@@ -751,11 +773,14 @@ class QuantWeight:
     """W8A8 projection weight: int8 [N, K] with per-channel scales (the model
     dtype when quantised here, the checkpoint's dtype when loaded), its packed
     streaming image when K % 256 == 0, and optionally a calibrated static
-    input scale (fp32 device tensor, one element; None = dynamic per token)."""
+    input scale (fp32 device tensor, one element; None = dynamic per token).
+    A [gate; up] weight also keeps the 64-row interleaved int8 copy the fused
+    prefill gate/up + SiLU tile kernel reads (q_il; None where the layout
+    does not apply)."""
 
     def __init__(self, w=None, gate_up=False):
         self.input_scale = None
-        self.packed = self.packed_gu = None
+        self.packed = self.packed_gu = self.q_il = None
         if w is None:
             return
         self.q, self.scale = quant_weight_per_channel(w)
@@ -764,7 +789,10 @@ class QuantWeight:
 
     def _pack(self, gate_up):
         """Streaming image for M <= 64: the plain layout, or for a [gate; up]
-        weight the fused gate/up + SiLU layout (decode uses only that one)."""
+        weight the fused gate/up + SiLU layout (decode uses only that one),
+        plus the interleaved copy for the tile kernel (M > 64)."""
+        if gate_up and self.shape[1] % 64 == 0:
+            self.q_il = interleave_gate_up(self.q)
         if self.shape[1] % 256 != 0:
             return
         if gate_up:
@@ -807,7 +835,7 @@ def quant_input(x, qw: QuantWeight):
 
 def gemm_w8a8_i32(xq, st, qw: QuantWeight) -> I8Partials:
     """The exact int32 product int8(x) @ int8(W)^T (the streaming kernel for
-    M <= 64, torch's int8 matmul above that) as partials with their scales."""
+    M <= 64, the int8 tile kernel above that) as partials with their scales."""
     M, K = xq.shape
     N = qw.shape[0]
     if M <= 64 and qw.packed is not None:
@@ -816,12 +844,7 @@ def gemm_w8a8_i32(xq, st, qw: QuantWeight) -> I8Partials:
         gemm_i8_splitk_packed(xq, qw.packed, part)
     else:
         s = 1
-        if M <= 16:  # the library int8 GEMM takes more than 16 rows: zero rows, exact
-            xp = torch.zeros((17, K), dtype=torch.int8, device=xq.device)
-            xp[:M] = xq
-            part = torch._int_mm(xp, qw.q.t())[:M]
-        else:
-            part = torch._int_mm(xq, qw.q.t())
+        part = gemm_i8_i32(xq, qw.q)
     return I8Partials(part, s, st, qw.scale)
 
 
@@ -869,7 +892,15 @@ def silu_and_mul_splitk_i32(p: I8Partials, out):
 
 
 def linear_w8a8(x, qw: QuantWeight, bias=None):
-    """dtype(linear_w8a8_fp32(x) + bias), the rounding of the fused consumers."""
+    """dtype(linear_w8a8_fp32(x) + bias), the rounding of the fused consumers
+    (above 64 rows in one launch: the tile kernel's dequantising epilogue
+    evaluates the same fp32 expression)."""
+    M, K = x.shape
+    N = qw.shape[0]
+    if (M > 64 and x.dtype in (torch.bfloat16, torch.float16) and gemm_i8_tiled_supported(M, N, K)
+            and (bias is None or bias.dtype == x.dtype)):
+        xq, st = quant_input(x, qw)
+        return gemm_i8_tiled(xq, st, qw.q, qw.scale, bias, out_dtype=x.dtype)
     y = linear_w8a8_fp32(x, qw)
     if bias is not None:
         y = y + bias.float()

@@ -119,3 +119,17 @@ def test_gemm_i8_gate_up_silu_tiled_bit_exact(cuda):
     gu = ops.gemm_i8_tiled(xd, std, wd, scd, out_dtype=torch.bfloat16)
     want = ops.silu_and_mul(gu, out=torch.empty((M, I), dtype=torch.bfloat16, device=cuda))
     assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("M,N,K,pad", [(70, 100, 36, 0), (300, 50, 100, 3), (129, 256, 128, 0),
+                                       (65, 2048, 8960, 0)])
+def test_gemm_i8_i32_any_shape_exact(cuda, M, N, K, pad):
+    """ll_gemm_i8_i32 (the W8A8 prefill product): the tile kernel where its
+    layout holds, the plain dot-product kernel elsewhere (K % 64 != 0, odd
+    row strides); exact int32 sums either way."""
+    g = torch.Generator().manual_seed(87)
+    xfull = torch.randint(-128, 128, (M, K + pad), generator=g, dtype=torch.int8)
+    wq = torch.randint(-128, 128, (N, K), generator=g, dtype=torch.int8)
+    print(f"case: gemm_i8_i32 M={M} N={N} K={K} pad={pad}", flush=True)
+    got = _ops().gemm_i8_i32(xfull.to(cuda)[:, :K], wq.to(cuda)).cpu()  # row stride K + pad
+    assert torch.equal(got, O.int8_gemm_i32(xfull[:, :K].contiguous(), wq))
