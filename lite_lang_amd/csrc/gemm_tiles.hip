@@ -5,22 +5,25 @@
 // (the reference's SmoothQuant module has no forward, quantize/smooth_quant/
 // layer.py:19-59).
 //
-// One workgroup (4 waves, one per SIMD) computes a 256 x 256 output tile:
+// One workgroup (8 waves, two per SIMD) computes a 256 x 256 output tile:
 //   * stages of 64 bytes of K per row (32 bf16/fp16 or 64 int8) for the
 //     tile's 256 weight rows and 256 activation rows (32 KB) are copied
 //     global -> LDS with global_load_lds_dwordx4 (no VGPR staging) into a
-//     ring of five stage buffers (160 KB), three stages in flight ahead of
+//     ring of five stage buffers (160 KB), four stages in flight ahead of
 //     the one being multiplied, one barrier per stage, placed between the stage's
 //     two MFMA k-steps so that the operand reads of the next stage overlap
 //     the multiplications of this one;
 //   * the 16-byte chunks of every LDS row are XOR-swizzled (tile_swz) so
 //     the MFMA operand reads (16 rows x 16 B per 16 lanes) hit distinct
 //     banks;
-//   * each wave multiplies a 128 x 128 quarter with v_mfma_f32_32x32x16_bf16
-//     (v_mfma_i32_32x32x32_i8 for int8) as C^T = W . X^T: the weight rows are
-//     the MFMA's row operand, so every lane ends with runs of 4 consecutive
-//     output columns of one token row (8-byte stores) in 16 accumulator
-//     blocks of 32 x 32;
+//   * each wave multiplies 128 weight rows by 64 activation rows with
+//     v_mfma_f32_32x32x16_bf16 (v_mfma_i32_32x32x32_i8 for int8) as
+//     C^T = W . X^T: the weight rows are the MFMA's row operand, so every
+//     lane ends with runs of 4 consecutive output columns of one token row
+//     (8-byte stores) in 8 accumulator blocks of 32 x 32. The second wave
+//     on each SIMD issues while the first waits on LDS or the barrier (one
+//     wave per SIMD reaches about 150 B/clk of LDS reads per CU, two about
+//     240);
 //   * the grid is XCD-aware: the workgroups the dispatcher deals to one XCD
 //     take a contiguous range of tiles in 4-row-tile groups, so tiles sharing
 //     activation or weight rows run together on one L2.
@@ -38,6 +41,14 @@ constexpr int kRB = 64;        // bytes of K per row per stage
 constexpr int kStageB = 2 * kT * kRB;  // 32 KB: weight rows, then activation rows
 constexpr int kNst = 5;        // stage buffers (160 KB of LDS)
 constexpr int kGroupM = 4;     // row tiles per group of the tile order
+constexpr int kWaves = 8;      // two per SIMD
+constexpr int kThreads = 64 * kWaves;
+constexpr int kPW = 4;         // 32-row weight blocks per wave (128 rows: wave column wn of 2)
+constexpr int kQX = 2;         // 32-row activation blocks per wave (64 rows: wave row wm of 4)
+constexpr int kNMf = kPW * kQX;  // MFMAs per wave per k-step
+constexpr int kDmaW = 2 * kT * kRB / 16 / kThreads;  // 16-byte copies per lane per stage
+static_assert(2 * 32 * kPW == kT && 4 * 32 * kQX == kT && kWaves == 8, "wave grid 2 x 4");
+static_assert(kDmaW == 4, "copy geometry: 4 instructions of 16 rows per wave per stage");
 
 enum { EPI_STORE = 0, EPI_SILU = 1, EPI_DEQ = 2, EPI_DEQ_SILU = 3, EPI_I32 = 4 };
 
@@ -89,16 +100,17 @@ struct TileArgs {
   const void* s_ch; int s_ch_dtype;  // int8: weight scale per channel [N]
 };
 
-// Swizzle of the 16-byte chunks of LDS row r (an involution on 0..3): the
-// operand reads of 16 lanes (rows r0..r0+15, one logical chunk) hit 16
-// distinct 16-byte bank groups of a 256-byte bank row, and so do those of
-// every 8 lanes within a 128-byte bank row.
-__device__ __forceinline__ int tile_swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+// Swizzle of the 16-byte chunks of 64-byte LDS row r (an involution on
+// 0..3): chunk c of row r sits at chunk c ^ ((r / 4) % 4). Measured with
+// ds_read_b128 over the fragment pattern (32 rows x one chunk per 32
+// lanes): about 205 B/clk per CU, as for contiguous reads, against 116 B/clk
+// for a swizzle on (r / 2) ^ (r / 8) and 63 B/clk unswizzled.
+__device__ __forceinline__ int tile_swz(int r) { return (r >> 2) & 3; }
 // LDS byte offset of chunk c (16 B) of tile row r within a stage half
 __device__ __forceinline__ int tile_lds_off(int r, int c) { return r * kRB + ((c ^ tile_swz(r)) << 4); }
 
 template <typename T, typename TO, int EPI>
-__global__ __launch_bounds__(256, 1) void gemm_tile_kernel(TileArgs a) {
+__global__ __launch_bounds__(kThreads, 1) void gemm_tile_kernel(TileArgs a) {
   typedef typename TileOp<T>::V V;
   typedef typename TileOp<T>::Acc Acc;
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -118,125 +130,148 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(TileArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int wn = wave & 1, wm = wave >> 1;
 
-  // ---- copy geometry: instruction u of this wave covers LDS rows
-  // 16 * (4 * wave + u) .. + 15 of the weight half (u < 4) or the
-  // activation half (u >= 4); lane -> row + l/4, LDS chunk l % 4
+  // ---- copy geometry: instruction u of this wave is copy j = u * 8 + wave
+  // of the stage's 32; copy j covers LDS rows 16 * (j % 16) .. + 15 of the
+  // weight half (j < 16) or the activation half; lane -> row + l/4, LDS chunk l % 4
   const int crow = lane >> 2;
-  uint32_t soff[8];  // byte offsets of this lane's copy sources (rows clamped into range)
+  uint32_t soff[kDmaW];  // byte offsets of this lane's copy sources (rows clamped into range)
 #pragma unroll
-  for (int u = 0; u < 8; ++u) {
-    const int r = 16 * (4 * wave + (u & 3)) + crow;
+  for (int u = 0; u < kDmaW; ++u) {
+    const int j = u * kWaves + wave;
+    const int r = 16 * (j & 15) + crow;
     const int gch = (lane & 3) ^ tile_swz(r);
-    if (u < 4) soff[u] = (uint32_t)((int64_t)min(n0 + r, a.N - 1) * a.ldw_b + gch * 16);
+    if (j < 16) soff[u] = (uint32_t)((int64_t)min(n0 + r, a.N - 1) * a.ldw_b + gch * 16);
     else soff[u] = (uint32_t)((int64_t)min(m0 + r, a.M - 1) * a.ldx_b + gch * 16);
   }
   const int nk = a.K_b / kRB;
-  auto issue = [&](int ks) {
-    char* base = smem + (ks % kNst) * kStageB + wave * 4096;
-    const char* wk = a.W + (int64_t)ks * kRB;
-    const char* xk = a.X + (int64_t)ks * kRB;
-#pragma unroll
-    for (int u = 0; u < 8; ++u)
-      tile_dma16((u < 4 ? wk : xk) + soff[u], base + (u >> 2) * (kT * kRB) + (u & 3) * 1024);
+  auto dma = [&](int ks, int u) {
+    const int j = u * kWaves + wave;
+    char* dst = smem + (ks % kNst) * kStageB + (j >> 4) * (kT * kRB) + (j & 15) * 1024;
+    tile_dma16((j < 16 ? a.W : a.X) + (int64_t)min(ks, nk - 1) * kRB + soff[u], dst);
   };
 
-  Acc acc[4][4];
+  Acc acc[kPW][kQX];
 #pragma unroll
-  for (int p = 0; p < 4; ++p)
+  for (int p = 0; p < kPW; ++p)
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
+    for (int q = 0; q < kQX; ++q)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[p][q][e] = 0;
 
-  // Schedule per stage ks (two MFMA k-steps of 16 bytes per row): the
-  // fragments of k-step 0 were read during the previous stage; k-step 1's
-  // are read while k-step 0 is multiplied; then the barrier publishes stage
-  // ks + 1 (and certifies that every wave has left stage ks - 1, whose
-  // buffer the copy of stage ks + 3 refills) and k-step 0 of stage ks + 1 is
-  // read while k-step 1 of stage ks is multiplied.
+  // Ping-pong schedule. Waves 0-3 (group A) and 4-7 (group B) hold one
+  // wave of each SIMD (the dispatcher places wave w on SIMD w % 4). Time is
+  // cut into phases separated by workgroup barriers; in phase 2s group A
+  // multiplies stage s from its registers while group B reads its fragments
+  // of stage s from LDS and issues its half of the copies of stage s + 4,
+  // and in phase 2s + 1 the roles swap (B multiplies stage s, A reads stage
+  // s + 1 and issues its half of stage s + 4). Each SIMD's MFMA pipe so
+  // always has one wave with a run of 16 independent MFMAs while the other
+  // wave's LDS reads and copies proceed. Ring invariants (five buffers,
+  // stage t in buffer t % 5):
+  //   * stage t lands before the barrier that ends phase 2t - 2 (A waits
+  //     vmcnt(8) at the end of its compute phase, B vmcnt(12) after
+  //     issuing), so A's reads in phase 2t - 1 and B's in phase 2t see it;
+  //   * the copies of stage t + 5 go to stage t's buffer in phases 2t + 2
+  //     and 2t + 3, after the barrier that ends B's last read of stage t
+  //     (phase 2t, closed by lgkmcnt(0)).
+  // Copies of stages past the last are issued from the last stage's source
+  // (in bounds, never read) so that every wave's vmcnt arithmetic is the
+  // same in every iteration; all copies have landed before the epilogue.
   const int lr = lane & 31, lc = lane >> 5;
-  const int wrow = wn * 128 + lr, xrow = wm * 128 + lr;
-  V w0[4], x0[4], w1[4], x1[4];
-  auto load_k = [&](int ks, int kstep, V (&wf)[4], V (&xf)[4]) {
-    const char* wb = smem + (ks % kNst) * kStageB;
-    const char* xb = wb + kT * kRB;
-    const int c = 2 * kstep + lc;
-#pragma unroll
-    for (int p = 0; p < 4; ++p) wf[p] = *(const V*)(wb + tile_lds_off(wrow + 32 * p, c));
-#pragma unroll
-    for (int q = 0; q < 4; ++q) xf[q] = *(const V*)(xb + tile_lds_off(xrow + 32 * q, c));
-  };
-  // wait until a stage has landed while `younger` later stages stay in flight
-  auto wait_stage = [&](int younger) {
-    if (younger >= 3) tile_vm_wait<24>();
-    else if (younger == 2) tile_vm_wait<16>();
-    else if (younger == 1) tile_vm_wait<8>();
-    else tile_vm_wait<0>();
-  };
-  static_assert(kNst >= 3 && kNst <= 5, "stage ring of 3 to 5 buffers");
-#pragma unroll
-  for (int st = 0; st < kNst - 1; ++st)
-    if (st < nk) issue(st);
-  wait_stage(min(kNst - 2, nk - 1));
-  tile_barrier();
-  load_k(0, 0, w0, x0);
-  // Per k-step the 16 MFMAs are issued in program order with one memory
-  // instruction after each of the first 8 (k-step 0: the reads of k-step 1;
-  // k-step 1: the stage copies, then the reads of the next stage's k-step 0
-  // after the next 8), and sched_barrier keeps that order: the wave issues
-  // its memory work while the MFMA pipe is busy instead of draining it.
+  const int wrow = wn * 128 + lr, xrow = wm * 64 + lr;
   const int c0 = lc, c1 = 2 + lc;  // LDS chunks of k-step 0 and 1 for this lane
+  V fw[2][kPW], fx[2][kQX];
   auto frag_w = [&](int ks, int c, int p) {
     return *(const V*)(smem + (ks % kNst) * kStageB + tile_lds_off(wrow + 32 * p, c));
   };
   auto frag_x = [&](int ks, int c, int q) {
     return *(const V*)(smem + (ks % kNst) * kStageB + kT * kRB + tile_lds_off(xrow + 32 * q, c));
   };
-  for (int ks = 0; ks < nk; ++ks) {
+  auto read_stage = [&](int ks) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      acc[i >> 2][i & 3] = tile_mma(w0[i >> 2], x0[i & 3], acc[i >> 2][i & 3]);
-      if (i < 4) w1[i] = frag_w(ks, c1, i);
-      else if (i < 8) x1[i - 4] = frag_x(ks, c1, i - 4);
+    for (int p = 0; p < kPW; ++p) fw[0][p] = frag_w(ks, c0, p);
+#pragma unroll
+    for (int q = 0; q < kQX; ++q) fx[0][q] = frag_x(ks, c0, q);
+#pragma unroll
+    for (int p = 0; p < kPW; ++p) fw[1][p] = frag_w(ks, c1, p);
+#pragma unroll
+    for (int q = 0; q < kQX; ++q) fx[1][q] = frag_x(ks, c1, q);
+  };
+  auto issue = [&](int t) {
+#pragma unroll
+    for (int u = 0; u < kDmaW; ++u) dma(t, u);
+  };
+  auto compute = [&]() {
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int i = 0; i < kNMf; ++i)
+        acc[i / kQX][i % kQX] = tile_mma(fw[kk][i / kQX], fx[kk][i % kQX], acc[i / kQX][i % kQX]);
+  };
+  static_assert(kNst == 5 && kDmaW == 4, "the ping-pong wait counts assume 5 buffers, 4 copies");
+  const bool group_a = wave < 4;
+  // prologue: B issues its halves of stages 0..3, A of stages 0..2; stage 0
+  // lands; A reads stage 0 and issues its half of stage 3 (phase -1)
+  issue(0);
+  issue(1);
+  issue(2);
+  if (group_a) {
+    tile_vm_wait<8>();
+  } else {
+    issue(3);
+    tile_vm_wait<12>();
+  }
+  tile_barrier();
+  if (group_a) {
+    read_stage(0);
+    issue(3);
+  }
+  tile_barrier();
+  // sched_barrier keeps every instruction inside its phase (MFMAs touch no
+  // memory, so nothing else stops the scheduler moving them across barriers)
+  if (group_a) {
+    for (int ks = 0; ks < nk; ++ks) {
       __builtin_amdgcn_sched_barrier(0);
-    }
-    const bool more = ks + 1 < nk;
-    if (more) {
-      // stage ks + 1 landed; stages up to ks + kNst - 2 may stay in flight
-      wait_stage(min(kNst - 3, nk - 2 - ks));
+      compute();                 // phase 2ks: stage ks
+      __builtin_amdgcn_sched_barrier(0);
+      tile_vm_wait<8>();         // own copies of stage ks + 1 landed
+      tile_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      read_stage(ks + 1);        // phase 2ks + 1
+      issue(ks + 4);
+      __builtin_amdgcn_sched_barrier(0);
       tile_barrier();
     }
-    const bool refill = ks + kNst - 1 < nk;  // into the buffer of stage ks - 1
-    char* rbase = smem + ((ks + kNst - 1) % kNst) * kStageB + wave * 4096;
-    const char* wk = a.W + (int64_t)(ks + kNst - 1) * kRB;
-    const char* xk = a.X + (int64_t)(ks + kNst - 1) * kRB;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      acc[i >> 2][i & 3] = tile_mma(w1[i >> 2], x1[i & 3], acc[i >> 2][i & 3]);
-      if (i < 8) {
-        if (refill)
-          tile_dma16((i < 4 ? wk : xk) + soff[i], rbase + (i >> 2) * (kT * kRB) + (i & 3) * 1024);
-      } else if (more) {
-        if (i < 12) w0[i - 8] = frag_w(ks + 1, c0, i - 8);
-        else x0[i - 12] = frag_x(ks + 1, c0, i - 12);
-      }
+  } else {
+    for (int ks = 0; ks < nk; ++ks) {
       __builtin_amdgcn_sched_barrier(0);
+      read_stage(ks);            // phase 2ks
+      issue(ks + 4);
+      __builtin_amdgcn_sched_barrier(0);
+      tile_vm_wait<12>();        // own copies of stage ks + 1 landed
+      tile_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      compute();                 // phase 2ks + 1: stage ks
+      __builtin_amdgcn_sched_barrier(0);
+      tile_barrier();
     }
   }
+  __builtin_amdgcn_sched_barrier(0);
+  tile_vm_wait<0>();
 
   // ---- epilogue: acc[p][q][4g + i] = C[m][n] with
-  //   m = m0 + wm*128 + 32q + l % 32,  n = n0 + wn*128 + 32p + 8g + 4(l / 32) + i
-  const int mrow = m0 + wm * 128 + lr;
+  //   m = m0 + wm*64 + 32q + l % 32,  n = n0 + wn*128 + 32p + 8g + 4(l / 32) + i
+  const int mrow = m0 + wm * 64 + lr;
   if constexpr (EPI == EPI_STORE || EPI == EPI_DEQ || EPI == EPI_I32) {
     const int ncol = n0 + wn * 128 + 4 * lc;
-    float st[4];
+    float st[kQX];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < kQX; ++q) {
       st[q] = 1.f;
       if constexpr (EPI == EPI_DEQ) st[q] = a.s_tok[min(mrow + 32 * q, a.M - 1)];
     }
 #pragma unroll
-    for (int p = 0; p < 4; ++p)
+    for (int p = 0; p < kPW; ++p)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int n = ncol + 32 * p + 8 * g;
@@ -252,7 +287,7 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(TileArgs a) {
           }
         }
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
+        for (int q = 0; q < kQX; ++q) {
           const int m = mrow + 32 * q;
           if (m >= a.M) continue;
           TO o[4];
@@ -281,9 +316,9 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(TileArgs a) {
     // c = n0 / 2 + wn * 64 + 32 (p % 2) + 8g + 4(l / 32) + i; N = 2 I
     const int I = a.N / 2;
     const int cbase = n0 / 2 + wn * 64 + 4 * lc;
-    float st[4];
+    float st[kQX];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < kQX; ++q) {
       st[q] = 1.f;
       if constexpr (EPI == EPI_DEQ_SILU) st[q] = a.s_tok[min(mrow + 32 * q, a.M - 1)];
     }
@@ -303,7 +338,7 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(TileArgs a) {
           }
         }
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
+        for (int q = 0; q < kQX; ++q) {
           const int m = mrow + 32 * q;
           if (m >= a.M) continue;
           TO o[4];
@@ -344,16 +379,32 @@ __global__ void interleave_gate_up_kernel(const u32x4* __restrict__ W, int64_t l
   out[u] = W[src * ldw16 + c];
 }
 
+// The kernel addresses its copy sources with 32-bit row offsets: the weight
+// must span less than 4 GiB (checked by the entry points), and the
+// activation rows are launched in chunks that do.
 template <typename T, typename TO, int EPI>
 int launch_tiles(const TileArgs& a0, hipStream_t stream) {
-  TileArgs a = a0;
-  a.tiles_m = ll_cdiv(a.M, kT);
-  a.tiles_n = ll_cdiv(a.N, kT);
-  const int tiles = a.tiles_m * a.tiles_n;
-  const int grid = 8 * ((tiles + 7) / 8);
-  hipLaunchKernelGGL((gemm_tile_kernel<T, TO, EPI>), dim3((unsigned)grid), dim3(256),
-                     (size_t)kNst * kStageB, stream, a);
-  LL_RETURN_LAUNCH();
+  const int64_t max_rows = (((int64_t)1 << 32) - 2 * kRB) / a0.ldx_b;
+  const int64_t chunk = max_rows >= a0.M ? a0.M : (max_rows / kT) * kT;
+  for (int64_t mo = 0; mo < a0.M; mo += chunk) {
+    TileArgs a = a0;
+    a.X += mo * a0.ldx_b;
+    a.Y = (char*)a0.Y + mo * a0.ldy * (int64_t)sizeof(TO);
+    if (a0.s_tok != nullptr) a.s_tok = a0.s_tok + mo;
+    a.M = (int)(a0.M - mo < chunk ? a0.M - mo : chunk);
+    a.tiles_m = ll_cdiv(a.M, kT);
+    a.tiles_n = ll_cdiv(a.N, kT);
+    const int tiles = a.tiles_m * a.tiles_n;
+    const int grid = 8 * ((tiles + 7) / 8);
+    hipLaunchKernelGGL((gemm_tile_kernel<T, TO, EPI>), dim3((unsigned)grid), dim3(kThreads),
+                       (size_t)kNst * kStageB, stream, a);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+      ll_set_error("HIP launch failed: %s", hipGetErrorString(e));
+      return LL_ERR_HIP;
+    }
+  }
+  return LL_OK;
 }
 
 int check_tile_args(const char* name, const void* X, int64_t ldx, const void* W, int64_t ldw,
@@ -366,6 +417,8 @@ int check_tile_args(const char* name, const void* X, int64_t ldx, const void* W,
                    (((uintptr_t)X | (uintptr_t)W) % 16) == 0,
                "%s: X and W rows must be 16 B aligned", name);
   LL_CHECK_ARG(M <= INT32_MAX && N <= INT32_MAX && K_b <= INT32_MAX, "%s: shape too large", name);
+  LL_CHECK_ARG((N - 1) * ldw * es + K_b < ((int64_t)1 << 32) && ldx * es < ((int64_t)1 << 31),
+               "%s: the weight must span less than 4 GiB", name);
   return LL_OK;
 }
 
