@@ -312,6 +312,52 @@ def bench_config5(dev, steps=300, warmup=2):
             "weight_bytes_per_step": int(wbytes)}
 
 
+def bench_prefill_gemms(dev, M=B * PROMPT, reps=20):
+    """The prefill projections of the 3B shape at M = 40 x 600 tokens on the
+    tile GEMMs (bf16: qkv, o, gate/up with the SiLU_and_Mul epilogue, down;
+    W8A8: the dequantising int8 kernels), events around `reps` launches each."""
+    from lite_lang_amd import ops
+    from lite_lang_amd.models.qwen2.weights import qwen25_3b_config
+    cfg = qwen25_3b_config()
+    hd, I = cfg.hidden_size, cfg.intermediate_size
+    qkv_n = (cfg.num_heads + 2 * cfg.num_key_value_heads) * cfg.head_dim
+    g = torch.Generator(device=dev).manual_seed(5)
+    out = {}
+
+    def timed(name, flops, fn):
+        fn()
+        torch.cuda.synchronize(dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize(dev)
+        us = e0.elapsed_time(e1) / reps * 1e3
+        out[name] = {"us": round(us, 1), "tflops": round(flops / us / 1e6, 1)}
+
+    for name, N, K in [("qkv", qkv_n, hd), ("o", hd, cfg.num_heads * cfg.head_dim),
+                       ("gate_up_silu", 2 * I, hd), ("down", hd, I)]:
+        x = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
+        w = (torch.randn(N, K, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+        if name == "gate_up_silu":
+            wil = ops.interleave_gate_up(w)
+            timed("bf16_" + name, 2.0 * M * N * K, lambda: ops.gate_up_silu_tiled(x, wil))
+        else:
+            timed("bf16_" + name, 2.0 * M * N * K, lambda: ops.gemm_tiled(x, w))
+        qw = ops.QuantWeight(w, gate_up=(name == "gate_up_silu"))
+        xq, st = ops.quant_per_token(x)
+        if name == "gate_up_silu":
+            timed("w8a8_" + name, 2.0 * M * N * K,
+                  lambda: ops.gemm_i8_gate_up_silu_tiled(xq, st, qw.q_il, qw.scale))
+        else:
+            timed("w8a8_" + name, 2.0 * M * N * K,
+                  lambda: ops.gemm_i8_tiled(xq, st, qw.q, qw.scale))
+        del x, w, qw, xq, st
+        torch.cuda.empty_cache()
+    return out
+
+
 # ------------------------------------------------------------------ main
 def main():
     ap = argparse.ArgumentParser()
@@ -325,6 +371,9 @@ def main():
     ap.add_argument("--attention-sweep", action="store_true",
                     help="time the config-2 decode attention at contexts 16..2400 (random "
                          "slot table; identity table at 600 and 1200), one JSON line each")
+    ap.add_argument("--prefill-gemm", action="store_true",
+                    help="time the 3B prefill projections (M = 24,000) on the tile GEMMs, "
+                         "bf16 and W8A8, one JSON line")
     ap.add_argument("--attention-only", action="store_true",
                     help="run only the config-2 decode attention launches plus a 256 MiB "
                          "device copy of known size (for rocprofv3 --pmc traffic runs)")
@@ -356,6 +405,9 @@ def main():
                               "us": round(sec * 1e6, 3), "bytes": nb,
                               "gbs": round(nb / sec / 1e9, 1)}), flush=True)
             torch.cuda.empty_cache()
+        return
+    if args.prefill_gemm:
+        print(json.dumps(bench_prefill_gemms(dev)), flush=True)
         return
     if args.attention_only:
         src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
