@@ -15,11 +15,11 @@
 // size is a multiple of 4, else 4), so every K/V tile staged in LDS serves 256
 // query rows. Per 64-key tile:
 //   * K and V rows are loaded through the slot table into registers while the
-//     previous tile is computed, then stored to LDS: K with its 16-byte chunks
-//     XOR-swizzled by row so that the MFMA operand reads are bank-conflict
-//     free, V transposed (4 keys x 8 d per thread) as V^T [d][key], the keys
-//     of every 16-key group permuted so that the 8 keys one MFMA lane needs
-//     form one 16-byte chunk (no copy into LDS is in flight while the tile is
+//     previous tile is computed, then stored to LDS key-major, their 16-byte
+//     chunks XOR-swizzled by row so that the MFMA operand reads are
+//     bank-conflict free; the P.V operand V^T is read from the key-major V
+//     tile with the gfx950 transposing LDS read (ds_read_b64_tr_b16), so no
+//     VALU work transposes V (no copy into LDS is in flight while the tile is
 //     computed, so its LDS reads wait for no global load);
 //   * each wave computes S^T = K . Q^T (2 key blocks of 32, Q^T fragments in
 //     registers, v_mfma_f32_32x32x16), the online softmax in the exp2 domain
@@ -61,29 +61,30 @@ struct PrefillArgs {
 };
 
 template <int D> struct FaGeom {
-  static constexpr int ROWB = D * 2;            // bytes of a K row
-  static constexpr int CH = ROWB / 16;          // 16 B chunks per K row
-  static constexpr int VTB = kBK * 2;           // bytes of a V^T row
-  static constexpr int K_B = kBK * ROWB;        // K tile
-  static constexpr int STAGE_B = K_B + D * VTB; // K tile, then V^T
-  static constexpr int VDG = D / 8;             // 8-wide d groups of a V row
+  static constexpr int ROWB = D * 2;            // bytes of a K or V row
+  static constexpr int CH = ROWB / 16;          // 16 B chunks per row
+  static constexpr int K_B = kBK * ROWB;        // K tile (V tile the same)
+  static constexpr int STAGE_B = 2 * K_B;       // K tile, then V tile
   // LDS chunk position of K chunk c of row r (an involution): the operand
   // reads of 16 lanes (16 rows, one chunk) hit 16 distinct 16 B bank slots
   static __device__ __forceinline__ int kswz(int c, int r) {
     return ROWB == 256 ? (c ^ (r & 15)) : (c ^ ((r >> 1) & 7));
   }
-  // V^T row d: chunk c of the (permuted) key positions. Rows are 128 B: the
-  // reads of 8 lanes (rows d..d+7, one chunk) hit 8 distinct chunks of a
-  // 128 B bank row, and those of 16 lanes 16 distinct slots of 256 B.
-  static __device__ __forceinline__ int vswz(int c, int d) { return c ^ (d & 7) ^ ((d >> 3) & 1); }
+  // LDS chunk position of V chunk c of row (key) r: a transposing read
+  // (ds_read_b64_tr_b16) of one P.V fragment touches 8 consecutive keys x 4
+  // consecutive chunks; this spreads them over all 16 bank slots of 256 B
+  // (each slot twice, the minimum for 512 B)
+  static __device__ __forceinline__ int vswz(int c, int r) {
+    return ROWB == 256 ? (c ^ ((r & 3) << 2)) : (c ^ (((r >> 1) & 1) << 2));
+  }
 };
 
-// position of tile key k in a V^T row: within each 16-key group, keys
-// 0-3, 8-11 | 4-7, 12-15, so MFMA lane half h reads keys 4h..4h+3 and
-// 8+4h..8+4h+3 of the group as one 16-byte chunk
-__device__ __forceinline__ int vt_pos(int k) {
-  const int k16 = k & 15;
-  return (k & ~15) | (((k16 >> 2) & 1) << 3) | (((k16 >> 3) & 1) << 2) | (k16 & 3);
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+// ds_read_b64_tr_b16: within each group of 16 lanes, lane i receives element
+// i % 4 of the 8 bytes addressed by lane 4 e + i / 4, as its element e
+__device__ __forceinline__ s16x4 lds_read_tr16(const char* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4*)(__attribute__((address_space(3))) char*)p);
 }
 
 // WPH: waves (of 32 query rows each) per head; the 8 waves of a workgroup
@@ -156,59 +157,33 @@ __global__ __launch_bounds__(512) void prefill_attn_fa_kernel(PrefillArgs a) {
   // flight, the compute's LDS reads need no wait on the global loads.
   const T* kbase = (const T*)a.k + (int64_t)kvh * a.k_sh;
   const T* vbase = (const T*)a.v + (int64_t)kvh * a.v_sh;
-  // K geometry: thread -> rows kr + KRS u (u < KR), 16-byte chunk kc; the
-  // lanes of one row write its whole LDS row (a permutation of the chunks)
-  constexpr int KR = kBK * FG::CH / NT;  // K chunks per thread per tile
+  // K and V geometry: thread -> rows kr + KRS u (u < KR), 16-byte chunk kc;
+  // the lanes of one row write its whole LDS row (a permutation of the
+  // chunks). V rows stay key-major in LDS and are transposed by the reads.
+  constexpr int KR = kBK * FG::CH / NT;  // chunks per thread per tile (each of K and V)
   constexpr int KRS = NT / FG::CH;       // rows covered per pass
   const int kc = threadIdx.x % FG::CH, kr = threadIdx.x / FG::CH;
-  // V geometry: thread -> 4 keys x 8 d, the 16 key groups of a tile over
-  // consecutive lanes (so the 16 lanes writing one V^T row cover its 128 bytes
-  // once); threads past 16 * VDG idle
-  const int vkg = threadIdx.x & 15, vdg = threadIdx.x >> 4;
-  const bool v_on = vdg < FG::VDG;
-  int32_t ksl[KR], vsl[4];  // slot ids of the next tile's K rows / V rows
+  int32_t ksl[KR];  // slot ids of the next tile's rows
   auto load_slots = [&](int t0) {
 #pragma unroll
     for (int u = 0; u < KR; ++u) ksl[u] = slot_row[min(t0 + kr + KRS * u, kv_end - 1)];
-    if (v_on) {
+  };
+  V8 kreg[KR], vreg[KR];
+  auto issue = [&]() {  // global loads of the tile whose slots are in ksl
 #pragma unroll
-      for (int i = 0; i < 4; ++i) vsl[i] = slot_row[min(t0 + 4 * vkg + i, kv_end - 1)];
+    for (int u = 0; u < KR; ++u) {
+      kreg[u] = *(const V8*)(kbase + (int64_t)ksl[u] * a.k_st + 8 * kc);
+      vreg[u] = *(const V8*)(vbase + (int64_t)ksl[u] * a.v_st + 8 * kc);
     }
   };
-  V8 kreg[KR], vreg[4];
-  auto issue = [&]() {  // global loads of the tile whose slots are in ksl/vsl
-#pragma unroll
-    for (int u = 0; u < KR; ++u) kreg[u] = *(const V8*)(kbase + (int64_t)ksl[u] * a.k_st + 8 * kc);
-    if (v_on) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) vreg[i] = *(const V8*)(vbase + (int64_t)vsl[i] * a.v_st + 8 * vdg);
-    }
-  };
-  auto store = [&](int buf) {  // the loaded rows into LDS: K swizzled, V transposed
+  auto store = [&](int buf) {  // the loaded rows into LDS, chunks swizzled
     char* kl = smem + buf * FG::STAGE_B;
+    char* vl = kl + FG::K_B;
 #pragma unroll
     for (int u = 0; u < KR; ++u) {
       const int r = kr + KRS * u;
       *(V8*)(kl + r * FG::ROWB + FG::kswz(kc, r) * 16) = kreg[u];
-    }
-    if (!v_on) return;
-    char* vt = kl + FG::K_B;
-    const int pk = vt_pos(4 * vkg);  // positions pk .. pk+3 (one 8-byte half chunk)
-    uint32_t w[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const u32x4 u = __builtin_bit_cast(u32x4, vreg[i]);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) w[i][e] = u[e];
-    }
-#pragma unroll
-    for (int dd = 0; dd < 8; ++dd) {
-      const int d = 8 * vdg + dd;
-      const int e = dd >> 1, sh = (dd & 1) * 16;
-      const uint32_t lo = ((w[0][e] >> sh) & 0xffffu) | (((w[1][e] >> sh) & 0xffffu) << 16);
-      const uint32_t hi = ((w[2][e] >> sh) & 0xffffu) | (((w[3][e] >> sh) & 0xffffu) << 16);
-      typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-      *(u32x2*)(vt + d * FG::VTB + FG::vswz(pk >> 3, d) * 16 + (pk & 7) * 2) = (u32x2){lo, hi};
+      *(V8*)(vl + r * FG::ROWB + FG::vswz(kc, r) * 16) = vreg[u];
     }
   };
 
@@ -286,8 +261,23 @@ __global__ __launch_bounds__(512) void prefill_attn_fa_kernel(PrefillArgs a) {
   // key steps (step s = keys 16 s + {4hf..4hf+3, 8+4hf..8+4hf+3}: S^T block
   // kb = s / 2, g = 2 (s % 2) and g + 1), the row sums into l_run, then
   // O^T[d 32 db + 8 g + 4 hf + i][query 32 qb + l32] += V^T . P^T
+  // V^T fragment of key step s, d block db (A operand: lane -> d = 32 db +
+  // l32, k-slots 8 hf .. 8 hf + 7 = keys 16 s + 4 hf + {0..3} and
+  // 16 s + 8 + 4 hf + {0..3}, the order of the P^T fragments): two
+  // transposing reads, the 16-lane group g = lane / 16 reading keys
+  // 16 s + 4 (g / 2) + j / 4 (+ 8), d 32 db + 16 (g % 2) + 4 (j % 4) .. + 3
+  const int tg = lane >> 4, tj = lane & 15;
+  auto vfrag = [&](const char* vl, int s, int db) -> V8 {
+    const int key = 16 * s + 4 * (tg >> 1) + (tj >> 2);
+    const int dbyte = 64 * db + 32 * (tg & 1) + 8 * (tj & 3);
+    const int c = dbyte >> 4, off = dbyte & 15;
+    const s16x4 lo = lds_read_tr16(vl + key * FG::ROWB + FG::vswz(c, key) * 16 + off);
+    const s16x4 hi = lds_read_tr16(vl + (key + 8) * FG::ROWB + FG::vswz(c, key + 8) * 16 + off);
+    typedef short s16x8 __attribute__((ext_vector_type(8)));
+    return __builtin_bit_cast(V8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  };
   auto accumulate = [&](int buf) {
-    const char* vt = smem + buf * FG::STAGE_B + FG::K_B;
+    const char* vl = smem + buf * FG::STAGE_B + FG::K_B;
     V8 pf[QB][4];
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
@@ -310,8 +300,7 @@ __global__ __launch_bounds__(512) void prefill_attn_fa_kernel(PrefillArgs a) {
     for (int s = 0; s < 4; ++s)
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
-        const int d = 32 * db + l32;
-        const V8 va = *(const V8*)(vt + d * FG::VTB + FG::vswz(2 * s + hf, d) * 16);
+        const V8 va = vfrag(vl, s, db);
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) acc[db][qb] = mfma32(va, pf[qb][s], acc[db][qb]);
       }
