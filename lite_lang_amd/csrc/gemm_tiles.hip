@@ -25,8 +25,9 @@
 //     wave per SIMD reaches about 150 B/clk of LDS reads per CU, two about
 //     240);
 //   * the grid is XCD-aware: the workgroups the dispatcher deals to one XCD
-//     take a contiguous range of tiles in 4-row-tile groups, so tiles sharing
-//     activation or weight rows run together on one L2.
+//     take a contiguous range of tiles in 2-row-tile groups, so tiles sharing
+//     activation or weight rows run together on one L2 (group sizes 1-16
+//     measured: 2 is best or level on every prefill shape).
 // Epilogues: the model dtype with an optional bias; SiLU_and_Mul of a
 // gate/up weight interleaved in 64-row blocks (ll_gemm_interleave_gate_up),
 // with the rounding sequence of ll_silu_and_mul; int8 sums dequantised as
@@ -40,7 +41,7 @@ constexpr int kT = 256;        // output tile: 256 activation rows x 256 weight 
 constexpr int kRB = 64;        // bytes of K per row per stage
 constexpr int kStageB = 2 * kT * kRB;  // 32 KB: weight rows, then activation rows
 constexpr int kNst = 5;        // stage buffers (160 KB of LDS)
-constexpr int kGroupM = 4;     // row tiles per group of the tile order
+constexpr int kGroupM = 2;     // row tiles per group of the tile order (2 measured best of 1-16)
 constexpr int kWaves = 8;      // two per SIMD
 constexpr int kThreads = 64 * kWaves;
 constexpr int kPW = 4;         // 32-row weight blocks per wave (128 rows: wave column wn of 2)

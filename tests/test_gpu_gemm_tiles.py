@@ -133,3 +133,26 @@ def test_gemm_i8_i32_any_shape_exact(cuda, M, N, K, pad):
     print(f"case: gemm_i8_i32 M={M} N={N} K={K} pad={pad}", flush=True)
     got = _ops().gemm_i8_i32(xfull.to(cuda)[:, :K], wq.to(cuda)).cpu()  # row stride K + pad
     assert torch.equal(got, O.int8_gemm_i32(xfull[:, :K].contiguous(), wq))
+
+
+def test_gemm_tiled_rows_past_4gib_chunked_bit_exact(cuda):
+    """Activations spanning more than 4 GiB are launched in row chunks (the
+    kernel's source offsets are 32-bit): the rows around the first chunk
+    boundary equal the same kernel's result on those rows alone (a
+    size-independent property; the oracle would take minutes at this size)."""
+    K, N = 2048, 256
+    row_b = K * 2
+    chunk = ((((1 << 32) - 128) // row_b) // 256) * 256  # rows per launch, as the host computes
+    M = chunk + 1024
+    ops = _ops()
+    g = torch.Generator(device=cuda).manual_seed(88)
+    print(f"case: gemm_tiled M={M} (chunk {chunk}) N={N} K={K}", flush=True)
+    x = torch.randn(M, K, device=cuda, generator=g).to(torch.bfloat16)
+    w = (torch.randn(N, K, device=cuda, generator=g) * 0.05).to(torch.bfloat16)
+    y = ops.gemm_tiled(x, w)
+    lo, hi = chunk - 512, chunk + 512
+    ref = ops.gemm_tiled(x[lo:hi].contiguous(), w)
+    assert torch.equal(y[lo:hi], ref)
+    assert torch.equal(y[-300:], ops.gemm_tiled(x[-300:].contiguous(), w))
+    del x, y
+    torch.cuda.empty_cache()
