@@ -572,7 +572,18 @@ extern "C" int ll_gemm_i8_i32(const int8_t* Xq, int64_t ldx, const int8_t* Wq, i
                     ((uintptr_t)Y) % 16 == 0;
   if (tile) return ll_gemm_i8_i32_tiled(Xq, ldx, Wq, ldw, Y, ldy, M, N, K, stream);
   const int vec4 = ldx % 4 == 0 && ldw % 4 == 0 && (((uintptr_t)Xq | (uintptr_t)Wq) % 4) == 0;
-  hipLaunchKernelGGL(gemm_i8_plain_kernel, dim3((unsigned)ll_cdiv(N, 64), (unsigned)ll_cdiv(M, 4)),
-                     dim3(256), 0, stream, Xq, ldx, Wq, ldw, Y, ldy, (int)M, (int)N, (int)K, vec4);
-  LL_RETURN_LAUNCH();
+  // rows in launches of at most 65535 blocks of 4 (the grid's y limit)
+  constexpr int64_t kRowsPerLaunch = 65535 * 4;
+  for (int64_t m0 = 0; m0 < M; m0 += kRowsPerLaunch) {
+    const int64_t mr = M - m0 < kRowsPerLaunch ? M - m0 : kRowsPerLaunch;
+    hipLaunchKernelGGL(gemm_i8_plain_kernel, dim3((unsigned)ll_cdiv(N, 64), (unsigned)ll_cdiv(mr, 4)),
+                       dim3(256), 0, stream, Xq + m0 * ldx, ldx, Wq, ldw, Y + m0 * ldy, ldy, (int)mr,
+                       (int)N, (int)K, vec4);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+      ll_set_error("HIP launch failed: %s", hipGetErrorString(e));
+      return LL_ERR_HIP;
+    }
+  }
+  return LL_OK;
 }
