@@ -122,11 +122,12 @@ def test_gemm_i8_gate_up_silu_tiled_bit_exact(cuda):
 
 
 @pytest.mark.parametrize("M,N,K,pad", [(70, 100, 36, 0), (300, 50, 100, 3), (129, 256, 128, 0),
-                                       (65, 2048, 8960, 0)])
+                                       (65, 2048, 8960, 0), (262200, 8, 36, 0)])
 def test_gemm_i8_i32_any_shape_exact(cuda, M, N, K, pad):
     """ll_gemm_i8_i32 (the W8A8 prefill product): the tile kernel where its
     layout holds, the plain dot-product kernel elsewhere (K % 64 != 0, odd
-    row strides); exact int32 sums either way."""
+    row strides; more than 65535 x 4 rows in several launches); exact int32
+    sums either way."""
     g = torch.Generator().manual_seed(87)
     xfull = torch.randint(-128, 128, (M, K + pad), generator=g, dtype=torch.int8)
     wq = torch.randint(-128, 128, (N, K), generator=g, dtype=torch.int8)
