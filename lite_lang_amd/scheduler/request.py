@@ -50,6 +50,7 @@ class Req:
     is_prefill: bool = True
     output_length: int = 0
     is_end: bool = False
+    refused: bool = False  # not queued: max_reqs requests were already waiting
 
     @property
     def length(self) -> int:

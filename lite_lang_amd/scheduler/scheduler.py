@@ -50,7 +50,7 @@ class Scheduler:
                        prompt="") -> Req:
         """add_req for callers that already hold token ids. A request arriving
         while max_reqs are waiting is not queued (it never runs), as in the
-        reference."""
+        reference; its `refused` flag tells the caller."""
         toks = [int(t) for t in input_tokens]
         req = Req(id=self._submitted % MAX_REQUEST_ID, status=ReqStatus.READY, prompt=prompt,
                   input_tokens=toks, output_tokens=[], max_total_length=self.max_total_length,
@@ -58,7 +58,7 @@ class Scheduler:
                   temperature=temperature, top_p=top_p, top_k=top_k, do_sample=do_sample,
                   input_length=len(toks), eos_token=self.tokenizer.eos_token_id)
         self._submitted += 1
-        self._room.submit(req)
+        req.refused = not self._room.submit(req)
         return req
 
     def has_work(self) -> bool:
