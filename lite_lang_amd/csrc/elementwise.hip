@@ -82,6 +82,97 @@ __global__ __launch_bounds__(BLOCK) void rmsnorm_kernel(
   }
 }
 
+// The same three forms for rows of N % 8 == 0 elements on 16-byte aligned
+// rows (the model's hidden states): each thread holds up to C chunks of 8
+// elements in registers (N <= 2048 C), so every element is read once with a
+// 16-byte load and written once; the per-thread sum of squares runs over its
+// chunks in order.
+template <typename T, int C>
+__global__ __launch_bounds__(256) void rmsnorm_vec8_kernel(
+    T* __restrict__ x, int64_t x_rs, const T* __restrict__ residual, int64_t r_rs,
+    const T* __restrict__ gamma, T* __restrict__ out, int64_t o_rs, int N, float eps,
+    const T* __restrict__ table, int64_t tab_rs, const void* ids, int ids64, int64_t vocab) {
+  typedef T V8 __attribute__((ext_vector_type(8)));
+  const int row = blockIdx.x, nch = N / 8;
+  T* xr = x + (int64_t)row * x_rs;
+  const T* src = xr;
+  if (table != nullptr) {
+    int64_t id = ll_load_idx(ids, row, ids64);
+    id = id < 0 ? 0 : (id >= vocab ? vocab - 1 : id);
+    src = table + id * tab_rs;
+  }
+  V8 h[C];
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const int ch = threadIdx.x + 256 * c;
+    if (ch < nch) {
+      V8 v = *(const V8*)(src + 8 * ch);
+      if (residual != nullptr) {
+        const V8 r = *(const V8*)(residual + (int64_t)row * r_rs + 8 * ch);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = ll_from_f32<T>(ll_to_f32(v[e]) + ll_to_f32(r[e]));
+      }
+      if (table != nullptr || residual != nullptr) *(V8*)(xr + 8 * ch) = v;
+      h[c] = v;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float f = ll_to_f32(v[e]);
+        ss += f * f;
+      }
+    }
+  }
+  __shared__ float red[4];
+  ss = ll_wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float tot = red[0] + red[1] + red[2] + red[3];
+  // reference: x / sqrt(sum(x^2)/N + eps) * gamma, all in fp32
+  const float denom = sqrtf(tot / (float)N + eps);
+  T* orow = out + (int64_t)row * o_rs;
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const int ch = threadIdx.x + 256 * c;
+    if (ch < nch) {
+      const V8 g = *(const V8*)(gamma + 8 * ch);
+      V8 o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = ll_from_f32<T>(ll_to_f32(h[c][e]) / denom * ll_to_f32(g[e]));
+      *(V8*)(orow + 8 * ch) = o;
+    }
+  }
+}
+
+// Launch of the RMSNorm forms: the 16-byte kernel when N % 8 == 0, N <= 8192
+// and every row is 16-byte aligned, the element-wise kernel otherwise.
+template <typename T>
+int launch_rmsnorm(T* x, int64_t x_rs, const T* residual, int64_t r_rs, const T* gamma, T* out,
+                   int64_t o_rs, int64_t M, int64_t N, float eps, const T* table, int64_t tab_rs,
+                   const void* ids, int ids64, int64_t vocab, hipStream_t stream) {
+  const auto al16 = [](const void* p, int64_t rs) {
+    return ((uintptr_t)p % 16) == 0 && (rs * (int64_t)sizeof(T)) % 16 == 0;
+  };
+  const bool vec = N % 8 == 0 && N <= 8192 && al16(x, x_rs) && al16(gamma, 0) && al16(out, o_rs) &&
+                   (residual == nullptr || al16(residual, r_rs)) &&
+                   (table == nullptr || al16(table, tab_rs));
+  if (vec) {
+    const int C = (int)((N + 2047) / 2048);
+    auto go = [&](auto kern) {
+      hipLaunchKernelGGL(kern, dim3((unsigned)M), dim3(256), 0, stream, x, x_rs, residual, r_rs,
+                         gamma, out, o_rs, (int)N, eps, table, tab_rs, ids, ids64, vocab);
+    };
+    if (C == 1) go(rmsnorm_vec8_kernel<T, 1>);
+    else if (C == 2) go(rmsnorm_vec8_kernel<T, 2>);
+    else if (C == 3) go(rmsnorm_vec8_kernel<T, 3>);
+    else go(rmsnorm_vec8_kernel<T, 4>);
+  } else {
+    hipLaunchKernelGGL((rmsnorm_kernel<T, 256>), dim3((unsigned)M), dim3(256), 0, stream, x, x_rs,
+                       residual, r_rs, gamma, out, o_rs, (int)N, eps, table, tab_rs, ids, ids64,
+                       vocab);
+  }
+  LL_RETURN_LAUNCH();
+}
+
 extern "C" int ll_rmsnorm(void* x, int64_t x_row_stride, const void* residual,
                           int64_t residual_row_stride, const void* gamma, void* out,
                           int64_t out_row_stride, int64_t M, int64_t N, float eps,
@@ -91,11 +182,9 @@ extern "C" int ll_rmsnorm(void* x, int64_t x_row_stride, const void* residual,
                (long long)N);
   if (M == 0) return LL_OK;
   return LL_DISPATCH_DTYPE(dtype, T, [&]() -> int {
-    hipLaunchKernelGGL((rmsnorm_kernel<T, 256>), dim3((unsigned)M), dim3(256), 0, stream,
-                       (T*)x, x_row_stride, (const T*)residual, residual_row_stride,
-                       (const T*)gamma, (T*)out, out_row_stride, (int)N, eps, (const T*)nullptr,
-                       (int64_t)0, (const void*)nullptr, 0, (int64_t)0);
-    LL_RETURN_LAUNCH();
+    return launch_rmsnorm<T>((T*)x, x_row_stride, (const T*)residual, residual_row_stride,
+                             (const T*)gamma, (T*)out, out_row_stride, M, N, eps, nullptr, 0,
+                             nullptr, 0, 0, stream);
   });
 }
 
@@ -110,11 +199,9 @@ extern "C" int ll_embedding_rmsnorm(const void* table, int64_t table_row_stride,
   LL_CHECK_ARG(vocab > 0 && ntok >= 0 && hidden > 0, "ll_embedding_rmsnorm: bad shape");
   if (ntok == 0) return LL_OK;
   return LL_DISPATCH_DTYPE(dtype, T, [&]() -> int {
-    hipLaunchKernelGGL((rmsnorm_kernel<T, 256>), dim3((unsigned)ntok), dim3(256), 0, stream,
-                       (T*)h, h_row_stride, (const T*)nullptr, (int64_t)0, (const T*)gamma,
-                       (T*)out, out_row_stride, (int)hidden, eps, (const T*)table,
-                       table_row_stride, ids, ids_i64, vocab);
-    LL_RETURN_LAUNCH();
+    return launch_rmsnorm<T>((T*)h, h_row_stride, nullptr, 0, (const T*)gamma, (T*)out,
+                             out_row_stride, ntok, hidden, eps, (const T*)table, table_row_stride,
+                             ids, ids_i64, vocab, stream);
   });
 }
 
@@ -341,7 +428,7 @@ __global__ void silu_and_mul_kernel(const T* x, int64_t x_rs, T* out, int64_t o_
   const int n = (int)(gid - m * N);
   const float g = ll_to_f32(x[m * x_rs + n]);
   const float u = ll_to_f32(x[m * x_rs + n + N]);
-  const T s = ll_from_f32<T>(g / (1.0f + __expf(-g)));
+  const T s = ll_from_f32<T>(ll_silu_f32(g));
   out[m * o_rs + n] = ll_from_f32<T>(u * ll_to_f32(s));
 }
 
@@ -361,7 +448,7 @@ __global__ __launch_bounds__(256) void silu_and_mul_vec8_kernel(const T* x, int6
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const float g = ll_to_f32(g8[e]);
-    const T s = ll_from_f32<T>(g / (1.0f + __expf(-g)));
+    const T s = ll_from_f32<T>(ll_silu_f32(g));
     o8[e] = ll_from_f32<T>(ll_to_f32(u8[e]) * ll_to_f32(s));
   }
   *(V8*)(out + m * o_rs + n) = o8;
@@ -773,7 +860,7 @@ __global__ void silu_and_mul_splitk_kernel(LLPartials P, T* __restrict__ out, in
   for (int e = 0; e < 4; ++e) {
     const float g = ll_to_f32(ll_from_f32<T>(g4[e]));
     const float u = ll_to_f32(ll_from_f32<T>(u4[e]));
-    const T sv = ll_from_f32<T>(g / (1.0f + __expf(-g)));
+    const T sv = ll_from_f32<T>(ll_silu_f32(g));
     op[e] = ll_from_f32<T>(u * ll_to_f32(sv));
   }
 }

@@ -304,7 +304,7 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, 
       for (int e = 0; e < 4; ++e) {
         const float g = ll_to_f32(ll_from_f32<TO>(g4[e]));
         const float u = ll_to_f32(ll_from_f32<TO>(u4[e]));
-        const TO sv = ll_from_f32<TO>(g / (1.0f + __expf(-g)));
+        const TO sv = ll_from_f32<TO>(ll_silu_f32(g));
         y[e] = ll_from_f32<TO>(u * ll_to_f32(sv));
       }
       const int c0 = blockIdx.x * HALF + cq;

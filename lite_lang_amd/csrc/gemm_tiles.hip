@@ -387,7 +387,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tile_kernel(TileArgs a) {
               }
               const float gv = ll_to_f32(ll_from_f32<TO>(gs));
               const float u = ll_to_f32(ll_from_f32<TO>(us));
-              const TO sv = ll_from_f32<TO>(gv / (1.0f + __expf(-gv)));
+              const TO sv = ll_from_f32<TO>(ll_silu_f32(gv));
               o[i] = ll_from_f32<TO>(u * ll_to_f32(sv));
             }
             const uint32_t off = (c_ok && m < a.M)

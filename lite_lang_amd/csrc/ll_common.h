@@ -56,6 +56,16 @@ __device__ __forceinline__ _Float16 ll_from_f32<_Float16>(float x) { return (_Fl
 template <>
 __device__ __forceinline__ __bf16 ll_from_f32<__bf16>(float x) { return (__bf16)x; }
 
+// silu(g) = g / (1 + exp(-g)) in fp32, the division done as a product with
+// the reciprocal instruction (v_rcp_f32, 1 ulp) rather than the IEEE
+// division sequence: the reference's Triton kernel divides with approximate
+// fp32 division as well (litelang/kernel/develop_silu_and_mul/
+// silu_and_mul.py:45). Every SiLU of the library goes through this function,
+// so the fused GEMM epilogues and the standalone kernels round alike.
+__device__ __forceinline__ float ll_silu_f32(float g) {
+  return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g));
+}
+
 // Index arrays arrive either as int32 or int64 (the reference builds them with
 // torch.tensor(list) -> int64, and the slot table is int32).
 __device__ __forceinline__ int64_t ll_load_idx(const void* p, int64_t i, int is64) {
