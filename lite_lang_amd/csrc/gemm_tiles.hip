@@ -28,9 +28,9 @@
 //     wave per SIMD reaches about 150 B/clk of LDS reads per CU, two about
 //     240);
 //   * the grid is XCD-aware: the workgroups the dispatcher deals to one XCD
-//     take a contiguous range of tiles in 2-row-tile groups, round robin, so
-//     tiles sharing activation or weight rows run together on one L2 (group
-//     sizes 1-16 measured: 2 is best or level on every prefill shape).
+//     take a contiguous range of tiles in groups of 1, 2 or 4 row tiles by
+//     shape (tile_group_m), round robin, so tiles sharing activation or
+//     weight rows run together on one L2.
 // Epilogues: the model dtype with an optional bias; SiLU_and_Mul of a
 // gate/up weight interleaved in 64-row blocks (ll_gemm_interleave_gate_up),
 // with the rounding sequence of ll_silu_and_mul; int8 sums dequantised as
@@ -47,7 +47,6 @@ constexpr int kT = 256;        // output tile: 256 activation rows x 256 weight 
 constexpr int kRB = 64;        // bytes of K per row per stage
 constexpr int kStageB = 2 * kT * kRB;  // 32 KB: weight rows, then activation rows
 constexpr int kNst = 5;        // stage buffers (160 KB of LDS)
-constexpr int kGroupM = 2;     // row tiles per group of the tile order (2 measured best of 1-16)
 constexpr int kWaves = 8;      // two per SIMD
 constexpr int kThreads = 64 * kWaves;
 constexpr int kPW = 4;         // 32-row weight blocks per wave (128 rows: wave column wn of 2)
@@ -101,6 +100,7 @@ struct TileArgs {
   const char* W; int64_t ldw_b;   // weight rows [N][K] (EPI_SILU*: interleaved gate/up)
   int M, N, K_b;                  // K in bytes
   int tiles_m, tiles_n;
+  int group_m;                    // row tiles per group of the tile order (tile_group_m)
   void* Y; int64_t ldy;           // output, row stride in elements of the output type
   int y_bytes;                    // bytes from Y to the end of its last row (< 2^31)
   const void* bias;               // [N] in the model dtype, or null
@@ -117,14 +117,26 @@ __device__ __forceinline__ int tile_swz(int r) { return (r >> 2) & 3; }
 // LDS byte offset of chunk c (16 B) of tile row r within a stage half
 __device__ __forceinline__ int tile_lds_off(int r, int c) { return r * kRB + ((c ^ tile_swz(r)) << 4); }
 
-// Output tile (m0, n0) of tile t of the grouped order: groups of kGroupM row
+// Output tile (m0, n0) of tile t of the grouped order: groups of group_m row
 // tiles, each group's column tiles in order with its row tiles innermost.
 __device__ __forceinline__ void tile_coords(const TileArgs& a, int t, int& m0, int& n0) {
-  const int gsz = kGroupM * a.tiles_n;
+  const int gsz = a.group_m * a.tiles_n;
   const int grp = t / gsz, rin = t - grp * gsz;
-  const int gm = min(kGroupM, a.tiles_m - grp * kGroupM);
-  m0 = (grp * kGroupM + rin % gm) * kT;
+  const int gm = min(a.group_m, a.tiles_m - grp * a.group_m);
+  m0 = (grp * a.group_m + rin % gm) * kT;
   n0 = (rin / gm) * kT;
+}
+
+// Row tiles per group of the tile order, by shape class, as measured on the
+// 3B prefill projections at M = 24,000 (group sizes 1, 2, 4 and 8, libraries
+// interleaved, best of 4 rounds): wide outputs (gate/up, 86 column tiles)
+// 4 (1788 us against 1813 with 2 and 1886-1898 with 1 or 8); long K
+// (down_proj, 172 stages) 1 (916 against 953 with 2); the narrow short-K
+// shapes (qkv, o_proj) level at every size (2).
+int tile_group_m(int64_t tiles_n, int64_t nk) {
+  if (tiles_n >= 32) return 4;
+  if (nk >= 128) return 1;
+  return 2;
 }
 
 // Buffer store of 4 consecutive outputs. A lane whose offset is kTileNoStore
@@ -561,6 +573,7 @@ int launch_tiles(const TileArgs& a0, hipStream_t stream) {
     a.y_bytes = (int)((a.M - 1) * yrow_b + a.N * (int64_t)sizeof(TO));
     a.tiles_m = ll_cdiv(a.M, kT);
     a.tiles_n = (int)tiles_n;
+    a.group_m = tile_group_m(tiles_n, nk);
     const int64_t per = ((int64_t)a.tiles_m * a.tiles_n + 7) / 8;
     const int64_t grid = 8 * std::min<int64_t>(per, std::max(1, cus / 8));
     hipLaunchKernelGGL((gemm_tile_kernel<T, TO, EPI>), dim3((unsigned)grid), dim3(kThreads),
