@@ -32,6 +32,9 @@
 namespace {
 
 constexpr int kBK = 64;   // keys per tile
+// s_waitcnt immediate for vmcnt(0) with expcnt and lgkmcnt left free (gfx9
+// encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
+constexpr int kVmcntZero = 0x0F70;
 
 template <typename T> struct Vec8;
 template <> struct Vec8<__bf16> { typedef bf16x8 type; };
@@ -203,6 +206,13 @@ __global__ __launch_bounds__(512) void prefill_attn_fa_kernel(PrefillArgs a) {
   load_slots(0);
   issue();
   store(0);
+  // every load so far (Q fragments included) has landed. Without this wait
+  // the compiler, which schedules the Q loads after tile 0's, meets them
+  // still outstanding at the loop header and counts vmcnt down to zero in
+  // every iteration's score product, which also waits for that iteration's
+  // prefetch of the next tile (one memory round trip per tile). A real
+  // s_waitcnt (not inline asm) is one the wait-insertion pass accounts for.
+  __builtin_amdgcn_s_waitcnt(kVmcntZero);
   if (kBK < kv_end) load_slots(kBK);
   __syncthreads();
 
