@@ -106,12 +106,21 @@ struct DecodeArgs {
   int8_t* qout; int64_t ldq; float* qscale; const float* qstatic;
 };
 
+// Partial kinds of the fused RoPE kernels (template MODE): 1 = fp32 partials
+// from at most kRopeF32Splits splits, summed by one fixed, branch-free set of
+// loads; 2 = any LLPartials (int32 with scales, or more fp32 splits). Kind 1
+// exists so that its loads are not preceded by the conservative vmcnt(0) the
+// compiler puts where the int32 and fp32 load sequences of a runtime branch
+// share registers: that wait would drain the K/V copies issued just before
+// and put a whole memory round trip in front of the q rebuild.
+constexpr int kRopeF32Splits = 8;
+
 // One job of the fused RoPE: 4 rotation pairs (i..i+3 with i+D/2..i+D/2+3) of
 // the head whose columns start at hcol, with the arithmetic of the split-K
 // RoPE/scatter kernel: sum of the partials in split order, + bias in fp32,
 // rounded to T, rotated in fp32 with explicit FMAs, rounded to T. V heads are
 // only rounded. Results go to LDS and, when glb is set, to global memory.
-template <typename T, int D>
+template <typename T, int D, int PK>
 __device__ __forceinline__ void rope_job(const DecodeArgs& a, int64_t m, int64_t row, int hcol,
                                          int i, const float* cs, const float* sn, bool rotate,
                                          T* lds, T* glb) {
@@ -134,7 +143,11 @@ __device__ __forceinline__ void rope_job(const DecodeArgs& a, int64_t m, int64_t
     sv[e] = sn[i + e];
   }
   f32x4 x0, x1;
-  ll_partials_sum4_pair(a.qkv, row + c0, row + c1, m, c0, c1, x0, x1);
+  if constexpr (PK == 1)
+    ll_sum_splits4_pair_upto<kRopeF32Splits>((const float*)a.qkv.p, a.qkv.splits, a.qkv.sstride,
+                                             row + c0, row + c1, x0, x1);
+  else
+    ll_partials_sum4_pair(a.qkv, row + c0, row + c1, m, c0, c1, x0, x1);
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const float s0 = x0[e] + ll_to_f32(rb0[e]), s1 = x1[e] + ll_to_f32(rb1[e]);
@@ -262,11 +275,12 @@ template <int D> struct TileGeom {
 // have read the slot before the write landed). Precondition: a sequence's new
 // slot appears in no other sequence's first seq_len entries and in its own
 // only within the last split (the decode step puts it at seq_len - 1).
-template <typename T, int D, bool ROPE>
+template <typename T, int D, int MODE>
 __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs a) {
   typedef typename Vec8<T>::type V8;
   typedef typename Vec4<T>::type V4;
   typedef TileGeom<D> TG;
+  constexpr bool ROPE = MODE != 0;  // q from the QKV partials (1: fp32, 2: any kind)
   constexpr int DS = D / 32;  // k-steps of the S^T product
   constexpr int DB = D / 16;  // 16-wide d blocks of the output
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -380,7 +394,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
     const float* sn = a.sin_tab + (int64_t)pos32 * a.tab_stride;
     if ((int)threadIdx.x < a.G * QD) {  // G * QD <= 16 * D / 8 <= 256
       const int g = threadIdx.x / QD, i = (threadIdx.x % QD) * 4;
-      rope_job<T, D>(a, b, qkv_row, (kvh * a.G + g) * D, i, cs, sn, true, s_q + g * D,
+      rope_job<T, D, MODE>(a, b, qkv_row, (kvh * a.G + g) * D, i, cs, sn, true, s_q + g * D,
                      nullptr);
     }
     writer = split == (ntiles > 0 ? (ntiles - 1) / per : 0);
@@ -390,7 +404,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
       const int i = (isv ? jb - QD : jb) * 4;
       T* glb = isv ? (T*)a.v + (int64_t)new_slot * a.v_st + (int64_t)kvh * a.v_sh
                    : (T*)a.k + (int64_t)new_slot * a.k_st + (int64_t)kvh * a.k_sh;
-      rope_job<T, D>(a, b, qkv_row, (a.H + (isv ? a.KVH : 0) + kvh) * D, i, cs, sn,
+      rope_job<T, D, MODE>(a, b, qkv_row, (a.H + (isv ? a.KVH : 0) + kvh) * D, i, cs, sn,
                      !isv, s_kv + (isv ? D : 0), glb);
     }
     __syncthreads();  // s_q and s_kv are complete
@@ -767,14 +781,14 @@ int64_t align256(int64_t x) { return ((x + 255) / 256) * 256; }
 
 
 
-template <int D, bool ROPE>
+template <int D, int MODE>
 void launch_split_stage(const DecodeArgs& a, int dtype, unsigned grid, size_t lds,
                         hipStream_t stream) {
   if (dtype == LL_BF16)
-    hipLaunchKernelGGL((decode_attn_dma_kernel<__bf16, D, ROPE>), dim3(grid), dim3(kWaves * 64),
+    hipLaunchKernelGGL((decode_attn_dma_kernel<__bf16, D, MODE>), dim3(grid), dim3(kWaves * 64),
                        lds, stream, a);
   else
-    hipLaunchKernelGGL((decode_attn_dma_kernel<_Float16, D, ROPE>), dim3(grid), dim3(kWaves * 64),
+    hipLaunchKernelGGL((decode_attn_dma_kernel<_Float16, D, MODE>), dim3(grid), dim3(kWaves * 64),
                        lds, stream, a);
 }
 
@@ -850,14 +864,17 @@ int launch_mfma(DecodeArgs& a, int64_t head_dim, int dtype, bool rope, int64_t m
   const int groups = (a.B + 7) / 8;  // sequences per XCD
   const unsigned grid = (unsigned)(groups * 8 * a.KVH * a.nsplit);
   const size_t extra = (size_t)a.slots_cap * 4 + (rope ? (size_t)(a.G + 2) * head_dim * 2 : 0);
+  const int mode = !rope ? 0 : (!a.qkv.i32 && a.qkv.splits <= kRopeF32Splits) ? 1 : 2;
   if (head_dim == 128) {
     const size_t lds = TileGeom<128>::MAIN_B + extra;
-    if (rope) launch_split_stage<128, true>(a, dtype, grid, lds, stream);
-    else launch_split_stage<128, false>(a, dtype, grid, lds, stream);
+    if (mode == 1) launch_split_stage<128, 1>(a, dtype, grid, lds, stream);
+    else if (mode == 2) launch_split_stage<128, 2>(a, dtype, grid, lds, stream);
+    else launch_split_stage<128, 0>(a, dtype, grid, lds, stream);
   } else {
     const size_t lds = TileGeom<64>::MAIN_B + extra;
-    if (rope) launch_split_stage<64, true>(a, dtype, grid, lds, stream);
-    else launch_split_stage<64, false>(a, dtype, grid, lds, stream);
+    if (mode == 1) launch_split_stage<64, 1>(a, dtype, grid, lds, stream);
+    else if (mode == 2) launch_split_stage<64, 2>(a, dtype, grid, lds, stream);
+    else launch_split_stage<64, 0>(a, dtype, grid, lds, stream);
   }
   if (a.nsplit > 1) {
     if (a.merge_cnt == nullptr) {
