@@ -289,6 +289,32 @@ int ll_gemm_splitk(const void* X, int64_t ldx, const void* W, int64_t ldw, int64
 int ll_add_rmsnorm_splitk(void* h, int64_t h_row_stride, const float* part, int splits,
                           const void* gamma, void* out, int64_t out_row_stride, int64_t M,
                           int64_t N, float eps, int dtype, hipStream_t stream);
+/* add + RMSNorm fused with the next layer's QKV projection, one launch
+ * (replaces ll_add_rmsnorm_splitk + ll_gemm_splitk_packed on the decode
+ * step: litelang/models/qwen2/layer/transformer_layer.py:77 (residual + the
+ * post-MLP norm's successor) and :61, :95-109 (input norm, q/k/v addmm)).
+ * h and x as ll_add_rmsnorm_splitk(h, ld_h, part, splits, gamma, x, hidden,
+ * ...) leaves them, bit for bit; qkv_part [qkv_splits][M][nqkv] gets the
+ * fp32 split-K partials of x . W^T from the ll_gemm_pack image of the
+ * [nqkv, hidden] weight, qkv_splits = ll_add_rmsnorm_qkv_splits(M, hidden,
+ * nqkv) (this kernel's own k split, so they sum in another order than
+ * ll_gemm_splitk_packed's). qkv_part may be part. Norm and GEMM workgroups
+ * meet on flags in `sync` (ll_decode_sync_bytes() bytes, zeroed once); a
+ * call's flags hold *epoch * 256 + tag + 1, which the caller keeps distinct
+ * from every earlier call's on the same sync words (a new *epoch per decode
+ * step, the layer index < 256 as tag). Calls on one sync buffer must not
+ * overlap. */
+int ll_add_rmsnorm_qkv_splits(int64_t M, int64_t hidden, int64_t nqkv); /* 0: not covered */
+int ll_add_rmsnorm_qkv_splitk(void* h, int64_t ld_h, const float* part, int splits,
+                              const void* gamma, float eps, void* x, const void* wqkv_packed,
+                              float* qkv_part, int64_t qkv_part_bytes, int64_t M, int64_t hidden,
+                              int64_t nqkv, int dtype, void* sync, const uint32_t* epoch,
+                              uint32_t tag, hipStream_t stream);
+int64_t ll_decode_sync_bytes(void);
+/* 1 when a flag wait gave up since the last reset (outputs then invalid), else
+ * 0; reset != 0 clears the sync words after such a failure (synchronises
+ * the stream) */
+int ll_decode_sync_status(void* sync, int reset, hipStream_t stream);
 /* part covers [M, 2N] (gate then up); out[m, n] = up * dtype(silu(gate)) */
 int ll_silu_and_mul_splitk(const float* part, int splits, void* out, int64_t out_row_stride,
                            int64_t M, int64_t N, int dtype, hipStream_t stream);

@@ -80,6 +80,11 @@ SIGNATURES = {
     "ll_dequant_splitk": (I32, [P, I32, P, P, I32, P, I64, I64, P]),
     "ll_add_rmsnorm_splitk": (I32, [P, I64, P, I32, P, P, I64, I64, I64, F32, I32, P]),
     "ll_silu_and_mul_splitk": (I32, [P, I32, P, I64, I64, I64, I32, P]),
+    "ll_add_rmsnorm_qkv_splits": (I32, [I64, I64, I64]),
+    "ll_add_rmsnorm_qkv_splitk": (I32, [P, I64, P, I32, P, F32, P, P, P, I64, I64, I64, I64, I32,
+                                        P, P, ctypes.c_uint32, P]),
+    "ll_decode_sync_bytes": (I64, []),
+    "ll_decode_sync_status": (I32, [P, I32, P]),
     "ll_decode_attention_rope_splitk": (I32, [P, I32, P, P, I32, P, P, I64, I32, P, P, I64, I64,
                                               P, I64, I64, P, I64, P, I32, P, I32, P, I64, I64,
                                               I64, I64, I64, I64, I64, F32, I32, P, I64, P]),

@@ -50,6 +50,9 @@ def reserve_model_workspaces(model, batch, max_len):
         ops.reserve_workspace(model.device, "splitk_part", model.splitk_part_numel(batch) * 4)
         if model.quant == "w8a8":
             ops.reserve_workspace(model.device, "w8a8_part", model.w8a8_part_bytes(batch))
+        if model.norm_qkv_splits(batch) > 0:
+            ops.decode_sync(model.device)
+            ops.reserve_workspace(model.device, "decode_epoch", 4)
 
 
 _CAPTURE_STREAMS: dict[int, torch.cuda.Stream] = {}

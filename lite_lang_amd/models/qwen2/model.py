@@ -52,6 +52,7 @@ class Qwen2Model:
         self.cfg = config
         self.dtype = dtype
         self.quant = quant
+        self.fuse_norm_qkv = True  # add + RMSNorm + next QKV in one decode launch
         self.device = torch.device(device)
         self.max_length = max_length
         self.cos, self.sin = rope_tables(max_length, config.head_dim, config.rope_theta,
@@ -131,7 +132,21 @@ class Qwen2Model:
         (W8A8: one dequantised split)."""
         if self.quant == "w8a8":
             return max(batch * n for n, _ in self._proj_shapes())
-        return max(ops.gemm_splitk_count(batch, n, k) * batch * n for n, k in self._proj_shapes())
+        need = max(ops.gemm_splitk_count(batch, n, k) * batch * n for n, k in self._proj_shapes())
+        qs = self.norm_qkv_splits(batch)
+        return max(need, qs * batch * self._proj_shapes()[0][0])
+
+    def norm_qkv_splits(self, batch):
+        """QKV split count of the add + RMSNorm + QKV launch of the fused
+        decode layer (ops.add_rmsnorm_qkv_splitk), 0 where it does not apply:
+        it needs the packed QKV weight of every layer and a shape the kernel
+        covers; fuse_norm_qkv = False turns it off."""
+        if not self.fuse_norm_qkv or self.quant == "w8a8" or not self.fused_decode_ok(batch):
+            return 0
+        if self.w is None or any(pk.get("wqkv") is None for pk in self.w.packed):
+            return 0
+        n, k = self._proj_shapes()[0]
+        return ops.add_rmsnorm_qkv_splits(batch, k, n)
 
     def w8a8_part_bytes(self, batch):
         """int32 partial bytes of the W8A8 projections at this batch size."""
@@ -207,8 +222,13 @@ class Qwen2Model:
                 return ops.gemm_splitk_packed(xin, pk[name], part)
             return ops.gemm_splitk(xin, lw[name], part)
 
+        # layers after the first take their QKV partials from the launch that
+        # finishes the previous layer (residual + RMSNorm + QKV projection)
+        fuse_qkv = self.norm_qkv_splits(B) > 0
+        epoch = ops.decode_epoch_advance(dev) if fuse_qkv else None
+        qkv_s = None
         for li, (lw, pk) in enumerate(zip(w.layers, w.packed)):
-            s = proj(x, lw, pk, "wqkv")
+            s = qkv_s if qkv_s is not None else proj(x, lw, pk, "wqkv")
             self._rope_attention(part, s, lw["bqkv"], q, attn, positions, slots, pool[li], r2t,
                                  rids, seq_len, max_len)
             s = proj(attn.view(B, H * D), lw, pk, "wo")
@@ -219,7 +239,11 @@ class Qwen2Model:
                 s = proj(x2, lw, pk, "wgu")
                 ops.silu_and_mul_splitk(part, s, act)
             s = proj(act, lw, pk, "wdown")
-            if li + 1 < nl:
+            if li + 1 < nl and fuse_qkv:
+                x, qkv_s = ops.add_rmsnorm_qkv_splitk(h, part, s, w.layers[li + 1]["ln1"],
+                                                      cfg.rms_norm_eps, w.packed[li + 1]["wqkv"],
+                                                      part, epoch, li)
+            elif li + 1 < nl:
                 x = ops.add_rmsnorm_splitk(h, part, s, w.layers[li + 1]["ln1"], cfg.rms_norm_eps)
             else:
                 x = ops.add_rmsnorm_splitk(h, part, s, w.norm, cfg.final_norm_eps)

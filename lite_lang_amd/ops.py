@@ -550,6 +550,64 @@ def add_rmsnorm_splitk(h, part, splits, gamma, eps, out=None):
     return out
 
 
+def add_rmsnorm_qkv_splits(M, hidden, nqkv):
+    """k splits of add_rmsnorm_qkv_splitk's QKV partials; 0 when the shape is
+    not covered (then run add_rmsnorm_splitk and the split-K GEMM)."""
+    return int(_L.ll_add_rmsnorm_qkv_splits(M, hidden, nqkv))
+
+
+def decode_sync(device):
+    """The flag words of the fused decode launches on the current stream."""
+    return workspace(device, "decode_sync", int(_L.ll_decode_sync_bytes()))
+
+
+def decode_epoch_advance(device):
+    """Advance the decode-step epoch word (a device-side add, so a captured
+    graph advances it on every replay) and return it: every fused launch of
+    one step uses it with its own tag."""
+    ep = workspace(device, "decode_epoch", 4).view(torch.int32)[:1]
+    ep.add_(1)
+    return ep
+
+
+def decode_sync_status(device, reset=False):
+    """1 when a fused launch's flag wait gave up (its outputs are invalid)."""
+    sync = decode_sync(device)
+    rc = _L.ll_decode_sync_status(sync.data_ptr(), int(bool(reset)),
+                                  torch.cuda.current_stream(device).cuda_stream)
+    if rc < 0:
+        _lib.check(rc, "ll_decode_sync_status")
+    return rc
+
+
+def add_rmsnorm_qkv_splitk(h, part, splits, gamma, eps, wp: PackedWeight, qkv_part, epoch, tag,
+                           x=None):
+    """h = dtype(h + dtype(sum part)); x = rmsnorm(h) * gamma (as
+    add_rmsnorm_splitk), and the QKV split-K partials of x @ w^T into
+    qkv_part (may be part) in the same launch. Returns (x, qkv splits)."""
+    _dev(h, part, gamma, qkv_part, epoch, x)
+    M, hidden = h.shape
+    nqkv = wp.shape[0]
+    assert wp.shape[1] == hidden and wp.dtype == h.dtype and h.stride(1) == 1
+    assert part.dtype == torch.float32 and qkv_part.dtype == torch.float32
+    assert epoch.dtype == torch.int32 and 0 <= int(tag) < 256
+    qs = add_rmsnorm_qkv_splits(M, hidden, nqkv)
+    if qs <= 0:
+        raise _lib.LiteLangError(f"add_rmsnorm_qkv_splitk: shape not covered (M={M} "
+                                 f"hidden={hidden} nqkv={nqkv})")
+    if x is None:
+        x = torch.empty((M, hidden), dtype=h.dtype, device=h.device)
+    assert x.shape == (M, hidden) and x.is_contiguous()
+    sync = decode_sync(h.device)
+    rc = _L.ll_add_rmsnorm_qkv_splitk(h.data_ptr(), h.stride(0), part.data_ptr(), splits,
+                                      gamma.data_ptr(), float(eps), x.data_ptr(),
+                                      wp.data.data_ptr(), qkv_part.data_ptr(),
+                                      qkv_part.numel() * 4, M, hidden, nqkv, dtype_code(h),
+                                      sync.data_ptr(), epoch.data_ptr(), int(tag), _stream(h))
+    _lib.check(rc, "ll_add_rmsnorm_qkv_splitk")
+    return x, qs
+
+
 def silu_and_mul_splitk(part, splits, out):
     """out[M, N] = up * dtype(silu(gate)) from partials of the [M, 2N] product."""
     _dev(part, out)
