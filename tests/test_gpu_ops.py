@@ -173,7 +173,8 @@ def test_prefill_attention_varlen(cuda, dtype, H, KVH, D):
 @pytest.mark.parametrize("H,KVH,lens,shared", [
     (28, 4, [600, 129, 1, 257], [0, 0, 0, 0]),     # odd group (7 q heads per KV head)
     (12, 2, [700, 333, 64], [0, 0, 0]),           # 1.5B geometry, several 128-row blocks
-    (16, 2, [650, 400, 90], [520, 17, 89])])      # long cached prefixes, one-row query
+    (16, 2, [650, 400, 90], [520, 17, 89]),       # long cached prefixes, one-row query
+    (16, 2, [1100, 257], [0, 0])])                # 3B geometry, rows past 1024
 def test_prefill_attention_long_and_odd_groups(cuda, H, KVH, lens, shared):
     print(f"case: prefill H={H} KVH={KVH} lens={lens} shared={shared}", flush=True)
     out, ref = _prefill_case(cuda, H, KVH, 128, lens, shared, torch.bfloat16, 12)
