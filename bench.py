@@ -358,6 +358,54 @@ def bench_prefill_gemms(dev, M=B * PROMPT, reps=20):
     return out
 
 
+def bench_norm_qkv(dev, reps=400, copies=32):
+    """The decode step's add + RMSNorm fused with the next layer's QKV
+    projection (ops.add_rmsnorm_qkv_splitk) at the 3B shape, batch 40: the
+    down_proj partials of the real split count, `copies` packed QKV weights
+    cycled (336 MB, past the 256 MB MALL), events around `reps` launches.
+    Algorithmic bytes per launch: down partials read, residual read and
+    written, gain, normalised rows written and read once by the QKV items,
+    the QKV weight, the QKV partials written."""
+    from lite_lang_amd import ops, _lib
+    from lite_lang_amd.models.qwen2.weights import qwen25_3b_config
+    cfg = qwen25_3b_config()
+    hd, I = cfg.hidden_size, cfg.intermediate_size
+    nqkv = (cfg.num_heads + 2 * cfg.num_key_value_heads) * cfg.head_dim
+    dsplits = int(_lib.load().ll_gemm_splitk_count(B, hd, I))
+    qs = ops.add_rmsnorm_qkv_splits(B, hd, nqkv)
+    g = torch.Generator(device=dev).manual_seed(7)
+    wps = [ops.PackedWeight((torch.randn(nqkv, hd, device=dev, generator=g) * 0.02)
+                            .to(torch.bfloat16)) for _ in range(copies)]
+    gamma = (torch.rand(hd, device=dev, generator=g) + 0.5).to(torch.bfloat16)
+    part = torch.randn(dsplits * B * hd, device=dev, generator=g) * 0.3
+    qpart = torch.empty(qs * B * nqkv, device=dev)
+    h = torch.randn(B, hd, device=dev, generator=g).to(torch.bfloat16)
+    x = torch.empty_like(h)
+    ops.decode_sync(dev)
+    ops.reserve_workspace(dev, "decode_epoch", 4)
+
+    def call(i):
+        ops.add_rmsnorm_qkv_splitk(h, part, dsplits, gamma, cfg.rms_norm_eps, wps[i % copies],
+                                   qpart, ops.decode_epoch_advance(dev), tag=i % 200, x=x)
+
+    for i in range(copies):
+        call(i)
+    torch.cuda.synchronize(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(reps):
+        call(i)
+    e1.record()
+    torch.cuda.synchronize(dev)
+    us = e0.elapsed_time(e1) / reps * 1e3  # includes the epoch-advance launch
+    nbytes = (dsplits * B * hd * 4 + 2 * B * hd * 2 + hd * 2 + 2 * B * hd * 2
+              + nqkv * hd * 2 + qs * B * nqkv * 4)
+    assert ops.decode_sync_status(dev) == 0
+    return {"kernel": "norm_qkv_kernel (add + RMSNorm + next QKV, Qwen2.5-3B, batch 40)",
+            "us_per_call_with_epoch_advance": round(us, 3), "bytes_per_launch": nbytes,
+            "down_splits": dsplits, "qkv_splits": qs}
+
+
 # ------------------------------------------------------------------ main
 def main():
     ap = argparse.ArgumentParser()
@@ -377,6 +425,9 @@ def main():
     ap.add_argument("--attention-only", action="store_true",
                     help="run only the config-2 decode attention launches plus a 256 MiB "
                          "device copy of known size (for rocprofv3 --pmc traffic runs)")
+    ap.add_argument("--norm-qkv", action="store_true",
+                    help="run only the fused add + RMSNorm + QKV launch of the 3B decode step "
+                         "plus a 256 MiB device copy of known size (for rocprofv3 runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU (tp=1, no collectives); "
@@ -408,6 +459,13 @@ def main():
         return
     if args.prefill_gemm:
         print(json.dumps(bench_prefill_gemms(dev)), flush=True)
+        return
+    if args.norm_qkv:
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)  # reference copy: 256 MiB read + 256 MiB written
+        torch.cuda.synchronize()
+        print(json.dumps(bench_norm_qkv(dev)), flush=True)
         return
     if args.attention_only:
         src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
