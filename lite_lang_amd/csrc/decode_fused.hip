@@ -50,7 +50,7 @@
 
 namespace {
 
-constexpr int kThreads = 256;          // 4 waves
+constexpr int kThreads = 512;          // 8 waves (items: 4 working, 4 at the barriers)
 constexpr int kRowB = 256;             // bytes of one row chunk (one stage)
 constexpr int kKC = 128;               // 16-bit elements per row chunk
 constexpr int kSpinMax = 1 << 18;      // polls before a barrier gives up
@@ -102,11 +102,11 @@ __device__ __forceinline__ void st_agent_4(T* p, const T (&y)[4], bool vec, int 
   }
 }
 
-// add + RMSNorm of one row from the split partials, as add_rmsnorm_splitk_kernel
-// computes it with 512 threads: thread i of this workgroup stands for that
-// kernel's threads i and i + 256, whose sums of squares are kept apart and
-// reduced through the same tree (wave sums, then the 8 wave totals in order).
-// h and out are written with agent-scope stores.
+// add + RMSNorm of one row from the split partials with the 512 threads of
+// the workgroup, in add_rmsnorm_splitk_kernel's layout and reduction tree
+// (thread i takes 4 columns at (512 ps + i) * 4; wave sums, then the 8 wave
+// totals in order), so the row is bit-identical to that kernel's. h and out
+// are written with agent-scope stores.
 template <typename T, int MAXP>
 __device__ void norm_row(int row, const float* __restrict__ part, int splits, int M, T* h,
                          int64_t ld_h, const T* __restrict__ gamma, float eps, T* out,
@@ -114,44 +114,37 @@ __device__ void norm_row(int row, const float* __restrict__ part, int splits, in
   constexpr int PER = 4, OB = 512;
   const int tid = threadIdx.x;
   T* hr = h + (int64_t)row * ld_h;
-  T hraw[2][MAXP][PER], graw[2][MAXP][PER];
+  T hraw[MAXP][PER], graw[MAXP][PER];
 #pragma unroll
-  for (int v = 0; v < 2; ++v)
+  for (int ps = 0; ps < MAXP; ++ps) {
+    const int c = min((ps * OB + tid) * PER, N - PER);
 #pragma unroll
-    for (int ps = 0; ps < MAXP; ++ps) {
-      const int c = min((ps * OB + v * 256 + tid) * PER, N - PER);
-#pragma unroll
-      for (int e = 0; e < PER; ++e) {
-        hraw[v][ps][e] = hr[c + e];
-        graw[v][ps][e] = gamma[c + e];
-      }
+    for (int e = 0; e < PER; ++e) {
+      hraw[ps][e] = hr[c + e];
+      graw[ps][e] = gamma[c + e];
     }
-  float hv[2][MAXP][PER];
-  float ss[2] = {0.f, 0.f};
+  }
+  float hv[MAXP][PER];
+  float ss = 0.f;
   const bool vec = ((ld_h | ld_o) & 3) == 0;
 #pragma unroll
-  for (int v = 0; v < 2; ++v)
+  for (int ps = 0; ps < MAXP; ++ps) {
+    const int c = (ps * OB + tid) * PER;
+    if (c < N) {
+      const f32x4 o = ll_sum_splits4(part, splits, (int64_t)M * N, (int64_t)row * N + c);
+      T nh[PER];
 #pragma unroll
-    for (int ps = 0; ps < MAXP; ++ps) {
-      const int c = (ps * OB + v * 256 + tid) * PER;
-      if (c < N) {
-        const f32x4 o = ll_sum_splits4(part, splits, (int64_t)M * N, (int64_t)row * N + c);
-        T nh[PER];
-#pragma unroll
-        for (int e = 0; e < PER; ++e) {
-          nh[e] = ll_from_f32<T>(ll_to_f32(hraw[v][ps][e]) + ll_to_f32(ll_from_f32<T>(o[e])));
-          hv[v][ps][e] = ll_to_f32(nh[e]);
-          ss[v] += hv[v][ps][e] * hv[v][ps][e];
-        }
-        st_agent_4(hr + c, nh, vec, N - c);
+      for (int e = 0; e < PER; ++e) {
+        nh[e] = ll_from_f32<T>(ll_to_f32(hraw[ps][e]) + ll_to_f32(ll_from_f32<T>(o[e])));
+        hv[ps][e] = ll_to_f32(nh[e]);
+        ss += hv[ps][e] * hv[ps][e];
       }
+      st_agent_4(hr + c, nh, vec, N - c);
     }
-  const int wave = tid >> 6;
-  const float s0 = ll_wave_sum(ss[0]), s1 = ll_wave_sum(ss[1]);
-  if ((tid & 63) == 0) {
-    red[wave] = s0;
-    red[wave + 4] = s1;
   }
+  const int wave = tid >> 6;
+  const float sw = ll_wave_sum(ss);
+  if ((tid & 63) == 0) red[wave] = sw;
   lds_barrier();
   float tot = 0.f;
 #pragma unroll
@@ -159,18 +152,16 @@ __device__ void norm_row(int row, const float* __restrict__ part, int splits, in
   const float denom = sqrtf(tot / (float)N + eps);
   T* orow = out + (int64_t)row * ld_o;
 #pragma unroll
-  for (int v = 0; v < 2; ++v)
+  for (int ps = 0; ps < MAXP; ++ps) {
+    const int c = (ps * OB + tid) * PER;
+    if (c < N) {
+      T y[PER];
 #pragma unroll
-    for (int ps = 0; ps < MAXP; ++ps) {
-      const int c = (ps * OB + v * 256 + tid) * PER;
-      if (c < N) {
-        T y[PER];
-#pragma unroll
-        for (int e = 0; e < PER; ++e)
-          y[e] = ll_from_f32<T>(hv[v][ps][e] / denom * ll_to_f32(graw[v][ps][e]));
-        st_agent_4(orow + c, y, vec, N - c);
-      }
+      for (int e = 0; e < PER; ++e)
+        y[e] = ll_from_f32<T>(hv[ps][e] / denom * ll_to_f32(graw[ps][e]));
+      st_agent_4(orow + c, y, vec, N - c);
     }
+  }
   lds_barrier();  // red is reused by the next row
 }
 
@@ -256,6 +247,9 @@ __global__ __launch_bounds__(kThreads) void norm_qkv_kernel(NormQkvArgs a) {
   const int nst = min(a.per, a.chunks - kc0);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int n = lane & 15, j = lane >> 4;
+  // waves 0-3 own the tile's 4 x 16 weight rows; waves 4-7 (there for the
+  // norm rows' 512 threads) only take part in the workgroup barriers
+  const bool work = wave < 4;
   // this wave's weight fragments of every chunk: packed block (kc, t) is the
   // 64 x 256-byte LDS image of the split-K GEMM (row r's 16-byte piece c at
   // r * 256 + (c ^ (r & 15)) * 16); the MFMA A operand of lane (n, j) at
@@ -264,7 +258,7 @@ __global__ __launch_bounds__(kThreads) void norm_qkv_kernel(NormQkvArgs a) {
   V8 wf[kMaxPer][4];
 #pragma unroll
   for (int st = 0; st < kMaxPer; ++st)
-    if (st < nst) {
+    if (st < nst && work) {
       const char* blk = (const char*)a.wqkv + ((int64_t)(kc0 + st) * a.tiles + t) * (64 * kRowB) +
                         lr * kRowB;
 #pragma unroll
@@ -280,13 +274,15 @@ __global__ __launch_bounds__(kThreads) void norm_qkv_kernel(NormQkvArgs a) {
   // loads on every path, so the compiler waits for each chunk's loads alone.
   const int xrow0 = 4 * MB * wave + (lane >> 4), p = lane & 15;
   V8 xv_in[kMaxPer][MB];
+  if (work) {
 #pragma unroll
-  for (int st = 0; st < kMaxPer; ++st) {
-    const T* g = (const T*)a.x + (int64_t)(kc0 + min(st, nst - 1)) * kKC + p * 8;
+    for (int st = 0; st < kMaxPer; ++st) {
+      const T* g = (const T*)a.x + (int64_t)(kc0 + min(st, nst - 1)) * kKC + p * 8;
 #pragma unroll
-    for (int e = 0; e < MB; ++e)
-      xv_in[st][e] = *(const V8*)(g + (int64_t)min(xrow0 + 4 * e, a.M - 1) * a.hidden);
-    __builtin_amdgcn_sched_barrier(0);  // chunk order kept: chunk 0's loads land first
+      for (int e = 0; e < MB; ++e)
+        xv_in[st][e] = *(const V8*)(g + (int64_t)min(xrow0 + 4 * e, a.M - 1) * a.hidden);
+      __builtin_amdgcn_sched_barrier(0);  // chunk order kept: chunk 0's loads land first
+    }
   }
   f32x4 acc[MB];
 #pragma unroll
@@ -295,23 +291,28 @@ __global__ __launch_bounds__(kThreads) void norm_qkv_kernel(NormQkvArgs a) {
   for (int st = 0; st < kMaxPer; ++st)
     if (st < nst) {
       char* xb = smem + st * XB;
+      if (work) {
 #pragma unroll
-      for (int e = 0; e < MB; ++e) {
-        const int r = xrow0 + 4 * e;
-        if (r < a.M) *(V8*)(xb + r * kRowB + ((p ^ (r & 15)) * 16)) = xv_in[st][e];
-      }
-      lds_barrier();  // every wave's rows of chunk st are in
-#pragma unroll
-      for (int s = 0; s < kKC / 32; ++s)
-#pragma unroll
-        for (int q = 0; q < MB; ++q) {
-          const int xr = 16 * q + n;
-          const V8 xv = *(const V8*)(xb + xr * kRowB + (((4 * s + j) ^ (xr & 15)) * 16));
-          acc[q] = mfma16(wf[st][s], xv, acc[q]);
+        for (int e = 0; e < MB; ++e) {
+          const int r = xrow0 + 4 * e;
+          if (r < a.M) *(V8*)(xb + r * kRowB + ((p ^ (r & 15)) * 16)) = xv_in[st][e];
         }
+      }
+      lds_barrier();  // every working wave's rows of chunk st are in
+      if (work) {
+#pragma unroll
+        for (int s = 0; s < kKC / 32; ++s)
+#pragma unroll
+          for (int q = 0; q < MB; ++q) {
+            const int xr = 16 * q + n;
+            const V8 xv = *(const V8*)(xb + xr * kRowB + (((4 * s + j) ^ (xr & 15)) * 16));
+            acc[q] = mfma16(wf[st][s], xv, acc[q]);
+          }
+      }
     }
   // acc[q][i] = Y[token 16 q + n][channel 64 t + 16 wave + 4 j + i]; fp32
   // partials qpart[split][m][n], read by the next kernel (plain stores)
+  if (!work) return;
   const int ch = t * 64 + wave * 16 + 4 * j;
 #pragma unroll
   for (int q = 0; q < MB; ++q) {
