@@ -79,10 +79,14 @@ int ll_decode_attention(const void* q, int64_t q_stride_b, int64_t q_stride_h,
  * more is rejected with LL_ERR_ARG (use ll_decode_attention with a
  * workspace). Nothing is allocated. Every call on one GPU shares that GPU's
  * array: two calls that overlap in time on one GPU (two streams, two threads)
- * race and give wrong results. The first call on a device looks the array up
- * and clears its tickets on `stream`; results are identical to
- * ll_decode_attention's. */
+ * race and give wrong results. The array starts zeroed (its split tickets at
+ * zero) and every call leaves the tickets at zero, so nothing is cleared. The
+ * first call on a device looks the array's device address up (no work is
+ * queued; this may happen under graph capture); ll_decode_attention_noalloc_init
+ * does that lookup for the current device ahead of time, for set-up code.
+ * Results are identical to ll_decode_attention's. */
 int64_t ll_decode_attention_noalloc_max_bytes(void);
+int ll_decode_attention_noalloc_init(void);
 int ll_decode_attention_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                                 const void* k_cache, int64_t k_stride_tok,
                                 int64_t k_stride_head, const void* v_cache,
@@ -105,6 +109,12 @@ int ll_decode_attention_noalloc(const void* q, int64_t q_stride_b, int64_t q_str
 int ll_decode_attention_xcc_probe(int64_t batch, int64_t q_heads, int64_t kv_heads,
                                   int64_t head_dim, int64_t max_len_in_batch, int32_t* out,
                                   int64_t out_len, hipStream_t stream);
+/* enable != 0 (the default): the split stage merges its splits itself when
+ * the shape allows; 0: every split call merges in a separate kernel, which
+ * needs no XCD premise (the runner switches it off when the probe above
+ * finds the premise broken). Process-wide; returns the previous setting. No
+ * reference counterpart. */
+int ll_decode_attention_set_same_launch_merge(int enable);
 
 /* NoPad varlen causal prefill attention reading K/V through the slot table,
  * with an optional shared (prompt-cache) prefix per request.
@@ -180,6 +190,15 @@ int ll_embedding_rmsnorm(const void* table, int64_t table_row_stride, int64_t vo
                          const void* ids, int ids_i64, void* h, int64_t h_row_stride,
                          const void* gamma, void* out, int64_t out_row_stride, int64_t ntok,
                          int64_t hidden, float eps, int dtype, hipStream_t stream);
+/* ll_embedding_rmsnorm that also adds 1 to *epoch (ntok >= 1): the decode
+ * step's first launch advances the epoch that the step's
+ * ll_add_rmsnorm_qkv_splitk calls read, so the step needs no launch of its
+ * own for it. Same reference lines as ll_embedding_rmsnorm. */
+int ll_embedding_rmsnorm_epoch(const void* table, int64_t table_row_stride, int64_t vocab,
+                               const void* ids, int ids_i64, void* h, int64_t h_row_stride,
+                               const void* gamma, void* out, int64_t out_row_stride,
+                               int64_t ntok, int64_t hidden, float eps, int dtype,
+                               uint32_t* epoch, hipStream_t stream);
 /* out[t, :] = table[ids[t], :].
  * Replaces torch.embedding in Qwen2PreLayer.Forward
  *   (litelang/models/qwen2/layer/pre_layer.py:15-19).
@@ -191,10 +210,18 @@ int ll_embedding(const void* table, int64_t table_row_stride, int64_t vocab, con
                  int dtype, hipStream_t stream);
 
 /* out[m] = first index of max(x[m, :]) (int64).
- * Replaces logits.argmax(dim=-1) (litelang/models/qwen2/layer/post_layer.py:105-107). */
+ * Replaces logits.argmax(dim=-1) (litelang/models/qwen2/layer/post_layer.py:75-77). */
 int64_t ll_argmax_workspace_size(int64_t M, int64_t N);
 int ll_argmax(const void* x, int64_t x_row_stride, int64_t M, int64_t N, int64_t* out,
               void* workspace, int64_t workspace_bytes, int dtype, hipStream_t stream);
+/* ll_argmax, except that every out[m] is -1 when *status is nonzero (status:
+ * the decode step's error word, ll_decode_sync_error_offset() bytes into the
+ * sync words). -1 is no token id: a runner reading the tokens raises on it,
+ * so a decode step whose fused launch gave up a flag wait is never taken for
+ * a valid one. Same reference line as ll_argmax. */
+int ll_argmax_status(const void* x, int64_t x_row_stride, int64_t M, int64_t N, int64_t* out,
+                     void* workspace, int64_t workspace_bytes, int dtype, const uint32_t* status,
+                     hipStream_t stream);
 
 /* req_to_tokens[rows[i], cols[i]] = slots[i] for i < n (int32 device arrays).
  * Replaces the slot-table writes of PageCache.alloc_token_idxs and add_refs
@@ -263,7 +290,7 @@ int ll_gemm_i8_gate_up_silu_tiled(const int8_t* Xq, int64_t ldx, const float* s_
 /* Y[M, N] = X[M, K] . W[N, K]^T (+ bias[N]) with fp32 accumulation.
  * W is the nn.Linear layout [out, in]. Replaces the torch.addmm / torch.mm /
  * matmul projections of transformer_layer.py:80,82,95-109,193 and the lm_head
- * product of post_layer.py:50-52 (the reference keeps W pre-transposed
+ * product of post_layer.py:20-22 (the reference keeps W pre-transposed
  * [in, out]; this library keeps [out, in] so both MFMA operands stream
  * 16-byte k-contiguous rows). X rows may be strided; Y is written with
  * row stride ldy. For M <= 64 with narrow N the product is split over K and
@@ -303,7 +330,10 @@ int ll_add_rmsnorm_splitk(void* h, int64_t h_row_stride, const float* part, int 
  * call's flags hold *epoch * 256 + tag + 1, which the caller keeps distinct
  * from every earlier call's on the same sync words (a new *epoch per decode
  * step, the layer index < 256 as tag). Calls on one sync buffer must not
- * overlap. */
+ * overlap. Every flag wait is bounded (ll_decode_sync_set_spin_limit); a
+ * QKV workgroup whose wait gives up stores nothing and sets the error word
+ * (ll_decode_sync_error_offset() bytes into `sync`), which stays set until
+ * ll_decode_sync_status resets it and does not affect later calls' waits. */
 int ll_add_rmsnorm_qkv_splits(int64_t M, int64_t hidden, int64_t nqkv); /* 0: not covered */
 int ll_add_rmsnorm_qkv_splitk(void* h, int64_t ld_h, const float* part, int splits,
                               const void* gamma, float eps, void* x, const void* wqkv_packed,
@@ -311,6 +341,12 @@ int ll_add_rmsnorm_qkv_splitk(void* h, int64_t ld_h, const float* part, int spli
                               int64_t nqkv, int dtype, void* sync, const uint32_t* epoch,
                               uint32_t tag, hipStream_t stream);
 int64_t ll_decode_sync_bytes(void);
+int64_t ll_decode_sync_error_offset(void);
+/* Polls a flag wait makes before it gives up, process-wide (0: the default,
+ * 2^18). A negative value -n is a test mode: the waits look for a flag value
+ * no producer writes and give up after n polls, so every consumer gives up
+ * while every kernel still exits normally. No reference counterpart. */
+int ll_decode_sync_set_spin_limit(int polls);
 /* 1 when a flag wait gave up since the last reset (outputs then invalid), else
  * 0; reset != 0 clears the sync words after such a failure (synchronises
  * the stream) */

@@ -25,6 +25,8 @@ SIGNATURES = {
     "ll_decode_attention_workspace_size": (I64, [I64, I64, I64, I64, I64]),
     "ll_decode_attention_xcc_probe": (I32, [I64, I64, I64, I64, I64, P, I64, P]),
     "ll_decode_attention_noalloc_max_bytes": (I64, []),
+    "ll_decode_attention_noalloc_init": (I32, []),
+    "ll_decode_attention_set_same_launch_merge": (I32, [I32]),
     "ll_decode_attention_noalloc": (I32, [P, I64, I64, P, I64, I64, P, I64, I64, P, I64, P, I32,
                                           P, I32, P, I64, I64, I64, I64, I64, I64, I64, F32, I32,
                                           P]),
@@ -41,9 +43,12 @@ SIGNATURES = {
     "ll_kv_store": (I32, [P, I64, I64, I64, I64, P, P, I64, I64, I64, I32, P]),
     "ll_silu_and_mul": (I32, [P, I64, P, I64, I64, I64, I32, P]),
     "ll_embedding_rmsnorm": (I32, [P, I64, I64, P, I32, P, I64, P, P, I64, I64, I64, F32, I32, P]),
+    "ll_embedding_rmsnorm_epoch": (I32, [P, I64, I64, P, I32, P, I64, P, P, I64, I64, I64, F32,
+                                         I32, P, P]),
     "ll_embedding": (I32, [P, I64, I64, P, I32, P, I64, I64, I64, I32, P]),
     "ll_argmax_workspace_size": (I64, [I64, I64]),
     "ll_argmax": (I32, [P, I64, I64, I64, P, P, I64, I32, P]),
+    "ll_argmax_status": (I32, [P, I64, I64, I64, P, P, I64, I32, P, P]),
     "ll_assign_slots": (I32, [P, I64, P, P, P, I64, P]),
     "ll_gemm_tiled_supported": (I32, [I64, I64, I64, I32]),
     "ll_gemm_tiled": (I32, [P, I64, P, I64, P, P, I64, I64, I64, I64, I32, P]),
@@ -84,6 +89,8 @@ SIGNATURES = {
     "ll_add_rmsnorm_qkv_splitk": (I32, [P, I64, P, I32, P, F32, P, P, P, I64, I64, I64, I64, I32,
                                         P, P, ctypes.c_uint32, P]),
     "ll_decode_sync_bytes": (I64, []),
+    "ll_decode_sync_error_offset": (I64, []),
+    "ll_decode_sync_set_spin_limit": (I32, [I32]),
     "ll_decode_sync_status": (I32, [P, I32, P]),
     "ll_decode_attention_rope_splitk": (I32, [P, I32, P, P, I32, P, P, I64, I32, P, P, I64, I64,
                                               P, I64, I64, P, I64, P, I32, P, I32, P, I64, I64,

@@ -1,17 +1,20 @@
 """FastAPI routes of the front end (counterpart of litelang/apis/api_server.py).
 
-Same routes and request body as the reference: `POST /generate` answers
-{"result": [text, ...]} once the request has finished, `POST
+Same routes and request body fields as the reference: `POST /generate`
+answers {"result": [text, ...]} once the request has finished, `POST
 /generate_stream` streams one `{"generated_text": text}` JSON object per
 generated piece, each followed by a blank line (text/event-stream). The
 reference's /generate reads `request.get()`, which its pydantic model does
 not have; here it returns the generated pieces. A request the waiting room
-refuses answers 503.
+refuses answers 503, and so does any request while no model is attached.
+
+The manager that serves the routes is attached with `attach(manager)` (or
+`serve`, which attaches it and runs uvicorn) and detached with
+`attach(None)`.
 """
 from __future__ import annotations
 
 import json
-from dataclasses import dataclass
 from typing import Iterator, Optional
 
 from fastapi import FastAPI, HTTPException
@@ -20,74 +23,70 @@ from pydantic import BaseModel
 
 from .http_server_manager import HttpServerManager, RequestRefused
 
-
-@dataclass
-class GObjs:
-    http_server_manager: Optional[HttpServerManager] = None
-    app: Optional[FastAPI] = None
-
-    default_temperature = 1.0
-    default_top_p = 1.0
-    default_top_k = 1
-    default_do_sample = False
-
+# sampling defaults of a request body that leaves a field out (greedy
+# decoding needs none of them; the scheduler records them per request)
+SAMPLING_DEFAULTS = {"temperature": 1.0, "top_p": 1.0, "top_k": 1, "do_sample": False}
 
 app = FastAPI()
-g_objs = GObjs(app=app)
+_manager_ref: list[Optional[HttpServerManager]] = [None]
+
+
+def attach(manager: Optional[HttpServerManager]) -> None:
+    """Serve the routes from `manager` (None: answer 503 until one is attached)."""
+    _manager_ref[0] = manager
+
+
+def attached() -> Optional[HttpServerManager]:
+    return _manager_ref[0]
 
 
 class GenerateRequest(BaseModel):
-    top_p: float = g_objs.default_top_p
-    temperature: float = g_objs.default_temperature
-    top_k: int = g_objs.default_top_k
-    do_sample: bool = g_objs.default_do_sample
+    """JSON body of both routes (field names as the reference's)."""
     prompt: str
+    temperature: float = SAMPLING_DEFAULTS["temperature"]
+    top_p: float = SAMPLING_DEFAULTS["top_p"]
+    top_k: int = SAMPLING_DEFAULTS["top_k"]
+    do_sample: bool = SAMPLING_DEFAULTS["do_sample"]
 
 
-def _manager() -> HttpServerManager:
-    m = g_objs.http_server_manager
-    if m is None:
+def _pieces(body: GenerateRequest) -> Iterator[str]:
+    """Submit the request and return its generator of text pieces. Submission
+    happens here, before any response byte is sent, so that a refusal (or a
+    missing model) becomes an HTTP 503."""
+    manager = attached()
+    if manager is None:
         raise HTTPException(status_code=503, detail="no model is being served")
-    return m
-
-
-def _start(request: GenerateRequest) -> Iterator[str]:
-    """The request's text generator, with its first step taken so that a
-    refusal becomes an HTTP error before any byte is sent."""
-    m = _manager()
     try:
-        req = m.submit(request.prompt, request.top_p, request.top_k, request.temperature,
-                       request.do_sample)
+        req = manager.submit(body.prompt, body.top_p, body.top_k, body.temperature,
+                             body.do_sample)
     except RequestRefused as e:
         raise HTTPException(status_code=503, detail=str(e))
+    return manager.stream(req)
 
-    return m.stream(req)
+
+def _json_bytes(obj) -> bytes:
+    return json.dumps(obj, ensure_ascii=False).encode("utf-8")
 
 
 @app.post("/generate")
-def generate(request: GenerateRequest):
-    output_prompts = list(_start(request))
-    return Response(content=json.dumps({"result": output_prompts},
-                                       ensure_ascii=False).encode("utf-8"),
+def generate(body: GenerateRequest):
+    return Response(content=_json_bytes({"result": list(_pieces(body))}),
                     media_type="application/json")
 
 
 @app.post("/generate_stream")
-def generate_stream(request: GenerateRequest):
-    gen = _start(request)
-
-    def stream_results():
-        for text in gen:
-            yield (json.dumps({"generated_text": text}, ensure_ascii=False) + "\n\n").encode("utf-8")
-
-    return StreamingResponse(stream_results(), media_type="text/event-stream")
+def generate_stream(body: GenerateRequest):
+    pieces = _pieces(body)
+    events = (_json_bytes({"generated_text": text}) + b"\n\n" for text in pieces)
+    return StreamingResponse(events, media_type="text/event-stream")
 
 
 def serve(manager: HttpServerManager, host: str = "127.0.0.1", port: int = 8080) -> None:
     """Serve `app` for `manager` with uvicorn (blocks until the server stops)."""
     import uvicorn
-    g_objs.http_server_manager = manager
+    attach(manager)
     try:
         uvicorn.run(app, host=host, port=port)
     finally:
+        attach(None)
         manager.stop()

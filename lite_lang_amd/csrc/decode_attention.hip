@@ -33,6 +33,7 @@
 // A generic VALU path covers fp32 and head dims other than 64/128.
 #include "ll_common.h"
 
+#include <atomic>
 #include <mutex>
 
 namespace {
@@ -822,6 +823,12 @@ void launch_combine(const DecodeArgs& a, int dtype, hipStream_t stream) {
 constexpr int kMergeUnits = 4096;
 constexpr int64_t kTicketBytes = kMergeUnits * 4;
 
+// Whether the split stage may merge its splits itself (it needs every
+// workgroup of a sequence on one XCD, which the dispatcher's round-robin
+// gives; ll_decode_attention_xcc_probe checks it). Off: the separate merge
+// kernels, which need no such premise.
+std::atomic<int> g_same_launch_merge{1};
+
 int64_t workspace_bytes_for(int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
                             int64_t max_len) {
   const int ns = choose_nsplit((int)batch, (int)kv_heads, max_len, head_dim);
@@ -852,7 +859,8 @@ int launch_mfma(DecodeArgs& a, int64_t head_dim, int dtype, bool rope, int64_t m
                           : (a.B <= kMergeUnits &&
                              row_b <= (head_dim == 128 ? TileGeom<128>::MAIN_B
                                                        : TileGeom<64>::MAIN_B));
-    a.merge_cnt = fits ? (unsigned*)w : nullptr;
+    a.merge_cnt = (fits && g_same_launch_merge.load(std::memory_order_relaxed)) ? (unsigned*)w
+                                                                                 : nullptr;
     w += kTicketBytes;
     const int64_t parts = (int64_t)a.B * a.H * a.nsplit;
     a.part_acc = (float*)w;
@@ -928,6 +936,11 @@ extern "C" int ll_decode_attention_xcc_probe(int64_t batch, int64_t q_heads, int
     return LL_ERR_HIP;
   }
   return (int)grid;
+}
+
+extern "C" int ll_decode_attention_set_same_launch_merge(int enable) {
+  const int old = g_same_launch_merge.exchange(enable ? 1 : 0);
+  return old;
 }
 
 extern "C" int64_t ll_decode_attention_workspace_size(int64_t batch, int64_t q_heads,
@@ -1008,15 +1021,13 @@ static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};
 
-// Zeroes the split-ticket words (every call leaves them at zero again).
-__global__ void zero_words_kernel(uint32_t* p, int n) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = 0u;
-}
-
-// The device address of this device's scratch array, looked up (and its
-// tickets cleared on `stream`) on the first call on the device.
-int scratch_for_current_device(hipStream_t stream, void** out) {
+// The device address of this device's scratch array, looked up on the first
+// call on the device (or by ll_decode_attention_noalloc_init). Nothing is
+// written to the array here: as a zero-initialised device global it starts
+// with every split ticket at zero, and every call leaves them at zero, so the
+// lookup queues no work on any stream (it may happen while a caller captures
+// a graph).
+int scratch_for_current_device(void** out) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
@@ -1033,15 +1044,6 @@ int scratch_for_current_device(hipStream_t stream, void** out) {
                    hipGetErrorString(e));
       return LL_ERR_HIP;
     }
-    const int words = (int)(kTicketBytes / 4);
-    hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0,
-                       stream, (uint32_t*)ptr, words);
-    e = hipGetLastError();
-    if (e != hipSuccess) {
-      ll_set_error("ll_decode_attention_noalloc: clearing the scratch tickets failed: %s",
-                   hipGetErrorString(e));
-      return LL_ERR_HIP;
-    }
     g_scratch_ptr[dev] = ptr;
   }
   *out = g_scratch_ptr[dev];
@@ -1049,6 +1051,11 @@ int scratch_for_current_device(hipStream_t stream, void** out) {
 }
 
 }  // namespace
+
+extern "C" int ll_decode_attention_noalloc_init(void) {
+  void* p = nullptr;
+  return scratch_for_current_device(&p);
+}
 
 extern "C" int64_t ll_decode_attention_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
 
@@ -1069,7 +1076,7 @@ extern "C" int ll_decode_attention_noalloc(
                (long long)need, (long long)kNoAllocScratchBytes);
   void* ws = nullptr;
   if (need > 0) {
-    const int rc = scratch_for_current_device(stream, &ws);
+    const int rc = scratch_for_current_device(&ws);
     if (rc != LL_OK) return rc;
   }
   return ll_decode_attention(q, q_stride_b, q_stride_h, k_cache, k_stride_tok, k_stride_head,

@@ -38,12 +38,17 @@
 // every earlier call's on the same sync words (a new epoch per decode step,
 // the layer index as tag), so flags are never reset and no consumer touches a
 // shared counter. Each flag sits in its own 64-byte line. Every poll is
-// bounded: a consumer that gives up sets the error word
-// (ll_decode_sync_status) and goes on, its output then being invalid.
+// bounded: a consumer that gives up sets the error word and stores nothing
+// (its QKV partials are then missing, so the step's outputs are invalid). The
+// decision is each launch's own: an error word left set by an earlier launch
+// does not shorten later waits. The word stays set until the host resets it
+// (ll_decode_sync_status with reset); ll_argmax_status turns a set word into
+// token ids of -1, which is how the runner sees it.
 //
 // The QKV partials may overwrite the down_proj partials (qkv_part == part):
 // every norm workgroup has read its rows of them before it raises its flag,
-// and no item stores before it has seen every flag.
+// and no item stores before it has seen every flag (an item that gave up
+// stores nothing at all).
 #include "ll_common.h"
 
 #include <atomic>
@@ -53,7 +58,7 @@ namespace {
 constexpr int kThreads = 512;          // 8 waves (items: 4 working, 4 at the barriers)
 constexpr int kRowB = 256;             // bytes of one row chunk (one stage)
 constexpr int kKC = 128;               // 16-bit elements per row chunk
-constexpr int kSpinMax = 1 << 18;      // polls before a barrier gives up
+constexpr int kSpinMax = 1 << 18;      // polls before a flag wait gives up (default)
 constexpr int kMaxLds = 160 * 1024;
 
 template <typename T> struct V8Of;
@@ -184,24 +189,31 @@ __device__ __forceinline__ void raise_flag(uint32_t* sync, int idx, uint32_t val
 }
 
 // Consumer: wave 0 polls the n (<= 64) flags, one per lane, until all hold
-// `value` (bounded; on failure the error word is set).
-__device__ __forceinline__ void wait_flags(uint32_t* sync, int n, uint32_t value) {
+// `value`, at most spin_max times. Returns, in every thread of the
+// workgroup, whether they did; on failure the error word is set.
+__device__ __forceinline__ bool wait_flags(uint32_t* sync, int n, uint32_t value, int spin_max,
+                                           int* s_ok) {
   if (threadIdx.x < 64) {
     const int lane = threadIdx.x;
     const uint32_t* f = sync + kFlagStride * (lane < n ? lane : 0);
-    int spins = 0;
-    for (;;) {
+    bool ok = false;
+    for (int spins = 0;; ++spins) {
       const uint32_t v = ld_agent(f);
-      if (__builtin_amdgcn_ballot_w64(v != value) == 0ull) break;
-      if (++spins >= kSpinMax || ld_agent(sync + kSyncErr) != 0u) {
-        if (lane == 0)
-          __hip_atomic_store(sync + kSyncErr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (__builtin_amdgcn_ballot_w64(v != value) == 0ull) {
+        ok = true;
         break;
       }
+      if (spins + 1 >= spin_max) break;
       __builtin_amdgcn_s_sleep(1);
+    }
+    if (lane == 0) {
+      *s_ok = ok ? 1 : 0;
+      if (!ok)
+        __hip_atomic_store(sync + kSyncErr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
   lds_barrier();
+  return *s_ok != 0;
 }
 
 struct NormQkvArgs {
@@ -219,6 +231,8 @@ struct NormQkvArgs {
   uint32_t* sync;
   const uint32_t* epoch;
   uint32_t tag;
+  int spin_max;            // polls before a flag wait gives up
+  uint32_t skew;           // 0; nonzero only in the test mode (waits that never succeed)
 };
 
 constexpr int kMaxPer = 4;        // k chunks per item (16 weight VGPRs each)
@@ -233,6 +247,7 @@ __global__ __launch_bounds__(kThreads) void norm_qkv_kernel(NormQkvArgs a) {
   constexpr int XB = XR * kRowB;        // LDS bytes per chunk
   extern __shared__ __attribute__((aligned(16))) char smem[];
   __shared__ float red[8];
+  __shared__ int s_ok;
   const int w = (int)blockIdx.x;
   const uint32_t value = *a.epoch * 256u + a.tag + 1u;
   if (w < a.M) {
@@ -264,7 +279,8 @@ __global__ __launch_bounds__(kThreads) void norm_qkv_kernel(NormQkvArgs a) {
 #pragma unroll
       for (int s = 0; s < 4; ++s) wf[st][s] = *(const V8*)(blk + (((4 * s + j) ^ (lr & 15)) * 16));
     }
-  wait_flags(a.sync, a.M, value);
+  // an item whose wait gave up stores nothing (the whole workgroup leaves)
+  if (!wait_flags(a.sync, a.M, value + a.skew, a.spin_max, &s_ok)) return;
   // activation chunks, all loaded at once (the rows are final: every flag is
   // up) through registers, whose per-CU ingest is faster than LDS DMA's: wave
   // `wave` takes rows 4 MB wave .. +4 MB of each chunk, 16 lanes a row, and
@@ -359,9 +375,24 @@ SplitPlan split_plan(int64_t M, int64_t N, int64_t K) {
   return p;
 }
 
+// Polls before a flag wait of the fused decode launches gives up: the
+// default, or a bound set by the host. A negative setting -n is a test mode:
+// the consumers wait for a flag value no producer writes and give up after n
+// polls, so a test sees every wait give up while every kernel still exits
+// normally. 0 restores the default.
+std::atomic<int> g_spin_max{kSpinMax};
+
 }  // namespace
 
 extern "C" int64_t ll_decode_sync_bytes(void) { return kSyncBytes; }
+
+extern "C" int64_t ll_decode_sync_error_offset(void) { return (int64_t)kSyncErr * 4; }
+
+extern "C" int ll_decode_sync_set_spin_limit(int polls) {
+  LL_CHECK_ARG(polls > -(1 << 20), "ll_decode_sync_set_spin_limit: bound out of range");
+  g_spin_max.store(polls == 0 ? kSpinMax : polls);
+  return LL_OK;
+}
 
 extern "C" int ll_decode_sync_status(void* sync, int reset, hipStream_t stream) {
   LL_CHECK_ARG(sync != nullptr, "ll_decode_sync_status: null sync words");
@@ -433,6 +464,9 @@ extern "C" int ll_add_rmsnorm_qkv_splitk(void* h, int64_t ld_h, const float* par
   a.sync = (uint32_t*)sync;
   a.epoch = epoch;
   a.tag = tag;
+  const int spin = g_spin_max.load();
+  a.spin_max = spin < 0 ? -spin : spin;
+  a.skew = spin < 0 ? 0x80000000u : 0u;
   return dtype == LL_BF16 ? launch_norm_qkv_mb<__bf16>(a, stream)
                           : launch_norm_qkv_mb<_Float16>(a, stream);
 }

@@ -8,7 +8,7 @@
 //   rotary       litelang/kernel/develop_rope/rope.py:9-151
 //   silu_and_mul litelang/kernel/develop_silu_and_mul/silu_and_mul.py:7-52
 //   embedding    litelang/models/qwen2/layer/pre_layer.py:15-19
-//   argmax       litelang/models/qwen2/layer/post_layer.py:105-107
+//   argmax       litelang/models/qwen2/layer/post_layer.py:75-77
 #include "ll_common.h"
 
 #include <string.h>
@@ -38,8 +38,10 @@ template <typename T, int BLOCK>
 __global__ __launch_bounds__(BLOCK) void rmsnorm_kernel(
     T* __restrict__ x, int64_t x_rs, const T* __restrict__ residual, int64_t r_rs,
     const T* __restrict__ gamma, T* __restrict__ out, int64_t o_rs, int N, float eps,
-    const T* __restrict__ table, int64_t tab_rs, const void* ids, int ids64, int64_t vocab) {
+    const T* __restrict__ table, int64_t tab_rs, const void* ids, int ids64, int64_t vocab,
+    uint32_t* __restrict__ bump) {
   const int row = blockIdx.x;
+  if (bump != nullptr && row == 0 && threadIdx.x == 0) *bump += 1u;
   T* xr = x + (int64_t)row * x_rs;
   T* orow = out + (int64_t)row * o_rs;
   float ss = 0.f;
@@ -91,9 +93,11 @@ template <typename T, int C>
 __global__ __launch_bounds__(256) void rmsnorm_vec8_kernel(
     T* __restrict__ x, int64_t x_rs, const T* __restrict__ residual, int64_t r_rs,
     const T* __restrict__ gamma, T* __restrict__ out, int64_t o_rs, int N, float eps,
-    const T* __restrict__ table, int64_t tab_rs, const void* ids, int ids64, int64_t vocab) {
+    const T* __restrict__ table, int64_t tab_rs, const void* ids, int ids64, int64_t vocab,
+    uint32_t* __restrict__ bump) {
   typedef T V8 __attribute__((ext_vector_type(8)));
   const int row = blockIdx.x, nch = N / 8;
+  if (bump != nullptr && row == 0 && threadIdx.x == 0) *bump += 1u;
   T* xr = x + (int64_t)row * x_rs;
   const T* src = xr;
   if (table != nullptr) {
@@ -148,7 +152,8 @@ __global__ __launch_bounds__(256) void rmsnorm_vec8_kernel(
 template <typename T>
 int launch_rmsnorm(T* x, int64_t x_rs, const T* residual, int64_t r_rs, const T* gamma, T* out,
                    int64_t o_rs, int64_t M, int64_t N, float eps, const T* table, int64_t tab_rs,
-                   const void* ids, int ids64, int64_t vocab, hipStream_t stream) {
+                   const void* ids, int ids64, int64_t vocab, hipStream_t stream,
+                   uint32_t* bump = nullptr) {
   const auto al16 = [](const void* p, int64_t rs) {
     return ((uintptr_t)p % 16) == 0 && (rs * (int64_t)sizeof(T)) % 16 == 0;
   };
@@ -159,7 +164,7 @@ int launch_rmsnorm(T* x, int64_t x_rs, const T* residual, int64_t r_rs, const T*
     const int C = (int)((N + 2047) / 2048);
     auto go = [&](auto kern) {
       hipLaunchKernelGGL(kern, dim3((unsigned)M), dim3(256), 0, stream, x, x_rs, residual, r_rs,
-                         gamma, out, o_rs, (int)N, eps, table, tab_rs, ids, ids64, vocab);
+                         gamma, out, o_rs, (int)N, eps, table, tab_rs, ids, ids64, vocab, bump);
     };
     if (C == 1) go(rmsnorm_vec8_kernel<T, 1>);
     else if (C == 2) go(rmsnorm_vec8_kernel<T, 2>);
@@ -168,7 +173,7 @@ int launch_rmsnorm(T* x, int64_t x_rs, const T* residual, int64_t r_rs, const T*
   } else {
     hipLaunchKernelGGL((rmsnorm_kernel<T, 256>), dim3((unsigned)M), dim3(256), 0, stream, x, x_rs,
                        residual, r_rs, gamma, out, o_rs, (int)N, eps, table, tab_rs, ids, ids64,
-                       vocab);
+                       vocab, bump);
   }
   LL_RETURN_LAUNCH();
 }
@@ -189,20 +194,50 @@ extern "C" int ll_rmsnorm(void* x, int64_t x_row_stride, const void* residual,
 }
 
 // h[t] = table[ids[t]] and out[t] = rmsnorm(h[t]) * gamma in one launch: the
-// results of ll_embedding followed by ll_rmsnorm, bit for bit.
-extern "C" int ll_embedding_rmsnorm(const void* table, int64_t table_row_stride, int64_t vocab,
-                                    const void* ids, int ids_i64, void* h, int64_t h_row_stride,
-                                    const void* gamma, void* out, int64_t out_row_stride,
-                                    int64_t ntok, int64_t hidden, float eps, int dtype,
-                                    hipStream_t stream) {
+// results of ll_embedding followed by ll_rmsnorm, bit for bit. With a
+// non-null `epoch`, the launch also adds 1 to that word (the decode step's
+// epoch, which the step's fused launches read to tell their flags from the
+// previous step's): the first launch of a decode step does it, so the step
+// needs no launch of its own for it.
+namespace {
+int embedding_rmsnorm_impl(const void* table, int64_t table_row_stride, int64_t vocab,
+                           const void* ids, int ids_i64, void* h, int64_t h_row_stride,
+                           const void* gamma, void* out, int64_t out_row_stride, int64_t ntok,
+                           int64_t hidden, float eps, int dtype, uint32_t* epoch,
+                           hipStream_t stream) {
   LL_CHECK_ARG(table && ids && h && gamma && out, "ll_embedding_rmsnorm: null pointer");
   LL_CHECK_ARG(vocab > 0 && ntok >= 0 && hidden > 0, "ll_embedding_rmsnorm: bad shape");
   if (ntok == 0) return LL_OK;
   return LL_DISPATCH_DTYPE(dtype, T, [&]() -> int {
     return launch_rmsnorm<T>((T*)h, h_row_stride, nullptr, 0, (const T*)gamma, (T*)out,
                              out_row_stride, ntok, hidden, eps, (const T*)table, table_row_stride,
-                             ids, ids_i64, vocab, stream);
+                             ids, ids_i64, vocab, stream, epoch);
   });
+}
+}  // namespace
+
+extern "C" int ll_embedding_rmsnorm(const void* table, int64_t table_row_stride, int64_t vocab,
+                                    const void* ids, int ids_i64, void* h, int64_t h_row_stride,
+                                    const void* gamma, void* out, int64_t out_row_stride,
+                                    int64_t ntok, int64_t hidden, float eps, int dtype,
+                                    hipStream_t stream) {
+  return embedding_rmsnorm_impl(table, table_row_stride, vocab, ids, ids_i64, h, h_row_stride,
+                                gamma, out, out_row_stride, ntok, hidden, eps, dtype, nullptr,
+                                stream);
+}
+
+extern "C" int ll_embedding_rmsnorm_epoch(const void* table, int64_t table_row_stride,
+                                          int64_t vocab, const void* ids, int ids_i64, void* h,
+                                          int64_t h_row_stride, const void* gamma, void* out,
+                                          int64_t out_row_stride, int64_t ntok, int64_t hidden,
+                                          float eps, int dtype, uint32_t* epoch,
+                                          hipStream_t stream) {
+  LL_CHECK_ARG(epoch != nullptr, "ll_embedding_rmsnorm_epoch: null epoch word");
+  LL_CHECK_ARG(ntok > 0, "ll_embedding_rmsnorm_epoch: needs at least one token (the epoch "
+                         "is advanced by the launch)");
+  return embedding_rmsnorm_impl(table, table_row_stride, vocab, ids, ids_i64, h, h_row_stride,
+                                gamma, out, out_row_stride, ntok, hidden, eps, dtype, epoch,
+                                stream);
 }
 
 // ============================================================== RoPE (drop-in)
@@ -509,7 +544,10 @@ extern "C" int ll_embedding(const void* table, int64_t table_row_stride, int64_t
 }
 
 // ============================================================== argmax
-// out[m] = first index of the maximum of row m (torch.argmax tie rule).
+// out[m] = first index of the maximum of row m (torch.argmax tie rule), or
+// -1 for every row when a status word is given and is nonzero (the decode
+// step's fused launches set it when a flag wait gave up; -1 is no token id,
+// so the host, which reads the tokens anyway, sees that the step is invalid).
 // Pass 1: every workgroup reduces an 8192-wide chunk of a row to a
 // (value, index) partial; pass 2 reduces the partials of each row. (Two
 // launches: an in-launch last-workgroup merge would need a device-scope
@@ -519,6 +557,11 @@ constexpr int kArgmaxChunkV = 8192;    // the same for the 16-byte-load pass
 
 __device__ __forceinline__ void argmax_merge(float& v, int& i, float ov, int oi) {
   if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
+}
+
+__device__ __forceinline__ int64_t argmax_result(int bi, const uint32_t* status) {
+  if (status != nullptr && *status != 0u) return -1;
+  return (int64_t)(bi == 0x7fffffff ? 0 : bi);
 }
 
 __device__ __forceinline__ void argmax_block_reduce(float& v, int& i, float* sv, int* si) {
@@ -540,7 +583,8 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const T* __restrict
                                                              int N, int chunk,
                                                              float* __restrict__ pval,
                                                              int* __restrict__ pidx,
-                                                             int64_t* __restrict__ out) {
+                                                             int64_t* __restrict__ out,
+                                                             const uint32_t* __restrict__ status) {
   __shared__ float sv[4];
   __shared__ int si[4];
   const int row = blockIdx.y, c = blockIdx.x, nchunk = gridDim.x;
@@ -552,7 +596,7 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const T* __restrict
   argmax_block_reduce(best, bi, sv, si);
   if (threadIdx.x == 0) {
     if (nchunk == 1) {
-      out[row] = (int64_t)(bi == 0x7fffffff ? 0 : bi);
+      out[row] = argmax_result(bi, status);
     } else {
       pval[row * nchunk + c] = best;
       pidx[row * nchunk + c] = bi;
@@ -569,7 +613,8 @@ __global__ __launch_bounds__(256) void argmax_partial_vec8_kernel(const T* __res
                                                                   int64_t x_rs, int N,
                                                                   float* __restrict__ pval,
                                                                   int* __restrict__ pidx,
-                                                                  int64_t* __restrict__ out) {
+                                                                  int64_t* __restrict__ out,
+                                                                  const uint32_t* __restrict__ status) {
   typedef T V8 __attribute__((ext_vector_type(8)));
   constexpr int PER = kArgmaxChunkV / (256 * 8);  // 16-byte loads per thread
   __shared__ float sv[4];
@@ -596,7 +641,7 @@ __global__ __launch_bounds__(256) void argmax_partial_vec8_kernel(const T* __res
   argmax_block_reduce(best, bi, sv, si);
   if (threadIdx.x == 0) {
     if (nchunk == 1) {
-      out[row] = (int64_t)(bi == 0x7fffffff ? 0 : bi);
+      out[row] = argmax_result(bi, status);
     } else {
       pval[row * nchunk + c] = best;
       pidx[row * nchunk + c] = bi;
@@ -606,7 +651,8 @@ __global__ __launch_bounds__(256) void argmax_partial_vec8_kernel(const T* __res
 
 __global__ __launch_bounds__(256) void argmax_final_kernel(const float* __restrict__ pval,
                                                            const int* __restrict__ pidx,
-                                                           int nchunk, int64_t* __restrict__ out) {
+                                                           int nchunk, int64_t* __restrict__ out,
+                                                           const uint32_t* __restrict__ status) {
   __shared__ float sv[4];
   __shared__ int si[4];
   const int row = blockIdx.x;
@@ -615,7 +661,7 @@ __global__ __launch_bounds__(256) void argmax_final_kernel(const float* __restri
   for (int i = threadIdx.x; i < nchunk; i += 256)
     argmax_merge(best, bi, pval[row * nchunk + i], pidx[row * nchunk + i]);
   argmax_block_reduce(best, bi, sv, si);
-  if (threadIdx.x == 0) out[row] = (int64_t)(bi == 0x7fffffff ? 0 : bi);
+  if (threadIdx.x == 0) out[row] = argmax_result(bi, status);
 }
 
 
@@ -624,8 +670,10 @@ extern "C" int64_t ll_argmax_workspace_size(int64_t M, int64_t N) {
   return nchunk > 1 ? M * nchunk * 8 : 0;
 }
 
-extern "C" int ll_argmax(const void* x, int64_t x_row_stride, int64_t M, int64_t N, int64_t* out,
-                         void* workspace, int64_t workspace_bytes, int dtype, hipStream_t stream) {
+namespace {
+int argmax_impl(const void* x, int64_t x_row_stride, int64_t M, int64_t N, int64_t* out,
+                void* workspace, int64_t workspace_bytes, int dtype, const uint32_t* status,
+                hipStream_t stream) {
   LL_CHECK_ARG(x && out, "ll_argmax: null pointer");
   LL_CHECK_ARG(N > 0, "ll_argmax: empty rows");
   if (M == 0) return LL_OK;
@@ -645,19 +693,36 @@ extern "C" int ll_argmax(const void* x, int64_t x_row_stride, int64_t M, int64_t
     if constexpr (sizeof(T) == 2) {
       if (vec)
         hipLaunchKernelGGL((argmax_partial_vec8_kernel<T>), dim3(nchunk, (unsigned)M), dim3(256),
-                           0, stream, (const T*)x, x_row_stride, (int)N, pval, pidx, out);
+                           0, stream, (const T*)x, x_row_stride, (int)N, pval, pidx, out, status);
       else
         hipLaunchKernelGGL((argmax_partial_kernel<T>), dim3(nchunk, (unsigned)M), dim3(256), 0,
-                           stream, (const T*)x, x_row_stride, (int)N, kArgmaxChunk, pval, pidx, out);
+                           stream, (const T*)x, x_row_stride, (int)N, kArgmaxChunk, pval, pidx, out,
+                           status);
     } else {
       hipLaunchKernelGGL((argmax_partial_kernel<T>), dim3(nchunk, (unsigned)M), dim3(256), 0,
-                         stream, (const T*)x, x_row_stride, (int)N, kArgmaxChunk, pval, pidx, out);
+                         stream, (const T*)x, x_row_stride, (int)N, kArgmaxChunk, pval, pidx, out,
+                         status);
     }
     if (nchunk > 1)
       hipLaunchKernelGGL(argmax_final_kernel, dim3((unsigned)M), dim3(256), 0, stream, pval, pidx,
-                         nchunk, out);
+                         nchunk, out, status);
     LL_RETURN_LAUNCH();
   });
+}
+}  // namespace
+
+extern "C" int ll_argmax(const void* x, int64_t x_row_stride, int64_t M, int64_t N, int64_t* out,
+                         void* workspace, int64_t workspace_bytes, int dtype, hipStream_t stream) {
+  return argmax_impl(x, x_row_stride, M, N, out, workspace, workspace_bytes, dtype, nullptr,
+                     stream);
+}
+
+extern "C" int ll_argmax_status(const void* x, int64_t x_row_stride, int64_t M, int64_t N,
+                                int64_t* out, void* workspace, int64_t workspace_bytes, int dtype,
+                                const uint32_t* status, hipStream_t stream) {
+  LL_CHECK_ARG(status != nullptr, "ll_argmax_status: null status word");
+  return argmax_impl(x, x_row_stride, M, N, out, workspace, workspace_bytes, dtype, status,
+                     stream);
 }
 
 // ============================================================== slot table

@@ -2,7 +2,7 @@
 //
 // Replaces the cuBLAS products of the reference token loop
 // (litelang/models/qwen2/layer/transformer_layer.py:80,82,95-109,193 and
-// post_layer.py:50-52). W keeps the nn.Linear [out, in] layout so that both
+// post_layer.py:20-22). W keeps the nn.Linear [out, in] layout so that both
 // MFMA operands are 16-byte k-contiguous loads.
 //
 // Kernels:

@@ -587,12 +587,20 @@ int launch_tiles(const TileArgs& a0, hipStream_t stream) {
   return LL_OK;
 }
 
+// ldx, ldw in elements of es bytes; ldy in elements of Y, whose rows hold
+// ny outputs (N, or N / 2 for the gate/up epilogues).
 int check_tile_args(const char* name, const void* X, int64_t ldx, const void* W, int64_t ldw,
-                    const void* Y, int64_t M, int64_t N, int64_t K_b, int64_t es) {
+                    const void* Y, int64_t ldy, int64_t ny, int64_t M, int64_t N, int64_t K_b,
+                    int64_t es) {
   LL_CHECK_ARG(X && W && Y, "%s: null pointer", name);
   LL_CHECK_ARG(M > 0 && N > 0 && N % 4 == 0 && K_b > 0 && K_b % kRB == 0,
                "%s: needs M > 0, N %% 4 == 0 and K a multiple of %lld (M=%lld N=%lld K=%lld)", name,
                (long long)(kRB / es), (long long)M, (long long)N, (long long)(K_b / es));
+  LL_CHECK_ARG(ldx * es >= K_b && ldw * es >= K_b && ldy >= ny,
+               "%s: row strides shorter than the rows (ldx=%lld ldw=%lld K=%lld, ldy=%lld for "
+               "%lld outputs per row)",
+               name, (long long)ldx, (long long)ldw, (long long)(K_b / es), (long long)ldy,
+               (long long)ny);
   LL_CHECK_ARG((ldx * es) % 16 == 0 && (ldw * es) % 16 == 0 &&
                    (((uintptr_t)X | (uintptr_t)W) % 16) == 0,
                "%s: X and W rows must be 16 B aligned", name);
@@ -623,7 +631,7 @@ extern "C" int ll_gemm_tiled(const void* X, int64_t ldx, const void* W, int64_t 
                              const void* bias, void* Y, int64_t ldy, int64_t M, int64_t N,
                              int64_t K, int dtype, hipStream_t stream) {
   LL_CHECK_ARG(dtype == LL_BF16 || dtype == LL_F16, "ll_gemm_tiled: bf16 or fp16 only");
-  const int rc = check_tile_args("ll_gemm_tiled", X, ldx, W, ldw, Y, M, N, K * 2, 2);
+  const int rc = check_tile_args("ll_gemm_tiled", X, ldx, W, ldw, Y, ldy, N, M, N, K * 2, 2);
   if (rc != LL_OK) return rc;
   LL_CHECK_ARG(ldy % 4 == 0 && ((uintptr_t)Y) % 8 == 0, "ll_gemm_tiled: Y rows must be 8 B aligned");
   LL_CHECK_ARG(((uintptr_t)bias) % 8 == 0, "ll_gemm_tiled: bias must be 8 B aligned");
@@ -651,7 +659,8 @@ extern "C" int ll_gemm_gate_up_silu_tiled(const void* X, int64_t ldx, const void
                                           int64_t ldy, hipStream_t stream) {
   LL_CHECK_ARG(dtype == LL_BF16 || dtype == LL_F16, "ll_gemm_gate_up_silu_tiled: bf16 or fp16 only");
   LL_CHECK_ARG(I % 128 == 0, "ll_gemm_gate_up_silu_tiled: I must be a multiple of 128");
-  const int rc = check_tile_args("ll_gemm_gate_up_silu_tiled", X, ldx, W_il, K, Y, M, 2 * I, K * 2, 2);
+  const int rc = check_tile_args("ll_gemm_gate_up_silu_tiled", X, ldx, W_il, K, Y, ldy, I, M,
+                                 2 * I, K * 2, 2);
   if (rc != LL_OK) return rc;
   LL_CHECK_ARG(ldy % 4 == 0 && ((uintptr_t)Y) % 8 == 0,
                "ll_gemm_gate_up_silu_tiled: Y rows must be 8 B aligned");
@@ -664,7 +673,7 @@ extern "C" int ll_gemm_i8_tiled(const int8_t* Xq, int64_t ldx, const float* s_to
                                 const int8_t* Wq, int64_t ldw, const void* s_ch, int s_ch_dtype,
                                 const void* bias, void* Y, int64_t ldy, int64_t M, int64_t N,
                                 int64_t K, int out_dtype, hipStream_t stream) {
-  const int rc = check_tile_args("ll_gemm_i8_tiled", Xq, ldx, Wq, ldw, Y, M, N, K, 1);
+  const int rc = check_tile_args("ll_gemm_i8_tiled", Xq, ldx, Wq, ldw, Y, ldy, N, M, N, K, 1);
   if (rc != LL_OK) return rc;
   LL_CHECK_ARG(out_dtype == LL_BF16 || out_dtype == LL_F16 || out_dtype == LL_F32,
                "ll_gemm_i8_tiled: bad output dtype %d", out_dtype);
@@ -685,7 +694,7 @@ extern "C" int ll_gemm_i8_tiled(const int8_t* Xq, int64_t ldx, const float* s_to
 extern "C" int ll_gemm_i8_i32_tiled(const int8_t* Xq, int64_t ldx, const int8_t* Wq, int64_t ldw,
                                     int32_t* Y, int64_t ldy, int64_t M, int64_t N, int64_t K,
                                     hipStream_t stream) {
-  const int rc = check_tile_args("ll_gemm_i8_i32_tiled", Xq, ldx, Wq, ldw, Y, M, N, K, 1);
+  const int rc = check_tile_args("ll_gemm_i8_i32_tiled", Xq, ldx, Wq, ldw, Y, ldy, N, M, N, K, 1);
   if (rc != LL_OK) return rc;
   LL_CHECK_ARG(ldy % 4 == 0 && ((uintptr_t)Y) % 16 == 0,
                "ll_gemm_i8_i32_tiled: Y rows must be 16 B aligned");
@@ -723,8 +732,8 @@ extern "C" int ll_gemm_i8_gate_up_silu_tiled(const int8_t* Xq, int64_t ldx, cons
                                              int out_dtype, void* Y, int64_t ldy,
                                              hipStream_t stream) {
   LL_CHECK_ARG(I % 128 == 0, "ll_gemm_i8_gate_up_silu_tiled: I must be a multiple of 128");
-  const int rc = check_tile_args("ll_gemm_i8_gate_up_silu_tiled", Xq, ldx, Wq_il, K, Y, M, 2 * I,
-                                 K, 1);
+  const int rc = check_tile_args("ll_gemm_i8_gate_up_silu_tiled", Xq, ldx, Wq_il, K, Y, ldy, I, M,
+                                 2 * I, K, 1);
   if (rc != LL_OK) return rc;
   LL_CHECK_ARG(out_dtype == LL_BF16 || out_dtype == LL_F16,
                "ll_gemm_i8_gate_up_silu_tiled: bf16 or fp16 output");

@@ -10,7 +10,7 @@ these fusions, each bit-identical to the unfused sequence:
   * RoPE of q and k + KV-pool scatter in one kernel reading cos/sin by
     position (transformer_layer.py:102-115,142-143);
   * the final residual add is applied only to the rows the post layer keeps
-    (post_layer.py:56-71), fused with the final RMSNorm.
+    (post_layer.py:26-41), fused with the final RMSNorm.
 """
 from __future__ import annotations
 
@@ -114,7 +114,7 @@ class Qwen2Model:
 
     def _post(self, hs, fs, out=None):
         """Final residual add + RMSNorm (eps 1e-5), lm_head, greedy argmax
-        (post_layer.py:44-54,105-107)."""
+        (post_layer.py:14-24,43-45,75-77)."""
         y = ops.rmsnorm(hs, self.w.norm, self.cfg.final_norm_eps, residual=fs)
         logits = ops.gemm(y, self.w.lm_head)
         self.last_logits = logits
@@ -215,17 +215,20 @@ class Qwen2Model:
             h = ops.embedding(w.embed, ids)
             return self._decode_w8a8(h, B, part, q, attn, act, positions, seq_len, rids, slots,
                                      pool, r2t, max_len, out)
-        h, x = ops.embedding_rmsnorm(w.embed, ids, w.layers[0]["ln1"], cfg.rms_norm_eps)
+        # layers after the first take their QKV partials from the launch that
+        # finishes the previous layer (residual + RMSNorm + QKV projection);
+        # those launches tell this step's flags by the epoch, which the
+        # step's first launch advances
+        fuse_qkv = self.norm_qkv_splits(B) > 0
+        epoch = ops.decode_epoch(dev) if fuse_qkv else None
+        h, x = ops.embedding_rmsnorm(w.embed, ids, w.layers[0]["ln1"], cfg.rms_norm_eps,
+                                     epoch=epoch)
 
         def proj(xin, lw, pk, name):
             if pk.get(name) is not None:
                 return ops.gemm_splitk_packed(xin, pk[name], part)
             return ops.gemm_splitk(xin, lw[name], part)
 
-        # layers after the first take their QKV partials from the launch that
-        # finishes the previous layer (residual + RMSNorm + QKV projection)
-        fuse_qkv = self.norm_qkv_splits(B) > 0
-        epoch = ops.decode_epoch_advance(dev) if fuse_qkv else None
         qkv_s = None
         for li, (lw, pk) in enumerate(zip(w.layers, w.packed)):
             s = qkv_s if qkv_s is not None else proj(x, lw, pk, "wqkv")
@@ -252,7 +255,9 @@ class Qwen2Model:
         else:
             logits = ops.gemm(x, w.lm_head)
         self.last_logits = logits
-        return ops.argmax(logits, out=out)
+        # a fused launch that gave up a flag wait turns every token into -1
+        # (the host raises on it, runner_batch.check_step_tokens)
+        return ops.argmax(logits, out=out, status=ops.decode_sync_error(dev) if fuse_qkv else None)
 
     def _decode_w8a8(self, h, B, part, q, attn, act, positions, seq_len, rids, slots, pool, r2t,
                      max_len, out):
@@ -341,7 +346,7 @@ class Qwen2Model:
                                   model_inputs.b_seq_len, max_len, r2t, b_shared_seq_len=shared)
 
         f = self._layers(h, T, mem_idxs, model_inputs.position_ids, pool, attention)
-        # last row of each request (post_layer.py:56-71)
+        # last row of each request (post_layer.py:26-41)
         rows = [s + (l - sh) - 1 for s, l, sh in zip(start_h, lens_h, shared_h)]
         rows_d = torch.from_numpy(np.asarray(rows, dtype=np.int64)).pin_memory().to(
             self.device, non_blocking=True)
@@ -411,7 +416,30 @@ class Qwen2ModelRunner:
                                   tp_rank=self.tp_rank_, tp_world_size=self.world_size_,
                                   kv_max_size=self.kv_max_size_arg_, device=self.device_)
         self.radix_cache = RadixTree() if self.use_radix_cache_ else None
+        self._check_merge_premise()
         return self.kv_cache.kv_max_size_
+
+    def _check_merge_premise(self):
+        """Decode attention merges its splits inside the split stage only
+        where all workgroups of a sequence share an XCD (the dispatcher's
+        round-robin gives that). Checked once on this machine at the decode
+        shape; when it does not hold, every decode attention call of the
+        process merges in a separate kernel instead."""
+        cfg = self.config_
+        self.same_launch_merge = ops.decode_attention_xcd_premise(
+            self.device_, min(self.max_batch_size_, 64), cfg.num_heads,
+            cfg.num_key_value_heads, cfg.head_dim, self.max_length_)
+        if not self.same_launch_merge:
+            ops.set_same_launch_merge(False)
+
+    def reset_decode_fault(self):
+        """Clear the error word a fused decode launch sets when it gives up a
+        flag wait (on the decode graphs' stream and on the current stream);
+        until then every decode step returns token ids of -1."""
+        from .decode_graph import _capture_stream
+        with torch.cuda.stream(_capture_stream(self.device_)):
+            ops.decode_sync_status(self.device_, reset=True)
+        ops.decode_sync_status(self.device_, reset=True)
 
     def _alloc_for_forward(self, model_inputs):
         """Slot allocation done by layer 0 in the reference (transformer_layer.py:53-60)."""

@@ -43,7 +43,7 @@ class Qwen2Config:
     vocab_size: int
     tie_word_embeddings: bool = True
     rms_norm_eps: float = 1e-6
-    final_norm_eps: float = 1e-5   # post_layer.py:42
+    final_norm_eps: float = 1e-5   # post_layer.py:12
     rope_theta: float = 1e6        # pre_layer.py:22
 
     @property

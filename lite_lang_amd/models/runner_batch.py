@@ -11,7 +11,10 @@ field names. Differences in mechanism, not in results:
     request's `output_tokens` list is completed on first read (and at
     filter / merge / radix insert), so a decode loop does not wait on the
     device every step (the reference reads 2*B scalars per step,
-    runner_batch.py:231-234).
+    runner_batch.py:231-234);
+  * a token id of -1 marks a decode step whose fused launch gave up a
+    bounded flag wait (ll_argmax_status): reading one raises DecodeStepError
+    instead of handing it to a request.
 """
 from __future__ import annotations
 
@@ -22,6 +25,22 @@ import torch
 
 from .cache import PageCache
 from .radix_cache import RadixTree
+
+
+class DecodeStepError(RuntimeError):
+    """A decode step returned token id -1: one of its fused launches gave up
+    a bounded flag wait, so that step's outputs (and those of every later step
+    until the error word is reset, Qwen2ModelRunner.reset_decode_fault) are
+    invalid."""
+
+
+def check_step_tokens(tokens, what="decode step"):
+    """Raise DecodeStepError when any token id of a step is negative."""
+    arr = np.asarray(tokens)
+    if arr.size and int(arr.min()) < 0:
+        raise DecodeStepError(
+            f"{what}: token id -1 from the device: a fused decode launch gave up waiting on "
+            "its producers (outputs of this step are invalid)")
 
 
 def get_no_padding_messages_host(input_reqs, is_prefill=True):
@@ -205,6 +224,13 @@ class RunnerBatch:
             return
         self._pending[-1][2].synchronize()
         ring = self._ring.numpy()
+        try:
+            for row, reqs, _ in self._pending:
+                check_step_tokens(ring[row, :len(reqs)])
+        except DecodeStepError:
+            self._pending = []  # the steps in flight are dropped with the error
+            self._next_row = 0
+            raise
         for row, reqs, _ in self._pending:
             for j, req in enumerate(reqs):
                 if req._output_tokens is None:
@@ -221,6 +247,7 @@ class RunnerBatch:
         row, reqs, ev = self._pending.pop(0)
         ev.synchronize()
         vals = self._ring[row].numpy()
+        check_step_tokens(vals[:len(reqs)])
         for j, req in enumerate(reqs):
             if req._output_tokens is None:
                 req._output_tokens = []

@@ -115,6 +115,41 @@ def decode_attention(q, req_to_tokens, b_req_idx, b_seq_len, max_len_in_batch, c
     return out
 
 
+def decode_attention_xcd_premise(device, batch, q_heads, kv_heads, head_dim, max_len,
+                                 launches=3):
+    """Checks, on this machine, the premise of the split stage's own merge:
+    the probe kernel runs on exactly the split stage's grid, block and LDS
+    size for this shape and reports every workgroup's XCD; the premise holds
+    when workgroups whose indices agree mod 8 ran on one XCD (the split stage
+    gives every workgroup of a sequence indices of one residue), which the
+    dispatcher's round-robin over 8 XCDs gives, and so does a device of one
+    XCD. Returns True/False (True when the shape runs no split stage: head
+    dims other than 64/128)."""
+    if head_dim not in (64, 128) or batch <= 0 or q_heads % kv_heads != 0:
+        return True
+    cap = 1 << 16
+    out = torch.full((cap,), -1, dtype=torch.int32, device=device)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    for _ in range(launches):
+        n = _L.ll_decode_attention_xcc_probe(batch, q_heads, kv_heads, head_dim, max_len,
+                                             out.data_ptr(), cap, stream)
+        if n < 0:
+            _lib.check(n, "ll_decode_attention_xcc_probe")
+        got = out[:n].cpu().long()
+        if int(got.min()) < 0:
+            return False
+        # workgroup i against workgroup i mod 8
+        if not bool(torch.all(got == got[torch.arange(n) % 8])):
+            return False
+    return True
+
+
+def set_same_launch_merge(enable):
+    """Process-wide: whether decode attention merges its splits in the split
+    stage (default) or in a separate kernel; returns the previous setting."""
+    return bool(_L.ll_decode_attention_set_same_launch_merge(int(bool(enable))))
+
+
 def prefill_attention(q, k, v, o, b_req_idx, b_start_loc, b_seq_len, max_input_len,
                       req_to_tokens, b_shared_seq_len=None, sm_scale=None):
     """NoPad causal prefill over the slot table (optionally with shared prefixes)."""
@@ -235,32 +270,43 @@ def embedding(table, ids, out=None):
     return out
 
 
-def embedding_rmsnorm(table, ids, gamma, eps):
-    """(h, out): h = table[ids], out = rmsnorm(h) * gamma, in one launch."""
-    _dev(table, ids, gamma)
+def embedding_rmsnorm(table, ids, gamma, eps, epoch=None):
+    """(h, out): h = table[ids], out = rmsnorm(h) * gamma, in one launch. With
+    `epoch` (the int32 word of decode_epoch), the launch also adds 1 to it."""
+    _dev(table, ids, gamma, epoch)
     V, Hd = table.shape
     T = ids.shape[0]
     assert table.stride(1) == 1 and gamma.shape == (Hd,)
     h = torch.empty((T, Hd), dtype=table.dtype, device=table.device)
     out = torch.empty_like(h)
-    rc = _L.ll_embedding_rmsnorm(table.data_ptr(), table.stride(0), V, ids.data_ptr(),
-                                 _idx(ids, "ids"), h.data_ptr(), h.stride(0), gamma.data_ptr(),
-                                 out.data_ptr(), out.stride(0), T, Hd, float(eps),
-                                 dtype_code(table), _stream(table))
+    head = (table.data_ptr(), table.stride(0), V, ids.data_ptr(), _idx(ids, "ids"), h.data_ptr(),
+            h.stride(0), gamma.data_ptr(), out.data_ptr(), out.stride(0), T, Hd, float(eps),
+            dtype_code(table))
+    if epoch is None:
+        rc = _L.ll_embedding_rmsnorm(*head, _stream(table))
+    else:
+        assert epoch.dtype == torch.int32 and epoch.numel() == 1
+        rc = _L.ll_embedding_rmsnorm_epoch(*head, epoch.data_ptr(), _stream(table))
     _lib.check(rc, "ll_embedding_rmsnorm")
     return h, out
 
 
-def argmax(x, out=None):
-    _dev(x, out)
+def argmax(x, out=None, status=None):
+    """First-index argmax of every row; with `status` (an int32 device word,
+    decode_sync_error's), every output is -1 while that word is nonzero."""
+    _dev(x, out, status)
     M, N = x.shape
     assert x.stride(1) == 1
     if out is None:
         out = torch.empty((M,), dtype=torch.int64, device=x.device)
     nbytes = _L.ll_argmax_workspace_size(M, N)
     ws = workspace(x.device, "argmax", nbytes)
-    rc = _L.ll_argmax(x.data_ptr(), x.stride(0), M, N, out.data_ptr(), ws.data_ptr(), ws.numel(),
-                      dtype_code(x), _stream(x))
+    head = (x.data_ptr(), x.stride(0), M, N, out.data_ptr(), ws.data_ptr(), ws.numel(),
+            dtype_code(x))
+    if status is None:
+        rc = _L.ll_argmax(*head, _stream(x))
+    else:
+        rc = _L.ll_argmax_status(*head, status.data_ptr(), _stream(x))
     _lib.check(rc, "ll_argmax")
     return out
 
@@ -561,13 +607,33 @@ def decode_sync(device):
     return workspace(device, "decode_sync", int(_L.ll_decode_sync_bytes()))
 
 
+def decode_epoch(device):
+    """The decode-step epoch word of the current stream (int32 [1]): every
+    fused launch of one step uses it with its own tag, and the step's first
+    launch advances it (embedding_rmsnorm(epoch=...))."""
+    return workspace(device, "decode_epoch", 4).view(torch.int32)[:1]
+
+
 def decode_epoch_advance(device):
-    """Advance the decode-step epoch word (a device-side add, so a captured
-    graph advances it on every replay) and return it: every fused launch of
-    one step uses it with its own tag."""
-    ep = workspace(device, "decode_epoch", 4).view(torch.int32)[:1]
+    """Advance the decode-step epoch word with a launch of its own (a
+    device-side add, so a captured graph advances it on every replay) and
+    return it; the model's decode step advances it inside its first launch
+    instead."""
+    ep = decode_epoch(device)
     ep.add_(1)
     return ep
+
+
+def decode_sync_error(device):
+    """The error word of the current stream's decode sync words (int32 [1]):
+    nonzero once a fused launch's flag wait gave up, until reset."""
+    off = int(_L.ll_decode_sync_error_offset())
+    return decode_sync(device)[off:off + 4].view(torch.int32)
+
+
+def set_decode_spin_limit(polls):
+    """Polls before a fused launch's flag wait gives up (0: the default)."""
+    _lib.check(_L.ll_decode_sync_set_spin_limit(int(polls)), "ll_decode_sync_set_spin_limit")
 
 
 def decode_sync_status(device, reset=False):

@@ -10,7 +10,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from lite_lang_amd.models.runner_batch import RunnerBatch
+from lite_lang_amd.models.runner_batch import RunnerBatch, check_step_tokens
 
 
 class IdTokenizer:
@@ -50,7 +50,9 @@ class LocalModelClient:
         batch = self.batchs_[batch_id]
         out = self.model_runner_.forward(batch)
         req_ids = batch.update_forward_message(out)
-        return out.view(-1, 1).cpu().numpy(), req_ids
+        toks = out.view(-1, 1).cpu().numpy()
+        check_step_tokens(toks)
+        return toks, req_ids
 
     def prefill(self, batch_id):
         return self._step(batch_id)

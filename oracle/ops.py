@@ -184,7 +184,7 @@ def linear(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None = None) -
 
 def argmax_first(x: torch.Tensor) -> torch.Tensor:
     """Index of the first maximum of each row (torch.argmax tie rule used by
-    Qwen2PostLayer._PostProcess, post_layer.py:105-107)."""
+    Qwen2PostLayer._PostProcess, post_layer.py:75-77)."""
     a = x.detach().cpu().numpy()
     return torch.from_numpy(np.argmax(a, axis=-1).astype(np.int64))
 

@@ -2,15 +2,15 @@
 
 Dataflow follows litelang/models/qwen2/model.py:48-59 (Qwen2Model.forward),
 layer/pre_layer.py:15-30, layer/transformer_layer.py:46-194 and
-layer/post_layer.py:44-107, with the reference quirks kept:
+layer/post_layer.py:14-77, with the reference quirks kept:
   * per-layer RMSNorm eps 1e-6 (transformer_layer.py:41), final norm eps 1e-5
-    (post_layer.py:42);
+    (post_layer.py:12);
   * RoPE theta 1e6, cos/sin table built in fp32 and stored fp16
     (pre_layer.py:21-30);
   * K rotated before it is written to the pool (transformer_layer.py:115,143);
   * o_proj bias ignored (transformer_layer.py:193);
   * residual adds stored in the model dtype (transformer_layer.py:69,76);
-  * greedy argmax on the stored logits, first index on ties (post_layer.py:105-107).
+  * greedy argmax on the stored logits, first index on ties (post_layer.py:75-77).
 Compute is float64 (fp32 inside ops.math_dtype(torch.float32), used for the
 full-width geometries only); `rnd` stores an intermediate in the model dtype
 wherever the reference stores a tensor.
@@ -165,7 +165,7 @@ class Qwen2Oracle:
             act = ops.rnd(ops.silu_and_mul(gu, dt), dt)
             f = ops.rnd(self._linear(act, w, ["wd"]), dt)
             h = ops.rnd(h + f, dt)
-        if is_prefill:  # last row of each request (post_layer.py:56-71)
+        if is_prefill:  # last row of each request (post_layer.py:26-41)
             rows = [st + (l - s) - 1 for st, l, s in zip(start, lens, shared)]
         else:
             rows = list(start)

@@ -6,7 +6,7 @@ implementation independent of all three.
 
 The HF config is set to what the reference hard-codes (RoPE theta 1e6,
 RMSNorm eps 1e-6); HF applies that eps to the final norm too, where the
-reference uses 1e-5 (post_layer.py:42), so comparisons set the final-norm eps
+reference uses 1e-5 (post_layer.py:12), so comparisons set the final-norm eps
 to HF's. Weights are seeded normals scaled so that greedy decoding moves
 between tokens with clear top-1 margins; norm gains U(0.8, 1.2). Token id 0
 is <|endoftext|> (eos and pad, as in Qwen2 checkpoints).

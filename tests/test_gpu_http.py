@@ -34,7 +34,7 @@ def test_http_generate_matches_oracle(cuda):
                     max_total_length=max_out + 1, max_output_length=max_out, max_reqs=32,
                     model_client=LocalModelClient(runner), busy_scale=0.9)
     m = HttpServerManager(sch)
-    api_server.g_objs.http_server_manager = m
+    api_server.attach(m)
     try:
         client = TestClient(api_server.app)
         out = [None] * len(prompts)
@@ -54,7 +54,7 @@ def test_http_generate_matches_oracle(cuda):
             t.join(120)
     finally:
         m.stop()
-        api_server.g_objs.http_server_manager = None
+        api_server.attach(None)
     for i, p in enumerate(prompts):
         ref = Qwen2Oracle(ocfg, sd, torch.float32, 8, 64, 1024).generate([p], max_out)[0].tolist()
         assert out[i] == ref, f"prompt {i}"

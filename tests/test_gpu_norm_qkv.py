@@ -188,4 +188,10 @@ def test_model_decode_fused_norm_qkv(cuda, graph):
         agree += int((ta == tb).sum())
         total += ta.numel()
     assert agree >= 0.95 * total, f"tokens agree on {agree} of {total}"
+    # the eager path's sync words are the current stream's; a decode graph's
+    # are its capture stream's (workspaces are keyed by stream)
     assert _ops().decode_sync_status(cuda) == 0
+    if graph:
+        from lite_lang_amd.models.qwen2.decode_graph import _capture_stream
+        with torch.cuda.stream(_capture_stream(cuda)):
+            assert _ops().decode_sync_status(cuda) == 0

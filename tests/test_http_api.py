@@ -90,12 +90,12 @@ def server():
                         model_client=PromptModel(fail=fail), busy_scale=0.8)
         m = HttpServerManager(sch)
         made.append(m)
-        api_server.g_objs.http_server_manager = m
+        api_server.attach(m)
         return TestClient(api_server.app), m
     yield make
     for m in made:
         m.stop()
-    api_server.g_objs.http_server_manager = None
+    api_server.attach(None)
 
 
 def test_generate_returns_every_piece(server):

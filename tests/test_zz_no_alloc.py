@@ -82,3 +82,74 @@ def test_noalloc_rejects_shapes_beyond_its_scratch(cuda):
                                        B, H, KVH, D, max_len, ctypes.c_float(0.1), 2,
                                        torch.cuda.current_stream().cuda_stream)
     assert rc == -1 and b"scratch" in L.ll_last_error()
+
+
+_CAPTURE_SCRIPT = r"""
+import ctypes, sys
+import numpy as np
+import torch
+sys.path.insert(0, ROOT)
+from lite_lang_amd import _lib
+L = _lib.load()
+dev = torch.device("cuda:0")
+B, H, KVH, D, max_len = 40, 12, 2, 128, 600
+rs = np.random.RandomState(9)
+P = B * max_len
+g = torch.Generator(device=dev).manual_seed(9)
+q = torch.randn(B, H, D, device=dev, generator=g).bfloat16()
+pool = torch.randn(P, 2 * KVH, D, device=dev, generator=g).bfloat16()
+r2t = torch.from_numpy(rs.permutation(P).astype(np.int32)).view(B, max_len).to(dev)
+rids = torch.arange(B, dtype=torch.int32, device=dev)
+lens = torch.from_numpy(rs.randint(1, max_len + 1, size=B)).to(dev)
+k, v = pool[:, :KVH], pool[:, KVH:]
+
+def args(out):
+    return (q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0), k.stride(1),
+            v.data_ptr(), v.stride(0), v.stride(1), r2t.data_ptr(), r2t.stride(0),
+            rids.data_ptr(), 0, lens.data_ptr(), 1, out.data_ptr(), out.stride(0), out.stride(1),
+            B, H, KVH, D, max_len, ctypes.c_float(1.0 / D ** 0.5), 2)
+
+torch.cuda.synchronize()
+s = torch.cuda.Stream()
+graph = torch.cuda.CUDAGraph()
+out = torch.zeros_like(q)
+with torch.cuda.stream(s):
+    with torch.cuda.graph(graph, stream=s):
+        # the process's first no-alloc call: the scratch lookup happens here
+        rc = L.ll_decode_attention_noalloc(*args(out), s.cuda_stream)
+assert rc == 0, L.ll_last_error()
+ws = torch.zeros(L.ll_decode_attention_workspace_size(B, H, KVH, D, max_len), dtype=torch.uint8,
+                 device=dev)
+want = torch.empty_like(q)
+assert L.ll_decode_attention(*args(want), ws.data_ptr(), ws.numel(),
+                             torch.cuda.current_stream().cuda_stream) == 0
+torch.cuda.synchronize()
+for rep in range(4):
+    out.zero_()
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out, want), f"replay {rep} differs"
+    # eager no-alloc call between replays (shares the scratch array)
+    again = torch.empty_like(q)
+    assert L.ll_decode_attention_noalloc(*args(again), torch.cuda.current_stream().cuda_stream) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(again, want)
+print("capture ok", flush=True)
+"""
+
+
+def test_noalloc_first_call_inside_graph_capture(cuda):
+    """In a fresh process, the first ll_decode_attention_noalloc call happens
+    under graph capture (its scratch lookup queues no work, so nothing but the
+    attention kernel is recorded); four replays, with eager no-alloc calls
+    between them, each equal the workspace entry point bit for bit."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    print("case: noalloc first call under capture (subprocess)", flush=True)
+    res = subprocess.run([sys.executable, "-c", f"ROOT = {root!r}\n" + _CAPTURE_SCRIPT],
+                         capture_output=True, text=True, timeout=180)
+    assert res.returncode == 0, res.stdout[-2000:] + res.stderr[-4000:]
+    assert "capture ok" in res.stdout
