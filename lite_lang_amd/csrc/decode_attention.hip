@@ -75,6 +75,13 @@ __device__ __forceinline__ void dma16(const void* g, void* lds) {
   __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0);
 }
 
+// Workgroup barrier for LDS data only: __syncthreads() also waits for every
+// outstanding global access (vmcnt(0)), which would drain the K/V copies in
+// flight.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 template <int N_> __device__ __forceinline__ void vm_wait() {
   static_assert(N_ >= 0 && N_ < 64, "vmcnt is a 6-bit counter");
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N_) : "memory");
@@ -349,45 +356,33 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
   // together; tail entries point at slot 0 (masked later). Only this wave reads them
   // (K/V copy addresses, the writer's patch test), and a wave's LDS accesses
   // are ordered, so no barrier stands between the slot loads and the wave's
-  // first K/V copies.
-  for (int r0 = 0; 4 * r0 < nw; r0 += 4) {  // rounds of 16 tiles, loads in flight together
-    int32_t sl[4];
+  // first K/V copies. The first round's loads are always issued (every
+  // index is clamped to a valid entry), so that the RoPE jobs' loads below
+  // share their round trip.
+  auto load_round = [&](int r0, int32_t (&sl)[4]) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int i = (wave + kWaves * (4 * (r0 + u) + (lane >> 4))) * kTT + (lane & 15);
       const int64_t t = min(tok0 + i, len > 0 ? len - 1 : (int64_t)0);  // always a valid entry
       sl[u] = slot_row[t];
     }
+  };
+  auto store_round = [&](int r0, const int32_t (&sl)[4]) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int tw = wave + kWaves * (4 * (r0 + u) + (lane >> 4));  // tile within the split
       const int i = tw * kTT + (lane & 15);                         // token within the split
       if (tw < te - tb) s_slots[i] = (i < ntok) ? sl[u] : 0;
     }
-  }
-
-  // DMA lane geometry: lane -> (row within an instruction's rows, LDS chunk position)
-  const int dr = lane / TG::CH, dp = lane % TG::CH;
-  auto issue = [&](int k) {
-    const int t0 = (wave + k * kWaves) * kTT;  // token offset of the tile within the split
-    char* buf = ring + (k % kRing) * TG::TILE_B;
-#pragma unroll
-    for (int i = 0; i < TG::IPT; ++i) {
-      const int r = i * TG::RPI + dr;
-      const int64_t slot = s_slots[t0 + r];
-      const int c = TG::swz(dp, r);
-      dma16(kbase + slot * kst + c * 16, buf + i * 1024);
-      dma16(vbase + slot * vst + c * 16, buf + kTT * TG::ROWB + i * 1024);
-    }
   };
-  // the first tiles' copies go out before the RoPE jobs and the q barrier
-#pragma unroll
-  for (int k = 0; k < kRing - 1; ++k)
-    if (k < nw) issue(k);
+  int32_t sl0[4];
+  load_round(0, sl0);
 
   // ROPE: q of the group's heads into LDS; the split holding the last tile
   // (split 0 for an empty sequence) also writes the new token's K and V (the
-  // last 2 * QD threads, one job each)
+  // last 2 * QD threads, one job each). Their loads are issued before any
+  // K/V copy: waiting for them then waits for no copy (loads and copies
+  // share the in-order vmcnt counter).
   bool writer = false;
   if constexpr (ROPE) {
     const int64_t qkv_row = (int64_t)b * ((a.H + 2 * a.KVH) * D);
@@ -408,7 +403,38 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
       rope_job<T, D, MODE>(a, b, qkv_row, (a.H + (isv ? a.KVH : 0) + kvh) * D, i, cs, sn,
                      !isv, s_kv + (isv ? D : 0), glb);
     }
-    __syncthreads();  // s_q and s_kv are complete
+  }
+  store_round(0, sl0);
+  for (int r0 = 4; 4 * r0 < nw; r0 += 4) {  // further rounds of 16 tiles (long splits)
+    int32_t sl[4];
+    load_round(r0, sl);
+    store_round(r0, sl);
+  }
+
+  // DMA lane geometry: lane -> (row within an instruction's rows, LDS chunk position)
+  const int dr = lane / TG::CH, dp = lane % TG::CH;
+  auto issue = [&](int k) {
+    const int t0 = (wave + k * kWaves) * kTT;  // token offset of the tile within the split
+    char* buf = ring + (k % kRing) * TG::TILE_B;
+#pragma unroll
+    for (int i = 0; i < TG::IPT; ++i) {
+      const int r = i * TG::RPI + dr;
+      const int64_t slot = s_slots[t0 + r];
+      const int c = TG::swz(dp, r);
+      dma16(kbase + slot * kst + c * 16, buf + i * 1024);
+      dma16(vbase + slot * vst + c * 16, buf + kTT * TG::ROWB + i * 1024);
+    }
+  };
+  // The first tile's copies go out before the q barrier; the next tile's at
+  // the top of the token loop. (Issuing both here, or refilling a buffer
+  // after computing it, measured no faster: the LDS read of the second
+  // tile's slot ids after the first tile's copies makes the compiler wait
+  // for those copies, as it cannot tell the LDS buffers apart.)
+  static_assert(kRing == 2, "the tile waits below assume two buffers per wave");
+  if (0 < nw) issue(0);
+
+  if constexpr (ROPE) {
+    lds_barrier();  // s_q and s_kv are complete (the copies stay in flight)
     const T* qs = s_q + min(n, a.G - 1) * D;
 #pragma unroll
     for (int s = 0; s < DS; ++s) qb[s] = *(const V8*)(qs + 32 * s + 8 * j);
@@ -423,9 +449,9 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
   float l_run = 0.f;        // this lane's share of the running sum
 
   for (int k = 0; k < nw; ++k) {
-    if (k + kRing - 1 < nw) {
-      issue(k + kRing - 1);
-      vm_wait<2 * TG::IPT * (kRing - 1)>();
+    if (k + 1 < nw) {
+      issue(k + 1);
+      vm_wait<2 * TG::IPT>();  // tile k's copies are done, tile k + 1's in flight
     } else {
       vm_wait<0>();
     }
