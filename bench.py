@@ -52,11 +52,7 @@ def log(msg):
 
 
 # ------------------------------------------------------------------ attention
-def bench_decode_attention(dev, iters=200, pools=28, L=600, identity=False):
-    """Config 2 (context L): returns (avg seconds per launch, algorithmic bytes
-    per launch). identity: slot table = arange instead of the seeded random
-    permutation."""
-    from lite_lang_amd import ops
+def _config2_inputs(dev, pools, L, identity=False):
     H, KVH, D = 12, 2, 128
     P = B * L
     g = torch.Generator(device=dev).manual_seed(0)
@@ -66,17 +62,15 @@ def bench_decode_attention(dev, iters=200, pools=28, L=600, identity=False):
     perm = torch.from_numpy(order.astype(np.int32)).view(B, L).to(dev)
     rids = torch.arange(B, dtype=torch.int32, device=dev)
     lens = torch.full((B,), L, dtype=torch.int64, device=dev)
-    out = torch.empty_like(q)
+    return q, pool_list, perm, rids, lens
 
-    def launch(i):
-        p = pool_list[i % pools]
-        ops.decode_attention(q, perm, rids, lens, L, p[:, :KVH], p[:, KVH:], out)
 
-    for i in range(pools):
-        launch(i)  # sizes the workspace outside the capture
+def _graph_time(dev, launch, iters, reps=5):
+    """Average seconds per launch of `iters` back-to-back launches replayed
+    from one HIP graph (events recorded on the replaying stream)."""
+    for i in range(min(iters, 32)):
+        launch(i)  # first use outside the capture (sizes workspaces)
     torch.cuda.synchronize()
-    # back-to-back launches replayed from a HIP graph, so host launch cost is
-    # not in the figure; events are recorded on the stream that replays it
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         for i in range(iters):
@@ -86,14 +80,81 @@ def bench_decode_attention(dev, iters=200, pools=28, L=600, identity=False):
     st = torch.cuda.current_stream(dev)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(st)
-    reps = 5
     for _ in range(reps):
         graph.replay()
     e1.record(st)
     torch.cuda.synchronize()
-    sec = e0.elapsed_time(e1) / 1e3 / (iters * reps)
+    return e0.elapsed_time(e1) / 1e3 / (iters * reps)
+
+
+def bench_decode_attention(dev, iters=200, pools=28, L=600, identity=False):
+    """Config 2 (context L): returns (avg seconds per launch, algorithmic bytes
+    per launch). identity: slot table = arange instead of the seeded random
+    permutation."""
+    from lite_lang_amd import ops
+    q, pool_list, perm, rids, lens = _config2_inputs(dev, pools, L, identity)
+    KVH = 2
+    B_, H, D = q.shape
+    out = torch.empty_like(q)
+
+    def launch(i):
+        p = pool_list[i % pools]
+        ops.decode_attention(q, perm, rids, lens, L, p[:, :KVH], p[:, KVH:], out)
+
+    sec = _graph_time(dev, launch, iters)
     nbytes = B * L * 2 * KVH * D * 2 + 2 * B * H * D * 2 + B * L * 4 + B * 8
     return sec, nbytes
+
+
+def bench_attention_floor(dev, iters=200, pools=28, L=600):
+    """What one launch of the config-2 K/V bytes costs at all on this GPU:
+    the decode attention itself, a plain contiguous read of each pool (the
+    same 24,576,000 K/V bytes) at several grid sizes, and the attention's
+    own gather (lengths and rows, slot ids, then every K/V row through the
+    slot table, on its split grid, no arithmetic) into registers and into
+    LDS. Every figure is one launch per pool, 28 pools cycled (688 MB, past
+    the 256 MB MALL), timed as the attention is (graph replay, events)."""
+    from lite_lang_amd import _lib, ops
+    Lb = _lib.load()
+    q, pool_list, perm, rids, lens = _config2_inputs(dev, pools, L)
+    KVH, D = 2, 128
+    out = torch.empty_like(q)
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    kv_bytes = B * L * 2 * KVH * D * 2
+    assert pool_list[0].numel() * 2 == kv_bytes
+    res = {"kv_bytes": kv_bytes, "pools": pools, "launches_per_graph": iters}
+
+    def attn(i):
+        p = pool_list[i % pools]
+        ops.decode_attention(q, perm, rids, lens, L, p[:, :KVH], p[:, KVH:], out)
+
+    res["attention_us"] = round(_graph_time(dev, attn, iters) * 1e6, 3)
+    stream = lambda: torch.cuda.current_stream(dev).cuda_stream
+    reads = {}
+    for wgs in (256, 512, 1024, 2048, 4096):
+        def read(i, wgs=wgs):
+            _lib.check(Lb.ll_probe_stream_read(pool_list[i % pools].data_ptr(), kv_bytes, wgs,
+                                               sink.data_ptr(), stream()), "ll_probe_stream_read")
+        reads[str(wgs)] = round(_graph_time(dev, read, iters) * 1e6, 3)
+    res["plain_read_us"] = reads
+    ns = int(Lb.ll_decode_attention_split_count(B, KVH, D, L))
+    res["split_count"] = ns
+    for mode, name in ((0, "gather_registers_us"), (1, "gather_lds_us")):
+        def gather(i, mode=mode):
+            p = pool_list[i % pools]
+            k, v = p[:, :KVH], p[:, KVH:]
+            _lib.check(Lb.ll_probe_kv_gather(k.data_ptr(), k.stride(0), k.stride(1), v.data_ptr(),
+                                              v.stride(0), v.stride(1), perm.data_ptr(),
+                                              perm.stride(0), rids.data_ptr(), 0, lens.data_ptr(),
+                                              1, B, KVH, D, 2, L, ns, mode, sink.data_ptr(),
+                                              stream()), "ll_probe_kv_gather")
+        res[name] = round(_graph_time(dev, gather, iters) * 1e6, 3)
+    best_read = min(reads.values())
+    res["plain_read_best_gbs"] = round(kv_bytes / best_read / 1e3, 1)
+    res["gather_best_us"] = min(res["gather_registers_us"], res["gather_lds_us"])
+    res["gather_frac_of_peak"] = round(kv_bytes / res["gather_best_us"] / 1e3 / HBM_PEAK_GBS, 4)
+    res["plain_read_frac_of_peak"] = round(kv_bytes / best_read / 1e3 / HBM_PEAK_GBS, 4)
+    return res
 
 
 # ------------------------------------------------------------------ model
@@ -425,6 +486,9 @@ def main():
     ap.add_argument("--attention-only", action="store_true",
                     help="run only the config-2 decode attention launches plus a 256 MiB "
                          "device copy of known size (for rocprofv3 --pmc traffic runs)")
+    ap.add_argument("--attention-floor", action="store_true",
+                    help="time the config-2 decode attention beside a plain read and a slot-table "
+                         "gather of the same K/V bytes (in-tree probe kernels), one JSON line")
     ap.add_argument("--norm-qkv", action="store_true",
                     help="run only the fused add + RMSNorm + QKV launch of the 3B decode step "
                          "plus a 256 MiB device copy of known size (for rocprofv3 runs)")
@@ -457,6 +521,9 @@ def main():
                               "gbs": round(nb / sec / 1e9, 1)}), flush=True)
             torch.cuda.empty_cache()
         return
+    if args.attention_floor:
+        print(json.dumps(bench_attention_floor(dev)), flush=True)
+        return
     if args.prefill_gemm:
         print(json.dumps(bench_prefill_gemms(dev)), flush=True)
         return
@@ -487,6 +554,12 @@ def main():
     fixed_us = (attn_sec - attn_bytes / (marg_gbs * 1e9)) * 1e6
     log(f"attention at ctx {2 * PROMPT}: {sec2 * 1e6:.2f} us; marginal {marg_gbs:.0f} GB/s, "
         f"fixed {fixed_us:.2f} us")
+
+    log("attention floor: plain read and gather of the same K/V bytes")
+    floor = bench_attention_floor(dev)
+    log(f"floor: plain read {min(floor['plain_read_us'].values()):.2f} us, gather "
+        f"{floor['gather_best_us']:.2f} us")
+    torch.cuda.empty_cache()
 
     log("building Qwen2.5-3B-shape runner (random init, bf16)")
     ref_new = PROMPT  # the reference harness generates 600 tokens per request
@@ -550,7 +623,15 @@ def main():
                                   "us": [round(attn_sec * 1e6, 3), round(sec2 * 1e6, 3)],
                                   "gbs": round(marg_gbs, 1),
                                   "frac": round(marg_gbs / HBM_PEAK_GBS, 4),
-                                  "fixed_us": round(fixed_us, 3)}},
+                                  "fixed_us": round(fixed_us, 3)},
+                     "floor": {"plain_read_us": min(floor["plain_read_us"].values()),
+                               "plain_read_frac": floor["plain_read_frac_of_peak"],
+                               "gather_us": floor["gather_best_us"],
+                               "gather_frac": floor["gather_frac_of_peak"],
+                               "note": "one launch over the same 24,576,000 K/V bytes: a "
+                                       "contiguous read (best grid), and the op's own gather "
+                                       "(same grid and dependent loads, no arithmetic); "
+                                       "bench.py --attention-floor"}},
         "cpu_baseline": cpu,
     }
     print(json.dumps(res), flush=True)

@@ -518,6 +518,28 @@ int ll_quant_static(const void* X, int64_t ldx, int64_t M, int64_t K, int dtype,
 int ll_dequant_splitk(const int32_t* part, int splits, const float* s_tok, const void* s_ch,
                       int s_ch_dtype, float* out, int64_t M, int64_t N, hipStream_t stream);
 
+/* ---- Measurement probes (no counterpart in the reference; bench.py
+ * --attention-floor times them against the decode attention).
+ * ll_probe_stream_read: a plain streaming read of `bytes` contiguous bytes
+ * (16 B aligned) by `workgroups` workgroups of 256 threads.
+ * ll_probe_kv_gather: the K/V rows ll_decode_attention reads, through the
+ * same slot table, request rows and lengths, on its split grid (nsplit as
+ * the attention chooses it), with no arithmetic: mode 0 into registers,
+ * mode 1 copied into LDS. `sink` is a device word written only in a case no
+ * input produces (it keeps the loads live). */
+int ll_probe_stream_read(const void* src, int64_t bytes, int64_t workgroups, uint32_t* sink,
+                         hipStream_t stream);
+int ll_probe_kv_gather(const void* k_cache, int64_t k_stride_tok, int64_t k_stride_head,
+                       const void* v_cache, int64_t v_stride_tok, int64_t v_stride_head,
+                       const int32_t* req_to_tokens, int64_t req_to_tokens_stride,
+                       const void* b_req_idx, int req_idx_i64, const void* b_seq_len,
+                       int seq_len_i64, int64_t batch, int64_t kv_heads, int64_t head_dim,
+                       int64_t elem_bytes, int64_t max_len_in_batch, int64_t nsplit, int mode,
+                       uint32_t* sink, hipStream_t stream);
+/* The split count ll_decode_attention uses for this shape (1: no split). */
+int ll_decode_attention_split_count(int64_t batch, int64_t kv_heads, int64_t head_dim,
+                                    int64_t max_len_in_batch);
+
 #ifdef __cplusplus
 }
 #endif

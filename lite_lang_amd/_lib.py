@@ -104,6 +104,10 @@ SIGNATURES = {
     "ll_silu_and_mul_splitk_i32": (I32, [P, I32, P, P, I32, P, I64, I64, I64, I32, P]),
     "ll_rope_kv_scatter_splitk": (I32, [P, I32, P, P, I64, I64, I64, I64, I64, P, I32, P, P, I64,
                                         I32, P, P, I64, I64, I32, P]),
+    "ll_probe_stream_read": (I32, [P, I64, I64, P, P]),
+    "ll_probe_kv_gather": (I32, [P, I64, I64, P, I64, I64, P, I64, P, I32, P, I32, I64, I64, I64,
+                                 I64, I64, I64, I32, P, P]),
+    "ll_decode_attention_split_count": (I32, [I64, I64, I64, I64]),
 }
 
 

@@ -969,6 +969,11 @@ extern "C" int ll_decode_attention_set_same_launch_merge(int enable) {
   return old;
 }
 
+extern "C" int ll_decode_attention_split_count(int64_t batch, int64_t kv_heads, int64_t head_dim,
+                                               int64_t max_len_in_batch) {
+  return choose_nsplit((int)batch, (int)kv_heads, max_len_in_batch, head_dim);
+}
+
 extern "C" int64_t ll_decode_attention_workspace_size(int64_t batch, int64_t q_heads,
                                                       int64_t kv_heads, int64_t head_dim,
                                                       int64_t max_len_in_batch) {
