@@ -64,6 +64,15 @@ __device__ __forceinline__ f32x4 mfma16x16x16(s16x4 a, s16x4 b, f32x4 c) {
 __device__ __forceinline__ f32x4 mfma16x16x16(f16x4 a, f16x4 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
 }
+// ds_read_b64_tr_b16: within each group of 16 lanes, lane i receives element
+// i % 4 of the 8 bytes addressed by lane 4 e + i / 4, as its element e
+__device__ __forceinline__ s16x4 lds_read_tr16(const char* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4*)(__attribute__((address_space(3))) char*)p);
+}
+__device__ __forceinline__ s16x4 as_v4(s16x4 x, s16x4) { return x; }
+__device__ __forceinline__ f16x4 as_v4(s16x4 x, f16x4) { return __builtin_bit_cast(f16x4, x); }
+
 // raw 16-bit pattern of an element (the 16x16x16 bf16 operands are short vectors)
 __device__ __forceinline__ short bits16(__bf16 x) { return __builtin_bit_cast(short, x); }
 __device__ __forceinline__ _Float16 bits16(_Float16 x) { return x; }
@@ -448,20 +457,12 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
   float m_run = -INFINITY;  // running max of head n (log2 domain)
   float l_run = 0.f;        // this lane's share of the running sum
 
-  for (int k = 0; k < nw; ++k) {
-    if (k + 1 < nw) {
-      issue(k + 1);
-      vm_wait<2 * TG::IPT>();  // tile k's copies are done, tile k + 1's in flight
-    } else {
-      vm_wait<0>();
-    }
-    char* kb = ring + (k % kRing) * TG::TILE_B;
-    const char* vb = kb + kTT * TG::ROWB;
-    const int t0 = (wave + k * kWaves) * kTT;
+  // ---- per-tile pieces of the token loop
+  // ROPE: rows of a tile that carry the new slot get the fresh K/V (in-wave
+  // LDS order puts these writes before the reads that follow)
+  auto patch = [&](char* kb, int t0) {
     if constexpr (ROPE) {
       if (writer) {
-        // rows of this tile that carry the new slot get the fresh K/V (in-wave
-        // LDS order puts these writes before the reads below)
         const bool hit = (t0 + n) < ntok && s_slots[t0 + n] == new_slot;
         uint64_t hits = __ballot(hit) & 0xffffull;
         while (hits) {
@@ -476,30 +477,27 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
         }
       }
     }
-
-    // S^T block: rows = tokens 4j+i, column = head n
+  };
+  // S^T block of a tile: rows = tokens 4j+i, column = head n; scaled into
+  // the log2 domain, -inf past the split's end
+  auto scores = [&](const char* kb, int t0, bool (&ok)[4], float (&x)[4]) {
     f32x4 s4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < DS; ++s) {
       const V8 ka = *(const V8*)(kb + n * TG::ROWB + TG::swz(4 * s + j, n) * 16);
       s4 = mfma16x16x32(ka, qb[s], s4);
     }
-    bool ok[4];
-    float x[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       ok[i] = (t0 + 4 * j + i) < ntok;
       x[i] = ok[i] ? s4[i] * a.scale_log2 : -INFINITY;
     }
-    float tmax = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const float m_new = fmaxf(m_run, tmax);  // finite: the tile's first token is valid
-    const float alpha = exp2f(m_run - m_new);
-    // P stays (nearly) fp32 as in the reference's fp32 p * v accumulation
-    // (flash_decoding.py:94-98): p = hi + lo with both parts in T, two MFMAs,
-    // relative error of hi + lo about 2^-17 (bf16) / 2^-22 (fp16)
-    V4 pb, pl;
+  };
+  // P stays (nearly) fp32 as in the reference's fp32 p * v accumulation
+  // (flash_decoding.py:94-98): p = hi + lo with both parts in T, two MFMAs,
+  // relative error of hi + lo about 2^-17 (bf16) / 2^-22 (fp16). Returns the
+  // sum of the tile's p.
+  auto probs = [&](const float (&x)[4], float m_new, V4& pb, V4& pl) {
     float psum = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -509,20 +507,52 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
       pb[i] = bits16(ph);
       pl[i] = bits16((T)(p - ll_to_f32(ph)));
     }
+    return psum;
+  };
+  // O^T[d, head] += V^T[d, tok] . P^T[tok, head]; k-slot i of lane group j
+  // is token 4j+i. The V^T fragment (d = 16c + n, tokens 4j..4j+3) comes
+  // from one transposing LDS read per d block: local lane 4e + q of lane
+  // group j addresses row 4j + e, columns 16c + 4q .. 16c + 4q + 3, so
+  // lane n receives V[4j + e][16c + n] as its element e.
+  const int vrow = 4 * j + (n >> 2);
+  auto v_frag = [&](const char* vb, const bool (&ok)[4], int c) {
+    const int chunk = 2 * c + ((n & 3) >> 1);  // 16-byte chunk of columns 16c + 4q
+    V4 va = as_v4(lds_read_tr16(vb + vrow * TG::ROWB + TG::swz(chunk, vrow) * 16 + (n & 1) * 8),
+                  V4{});
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (!ok[i]) va[i] = bits16((T)0.f);  // tokens past the split's end
+    return va;
+  };
+  auto row_max = [&](float t) {  // max over the 4 lane groups (all 16 tokens of a column)
+    t = fmaxf(t, __shfl_xor(t, 16, 64));
+    return fmaxf(t, __shfl_xor(t, 32, 64));
+  };
+
+  for (int k = 0; k < nw; ++k) {
+    if (k + 1 < nw) {
+      issue(k + 1);
+      vm_wait<2 * TG::IPT>();  // tile k's copies are done, tile k + 1's in flight
+    } else {
+      vm_wait<0>();
+    }
+    char* kb = ring + (k % kRing) * TG::TILE_B;
+    const char* vb = kb + kTT * TG::ROWB;
+    const int t0 = (wave + k * kWaves) * kTT;
+    patch(kb, t0);
+    bool ok[4];
+    float x[4];
+    scores(kb, t0, ok, x);
+    const float tmax = row_max(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])));
+    const float m_new = fmaxf(m_run, tmax);  // finite: the tile's first token is valid
+    const float alpha = exp2f(m_run - m_new);
+    V4 pb, pl;
+    const float psum = probs(x, m_new, pb, pl);
     l_run = l_run * alpha + psum;
     m_run = m_new;
-
-    // O^T[d, head] += V^T[d, tok] . P^T[tok, head]; k-slot i of lane group j is token 4j+i
 #pragma unroll
     for (int c = 0; c < DB; ++c) {
-      const int d = 16 * c + n;
-      V4 va;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = 4 * j + i;
-        const T v = *(const T*)(vb + r * TG::ROWB + TG::swz(d >> 3, r) * 16 + (d & 7) * 2);
-        va[i] = bits16(ok[i] ? v : (T)0.f);
-      }
+      const V4 va = v_frag(vb, ok, c);
       acc[c] = mfma16x16x16(va, pl, mfma16x16x16(va, pb, acc[c] * alpha));
     }
     // this buffer is refilled by the next issue: its LDS reads must be done
