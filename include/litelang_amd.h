@@ -447,6 +447,13 @@ int ll_gemm_splitk_packed(const void* X, int64_t ldx, const void* Wp, int64_t M,
 int ll_gemm_packed(const void* X, int64_t ldx, const void* Wp, const void* bias, void* Y,
                    int64_t ldy, int64_t M, int64_t N, int64_t K, int dtype, void* workspace,
                    int64_t workspace_bytes, hipStream_t stream);
+/* ll_gemm_packed with fp32 output Y [M, N] (the sums, + bias, never rounded
+ * to the weight dtype): the decode step's logits, argmaxed unrounded (the
+ * reference argmaxes its own fp16 logits, post_layer.py:20-22,75-77; fp32
+ * logits keep every one of them apart that fp16 keeps apart). */
+int ll_gemm_packed_f32(const void* X, int64_t ldx, const void* Wp, const void* bias, float* Y,
+                       int64_t ldy, int64_t M, int64_t N, int64_t K, int dtype, void* workspace,
+                       int64_t workspace_bytes, hipStream_t stream);
 /* Gate/up projection fused with SiLU_and_Mul (replaces the gate_up projection
  * plus silu_and_mul_fwd of transformer_layer.py:80-81 for M <= 64). The weight
  * is [gate; up] ([2I, K], the reference's two nn.Linear weights stacked);

@@ -604,38 +604,40 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const T* __restrict
   }
 }
 
-// Pass 1 with 16-byte loads (16-bit types, rows 16 B aligned, N % 8 == 0):
-// every thread issues the loads of its whole share of the chunk before the
-// first compare (clamped addresses, masked values), then merges them in index
-// order, so the first-index rule holds as in the scalar pass.
+// Pass 1 with 16-byte loads (VW = 16 / sizeof(T) elements each; rows 16 B
+// aligned, N % VW == 0): every thread issues the loads of its whole share of
+// the chunk before the first compare (clamped addresses, masked values),
+// then merges them in index order, so the first-index rule holds as in the
+// scalar pass.
 template <typename T>
-__global__ __launch_bounds__(256) void argmax_partial_vec8_kernel(const T* __restrict__ x,
-                                                                  int64_t x_rs, int N,
-                                                                  float* __restrict__ pval,
-                                                                  int* __restrict__ pidx,
-                                                                  int64_t* __restrict__ out,
-                                                                  const uint32_t* __restrict__ status) {
-  typedef T V8 __attribute__((ext_vector_type(8)));
-  constexpr int PER = kArgmaxChunkV / (256 * 8);  // 16-byte loads per thread
+__global__ __launch_bounds__(256) void argmax_partial_vec_kernel(const T* __restrict__ x,
+                                                                 int64_t x_rs, int N,
+                                                                 float* __restrict__ pval,
+                                                                 int* __restrict__ pidx,
+                                                                 int64_t* __restrict__ out,
+                                                                 const uint32_t* __restrict__ status) {
+  constexpr int VW = 16 / (int)sizeof(T);
+  typedef T VN __attribute__((ext_vector_type(VW)));
+  constexpr int PER = kArgmaxChunkV / (256 * VW);  // 16-byte loads per thread
   __shared__ float sv[4];
   __shared__ int si[4];
   const int row = blockIdx.y, c = blockIdx.x, nchunk = gridDim.x;
   const T* xr = x + (int64_t)row * x_rs;
   const int beg = c * kArgmaxChunkV, end = min(N, beg + kArgmaxChunkV);
-  V8 v[PER];
+  VN v[PER];
 #pragma unroll
   for (int q = 0; q < PER; ++q) {
-    const int p = beg + (q * 256 + (int)threadIdx.x) * 8;
-    v[q] = *(const V8*)(xr + min(p, end - 8));
+    const int p = beg + (q * 256 + (int)threadIdx.x) * VW;
+    v[q] = *(const VN*)(xr + min(p, end - VW));
   }
   float best = -INFINITY;
   int bi = 0x7fffffff;
 #pragma unroll
   for (int q = 0; q < PER; ++q) {
-    const int p = beg + (q * 256 + (int)threadIdx.x) * 8;
+    const int p = beg + (q * 256 + (int)threadIdx.x) * VW;
     if (p < end) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) argmax_merge(best, bi, ll_to_f32(v[q][e]), p + e);
+      for (int e = 0; e < VW; ++e) argmax_merge(best, bi, ll_to_f32(v[q][e]), p + e);
     }
   }
   argmax_block_reduce(best, bi, sv, si);
@@ -687,22 +689,16 @@ int argmax_impl(const void* x, int64_t x_row_stride, int64_t M, int64_t N, int64
     pval = (float*)workspace;
     pidx = (int*)(pval + M * nchunk);
   }
-  const bool vec = (dtype == LL_BF16 || dtype == LL_F16) && N % 8 == 0 && x_row_stride % 8 == 0 &&
-                   ((uintptr_t)x % 16) == 0;
+  const int vw = dtype == LL_F32 ? 4 : 8;  // elements per 16-byte load
+  const bool vec = N % vw == 0 && x_row_stride % vw == 0 && ((uintptr_t)x % 16) == 0;
   return LL_DISPATCH_DTYPE(dtype, T, [&]() -> int {
-    if constexpr (sizeof(T) == 2) {
-      if (vec)
-        hipLaunchKernelGGL((argmax_partial_vec8_kernel<T>), dim3(nchunk, (unsigned)M), dim3(256),
-                           0, stream, (const T*)x, x_row_stride, (int)N, pval, pidx, out, status);
-      else
-        hipLaunchKernelGGL((argmax_partial_kernel<T>), dim3(nchunk, (unsigned)M), dim3(256), 0,
-                           stream, (const T*)x, x_row_stride, (int)N, kArgmaxChunk, pval, pidx, out,
-                           status);
-    } else {
+    if (vec)
+      hipLaunchKernelGGL((argmax_partial_vec_kernel<T>), dim3(nchunk, (unsigned)M), dim3(256), 0,
+                         stream, (const T*)x, x_row_stride, (int)N, pval, pidx, out, status);
+    else
       hipLaunchKernelGGL((argmax_partial_kernel<T>), dim3(nchunk, (unsigned)M), dim3(256), 0,
                          stream, (const T*)x, x_row_stride, (int)N, kArgmaxChunk, pval, pidx, out,
                          status);
-    }
     if (nchunk > 1)
       hipLaunchKernelGGL(argmax_final_kernel, dim3((unsigned)M), dim3(256), 0, stream, pval, pidx,
                          nchunk, out, status);

@@ -17,6 +17,8 @@
 //   * fp32: plain FMA tiles for the fp32 parity path.
 #include "ll_common.h"
 
+#include <type_traits>
+
 namespace {
 
 // 16-byte operand fragment of one lane and the MFMA accumulator, per element type
@@ -354,9 +356,10 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, 
             for (int i = 0; i < 4 && ch + i < N; ++i) pp[i] = acc[b][t][i];
           }
         } else {
-          T* yp = Y + (int64_t)tok * ldy + ch;
+          // (TO: the output type, T or fp32 -- Y then points at TO elements)
+          TO* yp = (TO*)(void*)Y + (int64_t)tok * ldy + ch;
           for (int i = 0; i < 4 && ch + i < N; ++i)
-            yp[i] = ll_from_f32<T>(acc[b][t][i] + (bias != nullptr ? ll_to_f32(bias[ch + i]) : 0.f));
+            yp[i] = ll_from_f32<TO>(acc[b][t][i] + (bias != nullptr ? ll_to_f32(bias[ch + i]) : 0.f));
         }
       }
     }
@@ -498,9 +501,9 @@ __global__ __launch_bounds__(64 * KW) void gemm_direct_kernel(
   }
 }
 
-template <typename T>
+template <typename T, typename TO = T>
 __global__ void splitk_reduce_kernel(const float* __restrict__ part, int splits,
-                                     const T* __restrict__ bias, T* __restrict__ Y, int64_t ldy,
+                                     const T* __restrict__ bias, TO* __restrict__ Y, int64_t ldy,
                                      int M, int N) {
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= (int64_t)M * N) return;
@@ -508,7 +511,7 @@ __global__ void splitk_reduce_kernel(const float* __restrict__ part, int splits,
   float s = 0.f;
   for (int sp = 0; sp < splits; ++sp) s += part[((int64_t)sp * M + tok) * N + ch];
   if (bias != nullptr) s += ll_to_f32(bias[ch]);
-  Y[(int64_t)tok * ldy + ch] = ll_from_f32<T>(s);
+  Y[(int64_t)tok * ldy + ch] = ll_from_f32<TO>(s);
 }
 
 // ---------------------------------------------------------------- tiled
@@ -716,7 +719,7 @@ SkinnyPlan plan_skinny(int64_t N, int64_t K, int es = 2) {
 // up channels) once 64-row tiles would outnumber the CUs, as for plan_skinny.
 int gate_up_tr(int64_t I) { return ll_cdiv(I, 32) > 256 ? 128 : 64; }
 
-template <typename T, int MB>
+template <typename T, int MB, typename TO = T>
 void launch_skinny_mb(const SkinnyPlan& p, const T* X, int64_t ldx, const T* W, int64_t ldw,
                       const T* bias, T* Y, int64_t ldy, float* part, int M, int N, int K,
                       hipStream_t stream) {
@@ -724,7 +727,7 @@ void launch_skinny_mb(const SkinnyPlan& p, const T* X, int64_t ldx, const T* W, 
   if (p.dma) {
     const size_t lds = (size_t)p.nst * (p.tr + 16 * MB) * 256;
 #define LL_DMA_LAUNCH(S, PKD, TR_)                                                              \
-  hipLaunchKernelGGL((gemm_dma_kernel<T, MB, S, PKD, 0, TR_>), grid, dim3(256), lds, stream, X, \
+  hipLaunchKernelGGL((gemm_dma_kernel<T, MB, S, PKD, 0, TR_, TO>), grid, dim3(256), lds, stream, X, \
                      ldx, W, ldw, bias, Y, ldy, part, M, N, K, p.ksps, p.rotate, I8Epi{})
     if (p.tr == 128) {
       if (p.packed) LL_DMA_LAUNCH(3, true, 128); else LL_DMA_LAUNCH(3, false, 128);
@@ -736,22 +739,22 @@ void launch_skinny_mb(const SkinnyPlan& p, const T* X, int64_t ldx, const T* W, 
       if (p.nst == 3) LL_DMA_LAUNCH(3, false, 64); else LL_DMA_LAUNCH(2, false, 64);
     }
 #undef LL_DMA_LAUNCH
-  } else if constexpr (sizeof(T) == 2) {
+  } else if constexpr (sizeof(T) == 2 && std::is_same<T, TO>::value) {
     hipLaunchKernelGGL((gemm_direct_kernel<T, MB, kDirWR, kDirKW, kDirU>), grid,
                        dim3(64 * kDirKW), 0, stream, X, ldx, W, ldw, bias, Y, ldy, part, M, N, K,
                        p.ksps);
   }
 }
 
-template <typename T>
+template <typename T, typename TO = T>
 void launch_skinny(const SkinnyPlan& p, const T* X, int64_t ldx, const T* W, int64_t ldw,
                    const T* bias, T* Y, int64_t ldy, float* part, int M, int N, int K,
                    hipStream_t stream) {
   switch ((M + 15) / 16) {
-    case 1: launch_skinny_mb<T, 1>(p, X, ldx, W, ldw, bias, Y, ldy, part, M, N, K, stream); break;
-    case 2: launch_skinny_mb<T, 2>(p, X, ldx, W, ldw, bias, Y, ldy, part, M, N, K, stream); break;
-    case 3: launch_skinny_mb<T, 3>(p, X, ldx, W, ldw, bias, Y, ldy, part, M, N, K, stream); break;
-    default: launch_skinny_mb<T, 4>(p, X, ldx, W, ldw, bias, Y, ldy, part, M, N, K, stream); break;
+    case 1: launch_skinny_mb<T, 1, TO>(p, X, ldx, W, ldw, bias, Y, ldy, part, M, N, K, stream); break;
+    case 2: launch_skinny_mb<T, 2, TO>(p, X, ldx, W, ldw, bias, Y, ldy, part, M, N, K, stream); break;
+    case 3: launch_skinny_mb<T, 3, TO>(p, X, ldx, W, ldw, bias, Y, ldy, part, M, N, K, stream); break;
+    default: launch_skinny_mb<T, 4, TO>(p, X, ldx, W, ldw, bias, Y, ldy, part, M, N, K, stream); break;
   }
 }
 
@@ -952,15 +955,20 @@ extern "C" int ll_gemm_splitk_packed(const void* X, int64_t ldx, const void* Wp,
                           part_bytes, true, stream);
 }
 
-extern "C" int ll_gemm_packed(const void* X, int64_t ldx, const void* Wp, const void* bias, void* Y,
-                              int64_t ldy, int64_t M, int64_t N, int64_t K, int dtype,
-                              void* workspace, int64_t workspace_bytes, hipStream_t stream) {
-  LL_CHECK_ARG(X && Wp && Y, "ll_gemm_packed: null pointer");
+namespace {
+// The packed-weight GEMM for M <= 64 with output type TO (the model dtype,
+// or fp32 for logits that are argmaxed unrounded).
+int gemm_packed_impl(const char* name, const void* X, int64_t ldx, const void* Wp,
+                     const void* bias, void* Y, int64_t ldy, int64_t M, int64_t N, int64_t K,
+                     int dtype, bool out_f32, void* workspace, int64_t workspace_bytes,
+                     hipStream_t stream) {
+  LL_CHECK_ARG(X && Wp && Y, "%s: null pointer", name);
   LL_CHECK_ARG(M > 0 && M <= 64 && N > 0 && K > 0 && K % kDmaKC == 0,
-               "ll_gemm_packed: needs 0 < M <= 64 and K %% %d == 0", kDmaKC);
-  LL_CHECK_ARG(dtype == LL_BF16 || dtype == LL_F16, "ll_gemm_packed: bf16/fp16 only");
+               "%s: needs 0 < M <= 64 and K %% %d == 0", name, kDmaKC);
+  LL_CHECK_ARG(dtype == LL_BF16 || dtype == LL_F16, "%s: bf16/fp16 only", name);
   LL_CHECK_ARG(ldx % 8 == 0 && (((uintptr_t)X | (uintptr_t)Wp) % 16) == 0,
-               "ll_gemm_packed: X rows must be 16 B aligned");
+               "%s: X rows must be 16 B aligned", name);
+  LL_CHECK_ARG(ldx >= K && ldy >= N, "%s: row strides shorter than the rows", name);
   SkinnyPlan p = plan_skinny(N, K);
   p.packed = true;
   p.rotate = 0;
@@ -968,22 +976,42 @@ extern "C" int ll_gemm_packed(const void* X, int64_t ldx, const void* Wp, const 
   if (p.splits > 1) {
     const int64_t need = (int64_t)p.splits * M * N * 4;
     LL_CHECK_ARG(workspace != nullptr && workspace_bytes >= need,
-                 "ll_gemm_packed: workspace too small (need %lld bytes)", (long long)need);
+                 "%s: workspace too small (need %lld bytes)", name, (long long)need);
     part = (float*)workspace;
   }
-  auto run = [&](auto tag) {
+  auto run = [&](auto tag, auto otag) {
     typedef decltype(tag) T;
-    launch_skinny<T>(p, (const T*)X, ldx, (const T*)Wp, K, (const T*)bias, (T*)Y, ldy, part, (int)M,
-                     (int)N, (int)K, stream);
+    typedef decltype(otag) TO;
+    launch_skinny<T, TO>(p, (const T*)X, ldx, (const T*)Wp, K, (const T*)bias, (T*)Y, ldy, part,
+                         (int)M, (int)N, (int)K, stream);
     if (p.splits > 1) {
       const int64_t total = M * N;
-      hipLaunchKernelGGL((splitk_reduce_kernel<T>), dim3((unsigned)((total + 255) / 256)),
-                         dim3(256), 0, stream, part, p.splits, (const T*)bias, (T*)Y, ldy, (int)M,
+      hipLaunchKernelGGL((splitk_reduce_kernel<T, TO>), dim3((unsigned)((total + 255) / 256)),
+                         dim3(256), 0, stream, part, p.splits, (const T*)bias, (TO*)Y, ldy, (int)M,
                          (int)N);
     }
   };
-  if (dtype == LL_BF16) run(__bf16{}); else run(_Float16{});
+  if (dtype == LL_BF16) {
+    if (out_f32) run(__bf16{}, float{}); else run(__bf16{}, __bf16{});
+  } else {
+    if (out_f32) run(_Float16{}, float{}); else run(_Float16{}, _Float16{});
+  }
   LL_RETURN_LAUNCH();
+}
+}  // namespace
+
+extern "C" int ll_gemm_packed(const void* X, int64_t ldx, const void* Wp, const void* bias, void* Y,
+                              int64_t ldy, int64_t M, int64_t N, int64_t K, int dtype,
+                              void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  return gemm_packed_impl("ll_gemm_packed", X, ldx, Wp, bias, Y, ldy, M, N, K, dtype, false,
+                          workspace, workspace_bytes, stream);
+}
+
+extern "C" int ll_gemm_packed_f32(const void* X, int64_t ldx, const void* Wp, const void* bias,
+                                  float* Y, int64_t ldy, int64_t M, int64_t N, int64_t K, int dtype,
+                                  void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  return gemm_packed_impl("ll_gemm_packed_f32", X, ldx, Wp, bias, Y, ldy, M, N, K, dtype, true,
+                          workspace, workspace_bytes, stream);
 }
 
 extern "C" int ll_gemm(const void* X, int64_t ldx, const void* W, int64_t ldw, const void* bias,

@@ -112,11 +112,22 @@ class Qwen2Model:
             f = self._proj(act, li, "wdown")
         return f
 
+    def _logits(self, x):
+        """lm_head (post_layer.py:20-22). With 16-bit weights and at most 64
+        rows (decode; the last rows of a prefill), the packed weight stream
+        writes the logits in fp32, unrounded, and the argmax reads those (the
+        reference argmaxes its fp16 logits, post_layer.py:75-77; bf16 logits
+        would tie where fp16 ones do not). Otherwise the model dtype."""
+        w = self.w
+        if w.lm_head_p is not None and x.shape[0] <= 64:
+            return ops.gemm_packed(x, w.lm_head_p, out_dtype=torch.float32)
+        return ops.gemm(x, w.lm_head)
+
     def _post(self, hs, fs, out=None):
         """Final residual add + RMSNorm (eps 1e-5), lm_head, greedy argmax
         (post_layer.py:14-24,43-45,75-77)."""
         y = ops.rmsnorm(hs, self.w.norm, self.cfg.final_norm_eps, residual=fs)
-        logits = ops.gemm(y, self.w.lm_head)
+        logits = self._logits(y)
         self.last_logits = logits
         return ops.argmax(logits, out=out)
 
@@ -250,10 +261,7 @@ class Qwen2Model:
                 x = ops.add_rmsnorm_splitk(h, part, s, w.layers[li + 1]["ln1"], cfg.rms_norm_eps)
             else:
                 x = ops.add_rmsnorm_splitk(h, part, s, w.norm, cfg.final_norm_eps)
-        if w.lm_head_p is not None:
-            logits = ops.gemm_packed(x, w.lm_head_p)
-        else:
-            logits = ops.gemm(x, w.lm_head)
+        logits = self._logits(x)
         self.last_logits = logits
         # a fused launch that gave up a flag wait turns every token into -1
         # (the host raises on it, runner_batch.check_step_tokens)
@@ -318,7 +326,7 @@ class Qwen2Model:
                     xq, xs = ops.quant_input(x, nxt["wqkv_i8"])
             else:
                 x = ops.add_rmsnorm_splitk_i32(h, p, w.norm, cfg.final_norm_eps)
-        logits = ops.gemm_packed(x, w.lm_head_p) if w.lm_head_p is not None else ops.gemm(x, w.lm_head)
+        logits = self._logits(x)
         self.last_logits = logits
         return ops.argmax(logits, out=out)
 

@@ -562,23 +562,27 @@ def gemm_splitk_packed(x, wp: PackedWeight, part):
     return s
 
 
-def gemm_packed(x, wp: PackedWeight, bias=None, out=None):
-    """out[M, N] = x @ w^T (+ bias) for M <= 64 from a packed weight."""
+def gemm_packed(x, wp: PackedWeight, bias=None, out=None, out_dtype=None):
+    """out[M, N] = x @ w^T (+ bias) for M <= 64 from a packed weight; with
+    out_dtype=torch.float32 the sums are written unrounded (fp32)."""
     _dev(x, bias, out)
     M, K = x.shape
     N = wp.shape[0]
     assert wp.shape[1] == K and x.stride(1) == 1 and x.dtype == wp.dtype
+    out_dtype = out_dtype or (out.dtype if out is not None else x.dtype)
+    assert out_dtype in (x.dtype, torch.float32)
     if out is None:
-        out = torch.empty((M, N), dtype=x.dtype, device=x.device)
-    assert out.shape == (M, N) and out.stride(1) == 1
+        out = torch.empty((M, N), dtype=out_dtype, device=x.device)
+    assert out.shape == (M, N) and out.stride(1) == 1 and out.dtype == out_dtype
     nbytes = _L.ll_gemm_workspace_size(M, N, K)
     ws_ptr, ws_n = (None, 0)
     if nbytes > 0:
         ws = workspace(x.device, "gemm", nbytes)
         ws_ptr, ws_n = ws.data_ptr(), ws.numel()
-    rc = _L.ll_gemm_packed(x.data_ptr(), x.stride(0), wp.data.data_ptr(),
-                           bias.data_ptr() if bias is not None else None, out.data_ptr(),
-                           out.stride(0), M, N, K, dtype_code(x), ws_ptr, ws_n, _stream(x))
+    fn = _L.ll_gemm_packed_f32 if out_dtype == torch.float32 else _L.ll_gemm_packed
+    rc = fn(x.data_ptr(), x.stride(0), wp.data.data_ptr(),
+            bias.data_ptr() if bias is not None else None, out.data_ptr(),
+            out.stride(0), M, N, K, dtype_code(x), ws_ptr, ws_n, _stream(x))
     _lib.check(rc, "ll_gemm_packed")
     return out
 

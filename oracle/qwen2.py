@@ -10,7 +10,9 @@ layer/post_layer.py:14-77, with the reference quirks kept:
   * K rotated before it is written to the pool (transformer_layer.py:115,143);
   * o_proj bias ignored (transformer_layer.py:193);
   * residual adds stored in the model dtype (transformer_layer.py:69,76);
-  * greedy argmax on the stored logits, first index on ties (post_layer.py:75-77).
+  * greedy argmax, first index on ties (post_layer.py:75-77), on the logits
+    kept unrounded (fp32/fp64): the build writes fp32 logits and argmaxes
+    those (the reference stores its fp16 ones).
 Compute is float64 (fp32 inside ops.math_dtype(torch.float32), used for the
 full-width geometries only); `rnd` stores an intermediate in the model dtype
 wherever the reference stores a tensor.
@@ -170,7 +172,7 @@ class Qwen2Oracle:
         else:
             rows = list(start)
         hs = ops.rnd(ops.rmsnorm(h[torch.as_tensor(rows)], self.norm, cfg.final_eps), dt)
-        logits = ops.rnd(ops.linear(hs, self.lm_head), dt)
+        logits = ops.linear(hs, self.lm_head)  # not rounded to dt: fp32 logits
         return ops.argmax_first(logits), logits
 
     # ------------------------------------------------------------ greedy loop

@@ -18,24 +18,27 @@ Comparison (teacher forcing): the product generates greedily on its own; the
 CPU oracle, emulating the same storage dtype, is then run on the product's
 tokens (Qwen2Oracle.generate(feed=...)), so every step of both is evaluated
 on the same context. At every step and request:
-  * logits max-abs <= 0.032 (bf16 model: four bf16 ulps at the logits'
-    magnitude; the logits are bf16 values, and two prefill-attention kernels
-    whose outputs match the oracle to the same maximum error moved one
-    config-3 step from 2 to 3.7 ulps) or 0.15 (W8A8). The W8A8 bar is
-    wider because the per-token quantiser is a step function: a one-ulp bf16
-    difference in its input moves an int8 code by one step, and the change
-    travels through the rest of the network. Two faithful W8A8 executions of
-    the config-5 workload (the oracle in float64 and in float32 arithmetic)
-    already differ by up to 0.086 in the logits (0.038 on the tiny model),
-    and a broken kernel moves them by whole units. The int8 arithmetic
-    itself is compared bit for bit in tests/test_gpu_w8a8.py;
+  * logits max-abs <= 0.02 (bf16 model: the logits are
+    the lm_head's fp32 accumulators, compared with the oracle's unrounded
+    logits; about 0.017 observed at the full-width geometries) or 0.12
+    (W8A8). The W8A8 bar is wider because the per-token quantiser is a step
+    function: a one-ulp bf16 difference in its input moves an int8 code by
+    one step, and the change travels through the rest of the network. Two
+    faithful W8A8 executions of the config-5 workload (the oracle in float64
+    and in float32 arithmetic) already differ by up to 0.086 in the logits
+    (0.038 on the tiny model), and a broken kernel moves them by whole units.
+    The median over (request, step) pairs is held to 3/4 of the bar
+    (0.011-0.012 observed for bf16, 0.059 for W8A8). The int8 arithmetic itself is compared bit for bit in
+    tests/test_gpu_w8a8.py;
   * the product's token equals the oracle's argmax wherever the oracle's
-    top-1 margin exceeds 4x the logits difference observed at that step
-    (a smaller margin is a near tie that either side may break);
-  * enough (request, step) pairs are such decisive steps (60% for the
-    1024-token vocabulary, about 80% observed; 30% for the 151936-token one,
-    where the top-2 gap of the logits is several times smaller, about 45%
-    observed), and every request's tokens change over the run.
+    top-1 margin exceeds 2x the logits difference observed at that step
+    (with every logit within d of the oracle's, a margin above 2d cannot
+    change the argmax; a smaller one is a near tie either side may break);
+  * enough (request, step) pairs are such decisive steps (85% for the
+    1024-token vocabulary, 95% observed; 60% for the 151936-token one, where
+    the top-2 gap of the logits is several times smaller, 64-72% observed;
+    15% for W8A8, whose larger d leaves 17.5% decisive), and every
+    request's tokens change over the run.
 For the full-width geometries the oracle computes in fp32
 (oracle.ops.math_dtype), which stays within rounding of its float64 form.
 """
@@ -49,8 +52,8 @@ from tests.model_weights import moving_state_dict
 
 pytestmark = pytest.mark.gpu
 
-BF16_LOGITS = 0.032
-W8A8_LOGITS = 0.15
+BF16_LOGITS = 0.02
+W8A8_LOGITS = 0.12
 
 
 def _ocfg(cfg):
@@ -73,17 +76,20 @@ def _geometry(name):
 def check_teacher_forced(got, got_logits, ref, ref_logits, bar, what, min_decisive=None):
     """got/ref [B, S] tokens, *_logits [B, S, V]; see the module docstring."""
     if min_decisive is None:
-        min_decisive = 0.6 if ref_logits.shape[-1] <= 4096 else 0.3
+        min_decisive = 0.85 if ref_logits.shape[-1] <= 4096 else 0.6
     B, S = got.shape
     worst, decisive = 0.0, 0
+    ds = (got_logits.double() - ref_logits.double()).abs().amax(-1)  # [B, S]
+    med = float(ds.median())
+    assert med <= 0.75 * bar, f"{what}: median logits max-abs {med:.4f} > {0.75 * bar}"
     for b in range(B):
         for s in range(S):
-            d = float((got_logits[b, s].double() - ref_logits[b, s].double()).abs().max())
+            d = float(ds[b, s])
             worst = max(worst, d)
             assert d <= bar, f"{what}: request {b} step {s}: logits max-abs {d:.4f} > {bar}"
             top2 = ref_logits[b, s].double().topk(2).values
             margin = float(top2[0] - top2[1])
-            if margin > 4 * d:
+            if margin > 2 * d:
                 decisive += 1
                 assert int(got[b, s]) == int(ref[b, s]), (
                     f"{what}: request {b} step {s}: token {int(got[b, s])} vs oracle "
@@ -91,7 +97,8 @@ def check_teacher_forced(got, got_logits, ref, ref_logits, bar, what, min_decisi
     for b in range(B):
         assert len(set(got[b].tolist())) > 1, f"{what}: request {b} repeats one token"
     assert decisive >= min_decisive * B * S, f"{what}: only {decisive} of {B * S} steps decisive"
-    print(f"{what}: logits max-abs {worst:.4f}, {decisive}/{B * S} decisive steps", flush=True)
+    print(f"{what}: logits max-abs {worst:.4f} (median {med:.4f}), {decisive}/{B * S} decisive "
+          f"steps", flush=True)
     return worst
 
 
@@ -244,7 +251,7 @@ def test_config5_3b_geometry_radix_shared_prefix(cuda, quant):
                                                             feed=got, prefix=prefix)
     if quant == "w8a8":
         check_teacher_forced(got, got_logits, ref, ref_logits, W8A8_LOGITS, "config 5 w8a8",
-                             min_decisive=0.02)
+                             min_decisive=0.15)
     else:
         check_teacher_forced(got, got_logits, ref, ref_logits, BF16_LOGITS, "config 5 bf16")
 

@@ -12,6 +12,7 @@ Qwen2ModelRunner.forward, RunnerBatch.update_forward_message
 import pytest
 import torch
 
+from oracle import ops as O
 from oracle.qwen2 import Qwen2Cfg, Qwen2Oracle
 
 pytestmark = pytest.mark.gpu
@@ -109,17 +110,90 @@ def test_tiny_bf16_ragged_batch_logits(cuda, graph):
                 break
 
 
+@pytest.mark.parametrize("graph", [True, False])
+def test_fp32_free_running_32_steps_moving_tokens(cuda, graph):
+    """Config-1 geometry in fp32 on weights whose greedy tokens move
+    (tests/model_weights.moving_state_dict, seed 44): 1 prefill + 31 decode
+    forwards run free (each step feeds its own token), and all 32 tokens
+    equal the oracle's. The oracle's sequence is asserted to move and to have
+    no near tie (every top-1 margin above 1e-3, far above fp32 rounding), so
+    the identity says something about every step's KV reads."""
+    from tests.model_weights import moving_state_dict
+    cfg, ocfg = _cfgs()
+    sd = moving_state_dict(cfg, seed=44)
+    prompt = torch.randint(0, 1024, (16,), generator=torch.Generator().manual_seed(44)).tolist()
+    print(f"case: fp32 free-running 32 steps, moving weights, graph={graph}", flush=True)
+    ref, ref_logits = Qwen2Oracle(ocfg, sd, torch.float32, 8, 128, 1024).generate(
+        [prompt], 32, return_logits=True)
+    top2 = ref_logits[0].double().topk(2, dim=-1).values
+    assert float((top2[:, 0] - top2[:, 1]).min()) > 1e-3
+    assert len(set(ref[0].tolist())) >= 8, f"oracle tokens barely move: {ref[0].tolist()}"
+    got, _ = _run_product(cfg, sd, [prompt], 32, torch.float32, cuda, graph=graph)
+    assert got.tolist() == ref.tolist()
+
+
+def test_post_layer_logits_within_2e2_of_fp32(cuda):
+    """The post layer (post_layer.py:14-24,43-45,75-77) as the decode step
+    runs it, at the Qwen2.5-3B shape: final RMSNorm (eps 1e-5) of 40 bf16
+    hidden rows, the tied lm_head [151936, 2048] streamed from the packed
+    weight with fp32 output, first-index argmax. Against the fp32 reference
+    of the same op on the same bf16 inputs (float64 arithmetic): logits
+    within max-abs 2e-2 (observed ~1e-5 with the normalised rows rounded to
+    bf16 as the reference stores them, a few 1e-3 without that rounding);
+    the token equals the reference's wherever the top-1 margin exceeds twice
+    the logits difference (most rows here)."""
+    from lite_lang_amd import ops
+    g = torch.Generator().manual_seed(45)
+    h = (torch.randn(40, 2048, generator=g) * 2.0).bfloat16()
+    gamma = (torch.rand(2048, generator=g) * 0.4 + 0.8).bfloat16()
+    emb = (torch.randn(151936, 2048, generator=g) * 0.02).bfloat16()
+    print("case: post layer logits fp32 at the 3B shape", flush=True)
+    hd, gd = h.to(cuda), gamma.to(cuda)
+    wp = ops.PackedWeight(emb.to(cuda))
+    y = ops.rmsnorm(hd, gd, 1e-5)
+    logits = ops.gemm_packed(y, wp, out_dtype=torch.float32)
+    toks = ops.argmax(logits)
+    assert logits.dtype == torch.float32
+    got = logits.double().cpu()
+    yr = O.rmsnorm(h.double(), gamma.double(), 1e-5)
+    ref_rounded = yr.bfloat16().double() @ emb.double().t()
+    ref_exact = yr @ emb.double().t()
+    d1 = float((got - ref_rounded).abs().max())
+    d2 = float((got - ref_exact).abs().max())
+    print(f"logits max-abs vs fp32 reference: {d1:.2e} (bf16 row), {d2:.2e} (unrounded row)",
+          flush=True)
+    assert d1 <= 2e-2 and d2 <= 2e-2
+    assert d1 <= 1e-3
+    top2 = ref_rounded.topk(2, dim=-1)
+    decisive = 0
+    for b in range(40):
+        d = float((got[b] - ref_rounded[b]).abs().max())
+        if float(top2.values[b, 0] - top2.values[b, 1]) > 2 * d:
+            decisive += 1
+            assert int(toks[b]) == int(top2.indices[b, 0]), b
+    assert decisive >= 30
+
+
 def test_qwen25_3b_geometry_two_layers_batch40(cuda):
     """Qwen2.5-3B layer geometry (hidden 2048, 16/2 heads, D 128, I 11008,
     vocab 151936) with 2 layers, batch 40: exercises the wide-N LDS GEMM, the
     split-K fused decode layer and the graph path at the real shapes.
 
-    At this width the logits are O(5) and carry bf16 noise: an exact bf16
-    execution of the reference algorithm (the bf16-emulating oracle) is itself
-    ~6e-2 away from the fp32 oracle, so a fixed max-abs bar cannot separate a
-    bug from rounding. The check is instead that the GPU path is no less
-    accurate than that exact bf16 execution, measured against the fp32
-    oracle, for 3 steps; tokens must match the bf16 oracle except at near ties.
+    The logits are O(5). Two bars, both absolute, at every step for the
+    requests whose history still equals both oracles':
+      * within 0.05 of the oracle that stores the same bf16 intermediates
+        the product stores (the algorithm the product runs, in float64
+        arithmetic; 0.035 observed). At logits of this size bf16 rounding
+        flips alone exceed the north-star 0.02: the same oracle run in fp32
+        instead of float64 arithmetic is 0.033 away from itself (median
+        0.02). The config tests, whose logits are within 1.7, hold the
+        product to 0.02;
+      * within 0.1 of the oracle that keeps every intermediate in fp32. A
+        bf16 model cannot meet 0.02 there: the bf16-storage oracle, an
+        exact execution of the reference algorithm in bf16, is itself
+        0.062-0.064 away from it.
+    Tokens must match the bf16 oracle except at near ties (a top-1 margin
+    within twice the observed logits difference).
     """
     from lite_lang_amd.models.qwen2.weights import Qwen2Config, random_state_dict
     cfg = Qwen2Config(layer_nums=2, hidden_size=2048, num_heads=16, num_key_value_heads=2,
@@ -148,14 +222,18 @@ def test_qwen25_3b_geometry_two_layers_batch40(cuda):
         lg = runner.model_ins_.last_logits.double().cpu()
         got = out.view(-1).cpu()
         batch.update_forward_message(out)
-        err_gpu = float((lg[alive] - lf[alive, step]).abs().max())
-        err_bf16 = float((lb[alive, step] - lf[alive, step]).abs().max())
-        print(f"step {step}: |gpu - fp32| {err_gpu:.4f}  |bf16 exact - fp32| {err_bf16:.4f}")
-        assert err_gpu <= 1.25 * err_bf16 + 1e-3, f"step {step}: gpu {err_gpu} vs bf16 {err_bf16}"
+        err_b = float((lg[alive] - lb[alive, step]).abs().max())
+        err_f = float((lg[alive] - lf[alive, step]).abs().max())
+        err_bf = float((lb[alive, step] - lf[alive, step]).abs().max())
+        print(f"step {step}: |gpu - bf16 oracle| {err_b:.4f}  |gpu - fp32 oracle| {err_f:.4f}  "
+              f"|bf16 oracle - fp32 oracle| {err_bf:.4f}", flush=True)
+        assert err_b <= 0.05, f"step {step}: {err_b} from the bf16-storage oracle"
+        assert err_f <= 0.1, f"step {step}: {err_f} from the fp32 oracle"
         mism = (got != tb[:, step]) & alive
         for b in mism.nonzero().view(-1).tolist():
             top2 = lb[b, step].topk(2).values
-            assert float(top2[0] - top2[1]) <= 2 * err_bf16, f"request {b} diverged without a near tie"
+            d = float((lg[b] - lb[b, step]).abs().max())
+            assert float(top2[0] - top2[1]) <= 2 * d, f"request {b} diverged without a near tie"
         alive &= ~mism & (tb[:, step] == tf[:, step])
     assert int(alive.sum()) >= 30
 
