@@ -46,7 +46,6 @@ constexpr int kRing = 2;    // tile buffers per wave
 template <typename T> struct Vec8;
 template <> struct Vec8<__bf16> { typedef bf16x8 type; };
 template <> struct Vec8<_Float16> { typedef f16x8 type; };
-typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 template <typename T> struct Vec4;
 template <> struct Vec4<__bf16> { typedef s16x4 type; };
@@ -63,12 +62,6 @@ __device__ __forceinline__ f32x4 mfma16x16x16(s16x4 a, s16x4 b, f32x4 c) {
 }
 __device__ __forceinline__ f32x4 mfma16x16x16(f16x4 a, f16x4 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
-}
-// ds_read_b64_tr_b16: within each group of 16 lanes, lane i receives element
-// i % 4 of the 8 bytes addressed by lane 4 e + i / 4, as its element e
-__device__ __forceinline__ s16x4 lds_read_tr16(const char* p) {
-  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) s16x4*)(__attribute__((address_space(3))) char*)p);
 }
 __device__ __forceinline__ s16x4 as_v4(s16x4 x, s16x4) { return x; }
 __device__ __forceinline__ f16x4 as_v4(s16x4 x, f16x4) { return __builtin_bit_cast(f16x4, x); }
@@ -515,10 +508,12 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
   // group j addresses row 4j + e, columns 16c + 4q .. 16c + 4q + 3, so
   // lane n receives V[4j + e][16c + n] as its element e.
   const int vrow = 4 * j + (n >> 2);
-  auto v_frag = [&](const char* vb, const bool (&ok)[4], int c) {
+  auto v_read = [&](const char* vb, int c) {
     const int chunk = 2 * c + ((n & 3) >> 1);  // 16-byte chunk of columns 16c + 4q
-    V4 va = as_v4(lds_read_tr16(vb + vrow * TG::ROWB + TG::swz(chunk, vrow) * 16 + (n & 1) * 8),
-                  V4{});
+    return ll_lds_read_tr16(vb + vrow * TG::ROWB + TG::swz(chunk, vrow) * 16 + (n & 1) * 8);
+  };
+  auto v_frag = [&](s16x4 raw, const bool (&ok)[4]) {
+    V4 va = as_v4(raw, V4{});
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       if (!ok[i]) va[i] = bits16((T)0.f);  // tokens past the split's end
@@ -550,9 +545,13 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
     const float psum = probs(x, m_new, pb, pl);
     l_run = l_run * alpha + psum;
     m_run = m_new;
+    s16x4 vr[DB];
+#pragma unroll
+    for (int c = 0; c < DB; ++c) vr[c] = v_read(vb, c);
+    ll_lds_wait_tie(vr);
 #pragma unroll
     for (int c = 0; c < DB; ++c) {
-      const V4 va = v_frag(vb, ok, c);
+      const V4 va = v_frag(vr[c], ok);
       acc[c] = mfma16x16x16(va, pl, mfma16x16x16(va, pb, acc[c] * alpha));
     }
     // this buffer is refilled by the next issue: its LDS reads must be done

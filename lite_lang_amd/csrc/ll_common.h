@@ -15,6 +15,34 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// Transposing LDS read (ds_read_b64_tr_b16, gfx950): within each group of 16
+// lanes, lane i receives element i % 4 of the 8 bytes addressed by lane
+// 4 e + i / 4, as its element e. Issued as inline asm: for the compiler's
+// builtin of this instruction the wait insertion assumes that it may read
+// what any LDS DMA still in flight writes, and waits for all of them
+// (vmcnt(0)), which drains the copies of the tiles ahead of the one being
+// read. The value is not there until ll_lds_wait_tie() has run on it.
+__device__ __forceinline__ s16x4 ll_lds_read_tr16(const void* p) {
+  s16x4 r;
+  const uint32_t off =
+      (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)(const char*)p;
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(off) : "memory");
+  return r;
+}
+// Wait for every LDS read of this wave (lgkmcnt(0)); the values read by
+// ll_lds_read_tr16 pass through the wait as operands, so that no use of
+// them can be scheduled before it.
+template <int N> __device__ __forceinline__ void ll_lds_wait_tie(s16x4 (&v)[N]);
+template <> __device__ __forceinline__ void ll_lds_wait_tie<4>(s16x4 (&v)[4]) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3])::"memory");
+}
+template <> __device__ __forceinline__ void ll_lds_wait_tie<8>(s16x4 (&v)[8]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]),
+                 "+v"(v[6]), "+v"(v[7])::"memory");
+}
 
 #include "../../include/litelang_amd.h"
 

@@ -36,6 +36,30 @@ constexpr int kBK = 64;   // keys per tile
 // encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
 constexpr int kVmcntZero = 0x0F70;
 
+constexpr int kStages = 4;  // LDS ring depth (K/V tiles)
+
+// 16 B (4 B) global -> LDS DMA of one lane: lane i of the wave lands at
+// lds + 16 i (lds + 4 i).
+__device__ __forceinline__ void dma16(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0);
+}
+__device__ __forceinline__ void dma4(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, lds, 4, 0, 0);
+}
+
+// Wait until at most N of this wave's vector memory operations (LDS DMA
+// included) are in flight.
+template <int N_> __device__ __forceinline__ void vm_wait() {
+  static_assert(N_ >= 0 && N_ < 64, "vmcnt is a 6-bit counter");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N_) : "memory");
+}
+
+// Workgroup barrier for LDS data only: __syncthreads() would also wait for
+// every outstanding global access, the copies of the tiles ahead included.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 template <typename T> struct Vec8;
 template <> struct Vec8<__bf16> { typedef bf16x8 type; };
 template <> struct Vec8<_Float16> { typedef f16x8 type; };
@@ -82,13 +106,6 @@ template <int D> struct FaGeom {
   }
 };
 
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-// ds_read_b64_tr_b16: within each group of 16 lanes, lane i receives element
-// i % 4 of the 8 bytes addressed by lane 4 e + i / 4, as its element e
-__device__ __forceinline__ s16x4 lds_read_tr16(const char* p) {
-  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) s16x4*)(__attribute__((address_space(3))) char*)p);
-}
 
 // WPH: waves (of 32 query rows each) per head; the 8 waves of a workgroup
 // take 8 / WPH heads of one KV head and 32 * WPH query rows of each
@@ -155,39 +172,47 @@ __global__ __launch_bounds__(512) void prefill_attn_fa_kernel(PrefillArgs a) {
     for (int s = 0; s < DS; ++s) qreg[s] = *(const V8*)(qp + 16 * s);
   }
 
-  // K and V tiles are staged through registers (global loads, then LDS
-  // stores after the current tile's compute): with no copy into LDS in
-  // flight, the compute's LDS reads need no wait on the global loads.
+  // K and V tiles go from the pool straight into an NST-stage LDS ring
+  // (global_load_lds_dwordx4, no VGPR staging); the slot ids that address
+  // them are DMA'd likewise, by every wave into a ring of its own, NST - 1
+  // tiles before the tile's K/V copies. Per loop iteration t every wave
+  // issues one group: its K/V copies of tile t + NST - 1 (when that tile
+  // exists) and its slot ids of tile t + 2 NST - 2 (clamped, always), so
+  // that NST - 1 tiles are in flight while tile t is computed.
   const T* kbase = (const T*)a.k + (int64_t)kvh * a.k_sh;
   const T* vbase = (const T*)a.v + (int64_t)kvh * a.v_sh;
-  // K and V geometry: thread -> rows kr + KRS u (u < KR), 16-byte chunk kc;
-  // the lanes of one row write its whole LDS row (a permutation of the
-  // chunks). V rows stay key-major in LDS and are transposed by the reads.
-  constexpr int KR = kBK * FG::CH / NT;  // chunks per thread per tile (each of K and V)
-  constexpr int KRS = NT / FG::CH;       // rows covered per pass
-  const int kc = threadIdx.x % FG::CH, kr = threadIdx.x / FG::CH;
-  int32_t ksl[KR];  // slot ids of the next tile's rows
-  auto load_slots = [&](int t0) {
-#pragma unroll
-    for (int u = 0; u < KR; ++u) ksl[u] = slot_row[min(t0 + kr + KRS * u, kv_end - 1)];
+  constexpr int NST = kStages;
+  constexpr int RPI = 64 / FG::CH;                     // rows per DMA instruction
+  constexpr int IPW = kBK * FG::ROWB / 1024 / SH::NW;  // K (and V) instructions per wave per tile
+  constexpr int KVC = 2 * IPW;                         // K and V
+  static_assert(IPW >= 1 && IPW * SH::NW * 1024 == kBK * FG::ROWB, "tile rows over the waves");
+  char* wslots = smem + NST * FG::STAGE_B + wave * (NST * kBK * 4);
+  const int ntiles = (kv_end + kBK - 1) / kBK;
+  auto slot_copy = [&](int u) {  // slot ids of keys 64 u + lane (clamped) -> ring entry u % NST
+    dma4(slot_row + min(u * kBK + lane, kv_end - 1), wslots + (u % NST) * (kBK * 4));
   };
-  V8 kreg[KR], vreg[KR];
-  auto issue = [&]() {  // global loads of the tile whose slots are in ksl
-#pragma unroll
-    for (int u = 0; u < KR; ++u) {
-      kreg[u] = *(const V8*)(kbase + (int64_t)ksl[u] * a.k_st + 8 * kc);
-      vreg[u] = *(const V8*)(vbase + (int64_t)ksl[u] * a.v_st + 8 * kc);
-    }
-  };
-  auto store = [&](int buf) {  // the loaded rows into LDS, chunks swizzled
-    char* kl = smem + buf * FG::STAGE_B;
+  const int dr = lane / FG::CH, dp = lane % FG::CH;
+  auto kv_copy = [&](int u) {  // this wave's K and V rows of tile u -> stage u % NST
+    char* kl = smem + (u % NST) * FG::STAGE_B;
     char* vl = kl + FG::K_B;
+    const int32_t* sl = (const int32_t*)(wslots + (u % NST) * (kBK * 4));
 #pragma unroll
-    for (int u = 0; u < KR; ++u) {
-      const int r = kr + KRS * u;
-      *(V8*)(kl + r * FG::ROWB + FG::kswz(kc, r) * 16) = kreg[u];
-      *(V8*)(vl + r * FG::ROWB + FG::vswz(kc, r) * 16) = vreg[u];
+    for (int i = 0; i < IPW; ++i) {
+      const int ii = wave * IPW + i;
+      const int r = ii * RPI + dr;  // the LDS chunk position dp of row r holds chunk swz(dp, r)
+      const int64_t slot = sl[r];
+      dma16(kbase + slot * a.k_st + 8 * FG::kswz(dp, r), kl + ii * 1024);
+      dma16(vbase + slot * a.v_st + 8 * FG::vswz(dp, r), vl + ii * 1024);
     }
+  };
+  // at the top of iteration t only the groups of iterations t-NST+2 .. t-1
+  // may be in flight: NST - 2 slot copies and the K/V copies of the `later`
+  // tiles among t+1 .. t+NST-2 that exist
+  auto wait_tile = [&](int later) {
+    static_assert(NST == 3 || NST == 4, "waits below are written for 3 or 4 stages");
+    if (NST == 4 && later >= 2) vm_wait<(NST - 2) + 2 * KVC>();
+    else if (later >= 1) vm_wait<(NST - 2) + KVC>();
+    else vm_wait<NST - 2>();
   };
 
   f32x16 acc[DB][QB];
@@ -202,19 +227,18 @@ __global__ __launch_bounds__(512) void prefill_attn_fa_kernel(PrefillArgs a) {
     l_run[qb] = 0.f;
   }
 
-  // tile 0 into stage 0; the slot ids of tile 1 are loaded behind it
-  load_slots(0);
-  issue();
-  store(0);
-  // every load so far (Q fragments included) has landed. Without this wait
-  // the compiler, which schedules the Q loads after tile 0's, meets them
-  // still outstanding at the loop header and counts vmcnt down to zero in
-  // every iteration's score product, which also waits for that iteration's
-  // prefetch of the next tile (one memory round trip per tile). A real
-  // s_waitcnt (not inline asm) is one the wait-insertion pass accounts for.
+  // slot ids of tiles 0 .. NST-2, then (every load so far landed, Q
+  // fragments included: a real s_waitcnt, which the compiler's own wait
+  // insertion accounts for, so that it waits for none of them in the loop)
+  // the groups of iterations -NST+1 .. -1
+#pragma unroll
+  for (int u = 0; u < NST - 1; ++u) slot_copy(u);
   __builtin_amdgcn_s_waitcnt(kVmcntZero);
-  if (kBK < kv_end) load_slots(kBK);
-  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < NST - 1; ++u) {
+    if (u < ntiles) kv_copy(u);
+    slot_copy(u + NST - 1);
+  }
 
   // S^T[key 32 kb + 8 g + 4 hf + i][query 32 qb + l32] of the current tile in
   // sacc[kb][qb][4 g + i]; the row maxima it proposes in m_cand
@@ -277,14 +301,14 @@ __global__ __launch_bounds__(512) void prefill_attn_fa_kernel(PrefillArgs a) {
   // transposing reads, the 16-lane group g = lane / 16 reading keys
   // 16 s + 4 (g / 2) + j / 4 (+ 8), d 32 db + 16 (g % 2) + 4 (j % 4) .. + 3
   const int tg = lane >> 4, tj = lane & 15;
-  auto vfrag = [&](const char* vl, int s, int db) -> V8 {
+  // the two transposing reads of fragment (s, db): keys 16 s + 4 (g / 2) + j / 4
+  // and 8 keys further, d bytes 64 db + 32 (g % 2) + 8 (j % 4)
+  auto vfrag_reads = [&](const char* vl, int s, int db, s16x4& lo, s16x4& hi) {
     const int key = 16 * s + 4 * (tg >> 1) + (tj >> 2);
     const int dbyte = 64 * db + 32 * (tg & 1) + 8 * (tj & 3);
     const int c = dbyte >> 4, off = dbyte & 15;
-    const s16x4 lo = lds_read_tr16(vl + key * FG::ROWB + FG::vswz(c, key) * 16 + off);
-    const s16x4 hi = lds_read_tr16(vl + (key + 8) * FG::ROWB + FG::vswz(c, key + 8) * 16 + off);
-    typedef short s16x8 __attribute__((ext_vector_type(8)));
-    return __builtin_bit_cast(V8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    lo = ll_lds_read_tr16(vl + key * FG::ROWB + FG::vswz(c, key) * 16 + off);
+    hi = ll_lds_read_tr16(vl + (key + 8) * FG::ROWB + FG::vswz(c, key + 8) * 16 + off);
   };
   auto accumulate = [&](int buf) {
     const char* vl = smem + buf * FG::STAGE_B + FG::K_B;
@@ -307,22 +331,28 @@ __global__ __launch_bounds__(512) void prefill_attn_fa_kernel(PrefillArgs a) {
       l_run[qb] += psum;
     }
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
+    for (int s = 0; s < 4; ++s) {
+      s16x4 vr[2 * DB];  // lo, hi of each d block
+#pragma unroll
+      for (int db = 0; db < DB; ++db) vfrag_reads(vl, s, db, vr[2 * db], vr[2 * db + 1]);
+      ll_lds_wait_tie(vr);
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
-        const V8 va = vfrag(vl, s, db);
+        const V8 va = __builtin_bit_cast(
+            V8, __builtin_shufflevector(vr[2 * db], vr[2 * db + 1], 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) acc[db][qb] = mfma32(va, pf[qb][s], acc[db][qb]);
       }
-  };
-
-  int buf = 0;
-  for (int t0 = 0; t0 < kv_end; t0 += kBK, buf ^= 1) {
-    const bool has_next = t0 + kBK < kv_end;
-    if (has_next) {
-      issue();
-      if (t0 + 2 * kBK < kv_end) load_slots(t0 + 2 * kBK);
     }
+  };
+  for (int t = 0; t < ntiles; ++t) {
+    wait_tile(min(NST - 2, ntiles - 1 - t));
+    // every wave's copies of tile t are in; every wave is done with tile
+    // t - 1, whose stage the copies of tile t + NST - 1 refill
+    lds_barrier();
+    if (t + NST - 1 < ntiles) kv_copy(t + NST - 1);
+    slot_copy(t + 2 * NST - 2);
+    const int t0 = t * kBK, buf = t % NST;
     if (wave_ok && t0 < wave_kv_end) {
       scores(t0, buf);
       // running maxima; the output rows are rescaled when a row's max rises
@@ -339,11 +369,9 @@ __global__ __launch_bounds__(512) void prefill_attn_fa_kernel(PrefillArgs a) {
       }
       accumulate(buf);
     }
-    if (has_next) store(buf ^ 1);
-    // the next tile's K rows and V^T rows are in LDS, every wave is done
-    // reading this tile's stage
-    __syncthreads();
   }
+  // no copy may still be writing this workgroup's LDS when it ends
+  vm_wait<0>();
   if (!wave_ok) return;
   // acc[db][qb][4 g + i] = O^T[d = 32 db + 8 g + 4 hf + i][query row0 + 32 qb + l32]
 #pragma unroll
@@ -491,7 +519,7 @@ extern "C" int ll_prefill_attention(const void* q, int64_t q_stride_tok, int64_t
   auto launch = [&](auto tag, auto dtag) {
     typedef decltype(tag) T;
     constexpr int D = decltype(dtag)::value;
-    constexpr size_t lds = 2 * FaGeom<D>::STAGE_B;
+    constexpr size_t lds = kStages * FaGeom<D>::STAGE_B + 8 * kStages * kBK * 4;
     if (wph == 2) hipLaunchKernelGGL((prefill_attn_fa_kernel<T, D, 2>), grid, block, lds, stream, a);
     else hipLaunchKernelGGL((prefill_attn_fa_kernel<T, D, 4>), grid, block, lds, stream, a);
   };
