@@ -14,17 +14,18 @@
 // the workgroup takes 8 / WPH heads of one KV head (WPH = 2 when the group
 // size is a multiple of 4, else 4), so every K/V tile staged in LDS serves 256
 // query rows. Per 64-key tile:
-//   * K and V rows are loaded through the slot table into registers while the
-//     previous tile is computed, then stored to LDS key-major, their 16-byte
-//     chunks XOR-swizzled by row so that the MFMA operand reads are
-//     bank-conflict free; the P.V operand V^T is read from the key-major V
+//   * K and V rows are DMA'd through the slot table straight into a 4-stage
+//     LDS ring (global_load_lds_dwordx4), three tiles ahead of the one being
+//     computed, stored key-major with their 16-byte chunks XOR-swizzled by
+//     row so that the MFMA operand reads are bank-conflict free; the slot ids
+//     are DMA'd too, by every wave into a ring of its own, three tiles ahead
+//     of their K/V copies. The P.V operand V^T is read from the key-major V
 //     tile with the gfx950 transposing LDS read (ds_read_b64_tr_b16), so no
-//     VALU work transposes V (no copy into LDS is in flight while the tile is
-//     computed, so its LDS reads wait for no global load);
+//     VALU work transposes V;
 //   * each wave computes S^T = K . Q^T (2 key blocks of 32, Q^T fragments in
 //     registers, v_mfma_f32_32x32x16), the online softmax in the exp2 domain
 //     with fp32 state, and O^T += V^T . P^T with P rounded to the KV dtype;
-//   * two LDS stages, one barrier per tile.
+//   * one barrier per tile.
 #include <type_traits>
 
 #include "ll_common.h"
