@@ -300,7 +300,9 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
   map_block(blockIdx.x, a.KVH, a.nsplit, b, kvh, split);
   if (b >= a.B) return;
   const int unit = b * a.KVH + kvh;
-  const int wave = threadIdx.x >> 6;
+  // the wave index as a scalar (threadIdx.x / 64 is the same in every lane
+  // of a wave): branches on it are scalar branches
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int n = lane & 15;  // MFMA column (query head within the group) / row
   const int j = lane >> 4;  // lane group
@@ -686,7 +688,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
 template <typename T, int D>
 __global__ __launch_bounds__(kCombWaves * 64) void decode_attn_combine_kernel(DecodeArgs a) {
   constexpr int DPL = D / 64;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int bh = blockIdx.x * kCombWaves + wave;
   if (bh >= a.B * a.H) return;
   const int b = bh / a.H, h = bh - b * a.H;
@@ -703,7 +705,7 @@ __global__ __launch_bounds__(kCombWaves * 64) void decode_attn_combine_kernel(De
 template <typename T, int D, int HPW>
 __global__ __launch_bounds__(1024) void decode_attn_combine_quant_kernel(DecodeArgs a) {
   constexpr int DPL = D / 64;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int nw = blockDim.x >> 6;
   const int b = blockIdx.x;
   float y[HPW][DPL];

@@ -260,7 +260,7 @@ __global__ __launch_bounds__(kThreads) void norm_qkv_kernel(NormQkvArgs a) {
   const int split = item % a.qsplits, t = item / a.qsplits;
   const int kc0 = split * a.per;
   const int nst = min(a.per, a.chunks - kc0);
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int n = lane & 15, j = lane >> 4;
   // waves 0-3 own the tile's 4 x 16 weight rows; waves 4-7 (there for the
   // norm rows' 512 threads) only take part in the workgroup barriers

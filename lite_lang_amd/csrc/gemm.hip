@@ -145,7 +145,7 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, 
   constexpr int C = W_PER_WAVE + X_PER_WAVE;  // DMA instructions per wave per stage
   constexpr int STAGE_B = (TR + XR) * ROWB;
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int n = lane & 15, j = lane >> 4;
   const int row0 = blockIdx.x * TR;
   const int split = blockIdx.y;
@@ -410,7 +410,7 @@ __global__ __launch_bounds__(64 * KW) void gemm_direct_kernel(
     const T* __restrict__ bias, T* __restrict__ Y, int64_t ldy, float* __restrict__ part, int M,
     int N, int K, int ksps) {
   typedef typename Vec8<T>::type V8;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int n = lane & 15, j = lane >> 4;
   const int row0 = blockIdx.x * (16 * WR);
   const int split = blockIdx.y;

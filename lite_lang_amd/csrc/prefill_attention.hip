@@ -141,7 +141,7 @@ __global__ __launch_bounds__(512) void prefill_attn_fa_kernel(PrefillArgs a) {
   const int kvh = unit % a.KVH;
   const int b = (unit / a.KVH) % a.B;
   const int mblk = a.nblk - 1 - unit / (a.KVH * a.B);
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int l32 = lane & 31, hf = lane >> 5;
   const int gh = SH::HPW * hp + wave / SH::WPH;  // head within the KV head's group

@@ -22,7 +22,7 @@ __device__ float row_absmax(const T* __restrict__ row, int K, float* red) {
   float m = 0.f;
   for (int k = threadIdx.x; k < K; k += 256) m = fmaxf(m, fabsf(ll_to_f32(row[k])));
   m = ll_wave_max(m);
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (lane == 0) red[wave] = m;
   __syncthreads();
   m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
