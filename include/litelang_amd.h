@@ -454,6 +454,19 @@ int ll_gemm_packed(const void* X, int64_t ldx, const void* Wp, const void* bias,
 int ll_gemm_packed_f32(const void* X, int64_t ldx, const void* Wp, const void* bias, float* Y,
                        int64_t ldy, int64_t M, int64_t N, int64_t K, int dtype, void* workspace,
                        int64_t workspace_bytes, hipStream_t stream);
+/* The lm_head and the greedy pick of the post layer in one call (replaces
+ * post_layer.py:20-22 + the argmax at :77 for M <= 64): Y = ll_gemm_packed_f32's
+ * fp32 logits, tokens[m] = the first index of row m's maximum, exactly as
+ * ll_argmax on Y (-1 in every row while *status is nonzero, as
+ * ll_argmax_status; status may be NULL). For one-split plans the first argmax
+ * pass runs in the GEMM's epilogue (per-tile maxima), otherwise the GEMM and
+ * ll_argmax run one after the other. Workspace:
+ * ll_gemm_packed_f32_argmax_workspace_size(M, N, K) bytes. */
+int64_t ll_gemm_packed_f32_argmax_workspace_size(int64_t M, int64_t N, int64_t K);
+int ll_gemm_packed_f32_argmax(const void* X, int64_t ldx, const void* Wp, const void* bias,
+                              float* Y, int64_t ldy, int64_t M, int64_t N, int64_t K, int dtype,
+                              int64_t* tokens, const uint32_t* status, void* workspace,
+                              int64_t workspace_bytes, hipStream_t stream);
 /* Gate/up projection fused with SiLU_and_Mul (replaces the gate_up projection
  * plus silu_and_mul_fwd of transformer_layer.py:80-81 for M <= 64). The weight
  * is [gate; up] ([2I, K], the reference's two nn.Linear weights stacked);

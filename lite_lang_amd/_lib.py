@@ -68,6 +68,8 @@ SIGNATURES = {
     "ll_gemm_splitk_packed": (I32, [P, I64, P, I64, I64, I64, I32, P, I64, P]),
     "ll_gemm_packed": (I32, [P, I64, P, P, P, I64, I64, I64, I64, I32, P, I64, P]),
     "ll_gemm_packed_f32": (I32, [P, I64, P, P, P, I64, I64, I64, I64, I32, P, I64, P]),
+    "ll_gemm_packed_f32_argmax_workspace_size": (I64, [I64, I64, I64]),
+    "ll_gemm_packed_f32_argmax": (I32, [P, I64, P, P, P, I64, I64, I64, I64, I32, P, P, P, I64, P]),
     "ll_gemm_packed_gate_up_bytes": (I64, [I64, I64]),
     "ll_gemm_pack_gate_up": (I32, [P, I64, I64, I64, I32, P, I64, P]),
     "ll_gemm_packed_tile_rows": (I32, [I64, I64]),

@@ -667,6 +667,17 @@ __global__ __launch_bounds__(256) void argmax_final_kernel(const float* __restri
 }
 
 
+// The second pass on partials a producer wrote itself ([M][nparts] values
+// and indices), for kernels that fold the first pass into their epilogue.
+int ll_argmax_finish(const float* pval, const int* pidx, int64_t M, int64_t nparts, int64_t* out,
+                     const uint32_t* status, hipStream_t stream) {
+  LL_CHECK_ARG(pval && pidx && out && M > 0 && nparts > 0 && nparts < (1ll << 31),
+               "ll_argmax_finish: bad arguments");
+  hipLaunchKernelGGL(argmax_final_kernel, dim3((unsigned)M), dim3(256), 0, stream, pval, pidx,
+                     (int)nparts, out, status);
+  LL_RETURN_LAUNCH();
+}
+
 extern "C" int64_t ll_argmax_workspace_size(int64_t M, int64_t N) {
   const int64_t nchunk = (N + kArgmaxChunk - 1) / kArgmaxChunk;
   return nchunk > 1 ? M * nchunk * 8 : 0;

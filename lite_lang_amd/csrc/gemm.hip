@@ -111,6 +111,10 @@ __device__ __forceinline__ void wait_stage(int later) {
 // T(T(up) * T(silu(T(gate)))) for the TR/2 channels of the tile (N = 2 *
 // channels), the rounding sequence of ll_silu_and_mul_splitk applied to the
 // same fp32 sums.
+// EPI 2 (one split, bf16/fp16 operands, no partials): Y as EPI 0, and for
+// every token the tile's largest Y value with its first channel index,
+// written to e8.am_val / e8.am_idx[token][tile] (the first pass of a
+// first-index argmax over the row; argmax_final_kernel finishes it).
 // int8 gate/up epilogue (EPI 1 with int8 operands): the int32 sums are
 // dequantised as fp32(acc) * s_tok[m] * fp32(s_ch[col]) (col = channel for
 // gate, I + channel for up) and SiLU_and_Mul is written to y (type TO).
@@ -120,6 +124,9 @@ struct I8Epi {
   int s_ch_dtype;
   void* y;
   int64_t ldy;
+  // EPI 2: per-token argmax partials of the tile, [M][tiles] (value, index)
+  float* am_val;
+  int* am_idx;
 };
 
 template <typename T, int MB, int NST, bool PK, int EPI = 0, int TR = 64, typename TO = T>
@@ -319,6 +326,87 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, 
           for (int e = 0; e < 4 && c0 + e < I; ++e) yp[e] = y[e];
         }
       }
+    }
+    return;
+  } else if constexpr (EPI == 2) {
+    // fp32 logits and the argmax's first pass: every lane stores its RB
+    // channel quads of each token and keeps its (value, first index) per
+    // token, then the 4 lane groups of a token (shuffles) and the 4 waves
+    // (LDS, free after the last stage) merge theirs into the tile's partial.
+    // The picks are selects, not branches: no exec-masked joins.
+    static_assert(std::is_same<TO, float>::value, "the argmax epilogue writes fp32 logits");
+    float* Yf = (float*)(void*)Y;
+    const bool vec = ((ldy & 3) == 0) && (((uintptr_t)Yf & 15) == 0);
+    float bv[MB];
+    int bi[MB];
+#pragma unroll
+    for (int t = 0; t < MB; ++t) { bv[t] = -INFINITY; bi[t] = 0x7fffffff; }
+#pragma unroll
+    for (int b = 0; b < RB; ++b) {
+      const int ch = row0 + wave * 16 * RB + 16 * b + 4 * j;
+      float bb[4] = {0.f, 0.f, 0.f, 0.f};
+      if (bias != nullptr) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) bb[i] = ll_to_f32(bias[min(ch + i, N - 1)]);
+      }
+#pragma unroll
+      for (int t = 0; t < MB; ++t) {
+        const int tok = 16 * t + n;
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          v[i] = acc[b][t][i] + bb[i];
+          // channel indices rise with i, so a tie keeps the earlier pick
+          const bool take = (ch + i < N) & ((v[i] > bv[t]) | ((v[i] == bv[t]) & (bi[t] == 0x7fffffff)));
+          bv[t] = take ? v[i] : bv[t];
+          bi[t] = take ? ch + i : bi[t];
+        }
+        if (tok < M && ch < N) {
+          float* yp = Yf + (int64_t)tok * ldy + ch;
+          if (vec && ch + 3 < N) {
+            *(f32x4*)yp = (f32x4){v[0], v[1], v[2], v[3]};
+          } else {
+            for (int i = 0; i < 4 && ch + i < N; ++i) yp[i] = v[i];
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < MB; ++t) {
+#pragma unroll
+      for (int o = 16; o < 64; o <<= 1) {
+        const float ov = __shfl_xor(bv[t], o, 64);
+        const int oi = __shfl_xor(bi[t], o, 64);
+        const bool take = (ov > bv[t]) | ((ov == bv[t]) & (oi < bi[t]));
+        bv[t] = take ? ov : bv[t];
+        bi[t] = take ? oi : bi[t];
+      }
+    }
+    lds_barrier();  // every wave is done reading the last stage
+    float* sval = (float*)smem;
+    int* sidx = (int*)(sval + 4 * XR);
+    if (j == 0) {
+#pragma unroll
+      for (int t = 0; t < MB; ++t) {
+        sval[wave * XR + 16 * t + n] = bv[t];
+        sidx[wave * XR + 16 * t + n] = bi[t];
+      }
+    }
+    lds_barrier();
+    const int tok = (int)threadIdx.x;
+    if (tok < M) {
+      float v = sval[tok];
+      int i = sidx[tok];
+#pragma unroll
+      for (int w = 1; w < 4; ++w) {
+        const float ov = sval[w * XR + tok];
+        const int oi = sidx[w * XR + tok];
+        const bool take = (ov > v) | ((ov == v) & (oi < i));
+        v = take ? ov : v;
+        i = take ? oi : i;
+      }
+      e8.am_val[(int64_t)tok * gridDim.x + blockIdx.x] = v;
+      e8.am_idx[(int64_t)tok * gridDim.x + blockIdx.x] = i;
     }
     return;
   } else if constexpr (ES == 1) {
@@ -1012,6 +1100,87 @@ extern "C" int ll_gemm_packed_f32(const void* X, int64_t ldx, const void* Wp, co
                                   void* workspace, int64_t workspace_bytes, hipStream_t stream) {
   return gemm_packed_impl("ll_gemm_packed_f32", X, ldx, Wp, bias, Y, ldy, M, N, K, dtype, true,
                           workspace, workspace_bytes, stream);
+}
+
+namespace {
+// The packed GEMM with the EPI 2 epilogue (fp32 output + the argmax's first
+// pass); one-split plans only.
+template <typename T, int MB>
+void launch_argmax_mb(const SkinnyPlan& p, const T* X, int64_t ldx, const T* Wp, const T* bias,
+                      float* Y, int64_t ldy, int M, int N, int K, float* am_val, int* am_idx,
+                      hipStream_t stream) {
+  const dim3 grid((unsigned)p.tiles, 1u);
+  const size_t lds = (size_t)p.nst * (p.tr + 16 * MB) * 256;
+  I8Epi e{};
+  e.am_val = am_val;
+  e.am_idx = am_idx;
+#define LL_AM_LAUNCH(S, TR_)                                                                      \
+  hipLaunchKernelGGL((gemm_dma_kernel<T, MB, S, true, 2, TR_, float>), grid, dim3(256), lds,       \
+                     stream, X, ldx, Wp, (int64_t)K, bias, (T*)(void*)Y, ldy, nullptr, M, N, K,    \
+                     p.ksps, 0, e)
+  if (p.tr == 128) LL_AM_LAUNCH(3, 128);
+  else if (p.nst == 3) LL_AM_LAUNCH(3, 64);
+  else LL_AM_LAUNCH(2, 64);
+#undef LL_AM_LAUNCH
+}
+}  // namespace
+
+extern "C" int64_t ll_gemm_packed_f32_argmax_workspace_size(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || M > 64 || N <= 0 || K <= 0 || K % kDmaKC != 0) return 0;
+  const SkinnyPlan p = plan_skinny(N, K);
+  if (p.splits == 1) return M * p.tiles * 8;
+  return (int64_t)p.splits * M * N * 4 + ll_argmax_workspace_size(M, N);
+}
+
+extern "C" int ll_gemm_packed_f32_argmax(const void* X, int64_t ldx, const void* Wp,
+                                         const void* bias, float* Y, int64_t ldy, int64_t M,
+                                         int64_t N, int64_t K, int dtype, int64_t* tokens,
+                                         const uint32_t* status, void* workspace,
+                                         int64_t workspace_bytes, hipStream_t stream) {
+  const char* name = "ll_gemm_packed_f32_argmax";
+  LL_CHECK_ARG(X && Wp && Y && tokens, "%s: null pointer", name);
+  LL_CHECK_ARG(M > 0 && M <= 64 && N > 0 && K > 0 && K % kDmaKC == 0,
+               "%s: needs 0 < M <= 64 and K %% %d == 0", name, kDmaKC);
+  LL_CHECK_ARG(dtype == LL_BF16 || dtype == LL_F16, "%s: bf16/fp16 only", name);
+  LL_CHECK_ARG(ldx % 8 == 0 && (((uintptr_t)X | (uintptr_t)Wp) % 16) == 0,
+               "%s: X rows must be 16 B aligned", name);
+  LL_CHECK_ARG(ldx >= K && ldy >= N, "%s: row strides shorter than the rows", name);
+  const int64_t need = ll_gemm_packed_f32_argmax_workspace_size(M, N, K);
+  LL_CHECK_ARG(workspace != nullptr && workspace_bytes >= need,
+               "%s: workspace too small (need %lld bytes)", name, (long long)need);
+  SkinnyPlan p = plan_skinny(N, K);
+  p.packed = true;
+  p.rotate = 0;
+  if (p.splits > 1) {
+    // a plan with k splits: the GEMM and a separate argmax
+    const int64_t part_bytes = (int64_t)p.splits * M * N * 4;
+    const int rc = gemm_packed_impl(name, X, ldx, Wp, bias, Y, ldy, M, N, K, dtype, true,
+                                    workspace, part_bytes, stream);
+    if (rc != LL_OK) return rc;
+    void* aws = (char*)workspace + part_bytes;
+    const int64_t awsb = workspace_bytes - part_bytes;
+    return status != nullptr
+               ? ll_argmax_status(Y, ldy, M, N, tokens, aws, awsb, LL_F32, status, stream)
+               : ll_argmax(Y, ldy, M, N, tokens, aws, awsb, LL_F32, stream);
+  }
+  float* am_val = (float*)workspace;
+  int* am_idx = (int*)(am_val + M * p.tiles);
+  auto run = [&](auto tag) {
+    typedef decltype(tag) T;
+    switch ((M + 15) / 16) {
+      case 1: launch_argmax_mb<T, 1>(p, (const T*)X, ldx, (const T*)Wp, (const T*)bias, Y, ldy, (int)M, (int)N, (int)K, am_val, am_idx, stream); break;
+      case 2: launch_argmax_mb<T, 2>(p, (const T*)X, ldx, (const T*)Wp, (const T*)bias, Y, ldy, (int)M, (int)N, (int)K, am_val, am_idx, stream); break;
+      case 3: launch_argmax_mb<T, 3>(p, (const T*)X, ldx, (const T*)Wp, (const T*)bias, Y, ldy, (int)M, (int)N, (int)K, am_val, am_idx, stream); break;
+      default: launch_argmax_mb<T, 4>(p, (const T*)X, ldx, (const T*)Wp, (const T*)bias, Y, ldy, (int)M, (int)N, (int)K, am_val, am_idx, stream); break;
+    }
+  };
+  if (dtype == LL_BF16) run(__bf16{}); else run(_Float16{});
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    ll_set_error("%s: launch failed: %s", name, hipGetErrorString(e));
+    return LL_ERR_HIP;
+  }
+  return ll_argmax_finish(am_val, am_idx, M, p.tiles, tokens, status, stream);
 }
 
 extern "C" int ll_gemm(const void* X, int64_t ldx, const void* W, int64_t ldw, const void* bias,

@@ -52,6 +52,11 @@ enum { LL_F32 = LL_DTYPE_F32, LL_F16 = LL_DTYPE_F16, LL_BF16 = LL_DTYPE_BF16 };
 // Per-thread last-error text, returned by ll_last_error().
 void ll_set_error(const char* fmt, ...);
 
+// Second pass of the first-index argmax over per-row partials [M][nparts]
+// written by another kernel (elementwise.hip).
+int ll_argmax_finish(const float* pval, const int* pidx, int64_t M, int64_t nparts, int64_t* out,
+                     const uint32_t* status, hipStream_t stream);
+
 #define LL_CHECK_ARG(cond, ...)                 \
   do {                                          \
     if (!(cond)) {                              \

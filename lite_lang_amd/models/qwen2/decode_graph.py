@@ -42,6 +42,8 @@ def reserve_decode_workspaces(cfg, batch, max_len, device):
     ops.reserve_workspace(device, "gemm",
                           max(L.ll_gemm_workspace_size(batch, n, k) for n, k in shapes))
     ops.reserve_workspace(device, "argmax", L.ll_argmax_workspace_size(batch, cfg.vocab_size))
+    ops.reserve_workspace(device, "lm_argmax", L.ll_gemm_packed_f32_argmax_workspace_size(
+        batch, cfg.vocab_size, cfg.hidden_size))
 
 
 def reserve_model_workspaces(model, batch, max_len):

@@ -123,6 +123,20 @@ class Qwen2Model:
             return ops.gemm_packed(x, w.lm_head_p, out_dtype=torch.float32)
         return ops.gemm(x, w.lm_head)
 
+    def _logits_argmax(self, x, out, status=None):
+        """lm_head + greedy pick of the decode step: the fused call (the
+        argmax's first pass in the lm_head's epilogue) where the packed lm_head
+        applies, else _logits and ll_argmax. Sets last_logits; returns the
+        tokens (in `out` when given)."""
+        w = self.w
+        if w.lm_head_p is not None and x.shape[0] <= 64:
+            logits, toks = ops.gemm_packed_argmax(x, w.lm_head_p, out=out, status=status)
+        else:
+            logits = self._logits(x)
+            toks = ops.argmax(logits, out=out, status=status)
+        self.last_logits = logits
+        return toks
+
     def _post(self, hs, fs, out=None):
         """Final residual add + RMSNorm (eps 1e-5), lm_head, greedy argmax
         (post_layer.py:14-24,43-45,75-77)."""
@@ -261,11 +275,9 @@ class Qwen2Model:
                 x = ops.add_rmsnorm_splitk(h, part, s, w.layers[li + 1]["ln1"], cfg.rms_norm_eps)
             else:
                 x = ops.add_rmsnorm_splitk(h, part, s, w.norm, cfg.final_norm_eps)
-        logits = self._logits(x)
-        self.last_logits = logits
         # a fused launch that gave up a flag wait turns every token into -1
         # (the host raises on it, runner_batch.check_step_tokens)
-        return ops.argmax(logits, out=out, status=ops.decode_sync_error(dev) if fuse_qkv else None)
+        return self._logits_argmax(x, out, ops.decode_sync_error(dev) if fuse_qkv else None)
 
     def _decode_w8a8(self, h, B, part, q, attn, act, positions, seq_len, rids, slots, pool, r2t,
                      max_len, out):
@@ -326,9 +338,7 @@ class Qwen2Model:
                     xq, xs = ops.quant_input(x, nxt["wqkv_i8"])
             else:
                 x = ops.add_rmsnorm_splitk_i32(h, p, w.norm, cfg.final_norm_eps)
-        logits = self._logits(x)
-        self.last_logits = logits
-        return ops.argmax(logits, out=out)
+        return self._logits_argmax(x, out)
 
     # ------------------------------------------------------------ forward
     def forward(self, model_inputs, kv_cache: PageCache, mem_idxs: torch.Tensor):

@@ -562,6 +562,31 @@ def gemm_splitk_packed(x, wp: PackedWeight, part):
     return s
 
 
+def gemm_packed_argmax(x, wp: PackedWeight, logits=None, out=None, status=None):
+    """The fp32 logits x @ w^T (M <= 64, packed weight) and their first-index
+    argmax in one call (ll_gemm_packed_f32_argmax); with `status`, every token
+    is -1 while that word is nonzero. Returns (logits, tokens)."""
+    _dev(x, logits, out, status)
+    M, K = x.shape
+    N = wp.shape[0]
+    assert wp.shape[1] == K and x.stride(1) == 1 and x.dtype == wp.dtype
+    if logits is None:
+        logits = torch.empty((M, N), dtype=torch.float32, device=x.device)
+    if out is None:
+        out = torch.empty((M,), dtype=torch.int64, device=x.device)
+    assert logits.shape == (M, N) and logits.stride(1) == 1 and logits.dtype == torch.float32
+    assert out.numel() == M and out.dtype == torch.int64 and out.is_contiguous()
+    nbytes = _L.ll_gemm_packed_f32_argmax_workspace_size(M, N, K)
+    ws = workspace(x.device, "lm_argmax", nbytes)
+    rc = _L.ll_gemm_packed_f32_argmax(x.data_ptr(), x.stride(0), wp.data.data_ptr(), None,
+                                      logits.data_ptr(), logits.stride(0), M, N, K, dtype_code(x),
+                                      out.data_ptr(),
+                                      status.data_ptr() if status is not None else None,
+                                      ws.data_ptr(), ws.numel(), _stream(x))
+    _lib.check(rc, "ll_gemm_packed_f32_argmax")
+    return logits, out
+
+
 def gemm_packed(x, wp: PackedWeight, bias=None, out=None, out_dtype=None):
     """out[M, N] = x @ w^T (+ bias) for M <= 64 from a packed weight; with
     out_dtype=torch.float32 the sums are written unrounded (fp32)."""

@@ -647,3 +647,43 @@ def test_assign_slots(cuda):
         ops.assign_slots(r2t, torch.stack([slots, rows, cols]).to(cuda), n)
     torch.cuda.synchronize()
     assert torch.equal(r2t.cpu(), ref)
+
+
+@pytest.mark.parametrize("M,N,K,dtype", [
+    (40, 151936, 2048, torch.bfloat16),  # the 3B lm_head: one split, 128-row tiles
+    (1, 151936, 2048, torch.bfloat16),
+    (64, 151936, 2048, torch.float16),
+    (17, 1024, 256, torch.bfloat16),     # tiny vocabulary: one split, 64-row tiles
+    (40, 2048, 2048, torch.bfloat16),    # a plan with k splits: GEMM, then ll_argmax
+])
+def test_gemm_packed_argmax_equals_gemm_then_argmax(cuda, M, N, K, dtype):
+    """ll_gemm_packed_f32_argmax (the argmax's first pass in the lm_head
+    epilogue) against ll_gemm_packed_f32 followed by ll_argmax on the same
+    inputs: fp32 logits bit-identical, tokens identical. Rows 0 and 1 of the
+    weight are copied to the last rows and to a row in the middle (other
+    tiles), and token row 0 of x is scaled so those rows win: exact ties
+    across tiles, where the first index must win. With a set status word
+    every token is -1."""
+    ops = _ops()
+    g = torch.Generator().manual_seed(M + N + K)
+    w = (torch.randn(N, K, generator=g) * 0.05).to(dtype)
+    w[N - 1] = w[0]
+    w[N // 2 + 3] = w[0]
+    w[N - 2] = w[1]
+    x = torch.randn(M, K, generator=g).to(dtype)
+    x[0] = (w[0].float() * 4).to(dtype)  # row 0 of w (and its copies) is the maximum for token 0
+    print(f"case: gemm_packed_argmax M={M} N={N} K={K} {dtype}", flush=True)
+    xd, wp = x.to(cuda), ops.PackedWeight(w.to(cuda))
+    ref_logits = ops.gemm_packed(xd, wp, out_dtype=torch.float32)
+    ref_tok = ops.argmax(ref_logits)
+    logits, tok = ops.gemm_packed_argmax(xd, wp)
+    torch.cuda.synchronize()
+    assert torch.equal(logits, ref_logits)
+    assert torch.equal(tok, ref_tok)
+    assert int(tok[0]) == 0  # the first of the tied copies
+    status = torch.ones(1, dtype=torch.int32, device=cuda)
+    _, tok_err = ops.gemm_packed_argmax(xd, wp, status=status)
+    assert torch.equal(tok_err.cpu(), torch.full((M,), -1, dtype=torch.int64))
+    status.zero_()
+    _, tok_ok = ops.gemm_packed_argmax(xd, wp, status=status)
+    assert torch.equal(tok_ok, ref_tok)
