@@ -23,13 +23,14 @@
 //     length into that many tile-aligned chunks, so the grid does not depend
 //     on the lengths (graph safe);
 //   * the 8 waves merge in LDS; the splits of a (sequence, KV head) are merged
-//     by the last of them to finish, one wave per head with the partials of
-//     all splits in flight at once. All splits of a unit run on one XCD, so
-//     the ticket and the partials meet in that XCD's L2 (no device-scope
-//     write-back; a device-scope version was measured slower than a second
-//     launch). The quantising variant (one sequence's heads span units on
-//     different XCDs) and batches beyond kMergeUnits units merge in a second
-//     kernel instead.
+//     by its last split (the workgroup with the unit's highest index), which
+//     polls the others' partial words in the XCD's L2 (all splits of a unit
+//     run on one XCD) while it merges its own waves: no ticket, and no wait
+//     for stores to be acknowledged, on the way to the output (a device-scope
+//     version was measured slower than a second launch). The quantising
+//     variant (one sequence's heads span units on different XCDs) merges in
+//     the last workgroup of the sequence to take a ticket, and batches
+//     beyond kMergeUnits units in a second kernel.
 // A generic VALU path covers fp32 and head dims other than 64/128.
 #include "ll_common.h"
 
@@ -42,6 +43,9 @@ constexpr int kTT = 16;     // tokens per tile
 constexpr int kWaves = 8;   // waves per split-stage workgroup
 constexpr int kCombWaves = 4;  // waves (one (sequence, head) each) per combine workgroup
 constexpr int kRing = 2;    // tile buffers per wave
+constexpr int kUnitMergeSplits = 8;  // splits the per-unit merge holds in registers
+constexpr int kUnitMergeSpin = 1 << 20;  // polls before the per-unit merge gives up (never
+                                         // reached: the words are already on their way)
 
 template <typename T> struct Vec8;
 template <> struct Vec8<__bf16> { typedef bf16x8 type; };
@@ -244,6 +248,29 @@ __device__ __forceinline__ void combine_bh(const DecodeArgs& a, int bh, int lane
   else combine_bh_sb<D, 16>(a, bh, lane, o);
 }
 
+// Split partials in the workspace: +0.0 is stored as -0.0 (the merges only
+// add and multiply these words, where the two zeros give the same results),
+// so that a zero word means "not written". Every merge zeroes the rows it
+// consumed, so the partial rows are all zero between calls (the workspace
+// starts zeroed), and the per-unit merge can poll the words themselves
+// instead of waiting for their stores to be acknowledged.
+__device__ __forceinline__ float part_word(float x) { return x == 0.f ? -0.f : x; }
+
+__device__ __forceinline__ uint32_t ld_agent(const uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Zeroes the partial rows of (sequence, head) bh after one wave merged them
+// (its loads have returned: their values were used).
+template <int D>
+__device__ __forceinline__ void clear_bh(const DecodeArgs& a, int bh, int lane) {
+  const int64_t p0 = (int64_t)bh * a.nsplit;
+  for (int s = 0; s < a.nsplit; ++s)
+#pragma unroll
+    for (int q = 0; q < D / 64; ++q) a.part_acc[(p0 + s) * D + lane + 64 * q] = 0.f;
+  for (int i = lane; i < 2 * a.nsplit; i += 64) a.part_ml[p0 * 2 + i] = 0.f;
+}
+
 // XCD-aware mapping: the dispatcher deals the workgroups of a launch to the
 // 8 XCDs round-robin, workgroup i to XCD (i + r) mod 8 for one r per launch
 // (the round-robin continues from the previous launch, so r varies), and
@@ -277,6 +304,99 @@ template <int D> struct TileGeom {
   // LDS chunk position of global chunk c of tile row r (an involution)
   static __device__ __forceinline__ int swz(int c, int r) { return c ^ ((r / ROWS_PER_BANKS) & (CH - 1)); }
 };
+
+// Merge of a unit's splits by its split nsplit - 1, whose own partial
+// (own_merge: the merge of its waves) stays in registers, one (head, 4 d)
+// item per thread. That workgroup has the highest index of its unit, and
+// workgroups start in index order on an XCD, so the NO = nsplit - 1 others it
+// waits for started before it and wait for nothing themselves: they store
+// their partial words as soon as they have them. A zero word is one not yet
+// written. All splits of a unit run on one XCD (map_block), whose L2 the
+// polls read; each poll issues every load before looking at any, and the
+// first one is in flight while own_merge runs. The wait is bounded
+// (kUnitMergeSpin polls; the rows then come out NaN). The merge is
+// combine_bh's arithmetic, splits in order, so both merges give the same
+// bits. The merged rows are zeroed for the next call.
+template <typename T, int D, int NO, typename OwnMerge>
+__device__ __forceinline__ void unit_merge_tail(const DecodeArgs& a, bool item, int b, int kvh,
+                                                int g, int d0, int64_t pbase,
+                                                const OwnMerge& own_merge) {
+  const int ns = a.nsplit;
+  const int no = ns - 1;
+  const int64_t p0 = pbase + (int64_t)g * ns;  // this item's rows: p0 .. p0 + ns - 1
+  float M, L;
+  f32x4 A;
+  if (item) {
+    float am[NO][4], mm[NO], lm[NO];
+    bool gave_up = false;
+    uint32_t u[NO][6];
+    auto poll = [&]() {
+#pragma unroll
+      for (int s = 0; s < NO; ++s) {
+        const int64_t ps = p0 + min(s, no - 1);
+        const uint32_t* wa = (const uint32_t*)(a.part_acc + ps * D + d0);
+        const uint32_t* wm = (const uint32_t*)(a.part_ml + ps * 2);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) u[s][q] = ld_agent(wa + q);
+        u[s][4] = ld_agent(wm);
+        u[s][5] = ld_agent(wm + 1);
+      }
+    };
+    poll();
+    own_merge(M, L, A);  // this workgroup's merge while the first poll is in flight
+    for (int it = 0;; ++it) {
+      bool ready = true;
+#pragma unroll
+      for (int s = 0; s < NO; ++s) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) am[s][q] = __uint_as_float(u[s][q]);
+        mm[s] = __uint_as_float(u[s][4]);
+        lm[s] = __uint_as_float(u[s][5]);
+        const bool all = u[s][0] != 0u && u[s][1] != 0u && u[s][2] != 0u && u[s][3] != 0u &&
+                         u[s][4] != 0u && u[s][5] != 0u;
+        ready = ready && (s >= no || all);
+      }
+      if (ready) break;
+      if (it >= kUnitMergeSpin) {
+        gave_up = true;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+      poll();
+    }
+    float Mx = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < NO; ++s)
+      if (s < no) Mx = fmaxf(Mx, mm[s]);
+    Mx = fmaxf(Mx, M);
+    float Lx = 0.f, Ax[4] = {0.f, 0.f, 0.f, 0.f};
+    if (Mx != -INFINITY) {
+#pragma unroll
+      for (int s = 0; s < NO; ++s) {
+        if (s < no) {
+          const float w = exp2f(mm[s] - Mx);
+          Lx += lm[s] * w;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) Ax[q] += am[s][q] * w;
+        }
+      }
+      const float w = exp2f(M - Mx);
+      Lx += L * w;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) Ax[q] += A[q] * w;
+    }
+    T* op = (T*)a.out + (int64_t)b * a.o_sb + (int64_t)(kvh * a.G + g) * a.o_sh + d0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      op[q] = ll_from_f32<T>(gave_up ? __builtin_nanf("") : (Lx > 0.f ? Ax[q] / Lx : 0.f));
+    for (int s = 0; s < no; ++s)
+      *(f32x4*)&a.part_acc[(p0 + s) * D + d0] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  }
+  lds_barrier();  // every poll of the (m, l) words is done
+  if (item && d0 == 0) {
+    for (int i = 0; i < 2 * no; ++i) a.part_ml[p0 * 2 + i] = 0.f;
+  }
+}
 
 // ROPE: q comes from the QKV projection's split-K partials (bias, RoPE) instead
 // of a q tensor, and the workgroup whose split holds the sequence's last tile
@@ -582,51 +702,78 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
   }
   __syncthreads();
 
-  // four consecutive d of one head per thread
+  // Per-unit merge (several splits, rows not quantised): split nsplit - 1 of
+  // every (sequence, KV head) merges the others' partials (unit_merge_tail).
+  const bool whole_row = a.qout != nullptr;
+  const bool unit_merge = a.merge_cnt != nullptr && !whole_row && a.nsplit <= kUnitMergeSplits;
+
+  // four consecutive d of one head per thread (G * D / 4 <= kWaves * 64)
   constexpr int DQ = D / 4;
   const int64_t pbase = ((int64_t)b * a.H + (int64_t)kvh * G) * a.nsplit;
-  for (int e = threadIdx.x; e < G * DQ; e += kWaves * 64) {
-    const int g = e / DQ, d0 = (e - g * DQ) * 4;
-    float M = -INFINITY;
+  const int e = threadIdx.x;
+  const bool item = e < G * DQ;
+  const int g = item ? e / DQ : 0, d0 = item ? (e - g * DQ) * 4 : 0;
+  // this workgroup's (max, sum, accumulators) of the thread's item
+  auto wave_merge = [&](float& M, float& L, f32x4& A) {
+    M = -INFINITY;
+    L = 0.f;
+    A = (f32x4){0.f, 0.f, 0.f, 0.f};
+    if (item) {
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, comb_m(w)[g]);
-    float L = 0.f;
-    f32x4 A = {0.f, 0.f, 0.f, 0.f};
-    if (M != -INFINITY) {
+      for (int w = 0; w < kWaves; ++w) M = fmaxf(M, comb_m(w)[g]);
+      if (M != -INFINITY) {
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) {
-        const float sc = exp2f(comb_m(w)[g] - M);
-        L += comb_l(w)[g] * sc;
-        const f32x4 v = *(const f32x4*)(comb_acc(w, g) + d0);
+        for (int w = 0; w < kWaves; ++w) {
+          const float sc = exp2f(comb_m(w)[g] - M);
+          L += comb_l(w)[g] * sc;
+          const f32x4 v = *(const f32x4*)(comb_acc(w, g) + d0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) A[i] += v[i] * sc;
+          for (int i = 0; i < 4; ++i) A[i] += v[i] * sc;
+        }
       }
     }
-    if (a.nsplit == 1) {
+  };
+  if (unit_merge && split == a.nsplit - 1) {
+    if (a.nsplit == 2)
+      unit_merge_tail<T, D, 1>(a, item, b, kvh, g, d0, pbase, wave_merge);
+    else if (a.nsplit == 3)
+      unit_merge_tail<T, D, 2>(a, item, b, kvh, g, d0, pbase, wave_merge);
+    else if (a.nsplit == 4)
+      unit_merge_tail<T, D, 3>(a, item, b, kvh, g, d0, pbase, wave_merge);
+    else
+      unit_merge_tail<T, D, kUnitMergeSplits - 1>(a, item, b, kvh, g, d0, pbase, wave_merge);
+    return;
+  }
+  float M, L;
+  f32x4 A;
+  wave_merge(M, L, A);
+  if (a.nsplit == 1) {
+    if (item) {
       T* op = (T*)a.out + (int64_t)b * a.o_sb + (int64_t)(kvh * G + g) * a.o_sh + d0;
 #pragma unroll
       for (int i = 0; i < 4; ++i) op[i] = ll_from_f32<T>(L > 0.f ? A[i] / L : 0.f);
-    } else {
-      const int64_t p = pbase + (int64_t)g * a.nsplit + split;
-      *(f32x4*)&a.part_acc[p * D + d0] = A;
-      if (d0 == 0) {
-        a.part_ml[p * 2] = M;
-        a.part_ml[p * 2 + 1] = L;
-      }
+    }
+    return;
+  }
+  if (item) {
+    const int64_t p = pbase + (int64_t)g * a.nsplit + split;
+    *(f32x4*)&a.part_acc[p * D + d0] = (f32x4){part_word(A[0]), part_word(A[1]),
+                                               part_word(A[2]), part_word(A[3])};
+    if (d0 == 0) {
+      a.part_ml[p * 2] = part_word(M);
+      a.part_ml[p * 2 + 1] = part_word(L);
     }
   }
   if (a.merge_cnt == nullptr) return;
 
-  // ---- the last split of this (sequence, KV head) to finish merges all of
-  // them; with quantised output rows, the last workgroup of the sequence
-  // merges all its heads and quantises the row. All of them run on one XCD
-  // (map_block), so that XCD's L2 is where they meet: each thread's partial
-  // stores are acknowledged by L2 (the vector L1 is write-through) before the
-  // ticket is taken, and the merging workgroup drops its own L1 lines before
-  // reading the other workgroups' partials. The ticket wraps to zero on the
-  // last increment, so the counter is zero again for the next call.
+  if (unit_merge) return;
+
   __shared__ unsigned s_ticket;
-  const bool whole_row = a.qout != nullptr;
+  // ---- more splits than the per-unit merge holds, or quantised rows: the
+  // last split of the unit (or, with quantised rows, the last workgroup of the
+  // sequence, which merges all its heads and quantises the row) merges after
+  // every partial store has been acknowledged by the XCD's L2 (the vector L1
+  // is write-through) and drops its own L1 lines before reading them.
   const unsigned last = (unsigned)((whole_row ? a.KVH : 1) * a.nsplit - 1);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
@@ -637,10 +784,12 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
   if (s_ticket != last) return;
   asm volatile("buffer_inv sc0" ::: "memory");
   if (!whole_row) {
-    for (int g = wave; g < G; g += kWaves) {
+    for (int gg = wave; gg < G; gg += kWaves) {
       float o[D / 64];
-      combine_bh<D>(a, b * a.H + kvh * G + g, lane, o);
-      T* op = (T*)a.out + (int64_t)b * a.o_sb + (int64_t)(kvh * G + g) * a.o_sh;
+      const int bh = b * a.H + kvh * G + gg;
+      combine_bh<D>(a, bh, lane, o);
+      clear_bh<D>(a, bh, lane);
+      T* op = (T*)a.out + (int64_t)b * a.o_sb + (int64_t)(kvh * G + gg) * a.o_sh;
 #pragma unroll
       for (int q = 0; q < D / 64; ++q) op[lane + 64 * q] = ll_from_f32<T>(o[q]);
     }
@@ -654,6 +803,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
   for (int h = wave; h < a.H; h += kWaves) {
     float o[D / 64];
     combine_bh<D>(a, b * a.H + h, lane, o);
+    clear_bh<D>(a, b * a.H + h, lane);
     T* op = (T*)a.out + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh;
 #pragma unroll
     for (int q = 0; q < D / 64; ++q) {
@@ -694,6 +844,7 @@ __global__ __launch_bounds__(kCombWaves * 64) void decode_attn_combine_kernel(De
   const int b = bh / a.H, h = bh - b * a.H;
   float o[DPL];
   combine_bh<D>(a, bh, lane, o);
+  clear_bh<D>(a, bh, lane);
   T* op = (T*)a.out + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh;
 #pragma unroll
   for (int q = 0; q < DPL; ++q) op[lane + 64 * q] = ll_from_f32<T>(o[q]);
@@ -716,6 +867,7 @@ __global__ __launch_bounds__(1024) void decode_attn_combine_quant_kernel(DecodeA
     if (h < a.H) {
       float o[DPL];
       combine_bh<D>(a, b * a.H + h, lane, o);
+      clear_bh<D>(a, b * a.H + h, lane);
       T* op = (T*)a.out + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh;
 #pragma unroll
       for (int q = 0; q < DPL; ++q) {
