@@ -140,9 +140,9 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, 
   typedef typename Vec8<T>::type V8;
   typedef typename AccOf<T>::type AccT;
   constexpr int ES = (int)sizeof(T);
-  static_assert(TR == 64 || TR == 128, "64- or 128-row tiles");
+  static_assert(TR == 64 || TR == 96 || TR == 128, "64-, 96- or 128-row tiles");
   constexpr int XR = 16 * MB;
-  constexpr int RB = TR / 64;             // 16-row MFMA blocks per wave
+  constexpr int RB = (TR / 16 + 3) / 4;   // 16-row MFMA blocks per wave (at most)
   constexpr int KC = 256 / ES;            // elements per 256-byte row chunk (one stage)
   constexpr int CE = 16 / ES;             // elements per 16-byte fragment
   constexpr int KSTEP = 4 * CE;           // k per MFMA: 32 (16-bit types), 64 (int8)
@@ -156,6 +156,11 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, 
   const int n = lane & 15, j = lane >> 4;
   const int row0 = blockIdx.x * TR;
   const int split = blockIdx.y;
+  // the tile's 16-row MFMA blocks per wave: RB consecutive ones with 64 and
+  // 128 rows; with 96 rows waves 0 and 1 take blocks w and w + 4, waves 2
+  // and 3 block w alone (nb: the wave's block count, a scalar)
+  auto blk = [&](int b) { return TR == 96 ? wave + 4 * b : wave * RB + b; };
+  const int nb = TR == 96 ? (wave < 2 ? 2 : 1) : RB;
   const int k_beg = split * ksps * KSTEP;
   const int k_end = min(K, k_beg + ksps * KSTEP);
   const int nst = (k_end - k_beg) / KC;
@@ -205,15 +210,18 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, 
     const int I = N / 2;
 #pragma unroll
     for (int t = 0; t < MB; ++t) e_st[t] = e8.s_tok[min(16 * t + n, M - 1)];
-    const int cbase = blockIdx.x * (TR / 2) + 16 * RB * (wave & 1) + 4 * j;
-    const int coff = wave >= 2 ? I : 0;
     auto load_sc = [&](auto tag) {
       typedef decltype(tag) S;
       const S* s = (const S*)e8.s_ch;
 #pragma unroll
-      for (int b = 0; b < RB; ++b)
+      for (int b = 0; b < RB; ++b) {
+        const int row = 16 * blk(min(b, nb - 1)) + 4 * j;  // tile row of acc[b][.][0]
+        const bool up = row >= TR / 2;
+        const int cbase = blockIdx.x * (TR / 2) + row - (up ? TR / 2 : 0);
+        const int coff = up ? I : 0;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) e_sc[b][i] = s[coff + min(cbase + 16 * b + i, I - 1)];
+        for (int i = 0; i < 4; ++i) e_sc[b][i] = s[coff + min(cbase + i, I - 1)];
+      }
     };
     if (e8.s_ch_dtype == LL_F32) load_sc(uint32_t{});
     else load_sc((unsigned short){});
@@ -233,19 +241,22 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, 
       V8 a[RB];
 #pragma unroll
       for (int b = 0; b < RB; ++b) {
-        const int lr = wave * 16 * RB + 16 * b + n;
-        a[b] = *(const V8*)(wb + lr * ROWB + (((4 * s + j) ^ (lr & 15)) * 16));
+        if (b < nb) {
+          const int lr = 16 * blk(b) + n;
+          a[b] = *(const V8*)(wb + lr * ROWB + (((4 * s + j) ^ (lr & 15)) * 16));
+        }
       }
 #pragma unroll
       for (int t = 0; t < MB; ++t) {
         const int xr = 16 * t + n;
         const V8 xv = *(const V8*)(xb + xr * ROWB + (((4 * s + j) ^ (xr & 15)) * 16));
 #pragma unroll
-        for (int b = 0; b < RB; ++b) acc[b][t] = mfma16x16x32(a[b], xv, acc[b][t]);
+        for (int b = 0; b < RB; ++b)
+          if (b < nb) acc[b][t] = mfma16x16x32(a[b], xv, acc[b][t]);
       }
     }
   }
-  // acc[b][t][i] = Y[token 16t + n][channel row0 + 16*RB*wave + 16b + 4j + i]
+  // acc[b][t][i] = Y[token 16t + n][channel row0 + 16*blk(b) + 4j + i], b < nb
   if constexpr (EPI == 1) {
     // gate/up, one split: every wave puts its sums (int8: dequantised as
     // fp32(acc) * s_tok[m] * fp32(s_ch[col])) into LDS rows [token][channel],
@@ -286,15 +297,20 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, 
           for (int i = 0; i < 4; ++i) vs[b][t][i] = acc[b][t][i];
     }
     lds_barrier();  // every wave is done reading the last stage
-    float* dst = wave < 2 ? gbuf : ubuf;
 #pragma unroll
-    for (int b = 0; b < RB; ++b)
+    for (int b = 0; b < RB; ++b) {
+      if (b < nb) {
+        // a 16-row block is all gate (tile rows < HALF) or all up channels
+        const int row = 16 * blk(b) + 4 * j;
+        const bool up = row >= HALF;
+        float* dst = up ? ubuf : gbuf;
+        const int cl = row - (up ? HALF : 0);
 #pragma unroll
-      for (int t = 0; t < MB; ++t) {
-        const int cl = 16 * RB * (wave & 1) + 16 * b + 4 * j;
-        *(f32x4*)(dst + (16 * t + n) * PITCH + cl) =
-            (f32x4){vs[b][t][0], vs[b][t][1], vs[b][t][2], vs[b][t][3]};
+        for (int t = 0; t < MB; ++t)
+          *(f32x4*)(dst + (16 * t + n) * PITCH + cl) =
+              (f32x4){vs[b][t][0], vs[b][t][1], vs[b][t][2], vs[b][t][3]};
       }
+    }
     lds_barrier();
     TO* Yo = ES == 1 ? (TO*)e8.y : (TO*)Y;
     const int64_t ly = ES == 1 ? e8.ldy : ldy;
@@ -343,7 +359,8 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, 
     for (int t = 0; t < MB; ++t) { bv[t] = -INFINITY; bi[t] = 0x7fffffff; }
 #pragma unroll
     for (int b = 0; b < RB; ++b) {
-      const int ch = row0 + wave * 16 * RB + 16 * b + 4 * j;
+      if (b >= nb) continue;
+      const int ch = row0 + 16 * blk(b) + 4 * j;
       float bb[4] = {0.f, 0.f, 0.f, 0.f};
       if (bias != nullptr) {
 #pragma unroll
@@ -414,7 +431,8 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, 
     int32_t* ip = (int32_t*)part;
 #pragma unroll
     for (int b = 0; b < RB; ++b) {
-      const int ch = row0 + wave * 16 * RB + 16 * b + 4 * j;
+      if (b >= nb) continue;
+      const int ch = row0 + 16 * blk(b) + 4 * j;
 #pragma unroll
       for (int t = 0; t < MB; ++t) {
         const int tok = 16 * t + n;
@@ -431,7 +449,8 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, 
   } else {
 #pragma unroll
     for (int b = 0; b < RB; ++b) {
-      const int ch = row0 + wave * 16 * RB + 16 * b + 4 * j;
+      if (b >= nb) continue;
+      const int ch = row0 + 16 * blk(b) + 4 * j;
 #pragma unroll
       for (int t = 0; t < MB; ++t) {
         const int tok = 16 * t + n;
@@ -804,8 +823,18 @@ SkinnyPlan plan_skinny(int64_t N, int64_t K, int es = 2) {
 }
 
 // Tile height of the fused gate/up kernel (one split): 128 rows (64 gate + 64
-// up channels) once 64-row tiles would outnumber the CUs, as for plan_skinny.
+// up channels) once 64-row tiles would outnumber the CUs, as for plan_skinny
+// (int8 weights).
 int gate_up_tr(int64_t I) { return ll_cdiv(I, 32) > 256 ? 128 : 64; }
+// 16-bit weights: the lowest of 64, 96 and 128 rows whose tiles fit in one
+// dispatch round of the 256 CUs. At the Qwen2.5-3B shape (I = 11008) 96-row
+// tiles give 230 workgroups (128-row tiles: 172, leaving a third of the CUs
+// idle): 17.45 against 18.2 us per launch with cold weights, three stage
+// buffers (four measured 17.8).
+int gate_up_tr16(int64_t I) {
+  if (ll_cdiv(I, 32) <= 256) return 64;
+  return ll_cdiv(I, 48) <= 256 ? 96 : 128;
+}
 
 template <typename T, int MB, typename TO = T>
 void launch_skinny_mb(const SkinnyPlan& p, const T* X, int64_t ldx, const T* W, int64_t ldw,
@@ -936,7 +965,7 @@ extern "C" int ll_gemm_packed_tile_rows(int64_t N, int64_t K) {
 }
 
 extern "C" int ll_gemm_packed_gate_up_tile_rows(int64_t I) {
-  return I > 0 ? gate_up_tr(I) : 0;
+  return I > 0 ? gate_up_tr16(I) : 0;
 }
 
 extern "C" int64_t ll_gemm_packed_bytes(int64_t N, int64_t K) {
@@ -966,7 +995,7 @@ extern "C" int ll_gemm_pack(const void* W, int64_t ldw, int64_t N, int64_t K, in
 
 extern "C" int64_t ll_gemm_packed_gate_up_bytes(int64_t I, int64_t K) {
   if (I <= 0 || K <= 0 || K % kDmaKC != 0) return 0;
-  const int tr = gate_up_tr(I);
+  const int tr = gate_up_tr16(I);
   return ll_cdiv(I, tr / 2) * tr * K * 2;
 }
 
@@ -982,7 +1011,7 @@ extern "C" int ll_gemm_pack_gate_up(const void* W, int64_t ldw, int64_t I, int64
   LL_CHECK_ARG(wp_bytes >= bytes, "ll_gemm_pack_gate_up: output too small (need %lld bytes)",
                (long long)bytes);
   const int64_t units = bytes / 16;
-  const int tr = gate_up_tr(I);
+  const int tr = gate_up_tr16(I);
   const int tiles = (int)ll_cdiv(I, tr / 2);
   hipLaunchKernelGGL(gemm_pack_kernel, dim3((unsigned)ll_cdiv(units, 256)), dim3(256), 0, stream,
                      (const u32x4*)W, ldw / 8, (u32x4*)Wp, (int)(2 * I), tiles, units, (int)I, tr);
@@ -998,9 +1027,9 @@ extern "C" int ll_gemm_gate_up_silu_packed(const void* X, int64_t ldx, const voi
   LL_CHECK_ARG(dtype == LL_BF16 || dtype == LL_F16, "ll_gemm_gate_up_silu_packed: bf16/fp16 only");
   LL_CHECK_ARG(ldx % 8 == 0 && (((uintptr_t)X | (uintptr_t)Wp) % 16) == 0,
                "ll_gemm_gate_up_silu_packed: X rows must be 16 B aligned");
-  const int tr = gate_up_tr(I);
+  const int tr = gate_up_tr16(I);
   const int tiles = (int)ll_cdiv(I, tr / 2);
-  const int nst = (tr == 128 || tiles <= 256) ? 3 : 2;
+  const int nst = (tr != 64 || tiles <= 256) ? 3 : 2;
   const int ksps = (int)(K / 32);
   auto run = [&](auto tag) {
     typedef decltype(tag) T;
@@ -1011,7 +1040,11 @@ extern "C" int ll_gemm_gate_up_silu_packed(const void* X, int64_t ldx, const voi
 #define LL_GU(MB_)                                                                              \
   do {                                                                                          \
     const size_t lds = (size_t)nst * (tr + 16 * MB_) * kDmaKC * 2;                              \
-    if (tr == 128)                                                                              \
+    if (tr == 96)                                                                               \
+      hipLaunchKernelGGL((gemm_dma_kernel<T, MB_, 3, true, 1, 96>), grid, dim3(256), lds,        \
+                         stream, x, ldx, w, K, nullptr, y, ld_act, nullptr, (int)M, (int)(2 * I), \
+                         (int)K, ksps, 0, I8Epi{});                                             \
+    else if (tr == 128)                                                                         \
       hipLaunchKernelGGL((gemm_dma_kernel<T, MB_, 3, true, 1, 128>), grid, dim3(256), lds,       \
                          stream, x, ldx, w, K, nullptr, y, ld_act, nullptr, (int)M, (int)(2 * I), \
                          (int)K, ksps, 0, I8Epi{});                                             \

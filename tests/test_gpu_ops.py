@@ -490,7 +490,8 @@ def test_gemm_packed_with_bias(cuda, M, N, K):
     assert _close_rel(y, O.linear(x, w, b))
 
 
-@pytest.mark.parametrize("M,I,K", [(40, 11008, 2048), (1, 256, 128), (64, 200, 384), (17, 4864, 896 + 128)])
+@pytest.mark.parametrize("M,I,K", [(40, 11008, 2048), (64, 11008, 256), (40, 12300, 256), (1, 256, 128),
+                                    (64, 200, 384), (17, 4864, 896 + 128)])
 def test_gate_up_silu_fused_equals_unfused(cuda, M, I, K):
     """The fused epilogue rounds exactly as gemm_splitk + silu_and_mul_splitk do
     with one split: bit-identical output; and within tolerance of the oracle."""
@@ -513,7 +514,7 @@ def test_gate_up_silu_fused_equals_unfused(cuda, M, I, K):
     assert _close_rel(fused, ref)
 
 
-@pytest.mark.parametrize("I,K,tr", [(70, 256, 64), (8200, 128, 128)])
+@pytest.mark.parametrize("I,K,tr", [(70, 256, 64), (8200, 128, 96), (12300, 128, 128)])
 def test_gate_up_pack_layout(cuda, I, K, tr):
     from lite_lang_amd import _lib
     g = torch.Generator().manual_seed(49)
