@@ -822,16 +822,13 @@ SkinnyPlan plan_skinny(int64_t N, int64_t K, int es = 2) {
   return p;
 }
 
-// Tile height of the fused gate/up kernel (one split): 128 rows (64 gate + 64
-// up channels) once 64-row tiles would outnumber the CUs, as for plan_skinny
-// (int8 weights).
-int gate_up_tr(int64_t I) { return ll_cdiv(I, 32) > 256 ? 128 : 64; }
-// 16-bit weights: the lowest of 64, 96 and 128 rows whose tiles fit in one
-// dispatch round of the 256 CUs. At the Qwen2.5-3B shape (I = 11008) 96-row
-// tiles give 230 workgroups (128-row tiles: 172, leaving a third of the CUs
-// idle): 17.45 against 18.2 us per launch with cold weights, three stage
-// buffers (four measured 17.8).
-int gate_up_tr16(int64_t I) {
+// Tile height of the fused gate/up kernel (one split): the lowest of 64, 96
+// and 128 rows (half gate, half up channels) whose tiles fit in one dispatch
+// round of the 256 CUs. At the Qwen2.5-3B shape (I = 11008) 96-row tiles give
+// 230 workgroups (128-row tiles: 172, leaving a third of the CUs idle): 17.45
+// against 18.2 us per bf16 launch with cold weights, three stage buffers (four
+// measured 17.8).
+int gate_up_tr(int64_t I) {
   if (ll_cdiv(I, 32) <= 256) return 64;
   return ll_cdiv(I, 48) <= 256 ? 96 : 128;
 }
@@ -965,7 +962,7 @@ extern "C" int ll_gemm_packed_tile_rows(int64_t N, int64_t K) {
 }
 
 extern "C" int ll_gemm_packed_gate_up_tile_rows(int64_t I) {
-  return I > 0 ? gate_up_tr16(I) : 0;
+  return I > 0 ? gate_up_tr(I) : 0;
 }
 
 extern "C" int64_t ll_gemm_packed_bytes(int64_t N, int64_t K) {
@@ -995,7 +992,7 @@ extern "C" int ll_gemm_pack(const void* W, int64_t ldw, int64_t N, int64_t K, in
 
 extern "C" int64_t ll_gemm_packed_gate_up_bytes(int64_t I, int64_t K) {
   if (I <= 0 || K <= 0 || K % kDmaKC != 0) return 0;
-  const int tr = gate_up_tr16(I);
+  const int tr = gate_up_tr(I);
   return ll_cdiv(I, tr / 2) * tr * K * 2;
 }
 
@@ -1011,7 +1008,7 @@ extern "C" int ll_gemm_pack_gate_up(const void* W, int64_t ldw, int64_t I, int64
   LL_CHECK_ARG(wp_bytes >= bytes, "ll_gemm_pack_gate_up: output too small (need %lld bytes)",
                (long long)bytes);
   const int64_t units = bytes / 16;
-  const int tr = gate_up_tr16(I);
+  const int tr = gate_up_tr(I);
   const int tiles = (int)ll_cdiv(I, tr / 2);
   hipLaunchKernelGGL(gemm_pack_kernel, dim3((unsigned)ll_cdiv(units, 256)), dim3(256), 0, stream,
                      (const u32x4*)W, ldw / 8, (u32x4*)Wp, (int)(2 * I), tiles, units, (int)I, tr);
@@ -1027,7 +1024,7 @@ extern "C" int ll_gemm_gate_up_silu_packed(const void* X, int64_t ldx, const voi
   LL_CHECK_ARG(dtype == LL_BF16 || dtype == LL_F16, "ll_gemm_gate_up_silu_packed: bf16/fp16 only");
   LL_CHECK_ARG(ldx % 8 == 0 && (((uintptr_t)X | (uintptr_t)Wp) % 16) == 0,
                "ll_gemm_gate_up_silu_packed: X rows must be 16 B aligned");
-  const int tr = gate_up_tr16(I);
+  const int tr = gate_up_tr(I);
   const int tiles = (int)ll_cdiv(I, tr / 2);
   const int nst = (tr != 64 || tiles <= 256) ? 3 : 2;
   const int ksps = (int)(K / 32);
@@ -1314,6 +1311,7 @@ void launch_i8_gate_up_mb(const int8_t* x, int64_t ldx, const int8_t* w, int64_t
   const int tr = gate_up_tr(I);
   const unsigned tiles = (unsigned)ll_cdiv(I, tr / 2);
   if (tr == 128) launch_i8_gate_up<MB, 3, 128, TO>(x, ldx, w, M, I, K, tiles, e, stream);
+  else if (tr == 96) launch_i8_gate_up<MB, 3, 96, TO>(x, ldx, w, M, I, K, tiles, e, stream);
   else if (tiles <= 256) launch_i8_gate_up<MB, 3, 64, TO>(x, ldx, w, M, I, K, tiles, e, stream);
   else launch_i8_gate_up<MB, 2, 64, TO>(x, ldx, w, M, I, K, tiles, e, stream);
 }
