@@ -400,11 +400,12 @@ __device__ __forceinline__ void unit_merge_tail(const DecodeArgs& a, bool item, 
 
 // ROPE: q comes from the QKV projection's split-K partials (bias, RoPE) instead
 // of a q tensor, and the workgroup whose split holds the sequence's last tile
-// also builds the new token's K/V, writes them to new_slots[b] in the pool and
-// patches the tile rows carrying that slot in its own LDS copy (the DMA may
-// have read the slot before the write landed). Precondition: a sequence's new
-// slot appears in no other sequence's first seq_len entries and in its own
-// only within the last split (the decode step puts it at seq_len - 1).
+// also builds the new token's K/V, patches the tile rows carrying that slot in
+// its own LDS copy (its copies read the pool's old contents of the slot) and
+// writes them to new_slots[b] in the pool on its way out. Precondition: a
+// sequence's new slot appears in no other sequence's first seq_len entries
+// and in its own only within the last split (the decode step puts it at
+// seq_len - 1).
 template <typename T, int D, int MODE>
 __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs a) {
   typedef typename Vec8<T>::type V8;
@@ -508,6 +509,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
   // K/V copy: waiting for them then waits for no copy (loads and copies
   // share the in-order vmcnt counter).
   bool writer = false;
+  int jb = -1;  // ROPE, writer workgroup: this thread's new K/V job, or < 0
   if constexpr (ROPE) {
     const int64_t qkv_row = (int64_t)b * ((a.H + 2 * a.KVH) * D);
     const float* cs = a.cos_tab + (int64_t)pos32 * a.tab_stride;
@@ -518,16 +520,32 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
                      nullptr);
     }
     writer = split == (ntiles > 0 ? (ntiles - 1) / per : 0);
-    const int jb = (int)threadIdx.x - (kWaves * 64 - 2 * QD);
+    jb = (int)threadIdx.x - (kWaves * 64 - 2 * QD);
     if (writer && jb >= 0) {
       const bool isv = jb >= QD;
       const int i = (isv ? jb - QD : jb) * 4;
-      T* glb = isv ? (T*)a.v + (int64_t)new_slot * a.v_st + (int64_t)kvh * a.v_sh
-                   : (T*)a.k + (int64_t)new_slot * a.k_st + (int64_t)kvh * a.k_sh;
       rope_job<T, D, MODE>(a, b, qkv_row, (a.H + (isv ? a.KVH : 0) + kvh) * D, i, cs, sn,
-                     !isv, s_kv + (isv ? D : 0), glb);
+                     !isv, s_kv + (isv ? D : 0), nullptr);
     }
   }
+  // The new token's K/V go to the pool from s_kv when the workgroup leaves
+  // (no split reads that slot from the pool in this launch; the writer's own
+  // tile copy is patched from s_kv). Stored here, they would sit in the
+  // vector memory counter ahead of the K/V copies, and the first copy would
+  // wait for their acknowledgement.
+  auto store_new_kv = [&]() {
+    if constexpr (ROPE) {
+      if (writer && jb >= 0) {
+        const bool isv = jb >= QD;
+        const int i = (isv ? jb - QD : jb) * 4;
+        T* glb = isv ? (T*)a.v + (int64_t)new_slot * a.v_st + (int64_t)kvh * a.v_sh
+                     : (T*)a.k + (int64_t)new_slot * a.k_st + (int64_t)kvh * a.k_sh;
+        const T* src = s_kv + (isv ? D : 0);
+        *(uint64_t*)(glb + i) = *(const uint64_t*)(src + i);
+        *(uint64_t*)(glb + i + D / 2) = *(const uint64_t*)(src + i + D / 2);
+      }
+    }
+  };
   store_round(0, sl0);
   for (int r0 = 4; 4 * r0 < nw; r0 += 4) {  // further rounds of 16 tiles (long splits)
     int32_t sl[4];
@@ -742,6 +760,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
       unit_merge_tail<T, D, 3>(a, item, b, kvh, g, d0, pbase, wave_merge);
     else
       unit_merge_tail<T, D, kUnitMergeSplits - 1>(a, item, b, kvh, g, d0, pbase, wave_merge);
+    store_new_kv();
     return;
   }
   float M, L;
@@ -753,6 +772,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
 #pragma unroll
       for (int i = 0; i < 4; ++i) op[i] = ll_from_f32<T>(L > 0.f ? A[i] / L : 0.f);
     }
+    store_new_kv();
     return;
   }
   if (item) {
@@ -764,6 +784,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
       a.part_ml[p * 2 + 1] = part_word(L);
     }
   }
+  store_new_kv();
   if (a.merge_cnt == nullptr) return;
 
   if (unit_merge) return;
