@@ -46,7 +46,7 @@ const char* ll_last_error(void);
 /* ---------------------------------------------------------------- attention */
 
 /* Paged GQA decode attention, split-K (the last split of each (sequence,
- * KV head) to finish merges the partials, in the same launch).
+ * KV head) merges the partials, in the same launch).
  * Replaces token_decode_attention_flash_decoding
  *   (litelang/kernel/develop_flash_attn/flash_decoding.py:262-312).
  * q [batch, q_heads, head_dim]; k_cache / v_cache [P, kv_heads, head_dim]
@@ -55,9 +55,10 @@ const char* ll_last_error(void);
  * b_seq_len (it sizes the split count and the workspace; tokens beyond it are
  * ignored, as the reference's grid ignores them). workspace: at least
  * ll_decode_attention_workspace_size bytes (0 when no split is needed),
- * zero-filled before its first use: its first 16 KiB hold the split tickets,
- * which every call leaves at zero, so one buffer serves calls of any shape;
- * two calls in flight at once must not share it. */
+ * zero-filled before its first use: its first 16 KiB hold split tickets and
+ * the rest the split partials, whose zero words mean "not yet written"; every
+ * call leaves all of it at zero again, so one buffer serves calls of any
+ * shape; two calls in flight at once must not share it. */
 int64_t ll_decode_attention_workspace_size(int64_t batch, int64_t q_heads, int64_t kv_heads,
                                            int64_t head_dim, int64_t max_len_in_batch);
 int ll_decode_attention(const void* q, int64_t q_stride_b, int64_t q_stride_h,
@@ -79,8 +80,8 @@ int ll_decode_attention(const void* q, int64_t q_stride_b, int64_t q_stride_h,
  * more is rejected with LL_ERR_ARG (use ll_decode_attention with a
  * workspace). Nothing is allocated. Every call on one GPU shares that GPU's
  * array: two calls that overlap in time on one GPU (two streams, two threads)
- * race and give wrong results. The array starts zeroed (its split tickets at
- * zero) and every call leaves the tickets at zero, so nothing is cleared. The
+ * race and give wrong results. The array starts zeroed (split tickets and
+ * partials) and every call leaves it at zero, so nothing is cleared. The
  * first call on a device looks the array's device address up (no work is
  * queued; this may happen under graph capture); ll_decode_attention_noalloc_init
  * does that lookup for the current device ahead of time, for set-up code.
@@ -471,7 +472,8 @@ int ll_gemm_packed_f32_argmax(const void* X, int64_t ldx, const void* Wp, const 
  * plus silu_and_mul_fwd of transformer_layer.py:80-81 for M <= 64). The weight
  * is [gate; up] ([2I, K], the reference's two nn.Linear weights stacked);
  * ll_gemm_pack_gate_up packs it so that every tile of R rows
- * (ll_gemm_packed_gate_up_tile_rows: 64, or 128 when I > 8192) holds R/2 gate
+ * (ll_gemm_packed_gate_up_tile_rows: 64 when I <= 8192, else 96 when
+ * I <= 12288, else 128) holds R/2 gate
  * rows and the R/2 up rows of the same channels (size from
  * ll_gemm_packed_gate_up_bytes, 0 if K % 128 != 0). act[m, c] =
  * dtype(dtype(up) * dtype(silu(dtype(gate)))), the rounding sequence of
