@@ -89,9 +89,11 @@ def test_decode_attention_shapes(cuda, dtype, H, KVH, D):
 
 
 def test_decode_attention_repeat_calls_are_identical(cuda):
-    # the last split of each (sequence, KV head) merges, picked by a ticket in
-    # the shared workspace that wraps back to zero: calls of different shapes
-    # and split counts in a row must not interfere, and leave the tickets at 0
+    # the last split of each (sequence, KV head) merges the others' partial
+    # words, whose zero means "not yet written", and zeroes the rows it merged:
+    # calls of different shapes and split counts in a row share one workspace,
+    # must not interfere (no call may take an earlier call's words), and leave
+    # the whole workspace at zero
     print("case: decode repeat, interleaved shapes", flush=True)
     a, ref = _decode_case(cuda, 40, 16, 2, 128, [700] * 40, torch.bfloat16, 3)
     c, cref = _decode_case(cuda, 2, 16, 2, 128, [40, 2000], torch.bfloat16, 4)
@@ -103,6 +105,7 @@ def test_decode_attention_repeat_calls_are_identical(cuda):
         assert _maxdiff(out, r) <= BF16_ATOL
     ws = _ops()._WS[_ops()._ws_key(cuda, "decode_attention")]
     assert int(ws[:16384].count_nonzero()) == 0, "split tickets not back at zero"
+    assert int(ws.count_nonzero()) == 0, "split partials not back at zero"
 
 
 def test_decode_attention_reference_wrapper(cuda):
