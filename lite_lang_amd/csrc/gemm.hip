@@ -1133,12 +1133,201 @@ extern "C" int ll_gemm_packed_f32(const void* X, int64_t ldx, const void* Wp, co
 }
 
 namespace {
+// Persistent form of the packed GEMM with the argmax epilogue, for the plans
+// with 128-row tiles and one split (the lm_head): at most one workgroup per
+// CU (kLmCUs), each taking tiles blockIdx.x, blockIdx.x + gridDim.x, ...; its
+// LDS copy ring runs on from one tile into the next, so the next tile's first
+// stages are in flight while a tile is finished and stored, where a workgroup
+// per tile pays the first copies' round trip and its ramp once per tile. The
+// epilogue is EPI 2's (the tile's logits and per-token (value, first index))
+// with buffer stores: every wave issues the same number of them for every
+// tile (a masked lane's offset lies past the buffer), so the ring's vmcnt
+// waits count them: for two iterations after an epilogue its stores sit
+// among the copies in flight. No bias (the lm_head has none).
+constexpr int kLmCUs = 256;
+constexpr int kLmStages = 3;
+constexpr uint32_t kLmNoStore = 0x80000000u;
+
+template <typename T, int MB>
+__global__ __launch_bounds__(256) void lm_head_argmax_kernel(const T* __restrict__ X, int64_t ldx,
+                                                             const T* __restrict__ Wp,
+                                                             float* __restrict__ Y, int64_t ldy,
+                                                             int M, int N, int K, int tiles,
+                                                             float* __restrict__ am_val,
+                                                             int* __restrict__ am_idx) {
+  typedef typename Vec8<T>::type V8;
+  constexpr int TR = 128, NST = kLmStages, RB = 2, XR = 16 * MB;
+  constexpr int KC = 128, CE = 8, KSTEP = 32;
+  constexpr int ROWB = 256, CH = 16, RPI = 4;
+  constexpr int W_PER_WAVE = (TR / RPI) / 4;
+  constexpr int X_PER_WAVE = (XR / RPI) / 4;
+  constexpr int C = W_PER_WAVE + X_PER_WAVE;  // copies per wave per stage
+  constexpr int SY = RB * MB;                 // logit stores per wave per tile
+  constexpr int STAGE_B = (TR + XR) * ROWB;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  float* sval = (float*)(smem + NST * STAGE_B);  // the epilogue's rows, outside the ring
+  int* sidx = (int*)(sval + 4 * XR);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int n = lane & 15, j = lane >> 4;
+  const int lr_in = lane / CH, p = lane % CH;
+  const int nst = K / KC;
+  const int my_tiles = (tiles - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+  const int total = my_tiles * nst;  // stages of this workgroup, tile after tile
+  const __amdgpu_buffer_rsrc_t yres =
+      __builtin_amdgcn_make_buffer_rsrc(Y, (short)0, (int)((int64_t)M * ldy * 4), 0x00020000);
+  const __amdgpu_buffer_rsrc_t vres =
+      __builtin_amdgcn_make_buffer_rsrc(am_val, (short)0, M * tiles * 4, 0x00020000);
+  const __amdgpu_buffer_rsrc_t ires =
+      __builtin_amdgcn_make_buffer_rsrc(am_idx, (short)0, M * tiles * 4, 0x00020000);
+  auto issue = [&](int g) {  // stage g: k chunk g % nst of this workgroup's tile g / nst
+    const int jt = g / nst, kc = g - jt * nst;
+    const int tile = (int)blockIdx.x + jt * (int)gridDim.x;
+    char* base = smem + (g % NST) * STAGE_B;
+#pragma unroll
+    for (int q = 0; q < W_PER_WAVE; ++q) {
+      const int ii = wave * W_PER_WAVE + q;
+      const char* gp = (const char*)Wp + ((int64_t)kc * tiles + tile) * (TR * ROWB) + ii * 1024 +
+                       lane * 16;
+      dma16_stream(gp, base + ii * 1024);
+    }
+#pragma unroll
+    for (int q = 0; q < X_PER_WAVE; ++q) {
+      const int ii = wave + q * 4;
+      const int r = ii * RPI + lr_in;
+      const T* gp = X + (int64_t)min(r, M - 1) * ldx + kc * KC + (p ^ (r & 15)) * CE;
+      dma16(gp, base + TR * ROWB + ii * 1024);
+    }
+  };
+  f32x4 acc[RB][MB];
+#pragma unroll
+  for (int b = 0; b < RB; ++b)
+#pragma unroll
+    for (int t = 0; t < MB; ++t) acc[b][t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  // acc[b][t][i] = Y[token 16t + n][channel 128 tile + 32 wave + 16 b + 4 j + i]
+  auto epilogue = [&](int tile) {
+    float bv[MB];
+    int bi[MB];
+#pragma unroll
+    for (int t = 0; t < MB; ++t) { bv[t] = -INFINITY; bi[t] = 0x7fffffff; }
+#pragma unroll
+    for (int b = 0; b < RB; ++b) {
+      const int ch = tile * TR + wave * 16 * RB + 16 * b + 4 * j;
+#pragma unroll
+      for (int t = 0; t < MB; ++t) {
+        const int tok = 16 * t + n;
+        const f32x4 v = acc[b][t];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          // channel indices rise with (b, i), so a tie keeps the earlier pick
+          const bool take = (ch + i < N) & ((v[i] > bv[t]) | ((v[i] == bv[t]) & (bi[t] == 0x7fffffff)));
+          bv[t] = take ? v[i] : bv[t];
+          bi[t] = take ? ch + i : bi[t];
+        }
+        const uint32_t off = (tok < M && ch < N) ? (uint32_t)(((int64_t)tok * ldy + ch) * 4) : kLmNoStore;
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), yres, off, 0, 0);
+        asm volatile("" ::: "memory");
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < MB; ++t) {
+#pragma unroll
+      for (int o = 16; o < 64; o <<= 1) {
+        const float ov = __shfl_xor(bv[t], o, 64);
+        const int oi = __shfl_xor(bi[t], o, 64);
+        const bool take = (ov > bv[t]) | ((ov == bv[t]) & (oi < bi[t]));
+        bv[t] = take ? ov : bv[t];
+        bi[t] = take ? oi : bi[t];
+      }
+    }
+    if (j == 0) {
+#pragma unroll
+      for (int t = 0; t < MB; ++t) {
+        sval[wave * XR + 16 * t + n] = bv[t];
+        sidx[wave * XR + 16 * t + n] = bi[t];
+      }
+    }
+    lds_barrier();
+    if (wave == 0) {  // lane = token: its value and index over the four waves
+      const int tok = min(lane, XR - 1);
+      float v = sval[tok];
+      int i = sidx[tok];
+#pragma unroll
+      for (int w = 1; w < 4; ++w) {
+        const float ov = sval[w * XR + tok];
+        const int oi = sidx[w * XR + tok];
+        const bool take = (ov > v) | ((ov == v) & (oi < i));
+        v = take ? ov : v;
+        i = take ? oi : i;
+      }
+      const uint32_t off = lane < M ? (uint32_t)((lane * tiles + tile) * 4) : kLmNoStore;
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), vres, off, 0, 0);
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_raw_buffer_store_b32((uint32_t)i, ires, off, 0, 0);
+      asm volatile("" ::: "memory");
+    }
+  };
+#pragma unroll
+  for (int g = 0; g < NST - 1; ++g)
+    if (g < total) issue(g);
+  int last_ep = -NST;  // the iteration of the last epilogue
+  for (int g = 0; g < total; ++g) {
+    // stage g's copies are done; stage g + 1's may stay in flight, and so may
+    // the last epilogue's stores while they are younger than stage g's copies
+    const bool later = g + 1 < total;
+    if (g - last_ep <= 2) {
+      if (wave == 0) {
+        if (later) vm_wait<C + SY + 2>(); else vm_wait<SY + 2>();
+      } else {
+        if (later) vm_wait<C + SY>(); else vm_wait<SY>();
+      }
+    } else {
+      if (later) vm_wait<C>(); else vm_wait<0>();
+    }
+    lds_barrier();  // and every wave is done with stage g - 1, refilled here
+    if (g + NST - 1 < total) issue(g + NST - 1);
+    const char* wb = smem + (g % NST) * STAGE_B;
+    const char* xb = wb + TR * ROWB;
+#pragma unroll
+    for (int s = 0; s < KC / KSTEP; ++s) {
+      V8 a[RB];
+#pragma unroll
+      for (int b = 0; b < RB; ++b) {
+        const int lr = wave * 16 * RB + 16 * b + n;
+        a[b] = *(const V8*)(wb + lr * ROWB + (((4 * s + j) ^ (lr & 15)) * 16));
+      }
+#pragma unroll
+      for (int t = 0; t < MB; ++t) {
+        const int xr = 16 * t + n;
+        const V8 xv = *(const V8*)(xb + xr * ROWB + (((4 * s + j) ^ (xr & 15)) * 16));
+#pragma unroll
+        for (int b = 0; b < RB; ++b) acc[b][t] = mfma16x16x32(a[b], xv, acc[b][t]);
+      }
+    }
+    if (g % nst == nst - 1) {
+      epilogue((int)blockIdx.x + (g / nst) * (int)gridDim.x);
+#pragma unroll
+      for (int b = 0; b < RB; ++b)
+#pragma unroll
+        for (int t = 0; t < MB; ++t) acc[b][t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+      last_ep = g;
+    }
+  }
+}
+
 // The packed GEMM with the EPI 2 epilogue (fp32 output + the argmax's first
-// pass); one-split plans only.
+// pass); one-split plans only. 128-row plans without bias run persistent.
 template <typename T, int MB>
 void launch_argmax_mb(const SkinnyPlan& p, const T* X, int64_t ldx, const T* Wp, const T* bias,
                       float* Y, int64_t ldy, int M, int N, int K, float* am_val, int* am_idx,
                       hipStream_t stream) {
+  if (p.tr == 128 && bias == nullptr && N % 4 == 0 && ldy % 4 == 0 &&
+      ((uintptr_t)Y % 16) == 0 && (int64_t)M * ldy * 4 < ((int64_t)1 << 31)) {
+    const int grid = p.tiles < kLmCUs ? p.tiles : kLmCUs;
+    const size_t lds = (size_t)kLmStages * (128 + 16 * MB) * 256 + 4 * 16 * MB * 8;
+    hipLaunchKernelGGL((lm_head_argmax_kernel<T, MB>), dim3((unsigned)grid), dim3(256), lds,
+                       stream, X, ldx, Wp, Y, ldy, M, N, K, p.tiles, am_val, am_idx);
+    return;
+  }
   const dim3 grid((unsigned)p.tiles, 1u);
   const size_t lds = (size_t)p.nst * (p.tr + 16 * MB) * 256;
   I8Epi e{};
