@@ -460,8 +460,10 @@ int ll_gemm_packed_f32(const void* X, int64_t ldx, const void* Wp, const void* b
  * fp32 logits, tokens[m] = the first index of row m's maximum, exactly as
  * ll_argmax on Y (-1 in every row while *status is nonzero, as
  * ll_argmax_status; status may be NULL). For one-split plans the first argmax
- * pass runs in the GEMM's epilogue (per-tile maxima), otherwise the GEMM and
- * ll_argmax run one after the other. Workspace:
+ * pass runs in the GEMM's epilogue (per-tile maxima; with 128-row tiles, no
+ * bias and N, ldy multiples of 4, the GEMM is a persistent grid of at most
+ * one workgroup per CU), otherwise the GEMM and ll_argmax run one after the
+ * other. Workspace:
  * ll_gemm_packed_f32_argmax_workspace_size(M, N, K) bytes. */
 int64_t ll_gemm_packed_f32_argmax_workspace_size(int64_t M, int64_t N, int64_t K);
 int ll_gemm_packed_f32_argmax(const void* X, int64_t ldx, const void* Wp, const void* bias,
