@@ -393,7 +393,12 @@ int ll_rope_kv_scatter_splitk(const float* part, int splits, const void* bias, v
  * req_to_tokens[b_req_idx[b], b_seq_len[b] - 1] and appears in no other
  * sequence's first b_seq_len entries (what a decode step guarantees).
  * bf16/fp16, head_dim 64 or 128, q_heads/kv_heads <= 16, fp32 cos/sin tables;
- * other shapes use the two calls. workspace: ll_decode_attention_workspace_size. */
+ * other shapes use the two calls. workspace: ll_decode_attention_workspace_size.
+ * The same-launch split merge waits for the other splits' partials with a
+ * bound (the decode step's spin setting, ll_decode_sync_set_spin_limit; its
+ * test mode makes every such wait give up). A merge that gives up stores NaN
+ * rows and sets *error_word to 1 (error_word may be NULL), the decode step's
+ * error word (ll_decode_sync_error_offset), as the fused norm launch does. */
 int ll_decode_attention_rope_splitk(
     const float* qkv_part, int qkv_splits, const void* qkv_bias, const void* positions,
     int positions_i64, const void* cos_table, const void* sin_table, int64_t table_row_stride,
@@ -403,7 +408,7 @@ int ll_decode_attention_rope_splitk(
     int req_idx_i64, const void* b_seq_len, int seq_len_i64, void* out, int64_t out_stride_b,
     int64_t out_stride_h, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
     int64_t max_len_in_batch, float sm_scale, int dtype, void* workspace,
-    int64_t workspace_bytes, hipStream_t stream);
+    int64_t workspace_bytes, uint32_t* error_word, hipStream_t stream);
 /* The same with the W8A8 projection's int32 partials
  * [qkv_splits][batch][(q_heads + 2*kv_heads)*head_dim] and their scales in
  * place of fp32 partials: each column is dequantised as in ll_dequant_splitk
@@ -423,7 +428,7 @@ int ll_decode_attention_rope_splitk_i32(
     int seq_len_i64, void* out, int64_t out_stride_b, int64_t out_stride_h, int64_t batch,
     int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t max_len_in_batch,
     float sm_scale, int dtype, void* workspace, int64_t workspace_bytes, const float* q_static,
-    int8_t* q_out, int64_t ldq, float* q_scale, hipStream_t stream);
+    int8_t* q_out, int64_t ldq, float* q_scale, uint32_t* error_word, hipStream_t stream);
 
 /* Pre-packed weights for the decode projections (no reference counterpart:
  * a layout of the same nn.Linear weight [N, K], chosen for MI355X). The

@@ -97,11 +97,11 @@ SIGNATURES = {
     "ll_decode_sync_status": (I32, [P, I32, P]),
     "ll_decode_attention_rope_splitk": (I32, [P, I32, P, P, I32, P, P, I64, I32, P, P, I64, I64,
                                               P, I64, I64, P, I64, P, I32, P, I32, P, I64, I64,
-                                              I64, I64, I64, I64, I64, F32, I32, P, I64, P]),
+                                              I64, I64, I64, I64, I64, F32, I32, P, I64, P, P]),
     "ll_decode_attention_rope_splitk_i32": (I32, [P, I32, P, P, I32, P, P, I32, P, P, I64, I32, P,
                                                   P, I64, I64, P, I64, I64, P, I64, P, I32, P,
                                                   I32, P, I64, I64, I64, I64, I64, I64, I64, F32,
-                                                  I32, P, I64, P, P, I64, P, P]),
+                                                  I32, P, I64, P, P, I64, P, P, P]),
     "ll_add_rmsnorm_splitk_i32": (I32, [P, I64, P, I32, P, P, I32, P, P, I64, I64, I64, F32, I32,
                                         P, I64, P, P]),
     "ll_silu_and_mul_splitk_i32": (I32, [P, I32, P, P, I32, P, I64, I64, I64, I32, P]),

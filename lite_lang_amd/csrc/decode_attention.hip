@@ -44,8 +44,8 @@ constexpr int kWaves = 8;   // waves per split-stage workgroup
 constexpr int kCombWaves = 4;  // waves (one (sequence, head) each) per combine workgroup
 constexpr int kRing = 2;    // tile buffers per wave
 constexpr int kUnitMergeSplits = 8;  // splits the per-unit merge holds in registers
-constexpr int kUnitMergeSpin = 1 << 20;  // polls before the per-unit merge gives up (never
-                                         // reached: the words are already on their way)
+constexpr int kUnitMergeSpin = 1 << 20;  // default polls before the per-unit merge gives up
+                                         // (never reached: the words are already on their way)
 
 template <typename T> struct Vec8;
 template <> struct Vec8<__bf16> { typedef bf16x8 type; };
@@ -110,6 +110,9 @@ struct DecodeArgs {
   float* part_acc;    // [B*H*nsplit, D] unnormalised partial outputs
   float* part_ml;     // [B*H*nsplit, 2] running max (log2 domain) and sum
   unsigned* merge_cnt;  // [units] split tickets (zero between calls), or null: separate combine
+  int unit_spin;        // polls before the per-unit merge gives up (0: kUnitMergeSpin)
+  int unit_never;       // test mode: the per-unit merge never sees its words (gives up)
+  uint32_t* err;        // set to 1 when the per-unit merge gives up, or null
   // fused RoPE + new-token K/V write (ROPE kernels only)
   LLPartials qkv;          // [splits][B][(H + 2 KVH) * D] split-K partials (fp32, or int32 + scales)
   const void* qkv_bias;    // [(H + 2 KVH) * D] of the model dtype, or null
@@ -314,7 +317,9 @@ template <int D> struct TileGeom {
 // written. All splits of a unit run on one XCD (map_block), whose L2 the
 // polls read; each poll issues every load before looking at any, and the
 // first one is in flight while own_merge runs. The wait is bounded
-// (kUnitMergeSpin polls; the rows then come out NaN). The merge is
+// (a.unit_spin polls; the rows then come out NaN and *a.err, when given, is
+// set to 1, as the decode step's fused launches report a wait that gave up).
+// The merge is
 // combine_bh's arithmetic, splits in order, so both merges give the same
 // bits. The merged rows are zeroed for the next call.
 template <typename T, int D, int NO, typename OwnMerge>
@@ -356,8 +361,8 @@ __device__ __forceinline__ void unit_merge_tail(const DecodeArgs& a, bool item, 
                          u[s][4] != 0u && u[s][5] != 0u;
         ready = ready && (s >= no || all);
       }
-      if (ready) break;
-      if (it >= kUnitMergeSpin) {
+      if (ready && a.unit_never == 0) break;
+      if (it >= a.unit_spin) {
         gave_up = true;
         break;
       }
@@ -389,6 +394,8 @@ __device__ __forceinline__ void unit_merge_tail(const DecodeArgs& a, bool item, 
 #pragma unroll
     for (int q = 0; q < 4; ++q)
       op[q] = ll_from_f32<T>(gave_up ? __builtin_nanf("") : (Lx > 0.f ? Ax[q] / Lx : 0.f));
+    if (gave_up && a.err != nullptr)
+      __hip_atomic_store(a.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     for (int s = 0; s < no; ++s)
       *(f32x4*)&a.part_acc[(p0 + s) * D + d0] = (f32x4){0.f, 0.f, 0.f, 0.f};
   }
@@ -1075,6 +1082,7 @@ int64_t workspace_bytes_for(int64_t batch, int64_t q_heads, int64_t kv_heads, in
 int launch_mfma(DecodeArgs& a, int64_t head_dim, int dtype, bool rope, int64_t max_len,
                 void* workspace, int64_t workspace_bytes, hipStream_t stream) {
   a.nsplit = choose_nsplit(a.B, a.KVH, max_len, head_dim);
+  if (a.unit_spin <= 0) a.unit_spin = kUnitMergeSpin;
   if (a.nsplit > 1) {
     const int64_t need = workspace_bytes_for(a.B, a.H, a.KVH, head_dim, max_len);
     LL_CHECK_ARG(workspace != nullptr && workspace_bytes >= need,
@@ -1334,7 +1342,8 @@ int rope_attention_impl(const LLPartials& qkv, const void* qkv_bias, const void*
                         int64_t out_stride_h, int64_t batch, int64_t q_heads, int64_t kv_heads,
                         int64_t head_dim, int64_t max_len_in_batch, float sm_scale, int dtype,
                         void* workspace, int64_t workspace_bytes, const float* q_static,
-                        int8_t* q_out, int64_t ldq, float* q_scale, hipStream_t stream) {
+                        int8_t* q_out, int64_t ldq, float* q_scale, uint32_t* error_word,
+                        hipStream_t stream) {
   LL_CHECK_ARG((q_out == nullptr) == (q_scale == nullptr) &&
                    (q_out == nullptr || (out_stride_h == head_dim && ldq >= q_heads * head_dim)),
                "ll_decode_attention_rope_splitk: q_out needs q_scale, contiguous output rows "
@@ -1377,6 +1386,12 @@ int rope_attention_impl(const LLPartials& qkv, const void* qkv_bias, const void*
   a.tab_stride = table_row_stride;
   a.new_slots = new_slots;
   a.qout = q_out; a.ldq = ldq; a.qscale = q_scale; a.qstatic = q_static;
+  // the split merge's wait follows the decode step's spin setting and
+  // reports a give-up in the step's error word
+  const int spin = ll_decode_spin_setting();
+  a.unit_spin = spin < 0 ? -spin : spin;
+  a.unit_never = spin < 0 ? 1 : 0;
+  a.err = error_word;
   return launch_mfma(a, head_dim, dtype, true, max_len_in_batch, workspace, workspace_bytes,
                      stream);
 }
@@ -1392,14 +1407,15 @@ extern "C" int ll_decode_attention_rope_splitk(
     int req_idx_i64, const void* b_seq_len, int seq_len_i64, void* out, int64_t out_stride_b,
     int64_t out_stride_h, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
     int64_t max_len_in_batch, float sm_scale, int dtype, void* workspace,
-    int64_t workspace_bytes, hipStream_t stream) {
+    int64_t workspace_bytes, uint32_t* error_word, hipStream_t stream) {
   return rope_attention_impl(ll_partials_f32(qkv_part, qkv_splits, 0), qkv_bias, positions,
                              positions_i64, cos_table, sin_table, table_row_stride, cs_dtype,
                              new_slots, k_cache, k_stride_tok, k_stride_head, v_cache, v_stride_tok,
                              v_stride_head, req_to_tokens, req_to_tokens_stride, b_req_idx,
                              req_idx_i64, b_seq_len, seq_len_i64, out, out_stride_b, out_stride_h,
                              batch, q_heads, kv_heads, head_dim, max_len_in_batch, sm_scale, dtype,
-                             workspace, workspace_bytes, nullptr, nullptr, 0, nullptr, stream);
+                             workspace, workspace_bytes, nullptr, nullptr, 0, nullptr, error_word,
+                             stream);
 }
 
 extern "C" int ll_decode_attention_rope_splitk_i32(
@@ -1412,7 +1428,7 @@ extern "C" int ll_decode_attention_rope_splitk_i32(
     int seq_len_i64, void* out, int64_t out_stride_b, int64_t out_stride_h, int64_t batch,
     int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t max_len_in_batch,
     float sm_scale, int dtype, void* workspace, int64_t workspace_bytes, const float* q_static,
-    int8_t* q_out, int64_t ldq, float* q_scale, hipStream_t stream) {
+    int8_t* q_out, int64_t ldq, float* q_scale, uint32_t* error_word, hipStream_t stream) {
   LL_CHECK_ARG(s_tok && s_ch, "ll_decode_attention_rope_splitk_i32: null scale pointer");
   LL_CHECK_ARG(s_ch_dtype == LL_F32 || s_ch_dtype == LL_F16 || s_ch_dtype == LL_BF16,
                "ll_decode_attention_rope_splitk_i32: bad scale dtype %d", s_ch_dtype);
@@ -1425,5 +1441,5 @@ extern "C" int ll_decode_attention_rope_splitk_i32(
                              req_to_tokens_stride, b_req_idx, req_idx_i64, b_seq_len, seq_len_i64,
                              out, out_stride_b, out_stride_h, batch, q_heads, kv_heads, head_dim,
                              max_len_in_batch, sm_scale, dtype, workspace, workspace_bytes,
-                             q_static, q_out, ldq, q_scale, stream);
+                             q_static, q_out, ldq, q_scale, error_word, stream);
 }

@@ -381,8 +381,11 @@ SplitPlan split_plan(int64_t M, int64_t N, int64_t K) {
 // polls, so a test sees every wait give up while every kernel still exits
 // normally. 0 restores the default.
 std::atomic<int> g_spin_max{kSpinMax};
+std::atomic<int> g_spin_user{0};  // the setting as given (0: defaults)
 
 }  // namespace
+
+int ll_decode_spin_setting() { return g_spin_user.load(); }
 
 extern "C" int64_t ll_decode_sync_bytes(void) { return kSyncBytes; }
 
@@ -391,6 +394,7 @@ extern "C" int64_t ll_decode_sync_error_offset(void) { return (int64_t)kSyncErr 
 extern "C" int ll_decode_sync_set_spin_limit(int polls) {
   LL_CHECK_ARG(polls > -(1 << 20), "ll_decode_sync_set_spin_limit: bound out of range");
   g_spin_max.store(polls == 0 ? kSpinMax : polls);
+  g_spin_user.store(polls);
   return LL_OK;
 }
 

@@ -51,6 +51,10 @@ enum { LL_F32 = LL_DTYPE_F32, LL_F16 = LL_DTYPE_F16, LL_BF16 = LL_DTYPE_BF16 };
 
 // Per-thread last-error text, returned by ll_last_error().
 void ll_set_error(const char* fmt, ...);
+// The host's spin setting for the decode step's bounded waits
+// (ll_decode_sync_set_spin_limit: 0 = each wait's default, n > 0 = n polls,
+// -n = test mode: the wait never sees its data and gives up after n polls).
+int ll_decode_spin_setting();
 
 // Second pass of the first-index argmax over per-row partials [M][nparts]
 // written by another kernel (elementwise.hip).

@@ -50,10 +50,10 @@ def reserve_model_workspaces(model, batch, max_len):
     reserve_decode_workspaces(model.cfg, batch, max_len, model.device)
     if model.fused_decode_ok(batch):
         ops.reserve_workspace(model.device, "splitk_part", model.splitk_part_numel(batch) * 4)
+        ops.decode_sync(model.device)  # the error word of the fused launches' bounded waits
         if model.quant == "w8a8":
             ops.reserve_workspace(model.device, "w8a8_part", model.w8a8_part_bytes(batch))
         if model.norm_qkv_splits(batch) > 0:
-            ops.decode_sync(model.device)
             ops.reserve_workspace(model.device, "decode_epoch", 4)
 
 

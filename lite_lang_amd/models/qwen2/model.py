@@ -275,9 +275,10 @@ class Qwen2Model:
                 x = ops.add_rmsnorm_splitk(h, part, s, w.layers[li + 1]["ln1"], cfg.rms_norm_eps)
             else:
                 x = ops.add_rmsnorm_splitk(h, part, s, w.norm, cfg.final_norm_eps)
-        # a fused launch that gave up a flag wait turns every token into -1
+        # a fused launch that gave up a bounded wait (a flag wait of the norm +
+        # QKV launch, the attention's split merge) turns every token into -1
         # (the host raises on it, runner_batch.check_step_tokens)
-        return self._logits_argmax(x, out, ops.decode_sync_error(dev) if fuse_qkv else None)
+        return self._logits_argmax(x, out, ops.decode_sync_error(dev))
 
     def _decode_w8a8(self, h, B, part, q, attn, act, positions, seq_len, rids, slots, pool, r2t,
                      max_len, out):
@@ -452,12 +453,16 @@ class Qwen2ModelRunner:
 
     def reset_decode_fault(self):
         """Clear the error word a fused decode launch sets when it gives up a
-        flag wait (on the decode graphs' stream and on the current stream);
-        until then every decode step returns token ids of -1."""
+        bounded wait (on the decode graphs' stream and on the current stream);
+        until then every decode step returns token ids of -1. The decode
+        attention's workspace is zeroed too: a split merge that gave up may
+        have left partial words that the next merge would take as written."""
         from .decode_graph import _capture_stream
         with torch.cuda.stream(_capture_stream(self.device_)):
             ops.decode_sync_status(self.device_, reset=True)
+            ops.clear_workspace(self.device_, "decode_attention")
         ops.decode_sync_status(self.device_, reset=True)
+        ops.clear_workspace(self.device_, "decode_attention")
 
     def _alloc_for_forward(self, model_inputs):
         """Slot allocation done by layer 0 in the reference (transformer_layer.py:53-60)."""

@@ -82,6 +82,13 @@ def reserve_workspace(device: torch.device, name: str, nbytes: int) -> None:
     workspace(device, name, nbytes)
 
 
+def clear_workspace(device: torch.device, name: str) -> None:
+    """Zero the current stream's workspace `name`, if it exists."""
+    buf = _WS.get(_ws_key(device, name))
+    if buf is not None:
+        buf.zero_()
+
+
 # ------------------------------------------------------------------ attention
 def decode_attention(q, req_to_tokens, b_req_idx, b_seq_len, max_len_in_batch, cache_k, cache_v,
                      out, sm_scale=None):
@@ -733,7 +740,8 @@ def decode_attention_rope_splitk(part, splits, bias, positions, cos_table, sin_t
     """rope_kv_scatter_splitk + decode_attention in one launch: q is rebuilt
     from the QKV split-K partials inside the attention kernel and the new
     token's K/V are written to cache_k/cache_v[slots[b]] by the workgroup that
-    attends over that token."""
+    attends over that token. A split merge that gives up its bounded wait
+    sets the current stream's decode error word (decode_sync_error)."""
     _dev(part, positions, cos_table, sin_table, slots, req_to_tokens, b_req_idx, b_seq_len,
          cache_k, cache_v, out)
     B, H, D = out.shape
@@ -757,7 +765,7 @@ def decode_attention_rope_splitk(part, splits, bias, positions, cos_table, sin_t
         b_seq_len.data_ptr(), _idx(b_seq_len, "b_seq_len"),
         out.data_ptr(), out.stride(0), out.stride(1),
         B, H, KVH, D, max_len, float(sm_scale), dtype_code(out), ws.data_ptr(), ws.numel(),
-        _stream(out))
+        decode_sync_error(out.device).data_ptr(), _stream(out))
     _lib.check(rc, "ll_decode_attention_rope_splitk")
     return out
 
@@ -797,7 +805,8 @@ def decode_attention_rope_splitk_i32(p, bias, positions, cos_table, sin_table, s
         out.data_ptr(), out.stride(0), out.stride(1),
         B, H, KVH, D, max_len, float(sm_scale), dtype_code(out), ws.data_ptr(), ws.numel(),
         input_scale.data_ptr() if input_scale is not None else None,
-        q.data_ptr() if quant else None, H * D, s.data_ptr() if quant else None, _stream(out))
+        q.data_ptr() if quant else None, H * D, s.data_ptr() if quant else None,
+        decode_sync_error(out.device).data_ptr(), _stream(out))
     _lib.check(rc, "ll_decode_attention_rope_splitk_i32")
     return (out, q, s) if quant else out
 

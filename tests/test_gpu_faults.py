@@ -1,7 +1,8 @@
 """Failure handling of the decode step, forced from the host.
 
 The fused add + RMSNorm + QKV launch waits on flags with a bounded number of
-polls. A wait that gives up sets the step's error word; the step's argmax
+polls, and the fused attention's same-launch split merge waits for the other
+splits' partials the same way. A wait that gives up sets the step's error word; the step's argmax
 then writes token id -1 for every request (ll_argmax_status), and the host
 raises DecodeStepError as soon as it reads such a step's tokens, instead of
 handing invalid tokens to the requests. The conditions are forced from the
@@ -172,6 +173,44 @@ def test_scheduler_client_raises_on_invalid_step(cuda):
     with pytest.raises(DecodeStepError):
         client.decode("c")
     runner.reset_decode_fault()
+
+
+def test_attention_merge_give_up_sets_error_word(cuda):
+    """The fused decode attention's same-launch split merge waits for the
+    other splits' partial words with a bound. In the spin limit's test mode
+    (the merge never takes the words as written, 64 polls) every merge gives
+    up: its rows come out NaN, the decode error word is set, and every kernel
+    exits; the new token's K/V still reach the pool. After the word is reset
+    and the attention workspace cleared (what Qwen2ModelRunner.reset_decode_fault
+    does), the same call gives the default call's output bit for bit and
+    leaves the workspace at zero."""
+    from lite_lang_amd import _lib
+    from tests.test_gpu_decode_rope_fused import _case, _fused
+    ops = _ops()
+    B, H, KVH, D, S, dt = 40, 16, 2, 128, 4, torch.bfloat16
+    d, pool, max_len, _ = _case(cuda, B, H, KVH, D, [600] * B, S, dt, seed=12)
+    assert 2 <= _lib.load().ll_decode_attention_split_count(B, KVH, D, max_len) <= 8
+    print("case: attention merge gives up 40x16/2x128 len 600", flush=True)
+    ops.decode_sync_status(cuda, reset=True)
+    want, pool_want = _fused(cuda, d, pool, B, H, KVH, D, S, max_len, dt)
+    torch.cuda.synchronize()
+    assert ops.decode_sync_status(cuda) == 0
+    ops.set_decode_spin_limit(-64)
+    try:
+        got, pool_got = _fused(cuda, d, pool, B, H, KVH, D, S, max_len, dt)
+        torch.cuda.synchronize()
+    finally:
+        ops.set_decode_spin_limit(0)
+    assert ops.decode_sync_status(cuda) == 1
+    assert torch.isnan(got.float()).all()
+    assert torch.equal(pool_got, pool_want)
+    ops.decode_sync_status(cuda, reset=True)
+    ops.clear_workspace(cuda, "decode_attention")
+    again, _ = _fused(cuda, d, pool, B, H, KVH, D, S, max_len, dt)
+    torch.cuda.synchronize()
+    assert torch.equal(again, want)
+    assert ops.decode_sync_status(cuda) == 0
+    assert ops.workspace(cuda, "decode_attention", 0).count_nonzero() == 0
 
 
 @pytest.mark.parametrize("shape", [(40, 12, 2, 128, [600] * 40), (7, 16, 2, 64, None)])
