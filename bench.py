@@ -157,6 +157,35 @@ def bench_attention_floor(dev, iters=200, pools=28, L=600):
     return res
 
 
+def bench_launch_floor(dev, iters=100):
+    """What a launch costs by itself inside a HIP graph (the decode step is
+    221 of them): back-to-back launches of an empty 512-thread kernel at
+    several grid sizes, and of the same kernel writing 64 KB .. 16 MB with
+    16-byte stores (240 workgroups, the decode attention's grid), timed as
+    the attention is (graph replay, events). The buffer a launch writes is
+    its own (the writes are cold in the L2)."""
+    from lite_lang_amd import _lib
+    Lb = _lib.load()
+    stream = lambda: torch.cuda.current_stream(dev).cuda_stream
+    buf = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+    res = {"launches_per_graph": iters, "threads_per_workgroup": 512}
+    empty = {}
+    for wgs in (1, 240, 256, 1024):
+        def launch(i, wgs=wgs):
+            _lib.check(Lb.ll_probe_launch(None, 0, wgs, stream()), "ll_probe_launch")
+        empty[str(wgs)] = round(_graph_time(dev, launch, iters) * 1e6, 3)
+    res["empty_us"] = empty
+    writes = {}
+    for kb in (64, 256, 1024, 4096, 16384):
+        def launch(i, kb=kb):
+            off = (i % 2) * (32 << 20)
+            _lib.check(Lb.ll_probe_launch(buf.data_ptr() + off, kb * 1024, 240, stream()),
+                       "ll_probe_launch")
+        writes[str(kb)] = round(_graph_time(dev, launch, iters) * 1e6, 3)
+    res["write_kb_us"] = writes
+    return res
+
+
 # ------------------------------------------------------------------ model
 def build_runner(dev, cfg, max_length, seed=0):
     from lite_lang_amd.models.qwen2 import Qwen2ModelRunner
@@ -497,6 +526,9 @@ def main():
     ap.add_argument("--attention-floor", action="store_true",
                     help="time the config-2 decode attention beside a plain read and a slot-table "
                          "gather of the same K/V bytes (in-tree probe kernels), one JSON line")
+    ap.add_argument("--launch-floor", action="store_true",
+                    help="time graph-replayed launches of an empty kernel and of kernels that "
+                         "write 64 KB .. 16 MB (in-tree probe kernel), one JSON line")
     ap.add_argument("--norm-qkv", action="store_true",
                     help="run only the fused add + RMSNorm + QKV launch of the 3B decode step "
                          "plus a 256 MiB device copy of known size (for rocprofv3 runs)")
@@ -531,6 +563,9 @@ def main():
         return
     if args.attention_floor:
         print(json.dumps(bench_attention_floor(dev)), flush=True)
+        return
+    if args.launch_floor:
+        print(json.dumps(bench_launch_floor(dev)), flush=True)
         return
     if args.prefill_gemm:
         print(json.dumps(bench_prefill_gemms(dev)), flush=True)

@@ -548,7 +548,8 @@ int ll_dequant_splitk(const int32_t* part, int splits, const float* s_tok, const
                       int s_ch_dtype, float* out, int64_t M, int64_t N, hipStream_t stream);
 
 /* ---- Measurement probes (no counterpart in the reference; bench.py
- * --attention-floor times them against the decode attention).
+ * --attention-floor times the first two against the decode attention,
+ * bench.py --launch-floor the third).
  * ll_probe_stream_read: a plain streaming read of `bytes` contiguous bytes
  * (16 B aligned) by `workgroups` workgroups of 256 threads.
  * ll_probe_kv_gather: the K/V rows ll_decode_attention reads, through the
@@ -565,6 +566,9 @@ int ll_probe_kv_gather(const void* k_cache, int64_t k_stride_tok, int64_t k_stri
                        int seq_len_i64, int64_t batch, int64_t kv_heads, int64_t head_dim,
                        int64_t elem_bytes, int64_t max_len_in_batch, int64_t nsplit, int mode,
                        uint32_t* sink, hipStream_t stream);
+/* ll_probe_launch: `workgroups` workgroups of 512 threads that write
+ * write_bytes (16 B aligned; 0: an empty kernel) to dst with 16-byte stores. */
+int ll_probe_launch(void* dst, int64_t write_bytes, int64_t workgroups, hipStream_t stream);
 /* The split count ll_decode_attention uses for this shape (1: no split). */
 int ll_decode_attention_split_count(int64_t batch, int64_t kv_heads, int64_t head_dim,
                                     int64_t max_len_in_batch);

@@ -111,6 +111,7 @@ SIGNATURES = {
     "ll_probe_kv_gather": (I32, [P, I64, I64, P, I64, I64, P, I64, P, I32, P, I32, I64, I64, I64,
                                  I64, I64, I64, I32, P, P]),
     "ll_decode_attention_split_count": (I32, [I64, I64, I64, I64]),
+    "ll_probe_launch": (I32, [P, I64, I64, P]),
 }
 
 

@@ -14,6 +14,11 @@
 // LDS (global_load_lds_dwordx4, as the attention does). The rows are folded
 // into one word that is stored only if it equals a value no input produces,
 // so no load can be dropped.
+//
+// ll_probe_launch: what a launch costs by itself inside a HIP graph: a grid
+// of 512-thread workgroups that does nothing, or writes `write_bytes` with
+// 16-byte stores spread over the workgroups (the dirty bytes the launch
+// leaves in the L2 for the boundary to write back).
 #include "ll_common.h"
 
 namespace {
@@ -33,6 +38,12 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const u32x4* __restric
   for (; i < n16; i += stride) acc ^= src[i];
   const uint32_t x = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
   if (x == 0x9e3779b9u) sink[0] = x;
+}
+
+__global__ __launch_bounds__(512) void launch_probe_kernel(u32x4* __restrict__ dst, int64_t n16) {
+  const int64_t stride = (int64_t)gridDim.x * 512;
+  for (int64_t i = (int64_t)blockIdx.x * 512 + threadIdx.x; i < n16; i += stride)
+    dst[i] = (u32x4){(uint32_t)i, 1u, 2u, 3u};
 }
 
 __device__ __forceinline__ void dma16(const void* g, void* lds) {
@@ -146,5 +157,16 @@ extern "C" int ll_probe_kv_gather(const void* k_cache, int64_t k_stride_tok, int
     hipLaunchKernelGGL(kv_gather_kernel<0>, dim3(grid), dim3(kProbeWaves * 64), 0, stream, a);
   else
     hipLaunchKernelGGL(kv_gather_kernel<1>, dim3(grid), dim3(kProbeWaves * 64), lds, stream, a);
+  LL_RETURN_LAUNCH();
+}
+
+extern "C" int ll_probe_launch(void* dst, int64_t write_bytes, int64_t workgroups,
+                               hipStream_t stream) {
+  LL_CHECK_ARG(write_bytes >= 0 && write_bytes % 16 == 0 && ((uintptr_t)dst % 16) == 0 &&
+                   (write_bytes == 0 || dst != nullptr),
+               "ll_probe_launch: needs a 16-byte aligned buffer of 16-byte units");
+  LL_CHECK_ARG(workgroups > 0 && workgroups <= (1 << 20), "ll_probe_launch: bad grid");
+  hipLaunchKernelGGL(launch_probe_kernel, dim3((unsigned)workgroups), dim3(512), 0, stream,
+                     (u32x4*)dst, write_bytes / 16);
   LL_RETURN_LAUNCH();
 }
