@@ -44,7 +44,7 @@ B, PROMPT = 40, 600
 # rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of `bench.py --attention-only`,
 # scaled by what the counters read for a 256 MiB copy (fetch x2.0, write x1.0).
 # Measured on the current kernels; re-measure when they change.
-ATTN_TRAFFIC_BYTES = 26185087
+ATTN_TRAFFIC_BYTES = 25655985
 
 
 def log(msg):
@@ -67,12 +67,17 @@ def _config2_inputs(dev, pools, L, identity=False):
 
 def _graph_time(dev, launch, iters, reps=5):
     """Average seconds per launch of `iters` back-to-back launches replayed
-    from one HIP graph (events recorded on the replaying stream)."""
-    for i in range(min(iters, 32)):
-        launch(i)  # first use outside the capture (sizes workspaces)
+    from one HIP graph (events recorded on the replaying stream). The
+    launches are warmed up on the stream they are captured on, so the
+    library's per-stream workspaces are sized before the capture."""
+    cap = torch.cuda.Stream(dev)
+    cap.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(cap):
+        for i in range(min(iters, 32)):
+            launch(i)  # first use outside the capture (sizes workspaces)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+    with torch.cuda.graph(graph, stream=cap):
         for i in range(iters):
             launch(i)
     graph.replay()

@@ -994,13 +994,15 @@ __global__ __launch_bounds__(64) void decode_attn_generic_kernel(DecodeArgs a, i
 }
 
 constexpr int kMaxSplitTokens = 4096;  // LDS slot table bound per split (16 KB)
+constexpr int kSplitCostTiles2 = 13;    // twice the cost of one more split, in 16-token tiles
+constexpr int kMaxSplitsFill = 16;      // split bound from 8 units up (head_dim 128)
 
 int choose_nsplit(int B, int KVH, int64_t max_len, int64_t head_dim) {
   const int units = B * KVH;
   const int64_t tiles = (max_len + kTT - 1) / kTT;
-  // Fill one dispatch round of the 256 CUs, never more (as many split-stage
+  // At most one dispatch round of the 256 CUs (as many split-stage
   // workgroups per CU as their LDS allows: one at head_dim 128, two at 64),
-  // while giving every wave at least one tile and bounding the slot table.
+  // every wave at least one tile, the slot table bounded.
   // Measured at 40 sequences x 2 KV heads: one workgroup of 8 waves per CU
   // beats two of 4 waves from 600 tokens up (fewer splits to merge, the same
   // bytes in flight per CU).
@@ -1012,6 +1014,31 @@ int choose_nsplit(int B, int KVH, int64_t max_len, int64_t head_dim) {
   const int64_t min_ns = (tiles * kTT + kMaxSplitTokens - 1) / kMaxSplitTokens;
   if (ns < min_ns) ns = (int)min_ns;
   if (ns < 1) ns = 1;
+  // head_dim 128, from a sweep of split counts (16 or 12 query heads per 2
+  // KV heads, 4-64 sequences, 300-8000 tokens):
+  // * at most 16 splits from 8 units up: the merging workgroup reads every
+  //   split's partial rows (4 x 8000 tokens: 32 splits 27.2 us, 16 16.1);
+  // * from 64 units up (one dispatch round holds at most 4 splits), the
+  //   count with the least (tiles of a split) + kSplitCostTiles2 / 2 per
+  //   split: one split more costs about 6.5 tile times there, a workgroup's
+  //   ramp and a longer merge (40 x 600 tokens: 2 splits 10.34 us, 3 10.64;
+  //   40 x 700: 2 splits 11.54, 3 11.26; 32 x 600: 2 splits 10.02, 4 10.28).
+  //   With fewer units the CUs left idle by fewer splits cost more than the
+  //   merge, and the count above stands.
+  if (head_dim == 128) {
+    if (units >= 8 && ns > kMaxSplitsFill) ns = min_ns > kMaxSplitsFill ? (int)min_ns : kMaxSplitsFill;
+    if (units >= 64) {
+      int64_t best = -1;
+      const int lo = min_ns > 1 ? (int)min_ns : 1;
+      for (int s = lo, hi = ns; s <= hi; ++s) {
+        const int64_t c = 2 * ((tiles + s - 1) / s) + kSplitCostTiles2 * s;
+        if (best < 0 || c < best) {
+          best = c;
+          ns = s;
+        }
+      }
+    }
+  }
   return ns;
 }
 
