@@ -79,6 +79,22 @@ def test_decode_attention_config2_varlen(cuda):
     assert _maxdiff(out, ref) <= BF16_ATOL
 
 
+@pytest.mark.parametrize("B,L,splits", [(4, 8000, 16), (7, 3000, 16), (32, 600, 2), (40, 656, 3)])
+def test_decode_attention_split_counts(cuda, B, L, splits):
+    """Shapes on either side of the split-count rule (head_dim 128): at most
+    16 splits from 8 (sequence, KV head) units up (4 x 8000 tokens would
+    fill a dispatch round with 32, 7 x 3000 with 18; more than 8 splits merge
+    by ticket), and from 64 units up the count the cost fit picks (2 splits
+    at 32 x 600, 3 at 40 x 656). Each against the oracle."""
+    from lite_lang_amd import _lib
+    assert _lib.load().ll_decode_attention_split_count(B, 2, 128, L) == splits
+    lens = [L] * B
+    lens[0] = L - 5  # one shorter row: its last split holds fewer tiles
+    print(f"case: decode split count B={B} L={L} splits={splits}", flush=True)
+    out, ref = _decode_case(cuda, B, 16, 2, 128, lens, torch.bfloat16, 7)
+    assert _maxdiff(out, ref) <= BF16_ATOL
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("H,KVH,D", [(16, 2, 128), (8, 8, 64), (4, 2, 64), (6, 1, 128)])
 def test_decode_attention_shapes(cuda, dtype, H, KVH, D):
