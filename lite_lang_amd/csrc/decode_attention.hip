@@ -413,8 +413,15 @@ __device__ __forceinline__ void unit_merge_tail(const DecodeArgs& a, bool item, 
 // sequence's new slot appears in no other sequence's first seq_len entries
 // and in its own only within the last split (the decode step puts it at
 // seq_len - 1).
+// The split stage, for both kernels below. p_len .. idx64 are the fields of
+// the first loads (lengths, request rows, positions, new slots, the grid
+// geometry); idx64: bit 0 lengths, bit 1 request rows, bit 2 positions are
+// int64.
 template <typename T, int D, int MODE>
-__global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs a) {
+__device__ __forceinline__ void decode_attn_split_stage(
+    const int32_t* __restrict__ p_len, const int32_t* __restrict__ p_rid,
+    const int32_t* __restrict__ p_pos, const int32_t* __restrict__ p_nslot, int KVH, int nsplit,
+    int B, int idx64, const DecodeArgs& a) {
   typedef typename Vec8<T>::type V8;
   typedef typename Vec4<T>::type V4;
   typedef TileGeom<D> TG;
@@ -425,9 +432,20 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
   int32_t* s_slots = (int32_t*)(smem + TG::MAIN_B);
 
   int b, kvh, split;
-  map_block(blockIdx.x, a.KVH, a.nsplit, b, kvh, split);
-  if (b >= a.B) return;
-  const int unit = b * a.KVH + kvh;
+  map_block(blockIdx.x, KVH, nsplit, b, kvh, split);
+  if (b >= B) return;
+  const int unit = b * KVH + kvh;
+  // sequence length and request row (and with ROPE the position and the new
+  // slot), all loads in flight together and before anything that reads the
+  // argument block (the low word of an int64 entry is the value: lengths,
+  // rows and positions are below 2^31)
+  const int32_t len32 = p_len[(idx64 & 1) ? 2 * b : b];
+  const int32_t rid32 = p_rid[(idx64 & 2) ? 2 * b : b];
+  int32_t pos32 = 0, new_slot = 0;
+  if constexpr (MODE != 0) {
+    pos32 = p_pos[(idx64 & 4) ? 2 * b : b];
+    new_slot = p_nslot[b];
+  }
   // the wave index as a scalar (threadIdx.x / 64 is the same in every lane
   // of a wave): branches on it are scalar branches
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -448,30 +466,14 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
 #pragma unroll
     for (int s = 0; s < DS; ++s) qb[s] = *(const V8*)(qp + 32 * s + 8 * j);
   }
-  // sequence length and request row (and with ROPE the position and the new
-  // slot), all loads in flight together (the low word of an int64 entry is the
-  // value: lengths, rows and positions are below 2^31). The RoPE jobs come
-  // after the first slot loads are issued, so that the two dependent chains
-  // (length/row -> slots, position -> cos/sin) overlap.
-  // (the pointers and flags first, so that the four data loads go out together)
-  if constexpr (ROPE)
-    asm volatile("" ::"s"(a.seq_len), "s"(a.req_idx), "s"(a.len64), "s"(a.req64), "s"(a.pos),
-                 "s"(a.pos64), "s"(a.new_slots));
-  else
-    asm volatile("" ::"s"(a.seq_len), "s"(a.req_idx), "s"(a.len64), "s"(a.req64));
-  const int32_t len32 = ((const int32_t*)a.seq_len)[a.len64 ? 2 * b : b];
-  const int32_t rid32 = ((const int32_t*)a.req_idx)[a.req64 ? 2 * b : b];
-  int32_t pos32 = 0, new_slot = 0;
-  if constexpr (ROPE) {
-    pos32 = ((const int32_t*)a.pos)[a.pos64 ? 2 * b : b];
-    new_slot = a.new_slots[b];
-  }
-  asm volatile("" ::"s"(len32), "s"(rid32), "s"(pos32), "s"(new_slot));  // keeps the loads here
+  // The RoPE jobs come after the first slot loads are issued, so that the
+  // two dependent chains (length/row -> slots, position -> cos/sin) overlap.
+  asm volatile("" ::"s"(len32), "s"(rid32), "s"(pos32), "s"(new_slot));  // the loads are in
   int64_t len = len32 > a.max_len ? a.max_len : len32;
   const int64_t rid = rid32;
   const int32_t* slot_row = a.r2t + rid * a.r2t_s;
   const int ntiles = (int)((len + kTT - 1) / kTT);
-  const int per = (ntiles + a.nsplit - 1) / a.nsplit;
+  const int per = (ntiles + nsplit - 1) / nsplit;
   const int tb = min(ntiles, split * per);
   const int te = min(ntiles, tb + per);
   const int64_t tok0 = (int64_t)tb * kTT;
@@ -860,6 +862,31 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(DecodeArgs
   for (int i = threadIdx.x; i < a.H * D; i += kWaves * 64) qrow[i] = ll_quant1(row[i], sc);
 }
 
+// Plain attention (q given): the fields of the first loads come as scalar
+// arguments ahead of the DecodeArgs block. gfx950 preloads leading scalar
+// kernel arguments into SGPRs at dispatch, so the length and request-row
+// loads do not wait for the argument block's load (config 2: 10.35 -> 9.95
+// us per op).
+template <typename T, int D>
+__global__ __launch_bounds__(kWaves * 64) void decode_attn_dma_kernel(
+    const int32_t* __restrict__ p_len, const int32_t* __restrict__ p_rid, int KVH, int nsplit,
+    int B, int idx64, DecodeArgs a) {
+  decode_attn_split_stage<T, D, 0>(p_len, p_rid, nullptr, nullptr, KVH, nsplit, B, idx64, a);
+}
+
+// Fused RoPE variants: the argument block only (their q rebuild waits for the
+// positions' round trip either way, and preloaded arguments made the W8A8
+// decode step 7 us slower).
+template <typename T, int D, int MODE>
+__global__ __launch_bounds__(kWaves * 64) void decode_attn_rope_kernel(DecodeArgs a) {
+  asm volatile("" ::"s"(a.seq_len), "s"(a.req_idx), "s"(a.len64), "s"(a.req64), "s"(a.pos),
+               "s"(a.pos64), "s"(a.new_slots));  // the four data loads go out together
+  const int idx64 = (a.len64 ? 1 : 0) | (a.req64 ? 2 : 0) | (a.pos64 ? 4 : 0);
+  decode_attn_split_stage<T, D, MODE>((const int32_t*)a.seq_len, (const int32_t*)a.req_idx,
+                                      (const int32_t*)a.pos, a.new_slots, a.KVH, a.nsplit, a.B,
+                                      idx64, a);
+}
+
 // Separate merge kernels, for the shapes the split stage cannot merge itself
 // (more than kMergeUnits units, or a quantised row larger than the tile
 // rings): one wave per (sequence, head).
@@ -1049,12 +1076,24 @@ int64_t align256(int64_t x) { return ((x + 255) / 256) * 256; }
 template <int D, int MODE>
 void launch_split_stage(const DecodeArgs& a, int dtype, unsigned grid, size_t lds,
                         hipStream_t stream) {
-  if (dtype == LL_BF16)
-    hipLaunchKernelGGL((decode_attn_dma_kernel<__bf16, D, MODE>), dim3(grid), dim3(kWaves * 64),
-                       lds, stream, a);
-  else
-    hipLaunchKernelGGL((decode_attn_dma_kernel<_Float16, D, MODE>), dim3(grid), dim3(kWaves * 64),
-                       lds, stream, a);
+  const int idx64 = (a.len64 ? 1 : 0) | (a.req64 ? 2 : 0) | (a.pos64 ? 4 : 0);
+  const int32_t* p_len = (const int32_t*)a.seq_len;
+  const int32_t* p_rid = (const int32_t*)a.req_idx;
+  if constexpr (MODE == 0) {
+    if (dtype == LL_BF16)
+      hipLaunchKernelGGL((decode_attn_dma_kernel<__bf16, D>), dim3(grid), dim3(kWaves * 64), lds,
+                         stream, p_len, p_rid, a.KVH, a.nsplit, a.B, idx64, a);
+    else
+      hipLaunchKernelGGL((decode_attn_dma_kernel<_Float16, D>), dim3(grid), dim3(kWaves * 64), lds,
+                         stream, p_len, p_rid, a.KVH, a.nsplit, a.B, idx64, a);
+  } else {
+    if (dtype == LL_BF16)
+      hipLaunchKernelGGL((decode_attn_rope_kernel<__bf16, D, MODE>), dim3(grid),
+                         dim3(kWaves * 64), lds, stream, a);
+    else
+      hipLaunchKernelGGL((decode_attn_rope_kernel<_Float16, D, MODE>), dim3(grid),
+                         dim3(kWaves * 64), lds, stream, a);
+  }
 }
 
 template <int D>
