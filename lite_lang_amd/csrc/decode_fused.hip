@@ -240,8 +240,14 @@ constexpr int kMaxItemWgs = 256;  // norm rows + items: one workgroup per CU
 constexpr int kMaxSplits = 8;
 constexpr int kOneWgLds = 84 * 1024;  // > half the CU's LDS: one workgroup per CU
 
+// The norm rows' first loads (epoch, partials, residual, gamma) take their
+// fields from the leading scalar arguments, which gfx950 preloads into SGPRs
+// at dispatch, so they do not wait for the load of the argument block.
 template <typename T, int MB, int MAXP>
-__global__ __launch_bounds__(kThreads) void norm_qkv_kernel(NormQkvArgs a) {
+__global__ __launch_bounds__(kThreads) void norm_qkv_kernel(
+    const float* __restrict__ part, void* __restrict__ h, int64_t ld_h,
+    const void* __restrict__ gamma, const uint32_t* __restrict__ epoch, int M, int splits,
+    int hidden, uint32_t tag, NormQkvArgs a) {
   typedef typename V8Of<T>::type V8;
   constexpr int XR = 16 * MB;           // activation rows per chunk (clamped to M - 1)
   constexpr int XB = XR * kRowB;        // LDS bytes per chunk
@@ -249,10 +255,10 @@ __global__ __launch_bounds__(kThreads) void norm_qkv_kernel(NormQkvArgs a) {
   __shared__ float red[8];
   __shared__ int s_ok;
   const int w = (int)blockIdx.x;
-  const uint32_t value = *a.epoch * 256u + a.tag + 1u;
-  if (w < a.M) {
-    norm_row<T, MAXP>(w, a.part, a.splits, a.M, (T*)a.h, a.ld_h, (const T*)a.gamma, a.eps,
-                      (T*)a.x, (int64_t)a.hidden, a.hidden, red);
+  const uint32_t value = *epoch * 256u + tag + 1u;
+  if (w < M) {
+    norm_row<T, MAXP>(w, part, splits, M, (T*)h, ld_h, (const T*)gamma, a.eps, (T*)a.x,
+                      (int64_t)hidden, hidden, red);
     raise_flag(a.sync, w, value);
     return;
   }
@@ -343,9 +349,11 @@ int launch_norm_qkv(const NormQkvArgs& a, hipStream_t stream) {
   const size_t lds = (size_t)max(kMaxPer * 16 * MB * kRowB, kOneWgLds);
   const dim3 grid((unsigned)(a.M + a.tiles * a.qsplits));
   if (a.hidden <= 2048)
-    hipLaunchKernelGGL((norm_qkv_kernel<T, MB, 1>), grid, dim3(kThreads), lds, stream, a);
+    hipLaunchKernelGGL((norm_qkv_kernel<T, MB, 1>), grid, dim3(kThreads), lds, stream, a.part, a.h,
+                       a.ld_h, a.gamma, a.epoch, a.M, a.splits, a.hidden, a.tag, a);
   else
-    hipLaunchKernelGGL((norm_qkv_kernel<T, MB, 2>), grid, dim3(kThreads), lds, stream, a);
+    hipLaunchKernelGGL((norm_qkv_kernel<T, MB, 2>), grid, dim3(kThreads), lds, stream, a.part, a.h,
+                       a.ld_h, a.gamma, a.epoch, a.M, a.splits, a.hidden, a.tag, a);
   LL_RETURN_LAUNCH();
 }
 

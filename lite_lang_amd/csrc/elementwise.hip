@@ -775,9 +775,18 @@ __device__ __forceinline__ float ll_sum_splits(const float* __restrict__ part, i
 // rule: s = max |out| / 127, 1 for a zero row) into qout / qscale.
 template <typename T, int BLOCK, int MAXP>
 __global__ __launch_bounds__(BLOCK) void add_rmsnorm_splitk_kernel(
-    T* __restrict__ h, int64_t h_rs, LLPartials P, const T* __restrict__ gamma,
-    T* __restrict__ out, int64_t o_rs, int M, int N, float eps, int8_t* __restrict__ qout,
-    int64_t ldq, float* __restrict__ qscale) {
+    T* __restrict__ h, int64_t h_rs, const T* __restrict__ gamma, const void* __restrict__ part,
+    int64_t part_sstride, int N, int splits_i32, LLPartials Pa, T* __restrict__ out, int64_t o_rs,
+    int M, float eps, int8_t* __restrict__ qout, int64_t ldq, float* __restrict__ qscale) {
+  // the first loads' fields (residual, gamma, partials, row length) are the
+  // leading scalar arguments, which gfx950 preloads into SGPRs at dispatch,
+  // so those loads do not wait for the load of the argument block; Pa
+  // supplies the int32 partials' scales. splits_i32: splits | i32 << 16.
+  LLPartials P = Pa;
+  P.p = part;
+  P.sstride = part_sstride;
+  P.splits = splits_i32 & 0xffff;
+  P.i32 = splits_i32 >> 16;
   constexpr int PER = 4;
   const int row = blockIdx.x;
   T* hr = h + (int64_t)row * h_rs;
@@ -857,8 +866,9 @@ void launch_add_rmsnorm_t(void* h, int64_t h_rs, const LLPartials& P, const void
                           int64_t o_rs, int64_t M, int64_t N, float eps, int8_t* qout, int64_t ldq,
                           float* qscale, hipStream_t stream) {
   hipLaunchKernelGGL((add_rmsnorm_splitk_kernel<T, 512, MAXP>), dim3((unsigned)M), dim3(512), 0,
-                     stream, (T*)h, h_rs, P, (const T*)gamma, (T*)out, o_rs, (int)M, (int)N, eps,
-                     qout, ldq, qscale);
+                     stream, (T*)h, h_rs, (const T*)gamma, P.p, P.sstride, (int)N,
+                     P.splits | (P.i32 ? 1 << 16 : 0), P, (T*)out, o_rs, (int)M, eps, qout, ldq,
+                     qscale);
 }
 
 int launch_add_rmsnorm(void* h, int64_t h_row_stride, const LLPartials& P, const void* gamma,
@@ -883,9 +893,10 @@ extern "C" int ll_add_rmsnorm_splitk(void* h, int64_t h_row_stride, const float*
                                      int64_t M, int64_t N, float eps, int dtype,
                                      hipStream_t stream) {
   LL_CHECK_ARG(h && part && gamma && out, "ll_add_rmsnorm_splitk: null pointer");
-  LL_CHECK_ARG(splits >= 1 && N > 0 && N % 4 == 0 && N <= 4 * 512 * 4,
-               "ll_add_rmsnorm_splitk: N must be a multiple of 4 and <= 8192 (N=%lld)",
-               (long long)N);
+  LL_CHECK_ARG(splits >= 1 && splits < (1 << 16) && N > 0 && N % 4 == 0 && N <= 4 * 512 * 4,
+               "ll_add_rmsnorm_splitk: N must be a multiple of 4 and <= 8192 (N=%lld), "
+               "1 <= splits < 65536 (splits=%d)",
+               (long long)N, splits);
   LL_CHECK_ARG(((uintptr_t)part) % 16 == 0, "ll_add_rmsnorm_splitk: partials must be 16 B aligned");
   if (M == 0) return LL_OK;
   return launch_add_rmsnorm(h, h_row_stride, ll_partials_f32(part, splits, M * N), gamma, out,
@@ -899,9 +910,10 @@ extern "C" int ll_add_rmsnorm_splitk_i32(void* h, int64_t h_row_stride, const in
                                          int dtype, int8_t* q_out, int64_t ldq, float* q_scale,
                                          hipStream_t stream) {
   LL_CHECK_ARG(h && part && s_tok && s_ch && gamma && out, "ll_add_rmsnorm_splitk_i32: null pointer");
-  LL_CHECK_ARG(splits >= 1 && N > 0 && N % 4 == 0 && N <= 4 * 512 * 4,
-               "ll_add_rmsnorm_splitk_i32: N must be a multiple of 4 and <= 8192 (N=%lld)",
-               (long long)N);
+  LL_CHECK_ARG(splits >= 1 && splits < (1 << 16) && N > 0 && N % 4 == 0 && N <= 4 * 512 * 4,
+               "ll_add_rmsnorm_splitk_i32: N must be a multiple of 4 and <= 8192 (N=%lld), "
+               "1 <= splits < 65536 (splits=%d)",
+               (long long)N, splits);
   LL_CHECK_ARG(((uintptr_t)part) % 16 == 0, "ll_add_rmsnorm_splitk_i32: partials must be 16 B aligned");
   LL_CHECK_ARG((q_out == nullptr) == (q_scale == nullptr) && (q_out == nullptr || ldq >= N),
                "ll_add_rmsnorm_splitk_i32: q_out and q_scale go together (ldq >= N)");
