@@ -132,10 +132,13 @@ struct I8Epi {
 template <typename T, int MB, int NST, bool PK, int EPI = 0, int TR = 64, typename TO = T>
 __global__ __launch_bounds__(256) void gemm_dma_kernel(const T* __restrict__ X, int64_t ldx,
                                                        const T* __restrict__ W, int64_t ldw,
+                                                       int M, int N, int K, int ksps, int rotate,
                                                        const T* __restrict__ bias,
                                                        T* __restrict__ Y, int64_t ldy,
-                                                       float* __restrict__ part, int M, int N,
-                                                       int K, int ksps, int rotate, I8Epi e8) {
+                                                       float* __restrict__ part, I8Epi e8) {
+  // (what the first stage's copies need leads the list: gfx950 preloads the
+  // leading 16 SGPRs of scalar arguments at dispatch, so those copies do not
+  // wait for the load of the rest)
   static_assert(NST >= 2 && NST <= 4, "2 to 4 stage buffers");
   typedef typename Vec8<T>::type V8;
   typedef typename AccOf<T>::type AccT;
@@ -842,7 +845,7 @@ void launch_skinny_mb(const SkinnyPlan& p, const T* X, int64_t ldx, const T* W, 
     const size_t lds = (size_t)p.nst * (p.tr + 16 * MB) * 256;
 #define LL_DMA_LAUNCH(S, PKD, TR_)                                                              \
   hipLaunchKernelGGL((gemm_dma_kernel<T, MB, S, PKD, 0, TR_, TO>), grid, dim3(256), lds, stream, X, \
-                     ldx, W, ldw, bias, Y, ldy, part, M, N, K, p.ksps, p.rotate, I8Epi{})
+                     ldx, W, ldw, M, N, K, p.ksps, p.rotate, bias, Y, ldy, part, I8Epi{})
     if (p.tr == 128) {
       if (p.packed) LL_DMA_LAUNCH(3, true, 128); else LL_DMA_LAUNCH(3, false, 128);
       return;
@@ -1039,20 +1042,20 @@ extern "C" int ll_gemm_gate_up_silu_packed(const void* X, int64_t ldx, const voi
     const size_t lds = (size_t)nst * (tr + 16 * MB_) * kDmaKC * 2;                              \
     if (tr == 96)                                                                               \
       hipLaunchKernelGGL((gemm_dma_kernel<T, MB_, 3, true, 1, 96>), grid, dim3(256), lds,        \
-                         stream, x, ldx, w, K, nullptr, y, ld_act, nullptr, (int)M, (int)(2 * I), \
-                         (int)K, ksps, 0, I8Epi{});                                             \
+                         stream, x, ldx, w, K, (int)M, (int)(2 * I), (int)K, ksps, 0, nullptr, y, \
+                         ld_act, nullptr, I8Epi{});                                             \
     else if (tr == 128)                                                                         \
       hipLaunchKernelGGL((gemm_dma_kernel<T, MB_, 3, true, 1, 128>), grid, dim3(256), lds,       \
-                         stream, x, ldx, w, K, nullptr, y, ld_act, nullptr, (int)M, (int)(2 * I), \
-                         (int)K, ksps, 0, I8Epi{});                                             \
+                         stream, x, ldx, w, K, (int)M, (int)(2 * I), (int)K, ksps, 0, nullptr, y, \
+                         ld_act, nullptr, I8Epi{});                                             \
     else if (nst == 3)                                                                          \
       hipLaunchKernelGGL((gemm_dma_kernel<T, MB_, 3, true, 1>), grid, dim3(256), lds, stream, x, \
-                         ldx, w, K, nullptr, y, ld_act, nullptr, (int)M, (int)(2 * I), (int)K,  \
-                         ksps, 0, I8Epi{});                                                     \
+                         ldx, w, K, (int)M, (int)(2 * I), (int)K, ksps, 0, nullptr, y, ld_act,  \
+                         nullptr, I8Epi{});                                                     \
     else                                                                                        \
       hipLaunchKernelGGL((gemm_dma_kernel<T, MB_, 2, true, 1>), grid, dim3(256), lds, stream, x, \
-                         ldx, w, K, nullptr, y, ld_act, nullptr, (int)M, (int)(2 * I), (int)K,  \
-                         ksps, 0, I8Epi{});                                                     \
+                         ldx, w, K, (int)M, (int)(2 * I), (int)K, ksps, 0, nullptr, y, ld_act,  \
+                         nullptr, I8Epi{});                                                     \
   } while (0)
     switch ((M + 15) / 16) {
       case 1: LL_GU(1); break;
@@ -1335,8 +1338,8 @@ void launch_argmax_mb(const SkinnyPlan& p, const T* X, int64_t ldx, const T* Wp,
   e.am_idx = am_idx;
 #define LL_AM_LAUNCH(S, TR_)                                                                      \
   hipLaunchKernelGGL((gemm_dma_kernel<T, MB, S, true, 2, TR_, float>), grid, dim3(256), lds,       \
-                     stream, X, ldx, Wp, (int64_t)K, bias, (T*)(void*)Y, ldy, nullptr, M, N, K,    \
-                     p.ksps, 0, e)
+                     stream, X, ldx, Wp, (int64_t)K, M, N, K, p.ksps, 0, bias, (T*)(void*)Y, ldy,  \
+                     nullptr, e)
   if (p.tr == 128) LL_AM_LAUNCH(3, 128);
   else if (p.nst == 3) LL_AM_LAUNCH(3, 64);
   else LL_AM_LAUNCH(2, 64);
@@ -1490,8 +1493,8 @@ void launch_i8_gate_up(const int8_t* x, int64_t ldx, const int8_t* w, int64_t M,
                        int64_t K, unsigned tiles, const I8Epi& e, hipStream_t stream) {
   const size_t lds = (size_t)NST * (TR + 16 * MB) * 256;
   hipLaunchKernelGGL((gemm_dma_kernel<int8_t, MB, NST, true, 1, TR, TO>), dim3(tiles, 1),
-                     dim3(256), lds, stream, x, ldx, w, K, nullptr, nullptr, 0, nullptr, (int)M,
-                     (int)(2 * I), (int)K, (int)(K / 64), 0, e);
+                     dim3(256), lds, stream, x, ldx, w, K, (int)M, (int)(2 * I), (int)K,
+                     (int)(K / 64), 0, nullptr, nullptr, 0, nullptr, e);
 }
 
 template <int MB, typename TO>
