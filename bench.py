@@ -44,7 +44,7 @@ B, PROMPT = 40, 600
 # rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of `bench.py --attention-only`,
 # scaled by what the counters read for a 256 MiB copy (fetch x2.0, write x1.0).
 # Measured on the current kernels; re-measure when they change.
-ATTN_TRAFFIC_BYTES = 25655985
+ATTN_TRAFFIC_BYTES = 25676232
 
 
 def log(msg):
