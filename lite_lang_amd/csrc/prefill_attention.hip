@@ -118,8 +118,16 @@ template <int WPH_> struct FaShape {
   static constexpr int BQ = WPH * RW;    // query rows of one head per workgroup
 };
 
+// The fields of the first loads (lengths, shared prefixes, start offsets,
+// request rows and the grid geometry) come as scalar arguments ahead of the
+// PrefillArgs block: gfx950 preloads leading scalar kernel arguments into
+// SGPRs at dispatch, so those loads do not wait for the argument block's
+// load. idx64: bit 0 lengths, 1 shared, 2 starts, 3 request rows are int64.
 template <typename T, int D, int WPH>
-__global__ __launch_bounds__(512) void prefill_attn_fa_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(512) void prefill_attn_fa_kernel(
+    const void* __restrict__ p_len, const void* __restrict__ p_shared,
+    const void* __restrict__ p_start, const void* __restrict__ p_rid, int idx64, int nblk, int B,
+    int KVH, int G, PrefillArgs a) {
   typedef typename Vec8<T>::type V8;
   typedef FaGeom<D> FG;
   typedef FaShape<WPH> SH;
@@ -133,28 +141,30 @@ __global__ __launch_bounds__(512) void prefill_attn_fa_kernel(PrefillArgs a) {
   // head groups of one (row block, request, KV head) unit take consecutive
   // slots of the same XCD and read its K/V tiles through one L2; the longest
   // (last) row blocks are dispatched first
-  const int HP = (a.G + SH::HPW - 1) / SH::HPW;  // head groups per KV head
+  const int HP = (G + SH::HPW - 1) / SH::HPW;  // head groups per KV head
   const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
   const int unit = (slot / HP) * 8 + xcd;
-  if (unit >= a.nblk * a.B * a.KVH) return;
+  if (unit >= nblk * B * KVH) return;
   const int hp = slot % HP;
-  const int kvh = unit % a.KVH;
-  const int b = (unit / a.KVH) % a.B;
-  const int mblk = a.nblk - 1 - unit / (a.KVH * a.B);
+  const int kvh = unit % KVH;
+  const int b = (unit / KVH) % B;
+  const int mblk = nblk - 1 - unit / (KVH * B);
+  // every per-request value in one round trip (the start and the request
+  // row too, although a workgroup past its request's rows does not use them)
+  const int64_t L = ll_load_idx(p_len, b, idx64 & 1);
+  const int64_t S = p_shared ? ll_load_idx(p_shared, b, (idx64 >> 1) & 1) : 0;
+  const int64_t start = ll_load_idx(p_start, b, (idx64 >> 2) & 1);
+  const int64_t rid = ll_load_idx(p_rid, b, (idx64 >> 3) & 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int l32 = lane & 31, hf = lane >> 5;
   const int gh = SH::HPW * hp + wave / SH::WPH;  // head within the KV head's group
-  const bool head_ok = gh < a.G;
-  const int h = kvh * a.G + (head_ok ? gh : 0);
+  const bool head_ok = gh < G;
+  const int h = kvh * G + (head_ok ? gh : 0);
 
-  const int64_t L = ll_load_idx(a.seq_len, b, a.len64);
-  const int64_t S = a.shared ? ll_load_idx(a.shared, b, a.shared64) : 0;
   const int64_t qlen = L - S;
   const int64_t blk0 = (int64_t)mblk * SH::BQ;
   if (blk0 >= qlen) return;
-  const int64_t start = ll_load_idx(a.start_loc, b, a.start64);
-  const int64_t rid = ll_load_idx(a.req_idx, b, a.req64);
   const int32_t* slot_row = a.r2t + rid * a.r2t_s;
   // token indices within a request fit in 32 bits (lengths below 2^31)
   const int row0 = (int)blk0 + SH::RW * (wave % SH::WPH);  // this wave's first query row
@@ -521,8 +531,14 @@ extern "C" int ll_prefill_attention(const void* q, int64_t q_stride_tok, int64_t
     typedef decltype(tag) T;
     constexpr int D = decltype(dtag)::value;
     constexpr size_t lds = kStages * FaGeom<D>::STAGE_B + 8 * kStages * kBK * 4;
-    if (wph == 2) hipLaunchKernelGGL((prefill_attn_fa_kernel<T, D, 2>), grid, block, lds, stream, a);
-    else hipLaunchKernelGGL((prefill_attn_fa_kernel<T, D, 4>), grid, block, lds, stream, a);
+    const int idx64 = (a.len64 ? 1 : 0) | (a.shared64 ? 2 : 0) | (a.start64 ? 4 : 0) |
+                      (a.req64 ? 8 : 0);
+    if (wph == 2)
+      hipLaunchKernelGGL((prefill_attn_fa_kernel<T, D, 2>), grid, block, lds, stream, a.seq_len,
+                         a.shared, a.start_loc, a.req_idx, idx64, a.nblk, a.B, a.KVH, a.G, a);
+    else
+      hipLaunchKernelGGL((prefill_attn_fa_kernel<T, D, 4>), grid, block, lds, stream, a.seq_len,
+                         a.shared, a.start_loc, a.req_idx, idx64, a.nblk, a.B, a.KVH, a.G, a);
   };
   typedef std::integral_constant<int, 128> D128;
   typedef std::integral_constant<int, 64> D64;
