@@ -194,12 +194,17 @@ int ll_embedding_rmsnorm(const void* table, int64_t table_row_stride, int64_t vo
 /* ll_embedding_rmsnorm that also adds 1 to *epoch (ntok >= 1): the decode
  * step's first launch advances the epoch that the step's
  * ll_add_rmsnorm_qkv_splitk calls read, so the step needs no launch of its
- * own for it. Same reference lines as ll_embedding_rmsnorm. */
+ * own for it. With a non-NULL req_to_tokens the same launch also does
+ * ll_assign_slots(req_to_tokens, req_to_tokens_stride, slots, rows, cols,
+ * ntok), the step's slot-table update (again no launch of its own). Same
+ * reference lines as ll_embedding_rmsnorm and ll_assign_slots. */
 int ll_embedding_rmsnorm_epoch(const void* table, int64_t table_row_stride, int64_t vocab,
                                const void* ids, int ids_i64, void* h, int64_t h_row_stride,
                                const void* gamma, void* out, int64_t out_row_stride,
                                int64_t ntok, int64_t hidden, float eps, int dtype,
-                               uint32_t* epoch, hipStream_t stream);
+                               uint32_t* epoch, int32_t* req_to_tokens,
+                               int64_t req_to_tokens_stride, const int32_t* slots,
+                               const int32_t* rows, const int32_t* cols, hipStream_t stream);
 /* out[t, :] = table[ids[t], :].
  * Replaces torch.embedding in Qwen2PreLayer.Forward
  *   (litelang/models/qwen2/layer/pre_layer.py:15-19).

@@ -44,7 +44,7 @@ SIGNATURES = {
     "ll_silu_and_mul": (I32, [P, I64, P, I64, I64, I64, I32, P]),
     "ll_embedding_rmsnorm": (I32, [P, I64, I64, P, I32, P, I64, P, P, I64, I64, I64, F32, I32, P]),
     "ll_embedding_rmsnorm_epoch": (I32, [P, I64, I64, P, I32, P, I64, P, P, I64, I64, I64, F32,
-                                         I32, P, P]),
+                                         I32, P, P, I64, P, P, P, P]),
     "ll_embedding": (I32, [P, I64, I64, P, I32, P, I64, I64, I64, I32, P]),
     "ll_argmax_workspace_size": (I64, [I64, I64]),
     "ll_argmax": (I32, [P, I64, I64, I64, P, P, I64, I32, P]),

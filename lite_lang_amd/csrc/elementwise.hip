@@ -27,6 +27,23 @@ extern "C" const char* ll_last_error(void) { return g_err; }
 extern "C" int ll_version(void) { return LL_ABI_VERSION; }
 
 // ============================================================== RMSNorm
+// An optional slot-table update done by a launch: req_to_tokens[rows[i],
+// cols[i]] = slots[i] by thread 0 of grid row i (ll_assign_slots's update,
+// folded into the decode step's first launch so that the step needs no
+// launch of its own for it). r2t == nullptr: none.
+struct LLSlotWrite {
+  int32_t* r2t;
+  int64_t stride;
+  const int32_t* slots;
+  const int32_t* rows;
+  const int32_t* cols;
+};
+
+__device__ __forceinline__ void ll_slot_write(const LLSlotWrite& sw, int row) {
+  if (sw.r2t != nullptr && threadIdx.x == 0)
+    sw.r2t[(int64_t)sw.rows[row] * sw.stride + sw.cols[row]] = sw.slots[row];
+}
+
 // One workgroup per row. Pass 1 accumulates sum(x^2) in fp32, pass 2 scales.
 // If `residual` is non-null the kernel first forms h = T(x + residual), stores
 // it back into x (the reference's `hidden_states.add_()` at
@@ -39,9 +56,10 @@ __global__ __launch_bounds__(BLOCK) void rmsnorm_kernel(
     T* __restrict__ x, int64_t x_rs, const T* __restrict__ residual, int64_t r_rs,
     const T* __restrict__ gamma, T* __restrict__ out, int64_t o_rs, int N, float eps,
     const T* __restrict__ table, int64_t tab_rs, const void* ids, int ids64, int64_t vocab,
-    uint32_t* __restrict__ bump) {
+    uint32_t* __restrict__ bump, LLSlotWrite sw) {
   const int row = blockIdx.x;
   if (bump != nullptr && row == 0 && threadIdx.x == 0) *bump += 1u;
+  ll_slot_write(sw, row);
   T* xr = x + (int64_t)row * x_rs;
   T* orow = out + (int64_t)row * o_rs;
   float ss = 0.f;
@@ -94,10 +112,11 @@ __global__ __launch_bounds__(256) void rmsnorm_vec8_kernel(
     T* __restrict__ x, int64_t x_rs, const T* __restrict__ residual, int64_t r_rs,
     const T* __restrict__ gamma, T* __restrict__ out, int64_t o_rs, int N, float eps,
     const T* __restrict__ table, int64_t tab_rs, const void* ids, int ids64, int64_t vocab,
-    uint32_t* __restrict__ bump) {
+    uint32_t* __restrict__ bump, LLSlotWrite sw) {
   typedef T V8 __attribute__((ext_vector_type(8)));
   const int row = blockIdx.x, nch = N / 8;
   if (bump != nullptr && row == 0 && threadIdx.x == 0) *bump += 1u;
+  ll_slot_write(sw, row);
   T* xr = x + (int64_t)row * x_rs;
   const T* src = xr;
   if (table != nullptr) {
@@ -153,7 +172,7 @@ template <typename T>
 int launch_rmsnorm(T* x, int64_t x_rs, const T* residual, int64_t r_rs, const T* gamma, T* out,
                    int64_t o_rs, int64_t M, int64_t N, float eps, const T* table, int64_t tab_rs,
                    const void* ids, int ids64, int64_t vocab, hipStream_t stream,
-                   uint32_t* bump = nullptr) {
+                   uint32_t* bump = nullptr, const LLSlotWrite& sw = LLSlotWrite{}) {
   const auto al16 = [](const void* p, int64_t rs) {
     return ((uintptr_t)p % 16) == 0 && (rs * (int64_t)sizeof(T)) % 16 == 0;
   };
@@ -164,7 +183,7 @@ int launch_rmsnorm(T* x, int64_t x_rs, const T* residual, int64_t r_rs, const T*
     const int C = (int)((N + 2047) / 2048);
     auto go = [&](auto kern) {
       hipLaunchKernelGGL(kern, dim3((unsigned)M), dim3(256), 0, stream, x, x_rs, residual, r_rs,
-                         gamma, out, o_rs, (int)N, eps, table, tab_rs, ids, ids64, vocab, bump);
+                         gamma, out, o_rs, (int)N, eps, table, tab_rs, ids, ids64, vocab, bump, sw);
     };
     if (C == 1) go(rmsnorm_vec8_kernel<T, 1>);
     else if (C == 2) go(rmsnorm_vec8_kernel<T, 2>);
@@ -173,7 +192,7 @@ int launch_rmsnorm(T* x, int64_t x_rs, const T* residual, int64_t r_rs, const T*
   } else {
     hipLaunchKernelGGL((rmsnorm_kernel<T, 256>), dim3((unsigned)M), dim3(256), 0, stream, x, x_rs,
                        residual, r_rs, gamma, out, o_rs, (int)N, eps, table, tab_rs, ids, ids64,
-                       vocab, bump);
+                       vocab, bump, sw);
   }
   LL_RETURN_LAUNCH();
 }
@@ -198,20 +217,21 @@ extern "C" int ll_rmsnorm(void* x, int64_t x_row_stride, const void* residual,
 // non-null `epoch`, the launch also adds 1 to that word (the decode step's
 // epoch, which the step's fused launches read to tell their flags from the
 // previous step's): the first launch of a decode step does it, so the step
-// needs no launch of its own for it.
+// needs no launch of its own for it. The same launch can also do the step's
+// slot-table update (sw).
 namespace {
 int embedding_rmsnorm_impl(const void* table, int64_t table_row_stride, int64_t vocab,
                            const void* ids, int ids_i64, void* h, int64_t h_row_stride,
                            const void* gamma, void* out, int64_t out_row_stride, int64_t ntok,
                            int64_t hidden, float eps, int dtype, uint32_t* epoch,
-                           hipStream_t stream) {
+                           const LLSlotWrite& sw, hipStream_t stream) {
   LL_CHECK_ARG(table && ids && h && gamma && out, "ll_embedding_rmsnorm: null pointer");
   LL_CHECK_ARG(vocab > 0 && ntok >= 0 && hidden > 0, "ll_embedding_rmsnorm: bad shape");
   if (ntok == 0) return LL_OK;
   return LL_DISPATCH_DTYPE(dtype, T, [&]() -> int {
     return launch_rmsnorm<T>((T*)h, h_row_stride, nullptr, 0, (const T*)gamma, (T*)out,
                              out_row_stride, ntok, hidden, eps, (const T*)table, table_row_stride,
-                             ids, ids_i64, vocab, stream, epoch);
+                             ids, ids_i64, vocab, stream, epoch, sw);
   });
 }
 }  // namespace
@@ -223,7 +243,7 @@ extern "C" int ll_embedding_rmsnorm(const void* table, int64_t table_row_stride,
                                     hipStream_t stream) {
   return embedding_rmsnorm_impl(table, table_row_stride, vocab, ids, ids_i64, h, h_row_stride,
                                 gamma, out, out_row_stride, ntok, hidden, eps, dtype, nullptr,
-                                stream);
+                                LLSlotWrite{}, stream);
 }
 
 extern "C" int ll_embedding_rmsnorm_epoch(const void* table, int64_t table_row_stride,
@@ -231,12 +251,17 @@ extern "C" int ll_embedding_rmsnorm_epoch(const void* table, int64_t table_row_s
                                           int64_t h_row_stride, const void* gamma, void* out,
                                           int64_t out_row_stride, int64_t ntok, int64_t hidden,
                                           float eps, int dtype, uint32_t* epoch,
-                                          hipStream_t stream) {
+                                          int32_t* req_to_tokens, int64_t req_to_tokens_stride,
+                                          const int32_t* slots, const int32_t* rows,
+                                          const int32_t* cols, hipStream_t stream) {
   LL_CHECK_ARG(epoch != nullptr, "ll_embedding_rmsnorm_epoch: null epoch word");
   LL_CHECK_ARG(ntok > 0, "ll_embedding_rmsnorm_epoch: needs at least one token (the epoch "
                          "is advanced by the launch)");
+  LL_CHECK_ARG(req_to_tokens == nullptr || (slots && rows && cols),
+               "ll_embedding_rmsnorm_epoch: a slot-table update needs slots, rows and cols");
+  const LLSlotWrite sw = {req_to_tokens, req_to_tokens_stride, slots, rows, cols};
   return embedding_rmsnorm_impl(table, table_row_stride, vocab, ids, ids_i64, h, h_row_stride,
-                                gamma, out, out_row_stride, ntok, hidden, eps, dtype, epoch,
+                                gamma, out, out_row_stride, ntok, hidden, eps, dtype, epoch, sw,
                                 stream);
 }
 

@@ -9,7 +9,9 @@ decode forward for a fixed batch size is captured once into a HIP graph:
   * per-step metadata (new slot ids, request rows, slot-table columns,
     positions, lengths) lives in one static int32 device buffer [5, B] that
     the host refreshes with a single pinned upload before each replay;
-  * the slot-table write (ll_assign_slots) is the first node of the graph;
+  * the slot-table write is done by the graph's first launch (the embedding
+    + RMSNorm + epoch launch of the fused layer; ll_assign_slots of its own
+    otherwise);
   * the argmax writes the next tokens straight into the static token buffer
     the embedding of the next replay reads, so consecutive steps chain on the
     device without a host round trip;
@@ -95,9 +97,8 @@ class DecodeGraph:
         torch.cuda.synchronize(dev)
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph, stream=stream):
-            ops.assign_slots(kv_cache.req_to_tokens_, self.meta[0:3], batch_size)
             model.decode_tokens(self.ids, self.meta[3], self.meta[4], self.meta[1], self.meta[0],
-                                kv_cache, max_len, out=self.ids)
+                                kv_cache, max_len, out=self.ids, slot_write=self.meta[0:3])
         self.logits = model.last_logits  # the graph's own logits buffer
         torch.cuda.synchronize(dev)
 

@@ -204,7 +204,7 @@ class Qwen2Model:
         return self.dtype in (torch.bfloat16, torch.float16) and 0 < batch <= 64
 
     def decode_tokens(self, ids, positions, seq_len, rids, slots, kv_cache: PageCache, max_len,
-                      out=None):
+                      out=None, slot_write=None):
         """One decode forward from device-resident metadata only (no host
         reads, so it can be captured in a HIP graph). ids/positions/seq_len
         [B] int32 or int64, rids/slots [B] int32; max_len bounds seq_len.
@@ -214,11 +214,18 @@ class Qwen2Model:
         leave fp32 partials that the next kernel finishes (RoPE + KV scatter,
         residual + RMSNorm) and the gate/up projection applies SiLU_and_Mul in
         its own epilogue, 8 launches per layer; other cases run the generic
-        layer."""
+        layer.
+
+        slot_write: the step's slot-table update (int32 [3, >= B]: slots,
+        request rows, columns), done first: by the step's first launch where
+        that is the embedding + RMSNorm + epoch launch, else by assign_slots."""
         cfg = self.cfg
         H, KVH, D = cfg.num_heads, cfg.num_key_value_heads, cfg.head_dim
         B = ids.shape[0]
         pool, r2t = kv_cache.kv_cache_, kv_cache.req_to_tokens_
+        fuse_qkv = self.fused_decode_ok(B) and self.quant != "w8a8" and self.norm_qkv_splits(B) > 0
+        if slot_write is not None and not fuse_qkv:
+            ops.assign_slots(r2t, slot_write, B)
         if not self.fused_decode_ok(B):
             h = ops.embedding(self.w.embed, ids)
 
@@ -244,10 +251,11 @@ class Qwen2Model:
         # finishes the previous layer (residual + RMSNorm + QKV projection);
         # those launches tell this step's flags by the epoch, which the
         # step's first launch advances
-        fuse_qkv = self.norm_qkv_splits(B) > 0
         epoch = ops.decode_epoch(dev) if fuse_qkv else None
         h, x = ops.embedding_rmsnorm(w.embed, ids, w.layers[0]["ln1"], cfg.rms_norm_eps,
-                                     epoch=epoch)
+                                     epoch=epoch,
+                                     slot_write=(r2t, slot_write) if fuse_qkv and slot_write
+                                     is not None else None)
 
         def proj(xin, lw, pk, name):
             if pk.get(name) is not None:

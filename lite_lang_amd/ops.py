@@ -277,9 +277,11 @@ def embedding(table, ids, out=None):
     return out
 
 
-def embedding_rmsnorm(table, ids, gamma, eps, epoch=None):
+def embedding_rmsnorm(table, ids, gamma, eps, epoch=None, slot_write=None):
     """(h, out): h = table[ids], out = rmsnorm(h) * gamma, in one launch. With
-    `epoch` (the int32 word of decode_epoch), the launch also adds 1 to it."""
+    `epoch` (the int32 word of decode_epoch), the launch also adds 1 to it;
+    with slot_write = (req_to_tokens, packed) (and epoch), it also does
+    assign_slots(req_to_tokens, packed, len(ids))."""
     _dev(table, ids, gamma, epoch)
     V, Hd = table.shape
     T = ids.shape[0]
@@ -290,10 +292,19 @@ def embedding_rmsnorm(table, ids, gamma, eps, epoch=None):
             h.stride(0), gamma.data_ptr(), out.data_ptr(), out.stride(0), T, Hd, float(eps),
             dtype_code(table))
     if epoch is None:
+        assert slot_write is None, "embedding_rmsnorm: slot_write needs the epoch form"
         rc = _L.ll_embedding_rmsnorm(*head, _stream(table))
     else:
         assert epoch.dtype == torch.int32 and epoch.numel() == 1
-        rc = _L.ll_embedding_rmsnorm_epoch(*head, epoch.data_ptr(), _stream(table))
+        sw = (None, 0, None, None, None)
+        if slot_write is not None:
+            r2t, packed = slot_write
+            _dev(r2t, packed)
+            assert r2t.dtype == torch.int32 and r2t.stride(1) == 1
+            assert packed.dtype == torch.int32 and packed.shape[0] == 3 and packed.shape[1] >= T
+            sw = (r2t.data_ptr(), r2t.stride(0), packed[0].data_ptr(), packed[1].data_ptr(),
+                  packed[2].data_ptr())
+        rc = _L.ll_embedding_rmsnorm_epoch(*head, epoch.data_ptr(), *sw, _stream(table))
     _lib.check(rc, "ll_embedding_rmsnorm")
     return h, out
 

@@ -69,5 +69,9 @@ def test_host_only_settings():
     rc = lib.ll_argmax_status(256, 8, 4, 8, 256, None, 0, 2, None, None)
     assert rc == -1 and b"status" in lib.ll_last_error()
     rc = lib.ll_embedding_rmsnorm_epoch(256, 8, 8, 256, 0, 256, 8, 256, 256, 8, 4, 8,
-                                        _lib.F32(1e-6), 2, None, None)
+                                        _lib.F32(1e-6), 2, None, None, 0, None, None, None, None)
     assert rc == -1 and b"epoch" in lib.ll_last_error()
+    # a slot-table update without its slots, rows and columns
+    rc = lib.ll_embedding_rmsnorm_epoch(256, 8, 8, 256, 0, 256, 8, 256, 256, 8, 4, 8,
+                                        _lib.F32(1e-6), 2, 256, 256, 8, None, 256, 256, None)
+    assert rc == -1 and b"slot-table" in lib.ll_last_error()

@@ -57,6 +57,35 @@ def test_embedding_rmsnorm_advances_epoch(cuda):
         assert int(ep.item()) == 42 + k
 
 
+def test_embedding_rmsnorm_slot_write(cuda):
+    """The decode step's slot-table update folded into its first launch:
+    embedding + RMSNorm + epoch with slot_write leaves the table, h and out
+    exactly as assign_slots followed by the same launch without it."""
+    ops = _ops()
+    g = torch.Generator(device=cuda).manual_seed(5)
+    table = torch.randn(1000, 2048, device=cuda, generator=g).bfloat16()
+    gamma = (torch.rand(2048, device=cuda, generator=g) + 0.5).bfloat16()
+    B = 40
+    ids = torch.randint(0, 1000, (B,), device=cuda, generator=g)
+    r2t0 = torch.randint(0, 1 << 20, (48, 720), device=cuda, generator=g, dtype=torch.int32)
+    rows = torch.randperm(48, device=cuda, generator=g)[:B].int()
+    cols = torch.randint(0, 720, (B,), device=cuda, generator=g, dtype=torch.int32)
+    slots = torch.randint(0, 1 << 20, (B,), device=cuda, generator=g, dtype=torch.int32)
+    packed = torch.stack([slots, rows, cols]).contiguous()
+    print("case: embedding rmsnorm slot write B=40", flush=True)
+    want = r2t0.clone()
+    ops.assign_slots(want, packed, B)
+    ep0 = torch.full((1,), 7, dtype=torch.int32, device=cuda)
+    h0, x0 = ops.embedding_rmsnorm(table, ids, gamma, 1e-6, epoch=ep0)
+    got = r2t0.clone()
+    ep1 = torch.full((1,), 7, dtype=torch.int32, device=cuda)
+    h1, x1 = ops.embedding_rmsnorm(table, ids, gamma, 1e-6, epoch=ep1, slot_write=(got, packed))
+    torch.cuda.synchronize()
+    assert torch.equal(got, want) and not torch.equal(got, r2t0)
+    assert torch.equal(h0, h1) and torch.equal(x0, x1)
+    assert int(ep1.item()) == 8
+
+
 def _runner(cuda, graph):
     from lite_lang_amd.models.qwen2 import Qwen2ModelRunner
     from lite_lang_amd.models.qwen2.weights import Qwen2Config
