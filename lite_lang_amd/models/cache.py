@@ -133,10 +133,14 @@ class PageCache:
         s0 = self.physical_free_token_start_
         slots = self.physical_free_token_[s0:s0 + total].copy()
         self.physical_free_token_start_ += total
-        rows = np.repeat(np.asarray(rids, dtype=np.int32), new)
-        offs = np.arange(total, dtype=np.int32) - np.repeat(
-            np.cumsum([0] + new[:-1], dtype=np.int64).astype(np.int32), new)
-        cols = np.repeat(np.asarray(lens, dtype=np.int32), new) + offs
+        if all(v == 1 for v in new):  # one slot per request (a decode step)
+            rows = np.array(rids, dtype=np.int32)
+            cols = np.array(lens, dtype=np.int32)
+        else:
+            rows = np.repeat(np.asarray(rids, dtype=np.int32), new)
+            offs = np.arange(total, dtype=np.int32) - np.repeat(
+                np.cumsum([0] + new[:-1], dtype=np.int64).astype(np.int32), new)
+            cols = np.repeat(np.asarray(lens, dtype=np.int32), new) + offs
         self._check_and_mirror(slots, rows, cols)
         return slots, rows, cols
 
