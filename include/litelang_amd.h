@@ -318,7 +318,9 @@ int ll_gemm(const void* X, int64_t ldx, const void* W, int64_t ldw, const void* 
 int ll_gemm_splitk_count(int64_t M, int64_t N, int64_t K);
 int ll_gemm_splitk(const void* X, int64_t ldx, const void* W, int64_t ldw, int64_t M, int64_t N,
                    int64_t K, int dtype, float* part, int64_t part_bytes, hipStream_t stream);
-/* h = dtype(h + dtype(sum part)); out = rmsnorm(h) * gamma (h updated in place) */
+/* h = dtype(h + dtype(sum part)); out = rmsnorm(h) * gamma (h updated in place).
+ * N a multiple of 4, at most 8192; 1 <= splits < 65536 (also for the _i32
+ * form below). */
 int ll_add_rmsnorm_splitk(void* h, int64_t h_row_stride, const float* part, int splits,
                           const void* gamma, void* out, int64_t out_row_stride, int64_t M,
                           int64_t N, float eps, int dtype, hipStream_t stream);
