@@ -522,29 +522,6 @@ __global__ void interleave_gate_up_kernel(const u32x4* __restrict__ W, int64_t l
   out[u] = W[src * ldw16 + c];
 }
 
-// CUs of the current device, cached per device: the grid holds one
-// workgroup per CU (the LDS ring takes the whole CU), each looping over its
-// tiles.
-int tile_device_cus(int* cus_out) {
-  static std::atomic<int> cache[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) {
-    ll_set_error("hipGetDevice failed");
-    return LL_ERR_HIP;
-  }
-  int n = dev >= 0 && dev < 64 ? cache[dev].load(std::memory_order_relaxed) : 0;
-  if (n <= 0) {
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        n <= 0) {
-      ll_set_error("hipDeviceGetAttribute(MultiprocessorCount) failed");
-      return LL_ERR_HIP;
-    }
-    if (dev >= 0 && dev < 64) cache[dev].store(n, std::memory_order_relaxed);
-  }
-  *cus_out = n;
-  return LL_OK;
-}
-
 // The kernel addresses its copy sources with 32-bit row offsets and its
 // stores with 31-bit buffer offsets: the weight must span less than 4 GiB
 // (checked by the entry points), and the activation and output rows are
@@ -553,7 +530,7 @@ int tile_device_cus(int* cus_out) {
 template <typename T, typename TO, int EPI>
 int launch_tiles(const TileArgs& a0, hipStream_t stream) {
   int cus = 0;
-  const int rc = tile_device_cus(&cus);
+  const int rc = ll_device_cus(&cus);
   if (rc != LL_OK) return rc;
   const int64_t yrow_b = a0.ldy * (int64_t)sizeof(TO);
   const int64_t tiles_n = ll_cdiv(a0.N, kT), nk = a0.K_b / kRB;
@@ -621,6 +598,26 @@ TileArgs make_args(const void* X, int64_t ldx_b, const void* W, int64_t ldw_b, i
 }
 
 }  // namespace
+
+int ll_device_cus(int* cus_out) {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    ll_set_error("hipGetDevice failed");
+    return LL_ERR_HIP;
+  }
+  int n = dev >= 0 && dev < 64 ? cache[dev].load(std::memory_order_relaxed) : 0;
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0) {
+      ll_set_error("hipDeviceGetAttribute(MultiprocessorCount) failed");
+      return LL_ERR_HIP;
+    }
+    if (dev >= 0 && dev < 64) cache[dev].store(n, std::memory_order_relaxed);
+  }
+  *cus_out = n;
+  return LL_OK;
+}
 
 extern "C" int ll_gemm_tiled_supported(int64_t M, int64_t N, int64_t K, int dtype) {
   if (dtype != LL_BF16 && dtype != LL_F16) return 0;

@@ -55,6 +55,9 @@ void ll_set_error(const char* fmt, ...);
 // (ll_decode_sync_set_spin_limit: 0 = each wait's default, n > 0 = n polls,
 // -n = test mode: the wait never sees its data and gives up after n polls).
 int ll_decode_spin_setting();
+// CUs of the current device, cached per device (gemm_tiles.hip): the
+// persistent grids hold one workgroup per CU, each looping over its work.
+int ll_device_cus(int* cus_out);
 
 // Second pass of the first-index argmax over per-row partials [M][nparts]
 // written by another kernel (elementwise.hip).

@@ -246,6 +246,54 @@ def test_prefill_attention_prompt_cache(cuda, dtype):
     assert _maxdiff(out, ref) <= _tol(dtype)
 
 
+@pytest.mark.parametrize("H,KVH,B,maxlen,with_shared", [
+    (16, 2, 300, 260, False),   # 3B geometry: ~1,600 items over 256 workgroups
+    (28, 4, 120, 300, True)])   # odd group (128-row blocks), prompt-cache prefixes
+def test_prefill_attention_many_items_per_workgroup(cuda, H, KVH, B, maxlen, with_shared):
+    """Batches with far more work items (row block, request, KV head, head
+    group) than workgroups, so that each persistent workgroup streams several
+    items back to back, ragged lengths leaving many items empty."""
+    rs = np.random.RandomState(14)
+    lens = rs.randint(1, maxlen + 1, size=B).tolist()
+    shared = [int(rs.randint(0, l)) if with_shared and b % 3 == 0 else 0
+              for b, l in enumerate(lens)]
+    print(f"case: prefill many items H={H} KVH={KVH} B={B}", flush=True)
+    out, ref = _prefill_case(cuda, H, KVH, 128, lens, shared, torch.bfloat16, 15)
+    assert _maxdiff(out, ref) <= _tol(torch.bfloat16)
+
+
+def test_prefill_attention_grid_past_64_passes(cuda):
+    """16,800 work items: more than 64 per CU, so the grid grows past one
+    workgroup per CU. Bit-identical to the same requests launched 16 at a
+    time, where every workgroup takes a single item."""
+    H, KVH, D, B = 4, 4, 64, 4200
+    rs = np.random.RandomState(16)
+    lens = rs.randint(1, 41, size=B)
+    starts = np.concatenate([[0], np.cumsum(lens)[:-1]])
+    T = int(lens.sum())
+    g = torch.Generator().manual_seed(16)
+    q = torch.randn(T, H, D, generator=g).bfloat16().to(cuda)
+    pool = torch.randn(T + 8, 2 * KVH, D, generator=g).bfloat16().to(cuda)
+    r2t = torch.zeros(B, 40, dtype=torch.int32)
+    perm = torch.from_numpy(rs.permutation(T + 8).astype(np.int32))
+    for b in range(B):
+        r2t[b, :lens[b]] = perm[starts[b]:starts[b] + lens[b]]
+    r2t = r2t.to(cuda)
+    rids = torch.arange(B, dtype=torch.int32, device=cuda)
+    st = torch.from_numpy(starts).to(cuda)
+    ln = torch.from_numpy(lens).to(cuda)
+    ops = _ops()
+    print("case: prefill grid past 64 passes", flush=True)
+    whole = torch.empty_like(q)
+    ops.prefill_attention(q, pool[:, :KVH], pool[:, KVH:], whole, rids, st, ln, 40, r2t)
+    parts = torch.empty_like(q)
+    for b0 in range(0, B, 16):
+        ops.prefill_attention(q, pool[:, :KVH], pool[:, KVH:], parts, rids[b0:b0 + 16],
+                              st[b0:b0 + 16], ln[b0:b0 + 16], 40, r2t)
+    torch.cuda.synchronize()
+    assert torch.equal(whole, parts)
+
+
 # ------------------------------------------------------------ elementwise
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_rmsnorm_and_residual(cuda, dtype):
