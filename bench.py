@@ -413,6 +413,44 @@ def bench_config5(dev, steps=300, warmup=2):
             "prefill_s": round(t_prefill, 4), "prefix_tokens_reused": shared}
 
 
+def bench_prefill_attention(dev, reps=20):
+    """The causal prefill attention of 40 x 600-token prompts (the 3B shape,
+    16 query / 2 KV heads, and the 1.5B shape, 12 / 2; head_dim 128, bf16)
+    over a seeded random slot permutation, events around `reps` launches.
+    Causal flops: 4 * head_dim * (keys seen, summed over query rows) per
+    query head."""
+    from lite_lang_amd import ops
+    L, D = PROMPT, 128
+    T = B * L
+    out = {"workload": f"prefill attention {B} x {L}, head_dim {D}, bf16, random slot table"}
+    for H, KVH in ((16, 2), (12, 2)):
+        g = torch.Generator(device=dev).manual_seed(7)
+        q = torch.randn(T, H, D, generator=g, device=dev).bfloat16()
+        pool = torch.randn(T + 64, 2 * KVH, D, generator=g, device=dev).bfloat16()
+        o = torch.empty_like(q)
+        r2t = torch.from_numpy(np.random.RandomState(7).permutation(T).astype(np.int32)).view(B, L).to(dev)
+        rids = torch.arange(B, dtype=torch.int32, device=dev)
+        start = torch.arange(B, dtype=torch.int32, device=dev) * L
+        lens = torch.full((B,), L, dtype=torch.int32, device=dev)
+
+        def run():
+            ops.prefill_attention(q, pool[:, :KVH], pool[:, KVH:], o, rids, start, lens, L, r2t)
+
+        run()
+        torch.cuda.synchronize(dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            run()
+        e1.record()
+        torch.cuda.synchronize(dev)
+        us = e0.elapsed_time(e1) / reps * 1e3
+        flops = 4.0 * D * H * B * (L * (L + 1) / 2)
+        out[f"h{H}_kv{KVH}"] = {"us": round(us, 1), "tflops": round(flops / us / 1e6, 1),
+                                "frac_of_bf16_peak": round(flops / us / 1e6 / 2500.0, 3)}
+    return out
+
+
 def bench_prefill_gemms(dev, M=B * PROMPT, reps=20):
     """The prefill projections of the 3B shape at M = 40 x 600 tokens on the
     tile GEMMs (bf16: qkv, o, gate/up with the SiLU_and_Mul epilogue, down;
@@ -525,6 +563,9 @@ def main():
     ap.add_argument("--prefill-gemm", action="store_true",
                     help="time the 3B prefill projections (M = 24,000) on the tile GEMMs, "
                          "bf16 and W8A8, one JSON line")
+    ap.add_argument("--prefill-attention", action="store_true",
+                    help="time the 40 x 600 causal prefill attention (3B and 1.5B head "
+                         "shapes), one JSON line")
     ap.add_argument("--attention-only", action="store_true",
                     help="run only the config-2 decode attention launches plus a 256 MiB "
                          "device copy of known size (for rocprofv3 --pmc traffic runs)")
@@ -574,6 +615,9 @@ def main():
         return
     if args.prefill_gemm:
         print(json.dumps(bench_prefill_gemms(dev)), flush=True)
+        return
+    if args.prefill_attention:
+        print(json.dumps(bench_prefill_attention(dev)), flush=True)
         return
     if args.norm_qkv:
         src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)

@@ -150,11 +150,14 @@ template <int WPH_> struct FaShape {
 // KV head) 8 apart, so that they take workgroups of one XCD (workgroup i runs
 // on XCD i mod 8, up to a constant rotation) and read its K/V tiles through
 // one L2, and put the longest (last) row blocks first. The grid is
-// persistent: workgroup w takes the items of passes j = 0, 1, ... in snake
-// order, item jP + w on even passes and (j + 1)P - 1 - w on odd ones (P
-// workgroups, at most 64 passes).
+// persistent (P workgroups, P a multiple of 16, at most 64 passes):
+// workgroup w takes item jP + w on even passes j and, on odd passes, the
+// items of its XCD in reverse slot order, (j + 1)P - 8 (w / 8 + 1) + w mod 8
+// (a snake over the slots that keeps item mod 8 = w mod 8, so that the items
+// of one (request, KV head) stay on one XCD whenever 8 divides the items per
+// row block).
 __device__ __forceinline__ int64_t fa_item_of_pass(int j, int P, int w) {
-  return (j & 1) ? (int64_t)(j + 1) * P - 1 - w : (int64_t)j * P + w;
+  return (j & 1) ? (int64_t)(j + 1) * P - 8 * ((w >> 3) + 1) + (w & 7) : (int64_t)j * P + w;
 }
 
 // The fields of the first loads (lengths, shared prefixes, start offsets,
