@@ -126,7 +126,9 @@ int ll_decode_attention_set_same_launch_merge(int enable);
  *   (flash_attn_v2.py:699-762).
  * q / o [T, q_heads, head_dim] hold, for request b, the rows
  * b_start_loc[b] .. b_start_loc[b] + (b_seq_len[b] - shared[b]) - 1; the keys
- * are the first b_seq_len[b] slots of row b_req_idx[b] of req_to_tokens. */
+ * are the first b_seq_len[b] slots of row b_req_idx[b] of req_to_tokens.
+ * The bf16/fp16, head_dim 64/128 path rejects (LL_ERR_ARG) launches of 2^31
+ * or more work items (query-row blocks x requests x KV heads x head groups). */
 int ll_prefill_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_h,
                          const void* k_cache, int64_t k_stride_tok, int64_t k_stride_head,
                          const void* v_cache, int64_t v_stride_tok, int64_t v_stride_head,
