@@ -20,6 +20,9 @@ Also reported on the same JSON line:
                      (688 MB > the 256 MB MALL), HIP events on the stream
                      that replays the launches;
   decode_step        bytes and time of the steady decode step;
+  prefill_attention  the causal prefill attention of the 40 x 600 prompts
+                     (3B and 1.5B head shapes), events around 20 launches,
+                     causal TFLOP/s (bench.py --prefill-attention alone);
   cpu_baseline       the CPU oracle (oracle/qwen2.py) timed on the host
                      cores for a bounded number of full decode steps.
 
@@ -687,6 +690,12 @@ def main():
             configs[name] = {k: v for k, v in sub.items() if k not in ("n_gpus", "higher_is_better")}
             log(f"{name}: {sub.get('value')} {sub.get('unit', '')}")
             torch.cuda.empty_cache()
+    log("prefill attention")
+    try:
+        prefill_attn = bench_prefill_attention(dev)
+    except Exception as e:  # reported in the line, the headline still stands
+        prefill_attn = {"error": repr(e)}
+    torch.cuda.empty_cache()
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -740,6 +749,7 @@ def main():
                                        "(same grid and dependent loads, no arithmetic); "
                                        "bench.py --attention-floor"}},
         "configs": configs,
+        "prefill_attention": prefill_attn,
         "cpu_baseline": cpu,
     }
     print(json.dumps(res), flush=True)
